@@ -1,0 +1,208 @@
+"""Benchmark: config 3 sparse residual block on one MI355X.
+
+Workload: 256^3 grid, 1,040,679 active voxels (shell
+of a seeded union of 8 ellipsoids), C = 128, bf16 activations and weights
+with f32 accumulation.  One step = neighbour-map build for the coords +
+conv3x3x3 -> LayerNorm -> SiLU -> conv3x3x3 -> + x (residual fused into the
+second conv's epilogue).  Inputs are resident in HBM before timing.
+
+Prints one JSON line: value = voxels/s of the whole step; roofline = the
+dominant kernel (the MFMA conv) at its useful FLOPs 2*P*Cin*Cout per launch
+(P = valid (row, offset) pairs), timed with HIP events on the launch stream;
+cpu_baseline = the oracle's restatement of the reference CPU flex path
+(HashMap map + im2col + single-thread sgemm) timed on this host over a
+bounded sample of query rows.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "sparse-conv voxels/s + TFLOP/s (% bf16 MFMA peak), 256^3 grid ~1M voxels C=128"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--cpu-sample", type=int, default=65536,
+                    help="query rows of the CPU baseline sample (0 = skip)")
+    return ap.parse_args()
+
+
+def events_ms(fn, iters):
+    import torch
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(iters):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / iters
+
+
+def cpu_baseline(coords, x_f32, w1, w2, sample_rows):
+    """The reference CPU path (burn_flex_gmm flex: build_neighbor_rows with a
+    HashMap, im2col gather + single-thread sgemm) restated in C (oracle/), on
+    the same step: map build over all N coords + two convs, LN+SiLU and the
+    residual add over `sample_rows` query rows.  voxels/s = 1 / (t_map/N +
+    t_rest/sample)."""
+    import numpy as np
+    from oracle import oracle as O
+    O.build()
+    n = len(coords)
+    cfg = O.OracleConfig(128, 128)
+    b = np.zeros(128, np.float32)
+    t0 = time.perf_counter()
+    nbr = O.build_neighbor_rows(cfg, coords, lowest_row_on_duplicate=False)
+    t_map = time.perf_counter() - t0
+    rows = np.arange(sample_rows)
+    t0 = time.perf_counter()
+    h = O.conv_flex_precomputed(cfg, w1, b, x_f32, nbr[rows])
+    h = O.silu(O.layer_norm(h, None, None, 1e-6))
+    # conv2 reads conv1 output at neighbour rows; the sample's own rows stand in
+    # for the rest of the input (same work per row).
+    h_full = np.zeros_like(x_f32)
+    h_full[rows] = h
+    y = O.conv_flex_precomputed(cfg, w2, b, h_full, nbr[rows]) + x_f32[rows]
+    t_rest = time.perf_counter() - t0
+    assert y.shape == (sample_rows, 128)
+    per_voxel = t_map / n + t_rest / sample_rows
+    return {
+        "value": 1.0 / per_voxel,
+        "unit": "voxels/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"config 3 step: map build over all {n} coords ({t_map:.2f} s) + conv/LN/SiLU/"
+                   f"conv/add over the first {sample_rows} query rows ({t_rest:.2f} s), f32, "
+                   f"oracle/sc_oracle.c restating crates/burn_flex_gmm/src/lib.rs:69-109,242-375"),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the sparse-conv path shards by spatial slab with a halo exchange, not built here)",
+              file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    from bevy_synth_amd import flex_gmm as F
+    from bevy_synth_amd import synth
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    coords = synth.config3_coords()
+    n = len(coords)
+    C = 128
+    rng = np.random.default_rng(2026)
+    x_f32 = synth.bf16_to_f32(synth.bf16_bits(synth.normal_f32(rng, (n, C))))
+    std = 1.0 / np.sqrt(27 * C)
+    w1 = synth.bf16_to_f32(synth.bf16_bits(synth.conv_weight(rng, C, 27, C, std)))
+    w2 = synth.bf16_to_f32(synth.bf16_bits(synth.conv_weight(rng, C, 27, C, std)))
+
+    def to_bf16(a):
+        return torch.from_numpy(synth.bf16_bits(a).view(np.int16)).to(dev).view(torch.bfloat16)
+
+    coords_d = torch.from_numpy(coords).to(dev)
+    x = to_bf16(x_f32)
+    w1_d, w2_d = to_bf16(w1), to_bf16(w2)
+    bias = torch.zeros(C, dtype=torch.float32, device=dev)
+    cfg = F.SparseSubmConvConfig(C, C)
+    nbr = torch.empty((n, 27), dtype=torch.int32, device=dev)
+    ws = F.NeighborMapWorkspace(dev).get(n)
+    h = torch.empty((n, C), dtype=torch.bfloat16, device=dev)
+    out = torch.empty((n, C), dtype=torch.bfloat16, device=dev)
+
+    def map_build():
+        F.neighbor_map_build_into(cfg, coords_d, nbr, ws)
+
+    def conv1():
+        F.sparse_subm_conv_forward(cfg, x, nbr, w1_d, bias, out=h)
+
+    def ln_silu():
+        F.layer_norm(h, eps=1e-6, silu=True, out=h)
+
+    def conv2():
+        F.sparse_subm_conv_forward(cfg, h, nbr, w2_d, bias, residual=x, out=out)
+
+    def step():
+        map_build()
+        conv1()
+        ln_silu()
+        conv2()
+
+    for _ in range(max(args.warmup, 1)):
+        step()
+    F.neighbor_map_check(ws)
+    P = int((nbr >= 0).sum().item())
+    print(f"[bench] config3 voxels={n} pairs={P} warmup done", file=sys.stderr, flush=True)
+
+    torch.cuda.synchronize()
+    ms_step = events_ms(step, args.steps)
+    # Per-kernel launch durations (HIP events on the launch stream).
+    ms_map = events_ms(map_build, args.steps)
+    ms_conv = events_ms(conv1, args.steps)
+    ms_ln = events_ms(ln_silu, args.steps)
+    print(f"[bench] step {ms_step:.3f} ms  map {ms_map:.3f}  conv {ms_conv:.3f}  ln {ms_ln:.3f}",
+          file=sys.stderr, flush=True)
+
+    flops = 2.0 * P * C * C
+    conv_tflops = flops / (ms_conv * 1e-3) / 1e12
+    map_bytes = n * 16 + n * 27 * 4
+    map_gbps = map_bytes / (ms_map * 1e-3) / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("conv_mfma_kernel/config3", None)
+
+    cpu = None
+    if args.cpu_sample > 0:
+        print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(coords, x_f32, w1, w2, args.cpu_sample)
+
+    line = {
+        "metric": METRIC,
+        "value": n / (ms_step * 1e-3),
+        "unit": "voxels/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "config3 sparse residual block (map build + conv3x3x3 -> LN -> SiLU "
+                               "-> conv3x3x3 -> +x), 256^3 ellipsoid-union shell",
+                   "voxels": n, "channels": C, "kernel": "3x3x3", "valid_pairs": P,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "kernel": "conv_mfma_kernel<bf16,bf16,bf16>",
+                     "achieved": conv_tflops, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": conv_tflops / PEAK_BF16_TFLOPS, "traffic": traffic},
+        "components": {
+            "map_build_ms": ms_map, "conv_ms": ms_conv, "ln_silu_ms": ms_ln,
+            "map_build_gbps": map_gbps, "map_build_frac_hbm": map_gbps / PEAK_HBM_GBPS,
+            "conv_useful_tflops": conv_tflops,
+            "conv_issued_tflops_dense27": 2.0 * n * 27 * C * C / (ms_conv * 1e-3) / 1e12,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,413 @@
+// Status plumbing, config helpers and the row-wise block ops (LayerNorm[+SiLU],
+// residual add, row gather, C2S skip add, dtype conversion) for gfx950.
+#include <cmath>
+#include <cstring>
+#include <string>
+
+#include "sc_common.hpp"
+
+namespace sc {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string &msg) { g_last_error = msg; }
+void clear_error() { g_last_error.clear(); }
+
+int fail(int status, const std::string &msg)
+{
+    set_error(msg);
+    return status;
+}
+
+int hip_fail(hipError_t err, const char *what)
+{
+    return fail(SC_ERR_HIP, std::string(what) + ": " + hipGetErrorString(err));
+}
+
+// validate_config, crates/burn_flex_gmm/src/lib.rs:698-725 (same messages).
+int validate_config(const sc_conv_config *c)
+{
+    if (!c) return fail(SC_ERR_NULL, "sparse conv config is NULL");
+    if (c->in_channels <= 0 || c->out_channels <= 0)
+        return fail(SC_ERR_CONFIG, "sparse conv channel dimensions must be non-zero");
+    if (c->kernel_d <= 0 || c->kernel_h <= 0 || c->kernel_w <= 0)
+        return fail(SC_ERR_CONFIG, "sparse conv kernel dimensions must be non-zero");
+    if (c->groups <= 0) return fail(SC_ERR_CONFIG, "sparse conv groups must be non-zero");
+    int64_t t;
+    if (!mul_ok(c->in_channels_per_group, c->groups, &t) || t != c->in_channels)
+        return fail(SC_ERR_CONFIG, "sparse conv in_channels/group mismatch");
+    if (!mul_ok(c->out_channels_per_group, c->groups, &t) || t != c->out_channels)
+        return fail(SC_ERR_CONFIG, "sparse conv out_channels/group mismatch");
+    bool used[3] = {false, false, false};
+    for (int j = 0; j < 3; ++j) {
+        int a = c->axis_order[j];
+        if (a < 0 || a > 2 || used[a])
+            return fail(SC_ERR_CONFIG, "sparse conv axis_order must be a permutation of [0,1,2]");
+        used[a] = true;
+    }
+    int64_t k;
+    if (!mul_ok(c->kernel_d, c->kernel_h, &k) || !mul_ok(k, c->kernel_w, &k) || k > INT32_MAX)
+        return fail(SC_ERR_OVERFLOW, "sparse conv kernel rows overflow");
+    return SC_OK;
+}
+
+// ------------------------------------------------------------- kernels
+
+template <typename Tin, typename Tout>
+__global__ void convert_kernel(const Tin *__restrict__ in, Tout *__restrict__ out, int64_t n)
+{
+    int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        store_from_f32<Tout>(out, i, load_as_f32<Tin>(in, i));
+}
+
+template <typename T>
+__global__ void add_kernel(const T *__restrict__ a, const T *__restrict__ b, T *out, int64_t n)
+{
+    int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        store_from_f32<T>(out, i, load_as_f32<T>(a, i) + load_as_f32<T>(b, i));
+}
+
+// One wave64 per row, VPL values per lane held in registers (channels <=
+// 64*VPL).  Two-pass mean / biased variance in f32, as
+// layer_norm_row_stats_kernel (crates/burn_flex_gmm/src/wgpu/ops.rs:162-187)
+// and layer_norm_affine_silu_kernel (:418-446); the wave reduction sums in a
+// fixed tree order.
+template <typename Tin, typename Tout, int VPL>
+__global__ __launch_bounds__(256) void layer_norm_kernel(const Tin *in, int64_t rows, int channels,
+                                                         const float *__restrict__ w,
+                                                         const float *__restrict__ b, float eps,
+                                                         int apply_silu, Tout *out)
+{
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const Tin *x = in + row * channels;
+    float v[VPL];
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        int j = lane + 64 * i;
+        v[i] = j < channels ? load_as_f32<Tin>(x, j) : 0.f;
+        s += v[i];
+    }
+    const float inv_c = 1.0f / (float)channels;
+    const float mean = wave_sum(s) * inv_c;
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        int j = lane + 64 * i;
+        float d = v[i] - mean;
+        q += j < channels ? d * d : 0.f;
+    }
+    const float var = wave_sum(q) * inv_c;
+    const float inv_std = 1.0f / sqrtf(var + eps);
+    Tout *y = out + row * channels;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        int j = lane + 64 * i;
+        if (j < channels) {
+            float t = (v[i] - mean) * inv_std;
+            if (w) t *= w[j];
+            if (b) t += b[j];
+            if (apply_silu) t = t / (1.0f + expf(-t));
+            store_from_f32<Tout>(y, j, t);
+        }
+    }
+}
+
+// Same computation for rows wider than 1024 channels: three passes over the
+// row (it stays in L1/L2 between passes).
+template <typename Tin, typename Tout>
+__global__ __launch_bounds__(256) void layer_norm_wide_kernel(const Tin *in, int64_t rows,
+                                                              int channels,
+                                                              const float *__restrict__ w,
+                                                              const float *__restrict__ b,
+                                                              float eps, int apply_silu, Tout *out)
+{
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const Tin *x = in + row * channels;
+    float s = 0.f;
+    for (int j = lane; j < channels; j += 64) s += load_as_f32<Tin>(x, j);
+    const float inv_c = 1.0f / (float)channels;
+    const float mean = wave_sum(s) * inv_c;
+    float q = 0.f;
+    for (int j = lane; j < channels; j += 64) {
+        float d = load_as_f32<Tin>(x, j) - mean;
+        q += d * d;
+    }
+    const float inv_std = 1.0f / sqrtf(wave_sum(q) * inv_c + eps);
+    Tout *y = out + row * channels;
+    for (int j = lane; j < channels; j += 64) {
+        float t = (load_as_f32<Tin>(x, j) - mean) * inv_std;
+        if (w) t *= w[j];
+        if (b) t += b[j];
+        if (apply_silu) t = t / (1.0f + expf(-t));
+        store_from_f32<Tout>(y, j, t);
+    }
+}
+
+// out[a, :] = view[idx[a], :], moving V-sized words; an index outside the
+// view yields a zero row (never an out-of-bounds read).
+template <typename V>
+__global__ void gather_rows_kernel(const V *__restrict__ src, int64_t view_rows, int64_t row_words,
+                                   const int32_t *__restrict__ idx, int64_t n_out, V *__restrict__ out)
+{
+    int64_t total = n_out * row_words;
+    int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
+        int64_t a = e / row_words, w = e - a * row_words;
+        int64_t r = idx[a];
+        V v{};
+        if (r >= 0 && r < view_rows) v = src[r * row_words + w];
+        out[e] = v;
+    }
+}
+
+template <typename T, typename Tp>
+__global__ void c2s_skip_add_kernel(T *h, int64_t n, int64_t out_ch, const Tp *__restrict__ parent,
+                                    int64_t parent_rows, int64_t parent_ch,
+                                    const int32_t *__restrict__ idx, int64_t rep)
+{
+    const int64_t S = parent_ch / 8;
+    int64_t total = n * out_ch;
+    int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
+        int64_t a = e / out_ch, j = e - a * out_ch;
+        int64_t li = idx[a];
+        if (li < 0 || li >= parent_rows * 8) continue;  // out-of-range index: no skip term
+        int64_t p = li >> 3, c = li & 7;
+        float s = load_as_f32<Tp>(parent, p * parent_ch + c * S + j / rep);
+        store_from_f32<T>(h, e, load_as_f32<T>(h, e) + s);
+    }
+}
+
+template <typename Tin, typename Tout>
+int launch_layer_norm(const void *in, int64_t rows, int64_t ch, const float *w,
+                             const float *b, float eps, int silu, void *out, hipStream_t s)
+{
+    const unsigned g = grid_for(rows, 4, INT32_MAX);
+    const Tin *x = (const Tin *)in;
+    Tout *y = (Tout *)out;
+    const int C = (int)ch;
+    const int vpl = (C + 63) / 64;
+    if (vpl <= 1)
+        layer_norm_kernel<Tin, Tout, 1><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, y);
+    else if (vpl <= 2)
+        layer_norm_kernel<Tin, Tout, 2><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, y);
+    else if (vpl <= 4)
+        layer_norm_kernel<Tin, Tout, 4><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, y);
+    else if (vpl <= 8)
+        layer_norm_kernel<Tin, Tout, 8><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, y);
+    else if (vpl <= 16)
+        layer_norm_kernel<Tin, Tout, 16><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, y);
+    else
+        layer_norm_wide_kernel<Tin, Tout><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, y);
+    SC_LAUNCH_CHECK("layer_norm_kernel launch");
+    return SC_OK;
+}
+
+}  // namespace sc
+
+using namespace sc;
+
+extern "C" {
+
+int sc_abi_version(void) { return SC_ABI_VERSION; }
+
+const char *sc_status_string(int s)
+{
+    switch (s) {
+    case SC_OK: return "ok";
+    case SC_ERR_CONFIG: return "invalid sparse conv config";
+    case SC_ERR_SHAPE: return "shape mismatch";
+    case SC_ERR_DTYPE: return "unsupported dtype";
+    case SC_ERR_OVERFLOW: return "size overflow";
+    case SC_ERR_WORKSPACE: return "workspace too small";
+    case SC_ERR_COORD: return "invalid coordinates";
+    case SC_ERR_HIP: return "HIP runtime error";
+    case SC_ERR_NULL: return "null pointer";
+    case SC_ERR_UNSUPPORTED: return "unsupported";
+    default: return "unknown status";
+    }
+}
+
+const char *sc_last_error(void) { return g_last_error.c_str(); }
+
+int sc_validate_config(const sc_conv_config *cfg)
+{
+    clear_error();
+    return validate_config(cfg);
+}
+
+int sc_kernel_rows(const sc_conv_config *cfg, int64_t *rows)
+{
+    clear_error();
+    int rc = validate_config(cfg);
+    if (rc) return rc;
+    if (!rows) return fail(SC_ERR_NULL, "rows out-pointer is NULL");
+    *rows = cfg->kernel_d * cfg->kernel_h * cfg->kernel_w;
+    return SC_OK;
+}
+
+// kernel_layout, crates/burn_flex_gmm/src/lib.rs:727-752.
+int sc_kernel_offsets(const sc_conv_config *c, int32_t *offsets, int64_t capacity_rows)
+{
+    clear_error();
+    int rc = validate_config(c);
+    if (rc) return rc;
+    if (!offsets) return fail(SC_ERR_NULL, "offsets pointer is NULL");
+    int64_t K = c->kernel_d * c->kernel_h * c->kernel_w;
+    if (capacity_rows < K) return fail(SC_ERR_SHAPE, "offsets capacity below kernel rows");
+    const int32_t cd = (int32_t)(c->kernel_d / 2), ch = (int32_t)(c->kernel_h / 2),
+                  cw = (int32_t)(c->kernel_w / 2);
+    int64_t k = 0;
+    for (int64_t kd = 0; kd < c->kernel_d; ++kd)
+        for (int64_t kh = 0; kh < c->kernel_h; ++kh)
+            for (int64_t kw = 0; kw < c->kernel_w; ++kw, ++k) {
+                const int32_t d[3] = {c->axis_sign[0] * ((int32_t)kd - cd),
+                                      c->axis_sign[1] * ((int32_t)kh - ch),
+                                      c->axis_sign[2] * ((int32_t)kw - cw)};
+                int32_t o[3] = {0, 0, 0};
+                for (int j = 0; j < 3; ++j) o[c->axis_order[j]] = d[j];
+                offsets[3 * k + 0] = o[0];
+                offsets[3 * k + 1] = o[1];
+                offsets[3 * k + 2] = o[2];
+            }
+    return SC_OK;
+}
+
+int sc_convert(int in_dtype, const void *d_in, int out_dtype, void *d_out, int64_t n,
+               sc_stream stream)
+{
+    clear_error();
+    if (n < 0) return fail(SC_ERR_SHAPE, "negative element count");
+    if (n == 0) return SC_OK;
+    if (!d_in || !d_out) return fail(SC_ERR_NULL, "convert: NULL pointer");
+    hipStream_t s = as_stream(stream);
+    const unsigned g = grid_for(n, 256, 8192);
+    if (in_dtype == SC_DTYPE_F32 && out_dtype == SC_DTYPE_BF16)
+        convert_kernel<float, uint16_t><<<g, 256, 0, s>>>((const float *)d_in, (uint16_t *)d_out, n);
+    else if (in_dtype == SC_DTYPE_BF16 && out_dtype == SC_DTYPE_F32)
+        convert_kernel<uint16_t, float><<<g, 256, 0, s>>>((const uint16_t *)d_in, (float *)d_out, n);
+    else if (in_dtype == out_dtype && (in_dtype == SC_DTYPE_F32 || in_dtype == SC_DTYPE_BF16)) {
+        SC_HIP_CHECK(hipMemcpyAsync(d_out, d_in, (size_t)n * dtype_size(in_dtype),
+                                    hipMemcpyDeviceToDevice, s),
+                     "convert copy");
+        return SC_OK;
+    } else
+        return fail(SC_ERR_DTYPE, "convert: unsupported dtype pair");
+    SC_LAUNCH_CHECK("convert_kernel launch");
+    return SC_OK;
+}
+
+int sc_add(int dtype, const void *d_a, const void *d_b, int64_t n, void *d_out, sc_stream stream)
+{
+    clear_error();
+    if (n < 0) return fail(SC_ERR_SHAPE, "negative element count");
+    if (n == 0) return SC_OK;
+    if (!d_a || !d_b || !d_out) return fail(SC_ERR_NULL, "add: NULL pointer");
+    hipStream_t s = as_stream(stream);
+    const unsigned g = grid_for(n, 256, 8192);
+    if (dtype == SC_DTYPE_F32)
+        add_kernel<float><<<g, 256, 0, s>>>((const float *)d_a, (const float *)d_b, (float *)d_out, n);
+    else if (dtype == SC_DTYPE_BF16)
+        add_kernel<uint16_t><<<g, 256, 0, s>>>((const uint16_t *)d_a, (const uint16_t *)d_b,
+                                               (uint16_t *)d_out, n);
+    else
+        return fail(SC_ERR_DTYPE, "add: dtype must be f32 or bf16");
+    SC_LAUNCH_CHECK("add_kernel launch");
+    return SC_OK;
+}
+
+int sc_layer_norm(int in_dtype, const void *d_in, int64_t rows, int64_t channels, const float *d_w,
+                  const float *d_b, float eps, int apply_silu, int out_dtype, void *d_out,
+                  sc_stream stream)
+{
+    clear_error();
+    if (rows < 0 || channels <= 0 || channels > INT32_MAX)
+        return fail(SC_ERR_SHAPE, "layer_norm: invalid rows/channels");
+    if (rows == 0) return SC_OK;
+    if (!d_in || !d_out) return fail(SC_ERR_NULL, "layer_norm: NULL pointer");
+    hipStream_t s = as_stream(stream);
+    if (in_dtype == SC_DTYPE_F32 && out_dtype == SC_DTYPE_F32)
+        return launch_layer_norm<float, float>(d_in, rows, channels, d_w, d_b, eps, apply_silu, d_out, s);
+    if (in_dtype == SC_DTYPE_F32 && out_dtype == SC_DTYPE_BF16)
+        return launch_layer_norm<float, uint16_t>(d_in, rows, channels, d_w, d_b, eps, apply_silu, d_out, s);
+    if (in_dtype == SC_DTYPE_BF16 && out_dtype == SC_DTYPE_F32)
+        return launch_layer_norm<uint16_t, float>(d_in, rows, channels, d_w, d_b, eps, apply_silu, d_out, s);
+    if (in_dtype == SC_DTYPE_BF16 && out_dtype == SC_DTYPE_BF16)
+        return launch_layer_norm<uint16_t, uint16_t>(d_in, rows, channels, d_w, d_b, eps, apply_silu, d_out, s);
+    return fail(SC_ERR_DTYPE, "layer_norm: dtypes must be f32 or bf16");
+}
+
+int sc_gather_rows(int dtype, const void *d_src, int64_t src_rows, int64_t split, int64_t width,
+                   const int32_t *d_idx, int64_t n_out, void *d_out, sc_stream stream)
+{
+    clear_error();
+    const size_t ds = dtype_size(dtype);
+    if (!ds) return fail(SC_ERR_DTYPE, "gather_rows: unknown dtype");
+    if (src_rows < 0 || split <= 0 || width <= 0 || n_out < 0)
+        return fail(SC_ERR_SHAPE, "gather_rows: invalid shape");
+    if (n_out == 0) return SC_OK;
+    if (!d_src || !d_idx || !d_out) return fail(SC_ERR_NULL, "gather_rows: NULL pointer");
+    int64_t view_rows;
+    if (!mul_ok(src_rows, split, &view_rows)) return fail(SC_ERR_OVERFLOW, "gather_rows overflow");
+    hipStream_t s = as_stream(stream);
+    const int64_t row_bytes = width * (int64_t)ds;
+    const uintptr_t al = (uintptr_t)d_src | (uintptr_t)d_out;
+    if (row_bytes % 16 == 0 && al % 16 == 0) {
+        int64_t rw = row_bytes / 16;
+        gather_rows_kernel<uint4><<<grid_for(n_out * rw, 256, 65536), 256, 0, s>>>(
+            (const uint4 *)d_src, view_rows, rw, d_idx, n_out, (uint4 *)d_out);
+    } else if (row_bytes % 4 == 0 && al % 4 == 0) {
+        int64_t rw = row_bytes / 4;
+        gather_rows_kernel<uint32_t><<<grid_for(n_out * rw, 256, 65536), 256, 0, s>>>(
+            (const uint32_t *)d_src, view_rows, rw, d_idx, n_out, (uint32_t *)d_out);
+    } else {
+        gather_rows_kernel<uint8_t><<<grid_for(n_out * row_bytes, 256, 65536), 256, 0, s>>>(
+            (const uint8_t *)d_src, view_rows, row_bytes, d_idx, n_out, (uint8_t *)d_out);
+    }
+    SC_LAUNCH_CHECK("gather_rows_kernel launch");
+    return SC_OK;
+}
+
+int sc_c2s_skip_add(int dtype, void *d_h, int64_t n, int64_t out_channels, int parent_dtype,
+                    const void *d_parent, int64_t parent_rows, int64_t parent_channels,
+                    const int32_t *d_idx, sc_stream stream)
+{
+    clear_error();
+    if (n < 0 || out_channels <= 0 || parent_rows < 0 || parent_channels <= 0)
+        return fail(SC_ERR_SHAPE, "c2s_skip_add: invalid shape");
+    const int64_t S = parent_channels / 8;
+    if (parent_channels % 8 != 0 || S == 0 || out_channels % S != 0)
+        return fail(SC_ERR_SHAPE, "c2s_skip_add: invalid skip channel ratio (in=" +
+                                      std::to_string(parent_channels) +
+                                      ", out=" + std::to_string(out_channels) + ")");
+    if (n == 0) return SC_OK;
+    if (!d_h || !d_parent || !d_idx) return fail(SC_ERR_NULL, "c2s_skip_add: NULL pointer");
+    const int64_t rep = out_channels / S;
+    hipStream_t s = as_stream(stream);
+    const unsigned g = grid_for(n * out_channels, 256, 65536);
+#define SKIP_LAUNCH(T, TP)                                                                    \
+    c2s_skip_add_kernel<T, TP><<<g, 256, 0, s>>>((T *)d_h, n, out_channels, (const TP *)d_parent, \
+                                                 parent_rows, parent_channels, d_idx, rep)
+    if (dtype == SC_DTYPE_F32 && parent_dtype == SC_DTYPE_F32)
+        SKIP_LAUNCH(float, float);
+    else if (dtype == SC_DTYPE_F32 && parent_dtype == SC_DTYPE_BF16)
+        SKIP_LAUNCH(float, uint16_t);
+    else if (dtype == SC_DTYPE_BF16 && parent_dtype == SC_DTYPE_F32)
+        SKIP_LAUNCH(uint16_t, float);
+    else if (dtype == SC_DTYPE_BF16 && parent_dtype == SC_DTYPE_BF16)
+        SKIP_LAUNCH(uint16_t, uint16_t);
+    else
+        return fail(SC_ERR_DTYPE, "c2s_skip_add: dtypes must be f32 or bf16");
+#undef SKIP_LAUNCH
+    SC_LAUNCH_CHECK("c2s_skip_add_kernel launch");
+    return SC_OK;
+}
+
+}  // extern "C"

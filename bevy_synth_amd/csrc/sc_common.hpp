@@ -1,0 +1,115 @@
+// Shared helpers for the gfx950 sparse-conv library: status/error plumbing,
+// bf16 conversion, wave reductions and launch checks.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/sparseconv.h"
+
+namespace sc {
+
+// ---------------------------------------------------------------- errors
+void set_error(const std::string &msg);
+void clear_error();
+int fail(int status, const std::string &msg);
+int hip_fail(hipError_t err, const char *what);
+
+#define SC_HIP_CHECK(expr, what)                                  \
+    do {                                                          \
+        hipError_t _e = (expr);                                   \
+        if (_e != hipSuccess) return ::sc::hip_fail(_e, (what));  \
+    } while (0)
+
+// Launch check: catches launch-configuration errors without synchronising.
+#define SC_LAUNCH_CHECK(what)                                      \
+    do {                                                           \
+        hipError_t _e = hipGetLastError();                         \
+        if (_e != hipSuccess) return ::sc::hip_fail(_e, (what));   \
+    } while (0)
+
+int validate_config(const sc_conv_config *cfg);
+
+inline bool mul_ok(int64_t a, int64_t b, int64_t *out)
+{
+    if (a < 0 || b < 0) return false;
+    if (a != 0 && b > INT64_MAX / a) return false;
+    *out = a * b;
+    return true;
+}
+
+inline size_t dtype_size(int dt)
+{
+    switch (dt) {
+    case SC_DTYPE_F32: return 4;
+    case SC_DTYPE_BF16: return 2;
+    case SC_DTYPE_I8: return 1;
+    default: return 0;
+    }
+}
+
+inline hipStream_t as_stream(sc_stream s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline unsigned grid_for(int64_t n, int block, int64_t max_blocks = 1 << 20)
+{
+    int64_t g = (n + block - 1) / block;
+    if (g < 1) g = 1;
+    if (g > max_blocks) g = max_blocks;
+    return static_cast<unsigned>(g);
+}
+
+// ------------------------------------------------------------ bf16 bits
+// Round-to-nearest-even f32 -> bf16, no NaN special case: the rule of
+// bf16_round_to_f32 (crates/burn_flex_gmm/src/wgpu.rs:63-66).
+__host__ __device__ inline uint16_t f32_to_bf16(float f)
+{
+    uint32_t b = __builtin_bit_cast(uint32_t, f);
+    uint32_t lsb = (b >> 16) & 1u;
+    return static_cast<uint16_t>((b + 0x7fffu + lsb) >> 16);
+}
+
+__host__ __device__ inline float bf16_to_f32(uint16_t h)
+{
+    return __builtin_bit_cast(float, static_cast<uint32_t>(h) << 16);
+}
+
+template <typename T> __device__ inline float load_as_f32(const T *p, int64_t i);
+template <> __device__ inline float load_as_f32<float>(const float *p, int64_t i) { return p[i]; }
+template <> __device__ inline float load_as_f32<uint16_t>(const uint16_t *p, int64_t i)
+{
+    return bf16_to_f32(p[i]);
+}
+
+template <typename T> __device__ inline void store_from_f32(T *p, int64_t i, float v);
+template <> __device__ inline void store_from_f32<float>(float *p, int64_t i, float v) { p[i] = v; }
+template <> __device__ inline void store_from_f32<uint16_t>(uint16_t *p, int64_t i, float v)
+{
+    p[i] = f32_to_bf16(v);
+}
+
+// ---------------------------------------------------- wave64 reductions
+__device__ inline float wave_sum(float v)
+{
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ inline int wave_min_i32(int v)
+{
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = min(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+__device__ inline int wave_max_i32(int v)
+{
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+}  // namespace sc

@@ -1,0 +1,334 @@
+"""Device operator API of the sparse-conv path, over the C ABI.
+
+Mirrors burn_flex_gmm's public operator surface (crates/burn_flex_gmm/src/
+lib.rs and wgpu.rs:405-427) with torch tensors as the device buffers:
+
+===============================================  ==========================================
+reference (Rust)                                  here
+===============================================  ==========================================
+SparseSubmConvConfig (lib.rs:5-17)                SparseSubmConvConfig
+kernel_rows (lib.rs:59-67)                        kernel_rows
+kernel_layout / kernel_offsets (lib.rs:727-752)   kernel_offsets
+neighbor_rows_tensor_from_coords_tensor           neighbor_rows_tensor_from_coords_tensor
+  (wgpu/neighbor.rs:977-1006)
+sparse_subm_conv_forward_wgpu[_with_config]       sparse_subm_conv_forward
+  (wgpu/sparse_conv.rs:310-367)
+layer_norm_affine[_silu]_forward_wgpu             layer_norm
+  (wgpu/ops.rs:162-446)
+===============================================  ==========================================
+
+Errors: the reference returns ``Result<_, String>``; here a failing call
+raises ``SparseConvError`` carrying the status and the same kind of message.
+All work is queued on the current torch stream; nothing synchronises except
+where documented (the map status check, the subdivision child count).
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+from typing import Optional, Sequence, Tuple
+
+import numpy as np
+import torch
+
+from . import _capi
+from ._capi import SparseConvError, check
+
+INVALID_NEIGHBOR_ROW = -1
+
+_DTYPES = {
+    torch.float32: _capi.SC_DTYPE_F32,
+    torch.bfloat16: _capi.SC_DTYPE_BF16,
+    torch.int8: _capi.SC_DTYPE_I8,
+}
+
+
+def _dt(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise SparseConvError(3, f"unsupported dtype {t.dtype}") from None
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _require_cuda(name: str, t: torch.Tensor) -> None:
+    if not t.is_cuda:
+        raise SparseConvError(2, f"{name} must be a device tensor")
+    if not t.is_contiguous():
+        raise SparseConvError(2, f"{name} must be contiguous")
+
+
+@dataclass(frozen=True)
+class SparseSubmConvConfig:
+    """SparseSubmConvConfig, crates/burn_flex_gmm/src/lib.rs:5-17."""
+
+    in_channels: int
+    out_channels: int
+    kernel_d: int = 3
+    kernel_h: int = 3
+    kernel_w: int = 3
+    in_channels_per_group: Optional[int] = None
+    out_channels_per_group: Optional[int] = None
+    groups: int = 1
+    axis_order: Sequence[int] = field(default=(0, 1, 2))
+    axis_sign: Sequence[int] = field(default=(1, 1, 1))
+
+    def to_c(self) -> _capi.ScConvConfig:
+        c = _capi.ScConvConfig()
+        c.in_channels = self.in_channels
+        c.out_channels = self.out_channels
+        c.kernel_d = self.kernel_d
+        c.kernel_h = self.kernel_h
+        c.kernel_w = self.kernel_w
+        c.in_channels_per_group = (self.in_channels // self.groups
+                                   if self.in_channels_per_group is None
+                                   else self.in_channels_per_group)
+        c.out_channels_per_group = (self.out_channels // self.groups
+                                    if self.out_channels_per_group is None
+                                    else self.out_channels_per_group)
+        c.groups = self.groups
+        for j in range(3):
+            c.axis_order[j] = int(self.axis_order[j])
+            c.axis_sign[j] = int(self.axis_sign[j])
+        return c
+
+
+def validate_config(cfg: SparseSubmConvConfig) -> None:
+    check(_capi.load().sc_validate_config(ctypes.byref(cfg.to_c())))
+
+
+def kernel_rows(cfg: SparseSubmConvConfig) -> int:
+    out = ctypes.c_int64()
+    check(_capi.load().sc_kernel_rows(ctypes.byref(cfg.to_c()), ctypes.byref(out)))
+    return out.value
+
+
+def kernel_offsets(cfg: SparseSubmConvConfig) -> np.ndarray:
+    k = kernel_rows(cfg)
+    out = np.zeros((k, 3), dtype=np.int32)
+    check(_capi.load().sc_kernel_offsets(ctypes.byref(cfg.to_c()),
+                                         out.ctypes.data_as(ctypes.c_void_p), k))
+    return out
+
+
+def neighbor_map_workspace_bytes(n_rows: int) -> int:
+    out = ctypes.c_size_t()
+    check(_capi.load().sc_neighbor_map_workspace_size(int(n_rows), ctypes.byref(out)))
+    return out.value
+
+
+class NeighborMapWorkspace:
+    """Caller-owned workspace for the map build, grown on demand (the
+    reference caches per-device tensors in a thread-local map,
+    crates/burn_flex_gmm/src/wgpu.rs:349-382)."""
+
+    def __init__(self, device=None):
+        self.device = torch.device("cuda") if device is None else torch.device(device)
+        self.buf = torch.empty(0, dtype=torch.uint8, device=self.device)
+
+    def get(self, n_rows: int) -> torch.Tensor:
+        need = neighbor_map_workspace_bytes(n_rows)
+        if self.buf.numel() < need:
+            self.buf = torch.empty(need, dtype=torch.uint8, device=self.device)
+        return self.buf
+
+
+def neighbor_map_build_into(cfg: SparseSubmConvConfig, coords: torch.Tensor, out: torch.Tensor,
+                            workspace: torch.Tensor, query_rows: Optional[int] = None) -> None:
+    """Stream-ordered map build into a preallocated ``out`` [query_rows, K]."""
+    n = coords.shape[0]
+    q = n if query_rows is None else int(query_rows)
+    check(_capi.load().sc_neighbor_map_build(
+        ctypes.byref(cfg.to_c()), _ptr(coords), n, q, _ptr(out), _ptr(workspace),
+        workspace.numel(), _stream()))
+
+
+def neighbor_map_check(workspace: torch.Tensor) -> None:
+    """Syncs the current stream and raises on device-detected coord errors."""
+    check(_capi.load().sc_neighbor_map_check(_ptr(workspace), _stream()))
+
+
+def neighbor_rows_tensor_from_coords_tensor(
+        cfg: SparseSubmConvConfig, coords: torch.Tensor, query_rows: Optional[int] = None,
+        workspace: Optional[NeighborMapWorkspace] = None, check_status: bool = True) -> torch.Tensor:
+    """neighbor_rows_tensor_from_coords_tensor (crates/burn_flex_gmm/src/wgpu/neighbor.rs
+    :977-1006): coords [N,4] int32 (batch,x,y,z) -> map [N,K] int32, -1 where
+    absent, lowest row on duplicated coords.  With check_status (default) the
+    call syncs once to read the device status, as the reference reads its
+    overflow counter back (neighbor.rs:859-879)."""
+    _require_cuda("coords", coords)
+    if coords.dtype != torch.int32 or coords.dim() != 2 or coords.shape[1] != 4:
+        raise SparseConvError(2, f"coords must be int32 [N,4], got {tuple(coords.shape)} {coords.dtype}")
+    n = coords.shape[0]
+    q = n if query_rows is None else int(query_rows)
+    K = kernel_rows(cfg)
+    out = torch.empty((q, K), dtype=torch.int32, device=coords.device)
+    ws = (workspace or NeighborMapWorkspace(coords.device)).get(n)
+    neighbor_map_build_into(cfg, coords, out, ws, q)
+    if check_status:
+        neighbor_map_check(ws)
+    return out
+
+
+def sparse_subm_conv_forward(cfg: SparseSubmConvConfig, input: torch.Tensor,
+                             neighbor_rows: torch.Tensor, weight: torch.Tensor,
+                             bias: Optional[torch.Tensor] = None,
+                             w_scale: Optional[torch.Tensor] = None,
+                             residual: Optional[torch.Tensor] = None,
+                             out_dtype: Optional[torch.dtype] = None,
+                             out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """sparse_subm_conv_forward_wgpu (crates/burn_flex_gmm/src/wgpu/sparse_conv.rs:310-367).
+
+    input [N_in, Cin] f32|bf16; neighbor_rows [N_q, K] int32 (N_q <= N_in);
+    weight [Cout, KD, KH, KW, Cin_g] (or any view with that element count)
+    f32 (f32 input), bf16 or int8 (+ w_scale [Cout] f32) (bf16 input);
+    bias [Cout] f32 or None; residual [N_q, Cout] in the output dtype or None.
+    Returns [N_q, Cout] in out_dtype (default: the input dtype)."""
+    _require_cuda("input", input)
+    _require_cuda("neighbor_rows", neighbor_rows)
+    _require_cuda("weight", weight)
+    if input.dim() != 2 or input.shape[1] != cfg.in_channels:
+        raise SparseConvError(2, f"sparse conv input channel mismatch: got {tuple(input.shape)} "
+                                 f"expected [*, {cfg.in_channels}]")
+    K = kernel_rows(cfg)
+    if neighbor_rows.dtype != torch.int32 or neighbor_rows.dim() != 2 or neighbor_rows.shape[1] != K:
+        raise SparseConvError(2, f"sparse conv neighbor kernel rows mismatch: got "
+                                 f"{tuple(neighbor_rows.shape)} expected [*, {K}]")
+    c = cfg.to_c()
+    w_elems = cfg.out_channels * K * c.in_channels_per_group
+    if weight.numel() != w_elems:
+        raise SparseConvError(2, f"sparse conv weight len mismatch: got {weight.numel()} expected {w_elems}")
+    if bias is not None:
+        _require_cuda("bias", bias)
+        if bias.dtype != torch.float32 or bias.numel() != cfg.out_channels:
+            raise SparseConvError(2, f"sparse conv bias len mismatch: got {bias.numel()} "
+                                     f"expected {cfg.out_channels}")
+    if w_scale is not None:
+        _require_cuda("w_scale", w_scale)
+        if w_scale.dtype != torch.float32 or w_scale.numel() != cfg.out_channels:
+            raise SparseConvError(2, "w_scale must be f32 [Cout]")
+    n_q = neighbor_rows.shape[0]
+    od = input.dtype if out_dtype is None else out_dtype
+    if out is None:
+        out = torch.empty((n_q, cfg.out_channels), dtype=od, device=input.device)
+    else:
+        _require_cuda("out", out)
+        if out.shape != (n_q, cfg.out_channels) or out.dtype != od:
+            raise SparseConvError(2, "out has the wrong shape or dtype")
+    if residual is not None:
+        _require_cuda("residual", residual)
+        if residual.shape != (n_q, cfg.out_channels) or residual.dtype != od:
+            raise SparseConvError(2, "residual must be [N_q, Cout] in the output dtype")
+    check(_capi.load().sc_subm_conv_forward(
+        ctypes.byref(c), _dt(input), _ptr(input), input.shape[0], _ptr(neighbor_rows), n_q,
+        _dt(weight), _ptr(weight), _ptr(w_scale), _ptr(bias), _ptr(residual), _dt(out),
+        _ptr(out), _stream()))
+    return out
+
+
+def layer_norm(x: torch.Tensor, weight: Optional[torch.Tensor] = None,
+               bias: Optional[torch.Tensor] = None, eps: float = 1e-6, silu: bool = False,
+               out_dtype: Optional[torch.dtype] = None,
+               out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """layer_norm_affine[_silu]_forward_wgpu (crates/burn_flex_gmm/src/wgpu/ops.rs:162-446);
+    host form layer_norm_inplace + silu_inplace (sparse_decoder_wgpu_ops.rs:1642-1720)."""
+    _require_cuda("x", x)
+    rows, ch = x.shape
+    od = x.dtype if out_dtype is None else out_dtype
+    if out is None:
+        out = torch.empty((rows, ch), dtype=od, device=x.device)
+    for name, t in (("weight", weight), ("bias", bias)):
+        if t is not None and (t.dtype != torch.float32 or t.numel() != ch):
+            raise SparseConvError(2, f"layer_norm_inplace: invalid {name} len {t.numel()}, expected {ch}")
+    check(_capi.load().sc_layer_norm(_dt(x), _ptr(x), rows, ch, _ptr(weight), _ptr(bias),
+                                     ctypes.c_float(eps), int(silu), _dt(out), _ptr(out),
+                                     _stream()))
+    return out
+
+
+def add(a: torch.Tensor, b: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """add_inplace (sparse_decoder_wgpu_ops.rs:1747-1757) as out = a + b."""
+    if a.shape != b.shape or a.dtype != b.dtype:
+        raise SparseConvError(2, "add: operands differ in shape or dtype")
+    if out is None:
+        out = torch.empty_like(a)
+    check(_capi.load().sc_add(_dt(a), _ptr(a), _ptr(b), a.numel(), _ptr(out), _stream()))
+    return out
+
+
+def convert(x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """f32 <-> bf16 with the reference's round-to-nearest-even (wgpu.rs:57-67)."""
+    out = torch.empty(x.shape, dtype=dtype, device=x.device)
+    check(_capi.load().sc_convert(_dt(x), _ptr(x), _dt(out), _ptr(out), x.numel(), _stream()))
+    return out
+
+
+# ------------------------------------------------------------------ C2S
+
+def subdivision_build(parent_coords: torch.Tensor, logits: Optional[torch.Tensor] = None,
+                      mask: Optional[torch.Tensor] = None,
+                      thresholds: Optional[Sequence[float]] = None,
+                      with_pairs: bool = True
+                      ) -> Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
+    """subdivision_active_indices_wgpu + expand_subdivision_coords_and_linear_indices_wgpu
+    (sparse_decoder_wgpu_ops.rs:885-1054).  Returns (child_coords [A,4] int32,
+    linear_idx [A] int32, pairs [A,2] int32 or None).  Syncs once to read A, as
+    the reference's argwhere does."""
+    _require_cuda("parent_coords", parent_coords)
+    P = parent_coords.shape[0]
+    dev = parent_coords.device
+    if (logits is None) == (mask is None):
+        raise SparseConvError(8, "subdivision needs exactly one of logits or mask")
+    if logits is not None:
+        if logits.shape != (P, 8) or logits.dtype != torch.float32:
+            raise SparseConvError(2, "decoder subdivision logits tensor must be f32 [P, 8]")
+        th = (ctypes.c_float * 8)(*([0.0] * 8 if thresholds is None else list(thresholds)))
+    else:
+        if mask.shape != (P, 8) or mask.dtype not in (torch.uint8, torch.bool):
+            raise SparseConvError(2, "subdivision mask must be u8/bool [P, 8]")
+        mask = mask.to(torch.uint8).contiguous()
+        th = None
+    cap = max(8 * P, 1)
+    child = torch.empty((cap, 4), dtype=torch.int32, device=dev)
+    lin = torch.empty((cap,), dtype=torch.int32, device=dev)
+    pairs = torch.empty((cap, 2), dtype=torch.int32, device=dev) if with_pairs else None
+    count = torch.empty((1,), dtype=torch.int64, device=dev)
+    wsb = ctypes.c_size_t()
+    check(_capi.load().sc_subdivision_workspace_size(P, ctypes.byref(wsb)))
+    ws = torch.empty(max(wsb.value, 16), dtype=torch.uint8, device=dev)
+    check(_capi.load().sc_subdivision_build(
+        _ptr(logits), _ptr(mask), th, _ptr(parent_coords), P, _ptr(child), _ptr(lin),
+        _ptr(pairs), _ptr(count), _ptr(ws), ws.numel(), _stream()))
+    a = int(count.item())
+    return child[:a], lin[:a], (pairs[:a] if pairs is not None else None)
+
+
+def gather_rows(src: torch.Tensor, split: int, idx: torch.Tensor) -> torch.Tensor:
+    """select(0, idx) on the [rows*split, cols/split] view of src (conv1 child
+    selection, sparse_decoder_runtime_impl.rs:2249-2255)."""
+    _require_cuda("src", src)
+    rows, cols = src.shape
+    if cols % split != 0:
+        raise SparseConvError(2, "gather_rows: columns not divisible by split")
+    width = cols // split
+    out = torch.empty((idx.shape[0], width), dtype=src.dtype, device=src.device)
+    check(_capi.load().sc_gather_rows(_dt(src), _ptr(src), rows, split, width, _ptr(idx),
+                                      idx.shape[0], _ptr(out), _stream()))
+    return out
+
+
+def c2s_skip_add(h: torch.Tensor, parent: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
+    """In place: h += channel-repeated skip of the parent features
+    (sparse_decoder_runtime_impl.rs:1054-1076,1123-1133)."""
+    n, oc = h.shape
+    pr, pc = parent.shape
+    check(_capi.load().sc_c2s_skip_add(_dt(h), _ptr(h), n, oc, _dt(parent), _ptr(parent), pr, pc,
+                                       _ptr(idx), _stream()))
+    return h

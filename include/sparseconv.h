@@ -1,0 +1,223 @@
+/*
+ * sparseconv.h -- C ABI of the MI355X (gfx950) sparse 3D convolution path.
+ *
+ * Drop-in boundary for burn_flex_gmm's device operator API and the
+ * TRELLIS2 sparse decoder's conv seam (mosure/bevy_synth):
+ *   - neighbour map   : neighbor_rows_tensor_from_coords_tensor
+ *                       (crates/burn_flex_gmm/src/wgpu/neighbor.rs:977-1006)
+ *   - submanifold conv: sparse_subm_conv_forward_wgpu[_with_config]
+ *                       (crates/burn_flex_gmm/src/wgpu/sparse_conv.rs:310-367)
+ *   - C2S subdivision : subdivision_active_indices_wgpu / expand_subdivision_
+ *                       coords_and_linear_indices_wgpu / conv1 child select /
+ *                       skip add (crates/burn_trellis/src/runtime_model/
+ *                       sparse_decoder_wgpu_ops.rs:885-1054,
+ *                       sparse_decoder_runtime_impl.rs:1009-1144,2180-2426)
+ *   - block ops       : layer_norm[_silu], residual add
+ *                       (crates/burn_flex_gmm/src/wgpu/ops.rs:162-446)
+ *
+ * Rules: every device pointer is caller-allocated; calls are stream-ordered
+ * on the given hipStream_t (NULL = the default stream) and never synchronise
+ * unless documented ("syncs"); no call allocates device memory except the
+ * ones documented to (none in this header); the library keeps no mutable
+ * global state except the per-thread error message.  Every function returns
+ * an sc_status; on failure sc_last_error() holds a message on the calling
+ * thread (the reference returns Result<_, String>).
+ *
+ * Tensors are dense row-major.  bf16 is the upper 16 bits of an IEEE f32
+ * (uint16_t storage, same as torch.bfloat16).
+ */
+#ifndef SPARSECONV_H
+#define SPARSECONV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SC_ABI_VERSION 1
+#define SC_INVALID_NEIGHBOR_ROW (-1) /* crates/burn_flex_gmm/src/lib.rs:3 */
+
+/* Mirror of SparseSubmConvConfig, crates/burn_flex_gmm/src/lib.rs:5-17. */
+typedef struct sc_conv_config {
+    int64_t in_channels;
+    int64_t out_channels;
+    int64_t kernel_d;
+    int64_t kernel_h;
+    int64_t kernel_w;
+    int64_t in_channels_per_group;
+    int64_t out_channels_per_group;
+    int64_t groups;
+    int32_t axis_order[3];
+    int32_t axis_sign[3];
+} sc_conv_config;
+
+typedef enum sc_status {
+    SC_OK = 0,
+    SC_ERR_CONFIG = 1,      /* validate_config failures (lib.rs:698-725) */
+    SC_ERR_SHAPE = 2,       /* shape / length mismatch */
+    SC_ERR_DTYPE = 3,       /* unsupported dtype combination */
+    SC_ERR_OVERFLOW = 4,    /* size arithmetic overflow */
+    SC_ERR_WORKSPACE = 5,   /* workspace too small or misaligned */
+    SC_ERR_COORD = 6,       /* negative coordinate or coordinate span too wide */
+    SC_ERR_HIP = 7,         /* HIP runtime error (launch / copy) */
+    SC_ERR_NULL = 8,        /* required pointer is NULL */
+    SC_ERR_UNSUPPORTED = 9  /* valid request this build does not implement */
+} sc_status;
+
+typedef enum sc_dtype {
+    SC_DTYPE_F32 = 0,
+    SC_DTYPE_BF16 = 1,
+    SC_DTYPE_I8 = 2
+} sc_dtype;
+
+/* hipStream_t, passed through untyped so that the header needs no HIP. */
+typedef void *sc_stream;
+
+int sc_abi_version(void);
+const char *sc_status_string(int status);
+/* Message of the last failing call on this thread ("" if none). */
+const char *sc_last_error(void);
+
+/* ---------------------------------------------------------------- config */
+
+/* validate_config, crates/burn_flex_gmm/src/lib.rs:698-725. */
+int sc_validate_config(const sc_conv_config *cfg);
+/* kernel_rows, crates/burn_flex_gmm/src/lib.rs:59-67. */
+int sc_kernel_rows(const sc_conv_config *cfg, int64_t *rows);
+/* kernel_layout / kernel_offsets, crates/burn_flex_gmm/src/lib.rs:727-752 and
+ * crates/burn_flex_gmm/src/wgpu/neighbor.rs:190-217.  Host only: writes
+ * [K][3] (dx,dy,dz) into offsets; capacity_rows must be >= K. */
+int sc_kernel_offsets(const sc_conv_config *cfg, int32_t *offsets, int64_t capacity_rows);
+
+/* --------------------------------------------------------- neighbour map */
+
+/* Bytes of device workspace sc_neighbor_map_build needs for n_rows coords
+ * (a hash table of 2..4 slots per row plus a 256-byte header). */
+int sc_neighbor_map_workspace_size(int64_t n_rows, size_t *bytes);
+
+/*
+ * Replaces neighbor_rows_tensor_from_coords_tensor
+ * (crates/burn_flex_gmm/src/wgpu/neighbor.rs:977-1006) and the CPU
+ * build_neighbor_rows (crates/burn_flex_gmm/src/lib.rs:69-109).
+ *
+ * d_coords: [n_rows][4] int32 (batch, x, y, z), all >= 0.
+ * d_map   : [query_rows][K] int32 out; entry (r,k) is the row whose coord
+ *           equals coord[r] + offset[k] (same batch), or -1.  Duplicated
+ *           coords resolve to the LOWEST row, as every device algorithm of
+ *           the reference does (neighbor_kernels.rs:30-40,249-256,419-422).
+ *           query_rows <= n_rows maps the first query_rows coords against
+ *           the full coord set (sparse_decoder_tests.rs:239-292).
+ * Stream-ordered, no sync.  Coordinate problems (a negative component, or a
+ * bounding box whose cell count exceeds 2^64-1) are detected on the device:
+ * the map is then all -1 and sc_neighbor_map_check reports SC_ERR_COORD.
+ */
+int sc_neighbor_map_build(const sc_conv_config *cfg, const int32_t *d_coords, int64_t n_rows,
+                          int64_t query_rows, int32_t *d_map, void *d_workspace,
+                          size_t workspace_bytes, sc_stream stream);
+
+/* Syncs `stream` and returns the device-side status of the last build that
+ * used d_workspace (the reference reads its overflow counter back the same
+ * way, crates/burn_flex_gmm/src/wgpu/neighbor.rs:859-879). */
+int sc_neighbor_map_check(const void *d_workspace, sc_stream stream);
+
+/* ---------------------------------------------------- submanifold conv */
+
+/*
+ * Replaces sparse_subm_conv_forward_wgpu[_with_config]
+ * (crates/burn_flex_gmm/src/wgpu/sparse_conv.rs:310-367) and the CPU
+ * sparse_subm_conv_forward_flex_precomputed (crates/burn_flex_gmm/src/
+ * lib.rs:242-375):
+ *   out[r, o] = bias[o] + scale[o] * sum_{k : map[r,k] != -1}
+ *               sum_i in[map[r,k], g*Cin_g + i] * w[o, k, i],  g = o / Cout_g
+ *   (+ residual[r, o] when d_residual is not NULL).
+ *
+ * d_input    : [n_in][Cin], act_dtype f32 or bf16.
+ * d_map      : [n_q][K] int32 from sc_neighbor_map_build; n_q <= n_in.
+ * d_weight   : [Cout][KD][KH][KW][Cin_g] (the reference layout),
+ *              w_dtype f32 (act f32), bf16 (act bf16) or i8 (act bf16, with
+ *              d_w_scale [Cout] f32 per-output-channel scales).
+ * d_bias     : [Cout] f32 (may be NULL = zeros).
+ * d_residual : [n_q][Cout] in out_dtype, or NULL.
+ * d_out      : [n_q][Cout], out_dtype f32 or bf16 (bf16 is rounded to nearest
+ *              even from the f32 accumulator).
+ * Accumulation is fp32 in a fixed order: results are bit-identical run to run.
+ */
+int sc_subm_conv_forward(const sc_conv_config *cfg, int act_dtype, const void *d_input,
+                         int64_t n_in, const int32_t *d_map, int64_t n_q, int w_dtype,
+                         const void *d_weight, const float *d_w_scale, const float *d_bias,
+                         const void *d_residual, int out_dtype, void *d_out, sc_stream stream);
+
+/* ------------------------------------------------------------ block ops */
+
+/*
+ * Row LayerNorm with optional affine and SiLU: layer_norm_row_stats +
+ * layer_norm_affine[_silu] (crates/burn_flex_gmm/src/wgpu/ops.rs:162-446),
+ * host form layer_norm_inplace + silu_inplace (sparse_decoder_wgpu_ops.rs
+ * :1642-1720): two-pass f32 mean / biased variance, (x-mean)/sqrt(var+eps)
+ * [*w][+b], then x/(1+exp(-x)) if apply_silu.  d_w / d_b may be NULL.
+ * d_in may equal d_out when the dtypes match.
+ */
+int sc_layer_norm(int in_dtype, const void *d_in, int64_t rows, int64_t channels,
+                  const float *d_w, const float *d_b, float eps, int apply_silu, int out_dtype,
+                  void *d_out, sc_stream stream);
+
+/* out = a + b elementwise over n values (add_inplace, sparse_decoder_wgpu_ops.rs
+ * :1747-1757).  All three share `dtype`; d_out may alias d_a. */
+int sc_add(int dtype, const void *d_a, const void *d_b, int64_t n, void *d_out, sc_stream stream);
+
+/* ------------------------------------------------- C2S subdivision path */
+
+/* Workspace bytes for sc_subdivision_build with parent_rows parents. */
+int sc_subdivision_workspace_size(int64_t parent_rows, size_t *bytes);
+
+/*
+ * subdivision_active_indices_wgpu + expand_subdivision_coords_and_linear_
+ * indices_wgpu (sparse_decoder_wgpu_ops.rs:885-1054): child c of parent p is
+ * active when logits[p][c] > thresholds[c] (d_logits given) or mask[p][c] != 0
+ * (d_mask given; exactly one of the two).  Children are emitted parent-major,
+ * child-ascending (the argwhere order on [P,8]); for child a:
+ *   child_coords[a] = (b, 2x + (c&1), 2y + (c>>1 & 1), 2z + (c>>2 & 1))
+ *   linear_idx[a]   = 8*p + c
+ *   pairs[a]        = (p, c)          (d_pairs may be NULL)
+ * d_child_coords [8P][4], d_linear_idx [8P] and d_pairs [8P][2] are sized for
+ * the worst case.  The child count is written to d_count (int64, device).
+ * thresholds is a host array of 8 floats (ignored with a mask).
+ */
+int sc_subdivision_build(const float *d_logits, const uint8_t *d_mask, const float *thresholds,
+                         const int32_t *d_parent_coords, int64_t parent_rows,
+                         int32_t *d_child_coords, int32_t *d_linear_idx, int32_t *d_pairs,
+                         int64_t *d_count, void *d_workspace, size_t workspace_bytes,
+                         sc_stream stream);
+
+/*
+ * Row gather from a [src_rows*split][width] view of src ([src_rows][split*width]):
+ *   out[a, :] = view[idx[a], :]      for a < n_out
+ * This is conv1's child selection (reshape [P, 8*Cout] -> [8P, Cout], then
+ * select(linear_idx); sparse_decoder_runtime_impl.rs:2249-2255) with split=8.
+ */
+int sc_gather_rows(int dtype, const void *d_src, int64_t src_rows, int64_t split, int64_t width,
+                   const int32_t *d_idx, int64_t n_out, void *d_out, sc_stream stream);
+
+/*
+ * C2S channel-repeated skip (sparse_decoder_runtime_impl.rs:1054-1076,
+ * 1123-1133): with S = parent_channels/8 and R = out_channels/S,
+ *   h[a, j] += parent[idx[a] / 8, (idx[a] % 8)*S + j / R]
+ * h is [n][out_channels] (f32 or bf16, = dtype), parent [P][parent_channels]
+ * in parent_dtype.
+ */
+int sc_c2s_skip_add(int dtype, void *d_h, int64_t n, int64_t out_channels, int parent_dtype,
+                    const void *d_parent, int64_t parent_rows, int64_t parent_channels,
+                    const int32_t *d_idx, sc_stream stream);
+
+/* Element conversions (f32 <-> bf16 with round-to-nearest-even, the rule of
+ * bf16_round_to_f32, crates/burn_flex_gmm/src/wgpu.rs:57-67). */
+int sc_convert(int in_dtype, const void *d_in, int out_dtype, void *d_out, int64_t n,
+               sc_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPARSECONV_H */

@@ -1,0 +1,110 @@
+"""The C-ABI library loads on a GPU-less host, exports every symbol the header
+declares, and its host-only entry points (config validation, kernel offsets,
+workspace sizes, argument checks that fail before any device work) behave."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from bevy_synth_amd import _capi
+from bevy_synth_amd import flex_gmm as F
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_symbols():
+    txt = open(os.path.join(ROOT, "include", "sparseconv.h")).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char \*)\s*(sc_\w+)\s*\(", txt, re.M)))
+
+
+def test_library_exports_every_header_symbol():
+    L = _capi.load()
+    syms = header_symbols()
+    assert len(syms) >= 15
+    for s in syms:
+        assert hasattr(L, s), f"libsparseconv.so does not export {s}"
+    assert sorted(_capi.EXPORTED) == syms
+    assert L.sc_abi_version() == 1
+
+
+def test_status_strings():
+    L = _capi.load()
+    for code in range(10):
+        assert L.sc_status_string(code)
+
+
+@pytest.mark.parametrize("axis_order", [(0, 1, 2), (2, 1, 0), (1, 2, 0)])
+@pytest.mark.parametrize("axis_sign", [(1, 1, 1), (-1, 1, 1), (1, -1, -1)])
+@pytest.mark.parametrize("dims", [(3, 3, 3), (3, 1, 1), (3, 3, 1), (1, 1, 1), (5, 3, 2)])
+def test_kernel_offsets_match_oracle(oracle, axis_order, axis_sign, dims):
+    cfg = F.SparseSubmConvConfig(4, 4, *dims, axis_order=axis_order, axis_sign=axis_sign)
+    ocfg = oracle.OracleConfig(4, 4, *dims, axis_order=axis_order, axis_sign=axis_sign)
+    assert np.array_equal(F.kernel_offsets(cfg), oracle.kernel_layout(ocfg))
+    assert F.kernel_rows(cfg) == dims[0] * dims[1] * dims[2]
+
+
+@pytest.mark.parametrize("cfg,msg", [
+    (F.SparseSubmConvConfig(0, 4), "channel dimensions must be non-zero"),
+    (F.SparseSubmConvConfig(4, 4, 0, 3, 3), "kernel dimensions must be non-zero"),
+    (F.SparseSubmConvConfig(4, 4, groups=0, in_channels_per_group=4, out_channels_per_group=4),
+     "groups must be non-zero"),
+    (F.SparseSubmConvConfig(4, 8, groups=2, in_channels_per_group=3), "in_channels/group mismatch"),
+    (F.SparseSubmConvConfig(4, 8, groups=2, out_channels_per_group=3), "out_channels/group mismatch"),
+    (F.SparseSubmConvConfig(4, 4, axis_order=(0, 0, 2)), "permutation"),
+    (F.SparseSubmConvConfig(4, 4, axis_order=(0, 1, 3)), "permutation"),
+])
+def test_validate_config_errors(cfg, msg, oracle):
+    with pytest.raises(_capi.SparseConvError) as e:
+        F.validate_config(cfg)
+    assert msg in e.value.message and e.value.status == 1
+    c = cfg.to_c()
+    oc = oracle.OracleConfig(c.in_channels, c.out_channels, c.kernel_d, c.kernel_h, c.kernel_w,
+                             c.in_channels_per_group, c.out_channels_per_group, c.groups,
+                             tuple(c.axis_order), tuple(c.axis_sign))
+    assert not oracle.validate_config(oc)
+
+
+def test_workspace_sizes():
+    n = 1_040_679
+    b = F.neighbor_map_workspace_bytes(n)
+    assert 256 + 12 * 2 * n <= b <= 256 + 12 * 4 * n
+    assert F.neighbor_map_workspace_bytes(0) > 256
+    with pytest.raises(_capi.SparseConvError):
+        F.neighbor_map_workspace_bytes(-1)
+
+
+def test_argument_errors_before_device_work():
+    L = _capi.load()
+    cfg = F.SparseSubmConvConfig(64, 64).to_c()
+    # n_q > n_in
+    rc = L.sc_subm_conv_forward(ctypes.byref(cfg), 0, None, 5, None, 6, 0, None, None, None, None,
+                                0, None, None)
+    assert rc == 2 and b"exceeds input rows" in L.sc_last_error()
+    # f32 input with bf16 weights
+    rc = L.sc_subm_conv_forward(ctypes.byref(cfg), 0, None, 5, None, 5, 1, None, None, None, None,
+                                0, None, None)
+    assert rc == 3
+    # int8 weights without scales
+    rc = L.sc_subm_conv_forward(ctypes.byref(cfg), 1, None, 5, None, 5, 2, None, None, None, None,
+                                0, None, None)
+    assert rc == 8
+    # workspace too small
+    rc = L.sc_neighbor_map_build(ctypes.byref(cfg), None, 10, 10, None, ctypes.c_void_p(256), 16, None)
+    assert rc == 5 and b"too small" in L.sc_last_error()
+    # query rows beyond rows
+    rc = L.sc_neighbor_map_build(ctypes.byref(cfg), None, 10, 11, None, ctypes.c_void_p(256), 1 << 20, None)
+    assert rc == 2
+    # subdivision: needs exactly one of logits / mask
+    cnt = ctypes.c_void_p(256)
+    rc = L.sc_subdivision_build(None, None, None, None, 4, None, None, None, cnt, None, 0, None)
+    assert rc == 8
+    # skip ratio
+    rc = L.sc_c2s_skip_add(0, ctypes.c_void_p(256), 4, 12, 0, ctypes.c_void_p(256), 1, 64,
+                           ctypes.c_void_p(256), None)
+    assert rc == 2 and b"skip channel ratio" in L.sc_last_error()
+    # zero-size work is a no-op that succeeds without a device
+    assert L.sc_subm_conv_forward(ctypes.byref(cfg), 0, None, 0, None, 0, 0, None, None, None, None,
+                                  0, None, None) == 0
+    assert L.sc_add(0, None, None, 0, None, None) == 0

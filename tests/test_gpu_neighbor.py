@@ -1,0 +1,151 @@
+"""GPU parity: the HIP neighbour map is bit-exact against the oracle (device
+semantics: lowest row on duplicated coords), on the reference's own test
+shapes and on the benchmark geometries."""
+import numpy as np
+import pytest
+import torch
+
+from bevy_synth_amd import flex_gmm as F
+from bevy_synth_amd import synth
+from bevy_synth_amd._capi import SparseConvError
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def gpu_map(cfg, coords, query_rows=None):
+    out = F.neighbor_rows_tensor_from_coords_tensor(cfg, dev(coords.astype(np.int32)), query_rows)
+    return out.cpu().numpy()
+
+
+def ocfg(oracle, cfg):
+    return oracle.OracleConfig(cfg.in_channels, cfg.out_channels, cfg.kernel_d, cfg.kernel_h,
+                               cfg.kernel_w, groups=cfg.groups, axis_order=cfg.axis_order,
+                               axis_sign=cfg.axis_sign)
+
+
+def line_coords(n):
+    c = np.zeros((n, 4), np.int32)
+    c[:, 1] = np.arange(n)
+    return c
+
+
+def test_kat_query_chunks(oracle):
+    """sparse_decoder_tests.rs:239-292."""
+    cfg = F.SparseSubmConvConfig(1, 1, 3, 1, 1)
+    coords = np.array([[0, 0, 0, 0], [0, 1, 0, 0]], np.int32)
+    assert gpu_map(cfg, coords).reshape(-1).tolist() == [-1, 0, 1, 0, 1, -1]
+    assert gpu_map(cfg, coords[:1]).reshape(-1).tolist() == [-1, 0, -1]
+    assert gpu_map(cfg, coords, query_rows=1).reshape(-1).tolist() == [-1, 0, 1]
+
+
+@pytest.mark.parametrize("dims,n", [((3, 3, 1), 192), ((9, 9, 9), 256), ((9, 9, 9), 512),
+                                    ((3, 3, 3), 5000), ((1, 1, 1), 100)])
+def test_line_coords_match_scan(oracle, dims, n):
+    """wgpu/tests.rs:1752-1986 (hash / sorted / bucket == scan on line coords)."""
+    cfg = F.SparseSubmConvConfig(4, 4, *dims)
+    coords = line_coords(n)
+    exp = oracle.build_neighbor_rows(ocfg(oracle, cfg), coords)
+    if n <= 600:
+        assert np.array_equal(exp, oracle.build_neighbor_rows_scan(ocfg(oracle, cfg), coords))
+    assert np.array_equal(gpu_map(cfg, coords), exp)
+
+
+def test_duplicate_coords_lowest_row(oracle):
+    """wgpu/tests.rs:1802-1853: 128 line coords + duplicates of x=17 and x=32."""
+    cfg = F.SparseSubmConvConfig(4, 4, 3, 3, 1)
+    coords = np.concatenate([line_coords(128), np.array([[0, 17, 0, 0], [0, 32, 0, 0],
+                                                         [0, 17, 0, 0], [0, 32, 0, 0]], np.int32)])
+    got = gpu_map(cfg, coords)
+    assert np.array_equal(got, oracle.build_neighbor_rows_scan(ocfg(oracle, cfg), coords))
+
+
+@pytest.mark.parametrize("axis_order", [(0, 1, 2), (2, 1, 0), (1, 2, 0)])
+@pytest.mark.parametrize("axis_sign", [(1, 1, 1), (-1, 1, 1), (1, -1, -1)])
+def test_axis_permutations_checkerboard(oracle, axis_order, axis_sign):
+    cfg = F.SparseSubmConvConfig(6, 8, groups=2, axis_order=axis_order, axis_sign=axis_sign)
+    c = [(0, x, y, z) for x in range(6) for y in range(5) for z in range(4) if (x + y + z) % 2 == 0]
+    coords = np.array(c, np.int32)
+    assert np.array_equal(gpu_map(cfg, coords), oracle.build_neighbor_rows(ocfg(oracle, cfg), coords))
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_random_coords_batches_duplicates(oracle, seed):
+    rng = np.random.default_rng(seed)
+    n = 20000
+    c = np.zeros((n, 4), np.int32)
+    c[:, 0] = rng.integers(0, 3, n)
+    c[:, 1:] = rng.integers(0, 40, (n, 3))
+    cfg = F.SparseSubmConvConfig(1, 1)
+    assert np.array_equal(gpu_map(cfg, c), oracle.build_neighbor_rows(ocfg(oracle, cfg), c))
+
+
+def test_wide_coordinates_use_64bit_keys(oracle):
+    """A bbox of more than 2^32 cells takes the 64-bit key table."""
+    rng = np.random.default_rng(3)
+    n = 4000
+    base = rng.integers(0, 3000, (n, 3)).astype(np.int64)
+    base[: n // 2] *= 4000  # spread half of them wide
+    c = np.zeros((n, 4), np.int32)
+    c[:, 0] = rng.integers(0, 2, n)
+    c[:, 1:] = base.astype(np.int32)
+    # make sure some neighbours exist
+    c[n // 2: n // 2 + 100, 1:] = c[n // 2 + 100: n // 2 + 200, 1:] + np.array([1, 0, 0])
+    c[n // 2: n // 2 + 100, 0] = c[n // 2 + 100: n // 2 + 200, 0]
+    span = [int(c[:, j].max() - c[:, j].min() + 1) for j in range(4)]
+    assert np.prod(np.array(span, dtype=np.float64)) > 2.0 ** 32
+    cfg = F.SparseSubmConvConfig(1, 1)
+    exp = oracle.build_neighbor_rows(ocfg(oracle, cfg), c)
+    assert (exp >= 0).sum() > n
+    assert np.array_equal(gpu_map(cfg, c), exp)
+
+
+def test_negative_coordinate_is_rejected():
+    cfg = F.SparseSubmConvConfig(1, 1)
+    c = line_coords(64)
+    c[10, 2] = -5
+    with pytest.raises(SparseConvError) as e:
+        gpu_map(cfg, c)
+    assert e.value.status == 6
+
+
+def test_empty_and_single():
+    cfg = F.SparseSubmConvConfig(1, 1)
+    assert gpu_map(cfg, np.zeros((0, 4), np.int32)).shape == (0, 27)
+    one = gpu_map(cfg, np.array([[0, 5, 5, 5]], np.int32))
+    assert one.reshape(-1).tolist() == [-1] * 13 + [0] + [-1] * 13
+
+
+def test_config1_geometry(oracle):
+    coords = synth.config1_coords()
+    cfg = F.SparseSubmConvConfig(64, 64)
+    got = gpu_map(cfg, coords)
+    assert np.array_equal(got, oracle.build_neighbor_rows(ocfg(oracle, cfg), coords))
+    assert int((got >= 0).sum()) == 261416
+
+
+def test_config3_geometry_full_size(oracle):
+    coords = synth.config3_coords()
+    cfg = F.SparseSubmConvConfig(128, 128)
+    got = gpu_map(cfg, coords)
+    exp = oracle.build_neighbor_rows(ocfg(oracle, cfg), coords)
+    assert np.array_equal(got, exp)
+    # rebuild is deterministic
+    assert np.array_equal(gpu_map(cfg, coords), got)
+
+
+def test_shuffled_rows_relabel_consistently(oracle):
+    """Order independence at full config-2 size: permuting the coord rows
+    permutes and relabels the map."""
+    coords = synth.config2_coords()
+    cfg = F.SparseSubmConvConfig(1, 1)
+    base = gpu_map(cfg, coords)
+    perm = np.random.default_rng(0).permutation(len(coords))
+    inv = np.empty_like(perm)
+    inv[perm] = np.arange(len(perm))
+    shuf = gpu_map(cfg, coords[perm])
+    relabeled = np.where(base[perm] >= 0, inv[np.maximum(base[perm], 0)], -1)
+    assert np.array_equal(shuf, relabeled)

@@ -1,0 +1,210 @@
+"""GPU parity of the block ops and the C2S subdivision path."""
+import numpy as np
+import pytest
+import torch
+
+from bevy_synth_amd import decoder as D
+from bevy_synth_amd import flex_gmm as F
+from bevy_synth_amd import synth
+from tests.tolerance import TOL_BF16, TOL_F32, assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def bf16_dev(x_f32):
+    return dev(synth.bf16_bits(x_f32).view(np.int16)).view(torch.bfloat16)
+
+
+def rbf(x):
+    return synth.bf16_to_f32(synth.bf16_bits(x))
+
+
+@pytest.mark.parametrize("ch", [8, 64, 128, 200, 512, 1500])
+@pytest.mark.parametrize("affine,silu", [(True, True), (False, True), (True, False)])
+def test_layer_norm_silu_f32(oracle, ch, affine, silu):
+    rng = np.random.default_rng(ch)
+    x = (rng.standard_normal((777, ch)) * 2 + 0.5).astype(np.float32)
+    w = rng.standard_normal(ch).astype(np.float32) if affine else None
+    b = rng.standard_normal(ch).astype(np.float32) if affine else None
+    got = F.layer_norm(dev(x), None if w is None else dev(w), None if b is None else dev(b),
+                       eps=1e-6, silu=silu).cpu().numpy()
+    exp = oracle.layer_norm(x, w, b, 1e-6)
+    if silu:
+        exp = oracle.silu(exp)
+    assert_close(got, exp, TOL_F32, "layer_norm")
+
+
+def test_layer_norm_bf16_in_place(oracle):
+    rng = np.random.default_rng(1)
+    x = rbf(rng.standard_normal((5000, 128)).astype(np.float32))
+    t = bf16_dev(x)
+    F.layer_norm(t, eps=1e-6, silu=True, out=t)
+    exp = oracle.silu(oracle.layer_norm(x, None, None, 1e-6))
+    assert_close(t.float().cpu().numpy(), exp, TOL_BF16, "layer_norm bf16")
+
+
+def test_convert_bf16_matches_reference_rounding(oracle):
+    rng = np.random.default_rng(2)
+    x = (rng.standard_normal(100003) * 100).astype(np.float32)
+    got = F.convert(dev(x), torch.bfloat16).float().cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), oracle.bf16_round(x).view(np.uint32))
+
+
+def test_add():
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal(10001).astype(np.float32)
+    b = rng.standard_normal(10001).astype(np.float32)
+    assert np.array_equal(F.add(dev(a), dev(b)).cpu().numpy(), a + b)
+
+
+def test_subdivision_kat_child_expand():
+    """sparse_decoder_tests.rs:37-124: mask with (0,0),(0,3),(1,7) set."""
+    parents = np.array([[0, 0, 0, 0], [0, 1, 0, 0]], np.int32)
+    mask = np.zeros((2, 8), np.uint8)
+    mask[0, 0] = mask[0, 3] = mask[1, 7] = 1
+    cc, li, pairs = F.subdivision_build(dev(parents), mask=dev(mask))
+    assert cc.cpu().numpy().reshape(-1).tolist() == [0, 0, 0, 0, 0, 1, 1, 0, 0, 3, 1, 1]
+    assert li.cpu().numpy().tolist() == [0, 3, 15]
+    assert pairs.cpu().numpy().reshape(-1).tolist() == [0, 0, 0, 3, 1, 7]
+
+
+@pytest.mark.parametrize("P", [1, 5, 1023, 1024, 1025, 70000])
+def test_subdivision_logits_match_oracle(oracle, P):
+    rng = np.random.default_rng(P)
+    parents = np.zeros((P, 4), np.int32)
+    parents[:, 0] = rng.integers(0, 2, P)
+    parents[:, 1:] = rng.integers(0, 1000, (P, 3))
+    logits = rng.standard_normal((P, 8)).astype(np.float32)
+    thr = (rng.standard_normal(8) * 0.5).astype(np.float32)
+    cc, li, pairs = F.subdivision_build(dev(parents), logits=dev(logits), thresholds=thr.tolist())
+    exp_pairs = oracle.subdivision_active(logits, thr)
+    exp_cc, exp_li = oracle.subdivide_expand(parents, exp_pairs)
+    assert np.array_equal(pairs.cpu().numpy(), exp_pairs)
+    assert np.array_equal(cc.cpu().numpy(), exp_cc.astype(np.int32))
+    assert np.array_equal(li.cpu().numpy(), exp_li)
+
+
+def test_subdivision_empty():
+    cc, li, pairs = F.subdivision_build(dev(np.zeros((0, 4), np.int32)),
+                                        logits=dev(np.zeros((0, 8), np.float32)))
+    assert cc.shape == (0, 4) and li.shape == (0,)
+    cc, li, _ = F.subdivision_build(dev(np.zeros((3, 4), np.int32)),
+                                    mask=dev(np.zeros((3, 8), np.uint8)))
+    assert cc.shape == (0, 4)
+
+
+def test_gather_rows_and_skip_add(oracle):
+    rng = np.random.default_rng(4)
+    P, cin, cout = 500, 64, 32
+    parents = np.zeros((P, 4), np.uint32)
+    parents[:, 1:] = rng.integers(0, 100, (P, 3))
+    feats = rng.standard_normal((P, cin)).astype(np.float32)
+    mask = (rng.random((P, 8)) < 0.5).astype(np.uint8)
+    _, li, _ = F.subdivision_build(dev(parents.astype(np.int32)), mask=dev(mask))
+    cc, cf = oracle.channel2spatial(parents, feats, cin, mask)
+    got = F.gather_rows(dev(feats), 8, li).cpu().numpy()
+    assert np.array_equal(got, cf)
+    h = rng.standard_normal((len(cf), cout)).astype(np.float32)
+    hd = dev(h)
+    F.c2s_skip_add(hd, dev(feats), li)
+    assert np.array_equal(hd.cpu().numpy(), h + oracle.repeat_interleave(cf, cout // (cin // 8)))
+
+
+def _c2s_inputs(rng, P_grid=(8, 7, 6), cin=64, cout=32):
+    g = np.stack(np.meshgrid(*[np.arange(s) for s in P_grid], indexing="ij"), -1).reshape(-1, 3)
+    keep = rng.random(len(g)) < 0.6
+    g = g[keep]
+    parents = np.concatenate([np.zeros((len(g), 1), np.int32), g.astype(np.int32)], 1)
+    P = len(parents)
+    feats = rng.standard_normal((P, cin)).astype(np.float32)
+    mask = (rng.random((P, 8)) < 0.45).astype(np.uint8)
+    n1w = rng.standard_normal(cin).astype(np.float32)
+    n1b = rng.standard_normal(cin).astype(np.float32)
+    w1 = (rng.standard_normal((8 * cout, 27, cin)) / np.sqrt(27 * cin)).astype(np.float32)
+    b1 = (rng.standard_normal(8 * cout) * 0.1).astype(np.float32)
+    w2 = (rng.standard_normal((cout, 27, cout)) / np.sqrt(27 * cout)).astype(np.float32)
+    b2 = (rng.standard_normal(cout) * 0.1).astype(np.float32)
+    return parents, feats, mask, n1w, n1b, w1, b1, w2, b2
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_c2s_upsample_block_matches_oracle(oracle, dtype):
+    rng = np.random.default_rng(5)
+    cin, cout = 64, 32
+    parents, feats, mask, n1w, n1b, w1, b1, w2, b2 = _c2s_inputs(rng, cin=cin, cout=cout)
+    if dtype == torch.bfloat16:
+        feats, w1, w2 = rbf(feats), rbf(w1), rbf(w2)
+        put = bf16_dev
+    else:
+        put = dev
+    c1 = F.SparseSubmConvConfig(cin, 8 * cout)
+    c2 = F.SparseSubmConvConfig(cout, cout)
+    blk = D.C2SUpsampleBlock(cin, cout, dev(n1w), dev(n1b),
+                             D.ConvLayer(c1, put(w1), dev(b1)), D.ConvLayer(c2, put(w2), dev(b2)))
+    cc, out = blk(dev(parents), put(feats), mask=dev(mask))
+    o1 = oracle.OracleConfig(cin, 8 * cout)
+    o2 = oracle.OracleConfig(cout, cout)
+    exp_cc, exp = oracle.c2s_block(parents.astype(np.uint32), feats, mask, n1w, n1b, o1, w1, b1,
+                                   o2, w2, b2)
+    assert np.array_equal(cc.cpu().numpy(), exp_cc.astype(np.int32))
+    if dtype == torch.float32:
+        assert_close(out.cpu().numpy(), exp, TOL_F32, "c2s block f32")
+        return
+    # bf16 activations: the device rounds to bf16 after LN+SiLU, conv1, the
+    # child LN+SiLU, conv2 and the skip add; compose the oracle with the same
+    # rounding points.
+    r = oracle.bf16_round
+    pu = parents.astype(np.uint32)
+    h = r(oracle.silu(oracle.layer_norm(feats, n1w, n1b, 1e-6)))
+    h1 = r(oracle.conv_ref_f64(o1, w1, b1, h, oracle.build_neighbor_rows(o1, pu)).astype(np.float32))
+    pairs = np.argwhere(mask).astype(np.int32)
+    cc2, li = oracle.subdivide_expand(pu, pairs)
+    hup = r(oracle.silu(oracle.layer_norm(h1.reshape(-1, cout)[li], None, None, 1e-6)))
+    h2 = r(oracle.conv_ref_f64(o2, w2, b2, hup, oracle.build_neighbor_rows(o2, cc2)).astype(np.float32))
+    skip = feats.reshape(-1, cin // 8)[li]
+    exp_bf = r((h2.reshape(len(li), cin // 8, -1) + skip[:, :, None]).reshape(len(li), cout))
+    assert_close(out.float().cpu().numpy(), exp_bf, TOL_BF16, "c2s block bf16")
+
+
+def test_residual_block_matches_oracle(oracle):
+    coords = synth.config1_coords()
+    rng = np.random.default_rng(6)
+    n, c = len(coords), 64
+    x = synth.normal_f32(rng, (n, c))
+    w1 = synth.conv_weight(rng, c, 27, c, 1 / np.sqrt(27 * c))
+    w2 = synth.conv_weight(rng, c, 27, c, 1 / np.sqrt(27 * c))
+    b = np.zeros(c, np.float32)
+    cfg = F.SparseSubmConvConfig(c, c)
+    nbr = F.neighbor_rows_tensor_from_coords_tensor(cfg, dev(coords))
+    blk = D.ResidualBlock(D.ConvLayer(cfg, dev(w1), dev(b)), D.ConvLayer(cfg, dev(w2), dev(b)))
+    got = blk(dev(x), nbr).cpu().numpy()
+    oc = oracle.OracleConfig(c, c)
+    nb = nbr.cpu().numpy()
+    h = oracle.conv_flex_precomputed(oc, w1, b, x, nb)
+    h = oracle.silu(oracle.layer_norm(h, None, None, 1e-6))
+    exp = oracle.conv_flex_precomputed(oc, w2, b, h, nb) + x
+    assert_close(got, exp, TOL_F32, "residual block")
+
+
+def test_transposed_upsample_matches_oracle(oracle):
+    """Config 4 shape class: 2x2x2 transposed conv = C2S with a 1x1x1 conv1."""
+    g = synth.ShellCubeGeometry()
+    parents = g.coords()[:20000]
+    mask = synth.subdivision_mask_near_surface(parents, g)
+    rng = np.random.default_rng(7)
+    cin, cout = 128, 64
+    x = rbf(synth.normal_f32(rng, (len(parents), cin)))
+    w = rbf(synth.normal_f32(rng, (8 * cout, 1, cin), 1 / np.sqrt(8 * cin)))
+    b = np.zeros(8 * cout, np.float32)
+    cfg = F.SparseSubmConvConfig(cin, 8 * cout, 1, 1, 1)
+    cc, feats, li = D.transposed_upsample(dev(parents), bf16_dev(x),
+                                          D.ConvLayer(cfg, bf16_dev(w), dev(b)), dev(mask))
+    exp_cc, exp_f = oracle.channel2spatial(parents.astype(np.uint32),
+                                           x.astype(np.float64) @ w[:, 0, :].T.astype(np.float64),
+                                           8 * cout, mask)
+    assert np.array_equal(cc.cpu().numpy(), exp_cc.astype(np.int32))
+    assert_close(feats.float().cpu().numpy(), exp_f, TOL_BF16, "transposed upsample")
