@@ -34,6 +34,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cpu-sample", type=int, default=65536,
                     help="query rows of the CPU baseline sample (0 = skip)")
+    ap.add_argument("--only", choices=["map", "conv", "ln"], default=None,
+                    help="run just this part of the step --steps times (for rocprofv3) and exit")
     return ap.parse_args()
 
 
@@ -146,6 +148,11 @@ def main():
     for _ in range(max(args.warmup, 1)):
         step()
     F.neighbor_map_check(ws)
+    if args.only:
+        part = {"map": map_build, "conv": lambda: (conv1(), conv2()), "ln": ln_silu}[args.only]
+        ms = events_ms(part, args.steps)
+        print(f"[bench] only={args.only} {ms:.3f} ms per call", file=sys.stderr, flush=True)
+        return
     P = int((nbr >= 0).sum().item())
     print(f"[bench] config3 voxels={n} pairs={P} warmup done", file=sys.stderr, flush=True)
 
@@ -153,7 +160,8 @@ def main():
     ms_step = events_ms(step, args.steps)
     # Per-kernel launch durations (HIP events on the launch stream).
     ms_map = events_ms(map_build, args.steps)
-    ms_conv = events_ms(conv1, args.steps)
+    # both convs of the block are the same kernel; average one launch over the pair
+    ms_conv = events_ms(lambda: (conv1(), conv2()), args.steps) / 2.0
     ms_ln = events_ms(ln_silu, args.steps)
     print(f"[bench] step {ms_step:.3f} ms  map {ms_map:.3f}  conv {ms_conv:.3f}  ln {ms_ln:.3f}",
           file=sys.stderr, flush=True)

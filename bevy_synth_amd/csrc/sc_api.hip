@@ -117,6 +117,110 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const Tin *in, int64_t 
     }
 }
 
+// Vectorised form for rows of V = channels/VEC 16-byte vectors, V a multiple
+// of 8: LPR lanes per row (64/LPR rows per wave), NV vectors per lane, the
+// row reductions over the LPR-lane segment (same two-pass f32 statistics).
+template <typename Tin>
+struct Vec16 {
+    static constexpr int N = 16 / (int)sizeof(Tin);
+};
+
+template <typename Tin>
+__device__ inline void unpack16(const uint4 &u, float *f)
+{
+    if constexpr (sizeof(Tin) == 4) {
+        f[0] = __builtin_bit_cast(float, u.x);
+        f[1] = __builtin_bit_cast(float, u.y);
+        f[2] = __builtin_bit_cast(float, u.z);
+        f[3] = __builtin_bit_cast(float, u.w);
+    } else {
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f[2 * i] = bf16_to_f32((uint16_t)(w[i] & 0xffffu));
+            f[2 * i + 1] = bf16_to_f32((uint16_t)(w[i] >> 16));
+        }
+    }
+}
+
+template <int LPR>
+__device__ inline float seg_sum(float v)
+{
+#pragma unroll
+    for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+template <typename Tin, typename Tout, int LPR, int NV>
+__global__ __launch_bounds__(256) void layer_norm_vec_kernel(const Tin *in, int64_t rows, int channels,
+                                                             const float *__restrict__ w,
+                                                             const float *__restrict__ b, float eps,
+                                                             int apply_silu, Tout *out)
+{
+    constexpr int VEC = Vec16<Tin>::N;
+    constexpr int RPW = 64 / LPR;  // rows per wave
+    const int lane = threadIdx.x & 63;
+    const int seg = lane / LPR, sl = lane % LPR;
+    const int64_t row = ((int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * RPW + seg;
+    const bool live = row < rows;
+    const int64_t rr = live ? row : 0;
+    const uint4 *x = reinterpret_cast<const uint4 *>(in + rr * channels);
+    float v[NV][VEC];
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const uint4 u = x[sl + i * LPR];
+        unpack16<Tin>(u, v[i]);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) s += v[i][e];
+    }
+    const float inv_c = 1.0f / (float)channels;
+    const float mean = seg_sum<LPR>(s) * inv_c;
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+            const float d = v[i][e] - mean;
+            q += d * d;
+        }
+    const float inv_std = 1.0f / sqrtf(seg_sum<LPR>(q) * inv_c + eps);
+    if (!live) return;
+    Tout *y = out + row * channels;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c0 = (sl + i * LPR) * VEC;
+        float t[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+            float z = (v[i][e] - mean) * inv_std;
+            if (w) z *= w[c0 + e];
+            if (b) z += b[c0 + e];
+            if (apply_silu) z = z / (1.0f + expf(-z));
+            t[e] = z;
+        }
+        if constexpr (sizeof(Tout) == 2) {
+            if constexpr (VEC == 8) {
+                uint4 o;
+                o.x = (uint32_t)f32_to_bf16(t[0]) | ((uint32_t)f32_to_bf16(t[1]) << 16);
+                o.y = (uint32_t)f32_to_bf16(t[2]) | ((uint32_t)f32_to_bf16(t[3]) << 16);
+                o.z = (uint32_t)f32_to_bf16(t[4]) | ((uint32_t)f32_to_bf16(t[5]) << 16);
+                o.w = (uint32_t)f32_to_bf16(t[6]) | ((uint32_t)f32_to_bf16(t[7]) << 16);
+                *reinterpret_cast<uint4 *>(y + c0) = o;
+            } else {
+                uint2 o;
+                o.x = (uint32_t)f32_to_bf16(t[0]) | ((uint32_t)f32_to_bf16(t[1]) << 16);
+                o.y = (uint32_t)f32_to_bf16(t[2]) | ((uint32_t)f32_to_bf16(t[3]) << 16);
+                *reinterpret_cast<uint2 *>(y + c0) = o;
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < VEC; e += 4)
+                *reinterpret_cast<float4 *>(y + c0 + e) = make_float4(t[e], t[e + 1], t[e + 2], t[e + 3]);
+        }
+    }
+}
+
 // Same computation for rows wider than 1024 channels: three passes over the
 // row (it stays in L1/L2 between passes).
 template <typename Tin, typename Tout>
@@ -193,6 +297,31 @@ int launch_layer_norm(const void *in, int64_t rows, int64_t ch, const float *w,
     const Tin *x = (const Tin *)in;
     Tout *y = (Tout *)out;
     const int C = (int)ch;
+    constexpr int VEC = Vec16<Tin>::N;
+    const bool aligned = ((uintptr_t)in % 16 == 0) && ((uintptr_t)out % 16 == 0);
+    if (aligned && C % (VEC * 8) == 0) {
+        const int V = C / VEC;  // 16-byte vectors per row, a multiple of 8
+        int lpr = 8;
+        while (lpr < 64 && V % (lpr * 2) == 0) lpr *= 2;
+        const int nv = V / lpr;
+        const int64_t rows_per_block = 4 * (64 / lpr);
+        const unsigned gv = grid_for(rows, (int)rows_per_block, INT32_MAX);
+#define LN_VEC(L, N) layer_norm_vec_kernel<Tin, Tout, L, N><<<gv, 256, 0, s>>>(x, rows, C, w, b, eps, silu, y)
+        bool launched = true;
+        if (lpr == 8 && nv == 1) LN_VEC(8, 1);
+        else if (lpr == 16 && nv == 1) LN_VEC(16, 1);
+        else if (lpr == 32 && nv == 1) LN_VEC(32, 1);
+        else if (lpr == 64 && nv == 1) LN_VEC(64, 1);
+        else if (lpr == 64 && nv == 2) LN_VEC(64, 2);
+        else if (lpr == 64 && nv == 3) LN_VEC(64, 3);
+        else if (lpr == 64 && nv == 4) LN_VEC(64, 4);
+        else launched = false;
+#undef LN_VEC
+        if (launched) {
+            SC_LAUNCH_CHECK("layer_norm_vec_kernel launch");
+            return SC_OK;
+        }
+    }
     const int vpl = (C + 63) / 64;
     if (vpl <= 1)
         layer_norm_kernel<Tin, Tout, 1><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, y);

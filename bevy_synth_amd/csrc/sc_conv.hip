@@ -46,6 +46,7 @@ struct ConvArgs {
     const void *residual;
     void *out;
     int64_t n_q;
+    int64_t n_in;     // input rows; map entries outside [0, n_in) count as absent
     int64_t cin;      // input row pitch (elements) = in_channels
     int64_t cout;     // output row pitch = out_channels
     int cin_g;
@@ -58,7 +59,7 @@ struct ConvArgs {
 template <typename TA>
 __device__ inline uint4 load_a_chunk(const TA *input, int64_t cin, int32_t nbr, int64_t col_elem)
 {
-    if (nbr < 0) return make_uint4(0, 0, 0, 0);
+    if (nbr < 0) return make_uint4(0, 0, 0, 0);  // absent neighbour (or out of range)
     return *reinterpret_cast<const uint4 *>(input + (int64_t)nbr * cin + col_elem);
 }
 
@@ -135,7 +136,8 @@ __global__ __launch_bounds__(kThreads, 2) void conv_mfma_kernel(ConvArgs args)
     __syncthreads();
     const int32_t *map_tile = args.map + row0 * K;
     for (int e = tid; e < nrows * K; e += kThreads) {
-        if (map_tile[e] >= 0) {
+        const int32_t v = map_tile[e];
+        if (v >= 0 && v < args.n_in) {
             const int k = e % K;
             atomicOr(&s_kmask[k >> 5], 1u << (k & 31));
         }
@@ -174,9 +176,12 @@ __global__ __launch_bounds__(kThreads, 2) void conv_mfma_kernel(ConvArgs args)
         const int64_t w_row1 = ((out_col0 + o0 + ob + 64) * (int64_t)K) * args.cin_g;
         const int b_part_elems = kI8 ? (tid & 1) * 16 : pa * (16 / (int)sizeof(TW));
 
+        const int64_t n_in = args.n_in;
         auto load_nbr = [&](int k, int32_t &n0, int32_t &n1) {
             n0 = va0 ? map_tile[(int64_t)ra * K + k] : -1;
             n1 = va1 ? map_tile[(int64_t)(ra + 64) * K + k] : -1;
+            if (n0 >= n_in) n0 = -1;
+            if (n1 >= n_in) n1 = -1;
         };
 
         int32_t nb0, nb1, nn0 = -1, nn1 = -1;
@@ -323,7 +328,7 @@ __global__ __launch_bounds__(256) void conv_scalar_kernel(ConvArgs args)
         float acc = 0.f;
         for (int k = 0; k < args.K; ++k) {
             const int32_t nb = args.map[r * args.K + k];
-            if (nb < 0) continue;
+            if (nb < 0 || nb >= args.n_in) continue;
             const TA *a = input + (int64_t)nb * args.cin + g * args.cin_g;
             const TW *w = weight + (o * args.K + k) * args.cin_g;
             float part = 0.f;
@@ -410,6 +415,7 @@ extern "C" int sc_subm_conv_forward(const sc_conv_config *cfg, int act_dtype, co
     a.residual = d_residual;
     a.out = d_out;
     a.n_q = n_q;
+    a.n_in = n_in;
     a.cin = cfg->in_channels;
     a.cout = cfg->out_channels;
     a.cin_g = (int)cfg->in_channels_per_group;

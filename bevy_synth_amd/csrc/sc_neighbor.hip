@@ -10,7 +10,9 @@
 //   3. insert : key = mixed-radix index of (b,x,y,z) inside the bbox; a
 //               32-bit key packs with the row into one 64-bit slot (single
 //               atomicCAS, atomicMin on the slot keeps the LOWEST row of
-//               duplicates); wider keys use a u64 key array + u32 row array
+//               duplicates); wider keys use a u64 key array + u32 row array;
+//               a bbox beyond 2^64-1 cells uses a row-only table whose slots
+//               are compared through the coords themselves
 //   4. query  : R rows per block staged in LDS, one (row, k) entry per lane,
 //               coalesced map writes; neighbours outside the bbox (including
 //               negative ones) are rejected before probing
@@ -27,7 +29,6 @@ namespace {
 constexpr size_t kHeaderBytes = 256;
 constexpr uint64_t kEmpty64 = ~0ull;
 constexpr uint32_t kStatusNegative = 1u;
-constexpr uint32_t kStatusWide = 2u;
 constexpr int kMaxStagedRows = 256;
 constexpr int kMaxStagedOffsets = 512;
 
@@ -52,8 +53,17 @@ inline size_t workspace_bytes_for(int64_t n)
     return kHeaderBytes + (size_t)table_capacity(n) * 12u;
 }
 
+// splitmix64 finaliser (Steele, Lea & Flood, OOPSLA 2014).
+__device__ inline uint64_t mix64(uint64_t z)
+{
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
 struct Plan {
-    int mode;  // 0: no table (error), 1: 32-bit keys packed with rows, 2: 64-bit keys
+    int mode;  // 0: no table (error), 1: 32-bit keys packed with rows, 2: 64-bit keys,
+               // 3: row-only table compared through the coords
     int32_t lo[4];
     int32_t hi[4];
     uint64_t ext[4];
@@ -75,9 +85,19 @@ __device__ inline Plan make_plan(const NbrHeader *h)
         if (total != 0 && p.ext[j] > kEmpty64 / total) ovf = true;
         total *= p.ext[j];
     }
-    if (ovf) return p;
-    p.mode = total <= 0xffffffffull ? 1 : 2;
+    p.mode = ovf ? 3 : (total <= 0xffffffffull ? 1 : 2);
     return p;
+}
+
+__device__ inline uint64_t hash_coord(int32_t b, int32_t x, int32_t y, int32_t z)
+{
+    return mix64((uint64_t)(uint32_t)b ^ mix64(((uint64_t)(uint32_t)x << 32 | (uint32_t)y) ^
+                                               mix64((uint64_t)(uint32_t)z)));
+}
+
+__device__ inline bool same_coord(const int4 a, const int4 b)
+{
+    return a.x == b.x && a.y == b.y && a.z == b.z && a.w == b.w;
 }
 
 __device__ inline uint64_t pack_key(const Plan &p, int32_t b, int32_t x, int32_t y, int32_t z)
@@ -87,14 +107,6 @@ __device__ inline uint64_t pack_key(const Plan &p, int32_t b, int32_t x, int32_t
     k = k * p.ext[2] + (uint64_t)(y - p.lo[2]);
     k = k * p.ext[3] + (uint64_t)(z - p.lo[3]);
     return k;
-}
-
-// splitmix64 finaliser (Steele, Lea & Flood, OOPSLA 2014).
-__device__ inline uint64_t mix64(uint64_t z)
-{
-    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
-    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
-    return z ^ (z >> 31);
 }
 
 __global__ void nm_init_kernel(NbrHeader *h, uint64_t *words, uint64_t n_words)
@@ -164,13 +176,23 @@ __global__ __launch_bounds__(256) void nm_insert_kernel(const int4 *__restrict__
 {
     const Plan p = make_plan(h);
     const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (p.mode == 0) {
-        if (tid == 0 && !(h->status & kStatusNegative)) atomicOr(&h->status, kStatusWide);
-        return;
-    }
+    if (p.mode == 0) return;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t r = tid; r < n; r += stride) {
         const int4 c = coords[r];
+        if (p.mode == 3) {
+            uint64_t s = hash_coord(c.x, c.y, c.z, c.w) & mask;
+            for (uint64_t probe = 0; probe <= mask; ++probe) {
+                const uint32_t old = atomicCAS(&rows[s], 0xffffffffu, (uint32_t)r);
+                if (old == 0xffffffffu) break;
+                if (same_coord(coords[old], c)) {
+                    atomicMin(&rows[s], (uint32_t)r);
+                    break;
+                }
+                s = (s + 1) & mask;
+            }
+            continue;
+        }
         const uint64_t key = pack_key(p, c.x, c.y, c.z, c.w);
         uint64_t s = mix64(key) & mask;
         if (p.mode == 1) {
@@ -253,7 +275,20 @@ __global__ __launch_bounds__(256) void nm_query_kernel(const int4 *__restrict__ 
         // A negative neighbour is absent (crates/burn_flex_gmm/src/lib.rs:98-100);
         // so is any neighbour outside the bbox of the coord set.
         if (p.mode != 0 && nx >= p.lo[1] && nx <= p.hi[1] && ny >= p.lo[2] && ny <= p.hi[2] &&
-            nz >= p.lo[3] && nz <= p.hi[3]) {
+            nz >= p.lo[3] && nz <= p.hi[3] && p.mode == 3) {
+            const int4 q = make_int4(c.x, (int32_t)nx, (int32_t)ny, (int32_t)nz);
+            uint64_t s = hash_coord(q.x, q.y, q.z, q.w) & mask;
+            for (uint64_t probe = 0; probe <= mask; ++probe) {
+                const uint32_t v = rows[s];
+                if (v == 0xffffffffu) break;
+                if (same_coord(coords[v], q)) {
+                    found = (int32_t)v;
+                    break;
+                }
+                s = (s + 1) & mask;
+            }
+        } else if (p.mode != 0 && nx >= p.lo[1] && nx <= p.hi[1] && ny >= p.lo[2] && ny <= p.hi[2] &&
+                   nz >= p.lo[3] && nz <= p.hi[3]) {
             const uint64_t key = pack_key(p, c.x, (int32_t)nx, (int32_t)ny, (int32_t)nz);
             uint64_t s = mix64(key) & mask;
             if (p.mode == 1) {
@@ -373,8 +408,6 @@ int sc_neighbor_map_check(const void *d_workspace, sc_stream stream)
     SC_HIP_CHECK(hipStreamSynchronize(s), "neighbor map status sync");
     if (status & kStatusNegative)
         return fail(SC_ERR_COORD, "coord value exceeds i32::MAX (negative i32) for device neighbor kernel");
-    if (status & kStatusWide)
-        return fail(SC_ERR_COORD, "coordinate bounding box exceeds 2^64-1 cells");
     return SC_OK;
 }
 

@@ -169,9 +169,6 @@ int sc_subdivision_build(const float *d_logits, const uint8_t *d_mask, const flo
     clear_error();
     if (parent_rows < 0 || parent_rows > INT32_MAX / 8)
         return fail(SC_ERR_SHAPE, "subdivision parent rows out of range");
-    if ((d_logits == nullptr) == (d_mask == nullptr))
-        return fail(SC_ERR_NULL, "subdivision needs exactly one of logits or mask");
-    if (d_logits && !thresholds) return fail(SC_ERR_NULL, "subdivision thresholds are NULL");
     if (!d_count) return fail(SC_ERR_NULL, "subdivision count pointer is NULL");
     hipStream_t s = as_stream(stream);
     if (parent_rows == 0) {
@@ -179,6 +176,9 @@ int sc_subdivision_build(const float *d_logits, const uint8_t *d_mask, const flo
         SC_LAUNCH_CHECK("write_zero_count launch");
         return SC_OK;
     }
+    if ((d_logits == nullptr) == (d_mask == nullptr))
+        return fail(SC_ERR_NULL, "subdivision needs exactly one of logits or mask");
+    if (d_logits && !thresholds) return fail(SC_ERR_NULL, "subdivision thresholds are NULL");
     if (!d_parent_coords || !d_child_coords || !d_linear_idx || !d_workspace)
         return fail(SC_ERR_NULL, "subdivision: NULL pointer");
     const uintptr_t al = (uintptr_t)d_parent_coords | (uintptr_t)d_child_coords |

@@ -109,9 +109,10 @@ int sc_neighbor_map_workspace_size(int64_t n_rows, size_t *bytes);
  *           the reference does (neighbor_kernels.rs:30-40,249-256,419-422).
  *           query_rows <= n_rows maps the first query_rows coords against
  *           the full coord set (sparse_decoder_tests.rs:239-292).
- * Stream-ordered, no sync.  Coordinate problems (a negative component, or a
- * bounding box whose cell count exceeds 2^64-1) are detected on the device:
- * the map is then all -1 and sc_neighbor_map_check reports SC_ERR_COORD.
+ * Stream-ordered, no sync.  A negative coordinate component (a u32 coord
+ * above i32::MAX, rejected by the reference at crates/burn_flex_gmm/src/
+ * wgpu/neighbor.rs:252-263) is detected on the device: the map is then all
+ * -1 and sc_neighbor_map_check reports SC_ERR_COORD.
  */
 int sc_neighbor_map_build(const sc_conv_config *cfg, const int32_t *d_coords, int64_t n_rows,
                           int64_t query_rows, int32_t *d_map, void *d_workspace,
@@ -142,6 +143,7 @@ int sc_neighbor_map_check(const void *d_workspace, sc_stream stream);
  * d_residual : [n_q][Cout] in out_dtype, or NULL.
  * d_out      : [n_q][Cout], out_dtype f32 or bf16 (bf16 is rounded to nearest
  *              even from the f32 accumulator).
+ * Map entries outside [0, n_in) are treated as absent (-1).
  * Accumulation is fp32 in a fixed order: results are bit-identical run to run.
  */
 int sc_subm_conv_forward(const sc_conv_config *cfg, int act_dtype, const void *d_input,

@@ -83,23 +83,32 @@ def test_random_coords_batches_duplicates(oracle, seed):
     assert np.array_equal(gpu_map(cfg, c), oracle.build_neighbor_rows(ocfg(oracle, cfg), c))
 
 
-def test_wide_coordinates_use_64bit_keys(oracle):
-    """A bbox of more than 2^32 cells takes the 64-bit key table."""
-    rng = np.random.default_rng(3)
-    n = 4000
+def _wide_coords(rng, n, scale_axes):
     base = rng.integers(0, 3000, (n, 3)).astype(np.int64)
-    base[: n // 2] *= 4000  # spread half of them wide
+    for ax in scale_axes:
+        base[: n // 2, ax] *= 4000  # spread half of them wide
     c = np.zeros((n, 4), np.int32)
     c[:, 0] = rng.integers(0, 2, n)
     c[:, 1:] = base.astype(np.int32)
-    # make sure some neighbours exist
+    # plant neighbours (x + 1, same batch) and a few duplicates
     c[n // 2: n // 2 + 100, 1:] = c[n // 2 + 100: n // 2 + 200, 1:] + np.array([1, 0, 0])
     c[n // 2: n // 2 + 100, 0] = c[n // 2 + 100: n // 2 + 200, 0]
-    span = [int(c[:, j].max() - c[:, j].min() + 1) for j in range(4)]
-    assert np.prod(np.array(span, dtype=np.float64)) > 2.0 ** 32
+    c[n - 20:] = c[n - 40: n - 20]
+    return c
+
+
+@pytest.mark.parametrize("scale_axes,lo,hi", [((0,), 2.0 ** 32, 2.0 ** 64),
+                                              ((0, 1, 2), 2.0 ** 64, np.inf)])
+def test_wide_coordinates(oracle, scale_axes, lo, hi):
+    """Bboxes of more than 2^32 cells use 64-bit keys; beyond 2^64 cells the
+    row-only table compares coords directly."""
+    c = _wide_coords(np.random.default_rng(3), 4000, scale_axes)
+    span = [float(c[:, j].max() - c[:, j].min() + 1) for j in range(4)]
+    cells = float(np.prod(np.array(span, dtype=np.float64)))
+    assert lo < cells < hi
     cfg = F.SparseSubmConvConfig(1, 1)
     exp = oracle.build_neighbor_rows(ocfg(oracle, cfg), c)
-    assert (exp >= 0).sum() > n
+    assert (exp >= 0).sum() > len(c)
     assert np.array_equal(gpu_map(cfg, c), exp)
 
 
