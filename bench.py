@@ -36,6 +36,9 @@ def parse():
                     help="query rows of the CPU baseline sample (0 = skip)")
     ap.add_argument("--only", choices=["map", "conv", "ln"], default=None,
                     help="run just this part of the step --steps times (for rocprofv3) and exit")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run one 1 GiB device-to-device copy (the known-size kernel that "
+                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
 
 
@@ -148,6 +151,13 @@ def main():
     for _ in range(max(args.warmup, 1)):
         step()
     F.neighbor_map_check(ws)
+    if args.calibrate_copy:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        src.fill_(1)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     if args.only:
         part = {"map": map_build, "conv": lambda: (conv1(), conv2()), "ln": ln_silu}[args.only]
         ms = events_ms(part, args.steps)

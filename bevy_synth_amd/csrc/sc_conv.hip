@@ -5,23 +5,25 @@
 // (crates/burn_flex_gmm/src/wgpu/sparse_conv_kernels.rs K9-K17: one lane per
 // output value re-reading K*Cin inputs and weights from global memory).
 //
-// Tile = 128 query rows x 128 output channels of one group, 256 threads
-// (4 waves in 2x2, each 64x64 = 2x2 MFMA 32x32 blocks).  The reduction runs
-// over (kernel offset k, input-channel chunk of 64 bytes):
-//   A stage: the 128 neighbour rows map[r, k] of the tile, 64-byte slices,
-//            gathered into LDS (zero rows where map = -1);
+// Tile = 256 query rows x 128 output channels of one group, 256 threads
+// (4 waves; wave w owns 64 rows x 128 channels = 2x4 MFMA 32x32 blocks).  The
+// reduction runs over (kernel offset k, input-channel chunk of 64 bytes):
+//   A stage: each lane gathers its MFMA A fragments (neighbour rows
+//            map[r, k], 64-byte slices; zero where map = -1) directly into
+//            registers, one stage ahead -- A is private to a wave;
 //   B stage: w[o, k, chunk] for the tile's 128 output channels, read in the
 //            reference layout [Cout][K][Cin_g] (Cin-contiguous = the MFMA B
-//            operand's K-contiguous column), int8 widened to bf16 exactly.
+//            operand's K-contiguous column), int8 widened to bf16 exactly,
+//            staged through double-buffered LDS (shared by the 4 waves).
 // Offsets that no row of the tile uses are skipped (a per-tile bitmask built
-// from the map block before the main loop).  Double-buffered LDS, one
-// barrier per stage; neighbour indices are prefetched one offset ahead.
+// from the map block before the main loop).  One barrier per stage;
+// neighbour indices are prefetched one offset ahead.
 // bf16 uses v_mfma_f32_32x32x16_bf16, f32 uses v_mfma_f32_32x32x2_f32; both
 // accumulate in f32.  Epilogue: * scale[o] (int8) + bias[o] (+ residual).
 //
 // A scalar kernel (one lane per output value) covers shapes the tile cannot
-// take (channel counts that are not multiples of the 64-byte chunk, K > 1024,
-// unaligned pointers).
+// take (channel counts that are not multiples of the 64-byte chunk, K > 32,
+// unaligned pointers, tensors of 2 GiB or more).
 #include "sc_common.hpp"
 
 namespace sc {
@@ -30,12 +32,11 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kBM = 128;
-constexpr int kBN = 128;
+constexpr int kTileRows = 256;  // query rows per workgroup (64 per wave)
+constexpr int kBN = 128;        // output channels per workgroup
 constexpr int kThreads = 256;
-constexpr int kChunkBytes = 64;   // bytes of one row's reduction slice per stage
-constexpr int kLdsStride = 80;    // padded row pitch in LDS (conflict-free b128 reads)
-constexpr int kMaxMaskK = 1024;   // offsets tracked by the per-tile bitmask
+constexpr int kChunkBytes = 64;   // smallest per-stage reduction slice of a row (bytes)
+constexpr int kMaxTableK = 32;    // MFMA tile: kernels with at most 32 offsets
 
 struct ConvArgs {
     const void *input;
@@ -92,6 +93,68 @@ __device__ inline void widen_i8x16(uint4 q, uint4 &o0, uint4 &o1)
     o1.w = i8pair_to_bf16x2(q.w, 16);
 }
 
+// A fragments of one 32-row block for one stage: NP 16-byte pieces of the
+// gathered row's CB-byte slice.  Piece q of lane half h sits at byte
+// bf16: q*32 + h*16 (one MFMA k-step per piece); f32: h*CB/2 + q*16 (4
+// consecutive k-elements per piece).
+template <int NP>
+struct APiece {
+    uint4 p[NP];
+};
+
+template <bool kF32, int CB>
+__device__ inline int piece_offset(int q, int half)
+{
+    return kF32 ? half * (CB / 2) + q * 16 : q * 32 + half * 16;
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer loads: an offset at or beyond the descriptor's byte count reads as
+// zero, which is how absent neighbours, rows outside the input and channels
+// beyond Cout contribute nothing without a branch.
+constexpr uint32_t kOobOffset = 0xC0000000u;
+
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ inline uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+template <bool kF32, int CB>
+__device__ inline APiece<CB / 32> load_a_pieces(__amdgpu_buffer_rsrc_t r, uint32_t row_off, int kc,
+                                                 int half)
+{
+    APiece<CB / 32> a;
+#pragma unroll
+    for (int q = 0; q < CB / 32; ++q)
+        a.p[q] = bload16(r, row_off + (uint32_t)(kc * CB + piece_offset<kF32, CB>(q, half)));
+    return a;
+}
+
+__device__ inline float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
+
+// One piece of one 32x32 output block: bf16 -> one v_mfma_f32_32x32x16_bf16;
+// f32 -> four v_mfma_f32_32x32x2_f32 (element e of each lane half's piece).
+template <bool kF32>
+__device__ inline void mfma_piece(f32x16 &acc, const uint4 &a, const uint4 &b)
+{
+    if constexpr (!kF32) {
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                      __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
+    } else {
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(u2f(a.x), u2f(b.x), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(u2f(a.y), u2f(b.y), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(u2f(a.z), u2f(b.z), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(u2f(a.w), u2f(b.w), acc, 0, 0, 0);
+    }
+}
+
 __device__ inline int tile_for_block(int b, int G)
 {
     // Dispatch assigns workgroup b to XCD b % 8; give each XCD a contiguous
@@ -103,195 +166,230 @@ __device__ inline int tile_for_block(int b, int G)
 
 // ------------------------------------------------------------- MFMA tile
 
-template <typename TA, typename TW, typename TO>
-__global__ __launch_bounds__(kThreads, 2) void conv_mfma_kernel(ConvArgs args)
+// Per-tile list of kernel offsets (K <= 32) used by at least one row of the
+// tile: per-thread bit masks OR-reduced across the wave, one LDS atomic per
+// wave, then a serial compaction by thread 0.
+__device__ inline int build_offset_list(const int32_t *map_tile, int nrows, int K, int64_t n_in,
+                                        uint32_t *s_kmask, int16_t *s_klist, int *s_nk)
 {
-    constexpr bool kF32 = sizeof(TA) == 4;
-    constexpr int kBK = kChunkBytes / (int)sizeof(TA);  // elements per stage
-    constexpr bool kI8 = sizeof(TW) == 1;
-
-    __shared__ __attribute__((aligned(16))) unsigned char s_a[2][kBM * kLdsStride];
-    __shared__ __attribute__((aligned(16))) unsigned char s_b[2][kBN * kLdsStride];
-    __shared__ uint32_t s_kmask[kMaxMaskK / 32];
-    __shared__ int16_t s_klist[kMaxMaskK];
-    __shared__ int s_nk;
-
-    const TA *input = static_cast<const TA *>(args.input);
-    const TW *weight = static_cast<const TW *>(args.weight);
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int K = args.K;
-
-    const int tile = tile_for_block(blockIdx.x, gridDim.x);
-    const int64_t row0 = (int64_t)tile * kBM;
-    const int o0 = blockIdx.y * kBN;            // within the group
-    const int g = blockIdx.z;
-    const int64_t in_col0 = (int64_t)g * args.cin_g;
-    const int64_t out_col0 = (int64_t)g * args.cout_g;
-    const int nrows = (int)min<int64_t>(kBM, args.n_q - row0);
-
-    // ---- which offsets does this tile use?
-    for (int i = tid; i < (K + 31) / 32; i += kThreads) s_kmask[i] = 0;
+    const int tid = threadIdx.x, lane = tid & 63;
+    for (int i = tid; i < (K + 31) / 32; i += blockDim.x) s_kmask[i] = 0;
     __syncthreads();
-    const int32_t *map_tile = args.map + row0 * K;
-    for (int e = tid; e < nrows * K; e += kThreads) {
-        const int32_t v = map_tile[e];
-        if (v >= 0 && v < args.n_in) {
-            const int k = e % K;
-            atomicOr(&s_kmask[k >> 5], 1u << (k & 31));
+    {
+        // The tile's map block is contiguous: read it as int4, four loads in
+        // flight per thread before any is inspected.
+        uint32_t m = 0;
+        const int total = nrows * K;
+        const int4 *m4 = reinterpret_cast<const int4 *>(map_tile);
+        const int n4 = total >> 2;
+        for (int base = tid; base < n4; base += 4 * (int)blockDim.x) {
+            int4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int i4 = base + u * (int)blockDim.x;
+                v[u] = i4 < n4 ? m4[i4] : make_int4(-1, -1, -1, -1);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int e = 4 * (base + u * (int)blockDim.x);
+                const int32_t vv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (vv[c] >= 0 && vv[c] < n_in) m |= 1u << ((e + c) % K);
+            }
         }
+        for (int e = 4 * n4 + tid; e < total; e += blockDim.x) {
+            const int32_t v = map_tile[e];
+            if (v >= 0 && v < n_in) m |= 1u << (e % K);
+        }
+        uint32_t lo = (uint32_t)m;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) lo |= __shfl_xor(lo, off, 64);
+        if (lane == 0 && lo) atomicOr(&s_kmask[0], lo);
     }
     __syncthreads();
     if (tid == 0) {
         int nk = 0;
         for (int k = 0; k < K; ++k)
             if (s_kmask[k >> 5] & (1u << (k & 31))) s_klist[nk++] = (int16_t)k;
-        s_nk = nk;
+        *s_nk = nk;
     }
     __syncthreads();
-    const int nk = s_nk;
+    return *s_nk;
+}
+
+// Tile = 256 query rows x 128 output channels of one group; 4 waves, wave w
+// owns rows [64w, 64w+64) x all 128 channels (2 x 4 MFMA 32x32 blocks, 128
+// f32 accumulators per lane).  CB = bytes of a row's reduction slice per
+// stage (64 or 128); a stage is (used offset ki, input chunk kc).
+//
+// Prologue: the offsets used by the tile, then an LDS table of the byte
+// offsets of every (used offset, row) neighbour row in the input (an
+// out-of-range offset for absent neighbours), so the main loop issues no map
+// loads.  Main loop: a two-half software pipeline with no branches -- each
+// half issues the next stage's weight loads (-> LDS after the MFMAs) and A
+// loads (-> the other register set), then runs this stage's MFMAs.  The
+// stage count is padded to even with a zero-weight stage.
+template <typename TA, typename TW, typename TO, int CB>
+__global__ __launch_bounds__(kThreads, 2) void conv_mfma_kernel(ConvArgs args)
+{
+    constexpr bool kF32 = sizeof(TA) == 4;
+    constexpr int kBK = CB / (int)sizeof(TA);  // reduction elements per stage
+    constexpr bool kI8 = sizeof(TW) == 1;
+    constexpr int kRows = kTileRows;
+    constexpr int NP = CB / 32;                 // A/B pieces per lane per row block
+    constexpr int kStride = CB + 16;            // LDS pitch of one output channel
+    constexpr int kWBytes = kBK * (int)sizeof(TW);  // weight bytes per channel per stage
+    constexpr int kWPieces = kWBytes / 16;      // 16-byte weight pieces per channel
+    constexpr int kBPerThread = kBN * kWPieces / kThreads;
+    static_assert(kBPerThread >= 1, "weight pieces per thread");
+
+    __shared__ __attribute__((aligned(16))) unsigned char s_b[2][kBN * kStride];
+    __shared__ uint32_t s_aoff[kMaxTableK][kRows];
+    __shared__ uint32_t s_kmask[kMaxTableK / 32 + 1];
+    __shared__ int16_t s_klist[kMaxTableK];
+    __shared__ int s_nk;
+
+    const TA *input = static_cast<const TA *>(args.input);
+    const TW *weight = static_cast<const TW *>(args.weight);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6, half = lane >> 5;
+    const int K = args.K;
+
+    const int tile = tile_for_block(blockIdx.x, gridDim.x);
+    const int64_t row0 = (int64_t)tile * kRows;
+    const int o0 = blockIdx.y * kBN;  // within the group
+    const int g = blockIdx.z;
+    const int64_t in_col0 = (int64_t)g * args.cin_g;
+    const int64_t out_col0 = (int64_t)g * args.cout_g;
+    const int nrows = (int)min<int64_t>(kRows, args.n_q - row0);
+    const int32_t *map_tile = args.map + row0 * K;
+    const int64_t n_in = args.n_in;
+    const uint32_t row_bytes = (uint32_t)(args.cin * (int64_t)sizeof(TA));
+
+    const int nk = build_offset_list(map_tile, nrows, K, n_in, s_kmask, s_klist, &s_nk);
+    // Row-offset table: thread r fills row r for every used offset.
+    {
+        const int r = tid;  // kThreads == kRows
+        const int32_t *mrow = map_tile + (int64_t)min(r, nrows - 1) * K;
+        for (int k0 = 0; k0 < nk; k0 += 8) {
+            int32_t v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = k0 + u < nk ? mrow[s_klist[k0 + u]] : -1;
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (k0 + u < nk)
+                    s_aoff[k0 + u][r] = (r < nrows && v[u] >= 0 && v[u] < n_in)
+                                            ? (uint32_t)v[u] * row_bytes : kOobOffset;
+        }
+    }
+    __syncthreads();
+
     const int nkc = args.cin_g / kBK;  // chunks per offset
     const int S = nk * nkc;
+    const int S2 = S + (S & 1);
 
-    f32x16 acc[2][2];
+    f32x16 acc[2][4];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
     if (S > 0) {
-        // A: thread owns rows ra and ra+64, 16-byte part pa of the 64-byte slice.
-        const int ra = tid >> 2, pa = tid & 3;
-        const bool va0 = ra < nrows, va1 = ra + 64 < nrows;
-        const int64_t a_col = in_col0 + pa * (16 / (int)sizeof(TA));
-        // B (bf16/f32): output channels ra and ra+64, part pa.
-        // B (int8): output channel tid>>1, 16-int8 half (tid&1).
-        const int ob = kI8 ? (tid >> 1) : ra;
-        const bool vb0 = o0 + ob < args.cout_g;
-        const bool vb1 = !kI8 && (o0 + ob + 64 < args.cout_g);
-        const int64_t w_row0 = ((out_col0 + o0 + ob) * (int64_t)K) * args.cin_g;
-        const int64_t w_row1 = ((out_col0 + o0 + ob + 64) * (int64_t)K) * args.cin_g;
-        const int b_part_elems = kI8 ? (tid & 1) * 16 : pa * (16 / (int)sizeof(TW));
+        const int ar0 = wave * 64 + (lane & 31), ar1 = ar0 + 32;
+        const __amdgpu_buffer_rsrc_t a_rsrc =
+            make_rsrc(input + in_col0, (uint32_t)(n_in * row_bytes - in_col0 * (int64_t)sizeof(TA)));
+        const __amdgpu_buffer_rsrc_t w_rsrc =
+            make_rsrc(weight, (uint32_t)(args.cout * (int64_t)K * args.cin_g * (int64_t)sizeof(TW)));
 
-        const int64_t n_in = args.n_in;
-        auto load_nbr = [&](int k, int32_t &n0, int32_t &n1) {
-            n0 = va0 ? map_tile[(int64_t)ra * K + k] : -1;
-            n1 = va1 ? map_tile[(int64_t)(ra + 64) * K + k] : -1;
-            if (n0 >= n_in) n0 = -1;
-            if (n1 >= n_in) n1 = -1;
+        // Weight pieces: index t + 256*i -> channel idx / kWPieces, piece idx % kWPieces.
+        uint32_t w_base[kBPerThread];
+#pragma unroll
+        for (int i = 0; i < kBPerThread; ++i) {
+            const int idx = tid + kThreads * i;
+            const int ch = idx / kWPieces, pc = idx % kWPieces;
+            w_base[i] = o0 + ch < args.cout_g
+                            ? (uint32_t)((out_col0 + o0 + ch) * (int64_t)K * args.cin_g * (int64_t)sizeof(TW)) + pc * 16
+                            : kOobOffset;
+        }
+        const uint32_t w_k_bytes = (uint32_t)(args.cin_g * (int64_t)sizeof(TW));
+        uint4 rb[kBPerThread];
+        // Loads of stage t (t >= S: zero weights, zero A).
+        auto load_stage = [&](int t, APiece<NP> &f0, APiece<NP> &f1) {
+            const bool live = t < S;
+            const int tt = live ? t : 0;
+            const int ki = tt / nkc, kc = tt - ki * nkc;
+            const int k = s_klist[ki];
+            const uint32_t wk = (uint32_t)k * w_k_bytes + (uint32_t)(kc * kWBytes);
+#pragma unroll
+            for (int i = 0; i < kBPerThread; ++i) rb[i] = bload16(w_rsrc, live ? w_base[i] + wk : kOobOffset);
+            const uint32_t o_a0 = live ? s_aoff[ki][ar0] : kOobOffset;
+            const uint32_t o_a1 = live ? s_aoff[ki][ar1] : kOobOffset;
+            f0 = load_a_pieces<kF32, CB>(a_rsrc, o_a0, kc, half);
+            f1 = load_a_pieces<kF32, CB>(a_rsrc, o_a1, kc, half);
         };
-
-        int32_t nb0, nb1, nn0 = -1, nn1 = -1;
-        load_nbr(s_klist[0], nb0, nb1);
-        if (nk > 1) load_nbr(s_klist[1], nn0, nn1);
-
-        uint4 ra0, ra1, rb0, rb1;
-        auto issue_loads = [&](int k, int kc) {
-            const int64_t c = a_col + (int64_t)kc * kBK;
-            ra0 = load_a_chunk<TA>(input, args.cin, nb0, c);
-            ra1 = load_a_chunk<TA>(input, args.cin, nb1, c);
-            const int64_t wc = (int64_t)k * args.cin_g + (int64_t)kc * kBK + b_part_elems;
-            rb0 = load_w_chunk<TW>(weight, w_row0 + wc, vb0);
-            if (!kI8) rb1 = load_w_chunk<TW>(weight, w_row1 + wc, vb1);
-        };
-        auto store_lds = [&](int buf) {
-            unsigned char *a = s_a[buf];
-            *reinterpret_cast<uint4 *>(a + ra * kLdsStride + pa * 16) = ra0;
-            *reinterpret_cast<uint4 *>(a + (ra + 64) * kLdsStride + pa * 16) = ra1;
+        auto store_b = [&](int buf) {
             unsigned char *b = s_b[buf];
-            if (kI8) {
-                uint4 w0, w1;
-                widen_i8x16(rb0, w0, w1);
-                *reinterpret_cast<uint4 *>(b + ob * kLdsStride + (tid & 1) * 32) = w0;
-                *reinterpret_cast<uint4 *>(b + ob * kLdsStride + (tid & 1) * 32 + 16) = w1;
-            } else {
-                *reinterpret_cast<uint4 *>(b + ra * kLdsStride + pa * 16) = rb0;
-                *reinterpret_cast<uint4 *>(b + (ra + 64) * kLdsStride + pa * 16) = rb1;
+#pragma unroll
+            for (int i = 0; i < kBPerThread; ++i) {
+                const int idx = tid + kThreads * i;
+                const int ch = idx / kWPieces, pc = idx % kWPieces;
+                if constexpr (kI8) {
+                    uint4 w0, w1;
+                    widen_i8x16(rb[i], w0, w1);
+                    *reinterpret_cast<uint4 *>(b + ch * kStride + pc * 32) = w0;
+                    *reinterpret_cast<uint4 *>(b + ch * kStride + pc * 32 + 16) = w1;
+                } else {
+                    *reinterpret_cast<uint4 *>(b + ch * kStride + pc * 16) = rb[i];
+                }
+            }
+        };
+        const int bcol = lane & 31;
+        auto compute = [&](int buf, const APiece<NP> &c0, const APiece<NP> &c1) {
+            const unsigned char *b = s_b[buf];
+#pragma unroll
+            for (int q = 0; q < NP; ++q) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint4 bq = *reinterpret_cast<const uint4 *>(
+                        b + (j * 32 + bcol) * kStride + piece_offset<kF32, CB>(q, half));
+                    mfma_piece<kF32>(acc[0][j], c0.p[q], bq);
+                    mfma_piece<kF32>(acc[1][j], c1.p[q], bq);
+                }
             }
         };
 
-        issue_loads(s_klist[0], 0);
-        store_lds(0);
+        APiece<NP> x0, x1, y0, y1;
+        load_stage(0, x0, x1);
+        store_b(0);
         __syncthreads();
-
-        int ki_next = 0, kc_next = 0;  // decoded (offset index, chunk) of stage s+1
-        const int arow = wm * 64 + (lane & 31);
-        const int brow = wn * 64 + (lane & 31);
-        const int half = lane >> 5;
-        for (int s = 0; s < S; ++s) {
-            const bool more = s + 1 < S;
-            if (more) {
-                if (++kc_next == nkc) {
-                    kc_next = 0;
-                    ++ki_next;
-                    nb0 = nn0;
-                    nb1 = nn1;
-                    if (ki_next + 1 < nk) load_nbr(s_klist[ki_next + 1], nn0, nn1);
-                }
-                issue_loads(s_klist[ki_next], kc_next);
-            }
-            const unsigned char *a = s_a[s & 1];
-            const unsigned char *b = s_b[s & 1];
-            if constexpr (!kF32) {
-#pragma unroll
-                for (int kk = 0; kk < 2; ++kk) {
-                    const int off = kk * 32 + half * 16;
-                    bf16x8 af[2], bfr[2];
-#pragma unroll
-                    for (int i = 0; i < 2; ++i)
-                        af[i] = __builtin_bit_cast(
-                            bf16x8, *reinterpret_cast<const uint4 *>(a + (arow + i * 32) * kLdsStride + off));
-#pragma unroll
-                    for (int j = 0; j < 2; ++j)
-                        bfr[j] = __builtin_bit_cast(
-                            bf16x8, *reinterpret_cast<const uint4 *>(b + (brow + j * 32) * kLdsStride + off));
-#pragma unroll
-                    for (int i = 0; i < 2; ++i)
-#pragma unroll
-                        for (int j = 0; j < 2; ++j)
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
-                }
-            } else {
-                // Lane half h holds k-elements h*8 .. h*8+7 of the 16-float slice;
-                // step kk multiplies element kk of each half.
-                float af[2][8], bfr[2][8];
-#pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    const float4 *p = reinterpret_cast<const float4 *>(a + (arow + i * 32) * kLdsStride + half * 32);
-                    const float4 x0 = p[0], x1 = p[1];
-                    af[i][0] = x0.x; af[i][1] = x0.y; af[i][2] = x0.z; af[i][3] = x0.w;
-                    af[i][4] = x1.x; af[i][5] = x1.y; af[i][6] = x1.z; af[i][7] = x1.w;
-                }
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const float4 *p = reinterpret_cast<const float4 *>(b + (brow + j * 32) * kLdsStride + half * 32);
-                    const float4 x0 = p[0], x1 = p[1];
-                    bfr[j][0] = x0.x; bfr[j][1] = x0.y; bfr[j][2] = x0.z; bfr[j][3] = x0.w;
-                    bfr[j][4] = x1.x; bfr[j][5] = x1.y; bfr[j][6] = x1.z; bfr[j][7] = x1.w;
-                }
-#pragma unroll
-                for (int kk = 0; kk < 8; ++kk)
-#pragma unroll
-                    for (int i = 0; i < 2; ++i)
-#pragma unroll
-                        for (int j = 0; j < 2; ++j)
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][kk], bfr[j][kk], acc[i][j], 0, 0, 0);
-            }
-            if (more) store_lds((s + 1) & 1);
+        // sched_barrier keeps the next stage's loads ahead of this stage's
+        // MFMAs (the scheduler would otherwise sink them below).
+        for (int t = 0; t < S2; t += 2) {
+            load_stage(t + 1, y0, y1);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(0, x0, x1);
+            store_b(1);
+            __syncthreads();
+            load_stage(t + 2, x0, x1);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(1, y0, y1);
+            store_b(0);
             __syncthreads();
         }
     }
 
     // ---- epilogue.  32x32 MFMA result layout: lane l, element e ->
     //      row 8*(e/4) + 4*(l/32) + e%4, column l%32.
-    TO *out = static_cast<TO *>(args.out);
-    const TO *res = static_cast<const TO *>(args.residual);
+    // Each output element is read (residual) and written by one lane exactly
+    // once, so the restrict qualifiers hold even when residual == out.
+    TO *__restrict__ out = static_cast<TO *>(args.out);
+    const TO *__restrict__ res = static_cast<const TO *>(args.residual);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int oc = o0 + wn * 64 + j * 32 + (lane & 31);
+    for (int j = 0; j < 4; ++j) {
+        const int oc = o0 + j * 32 + (lane & 31);
         if (oc >= args.cout_g) continue;
         const int64_t o = out_col0 + oc;
         const float bias = args.bias ? args.bias[o] : 0.f;
@@ -300,7 +398,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv_mfma_kernel(ConvArgs args)
         for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const int r = wm * 64 + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                const int r = wave * 64 + i * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
                 if (r < nrows) {
                     const int64_t idx = (row0 + r) * args.cout + o;
                     float v = kI8 ? acc[i][j][e] * scale + bias : acc[i][j][e] + bias;
@@ -353,12 +451,16 @@ template <typename TA, typename TW, typename TO>
 int launch_conv(const ConvArgs &a, int groups, bool mfma, hipStream_t s)
 {
     if (mfma) {
-        const int64_t tiles = (a.n_q + kBM - 1) / kBM;
+        const bool wide = a.cin_g % (128 / (int)sizeof(TA)) == 0;
+        const int64_t tiles = (a.n_q + kTileRows - 1) / kTileRows;
         const int64_t ntile = (a.cout_g + kBN - 1) / kBN;
         if (tiles > INT32_MAX || ntile > 65535 || groups > 65535)
             return fail(SC_ERR_OVERFLOW, "sparse conv grid overflow");
         dim3 grid((unsigned)tiles, (unsigned)ntile, (unsigned)groups);
-        conv_mfma_kernel<TA, TW, TO><<<grid, kThreads, 0, s>>>(a);
+        if (wide)
+            conv_mfma_kernel<TA, TW, TO, 128><<<grid, kThreads, 0, s>>>(a);
+        else
+            conv_mfma_kernel<TA, TW, TO, 64><<<grid, kThreads, 0, s>>>(a);
         SC_LAUNCH_CHECK("conv_mfma_kernel launch");
     } else {
         conv_scalar_kernel<TA, TW, TO><<<grid_for(a.n_q * a.cout, 256, 65536), 256, 0, s>>>(a);
@@ -424,8 +526,14 @@ extern "C" int sc_subm_conv_forward(const sc_conv_config *cfg, int act_dtype, co
 
     const size_t asz = dtype_size(act_dtype);
     const int bk = kChunkBytes / (int)asz;
-    const uintptr_t align = (uintptr_t)d_input | (uintptr_t)d_weight;
-    const bool mfma = (a.cin_g % bk == 0) && K <= kMaxMaskK && (align % 16 == 0);
+    const uintptr_t align = (uintptr_t)d_input | (uintptr_t)d_weight | (uintptr_t)d_map;
+    // The MFMA kernel addresses input and weights through buffer descriptors
+    // with 32-bit byte offsets (absent rows use offsets >= 3 GiB): both
+    // tensors must stay below 2 GiB.
+    const int64_t in_bytes = n_in * cfg->in_channels * (int64_t)asz;
+    const int64_t w_bytes = cfg->out_channels * K * cfg->in_channels_per_group * (int64_t)dtype_size(w_dtype);
+    const bool mfma = (a.cin_g % bk == 0) && K <= kMaxTableK && (align % 16 == 0) &&
+                      in_bytes < (int64_t)1 << 31 && w_bytes < (int64_t)1 << 31;
     const int groups = (int)cfg->groups;
     hipStream_t s = as_stream(stream);
     if (act_f32) {
