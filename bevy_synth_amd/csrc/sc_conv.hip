@@ -53,6 +53,7 @@ struct ConvArgs {
     int cin_g;
     int cout_g;
     int K;
+    int vec_out;      // 4-channel packed output stores allowed (counts and pointers aligned)
 };
 
 // ------------------------------------------------------------ loaders
@@ -139,21 +140,54 @@ __device__ inline APiece<CB / 32> load_a_pieces(__amdgpu_buffer_rsrc_t r, uint32
 
 __device__ inline float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
 
-// One piece of one 32x32 output block: bf16 -> one v_mfma_f32_32x32x16_bf16;
+// One piece of one 32x32 output block, computed transposed: the weight
+// fragment w (32 output channels) is the MFMA A operand and the gathered
+// input fragment x (32 voxel rows) the B operand, so D[o][r] = sum_k w[o][k]
+// x[r][k] and a lane ends up holding 4 consecutive output channels of one
+// row (packed stores in the epilogue).  bf16 -> one v_mfma_f32_32x32x16_bf16;
 // f32 -> four v_mfma_f32_32x32x2_f32 (element e of each lane half's piece).
 template <bool kF32>
-__device__ inline void mfma_piece(f32x16 &acc, const uint4 &a, const uint4 &b)
+__device__ inline void mfma_piece(f32x16 &acc, const uint4 &x, const uint4 &w)
 {
     if constexpr (!kF32) {
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
-                                                      __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w),
+                                                      __builtin_bit_cast(bf16x8, x), acc, 0, 0, 0);
     } else {
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(u2f(a.x), u2f(b.x), acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(u2f(a.y), u2f(b.y), acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(u2f(a.z), u2f(b.z), acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(u2f(a.w), u2f(b.w), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(u2f(w.x), u2f(x.x), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(u2f(w.y), u2f(x.y), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(u2f(w.z), u2f(x.z), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(u2f(w.w), u2f(x.w), acc, 0, 0, 0);
     }
 }
+
+// Packs / unpacks 4 consecutive output values.
+template <typename TO>
+struct Out4;
+template <>
+struct Out4<float> {
+    typedef float4 V;
+    static __device__ inline V pack(const float *v) { return make_float4(v[0], v[1], v[2], v[3]); }
+    static __device__ inline void unpack(const V &u, float *v)
+    {
+        v[0] = u.x; v[1] = u.y; v[2] = u.z; v[3] = u.w;
+    }
+};
+template <>
+struct Out4<uint16_t> {
+    typedef uint2 V;
+    static __device__ inline V pack(const float *v)
+    {
+        return make_uint2((uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16),
+                          (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16));
+    }
+    static __device__ inline void unpack(const V &u, float *v)
+    {
+        v[0] = bf16_to_f32((uint16_t)(u.x & 0xffffu));
+        v[1] = bf16_to_f32((uint16_t)(u.x >> 16));
+        v[2] = bf16_to_f32((uint16_t)(u.y & 0xffffu));
+        v[3] = bf16_to_f32((uint16_t)(u.y >> 16));
+    }
+};
 
 __device__ inline int tile_for_block(int b, int G)
 {
@@ -381,29 +415,48 @@ __global__ __launch_bounds__(kThreads, 2) void conv_mfma_kernel(ConvArgs args)
         }
     }
 
-    // ---- epilogue.  32x32 MFMA result layout: lane l, element e ->
-    //      row 8*(e/4) + 4*(l/32) + e%4, column l%32.
-    // Each output element is read (residual) and written by one lane exactly
-    // once, so the restrict qualifiers hold even when residual == out.
+    // ---- epilogue.  32x32 MFMA result layout (transposed product): lane l,
+    //      element e -> output channel 8*(e/4) + 4*(l/32) + e%4 of the block,
+    //      voxel row l%32.  Each run of 4 elements is 4 consecutive channels.
     TO *__restrict__ out = static_cast<TO *>(args.out);
     const TO *__restrict__ res = static_cast<const TO *>(args.residual);
+    const bool vec_ok = args.vec_out != 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int oc = o0 + j * 32 + (lane & 31);
-        if (oc >= args.cout_g) continue;
-        const int64_t o = out_col0 + oc;
-        const float bias = args.bias ? args.bias[o] : 0.f;
-        const float scale = (kI8 && args.w_scale) ? args.w_scale[o] : 1.f;
+    for (int i = 0; i < 2; ++i) {
+        const int r = wave * 64 + i * 32 + (lane & 31);
+        if (r >= nrows) continue;
+        const int64_t rowbase = (row0 + r) * args.cout + out_col0;
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int r = wave * 64 + i * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
-                if (r < nrows) {
-                    const int64_t idx = (row0 + r) * args.cout + o;
-                    float v = kI8 ? acc[i][j][e] * scale + bias : acc[i][j][e] + bias;
-                    if (res) v += load_as_f32<TO>(res, idx);
-                    store_from_f32<TO>(out, idx, v);
+            for (int e4 = 0; e4 < 4; ++e4) {
+                const int oc = o0 + j * 32 + 8 * e4 + 4 * half;  // first of 4 channels
+                float v[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int o = oc + c;
+                    const float bias = (args.bias && o < args.cout_g) ? args.bias[out_col0 + o] : 0.f;
+                    const float scale = (kI8 && args.w_scale && o < args.cout_g) ? args.w_scale[out_col0 + o] : 1.f;
+                    const float a = acc[i][j][4 * e4 + c];
+                    v[c] = kI8 ? a * scale + bias : a + bias;
+                }
+                if (vec_ok && oc + 3 < args.cout_g) {
+                    typename Out4<TO>::V *dst = reinterpret_cast<typename Out4<TO>::V *>(out + rowbase + oc);
+                    if (res) {
+                        float rv[4];
+                        Out4<TO>::unpack(*reinterpret_cast<const typename Out4<TO>::V *>(res + rowbase + oc), rv);
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) v[c] += rv[c];
+                    }
+                    *dst = Out4<TO>::pack(v);
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        if (oc + c >= args.cout_g) continue;
+                        float t = v[c];
+                        if (res) t += load_as_f32<TO>(res, rowbase + oc + c);
+                        store_from_f32<TO>(out, rowbase + oc + c, t);
+                    }
                 }
             }
     }
@@ -523,6 +576,8 @@ extern "C" int sc_subm_conv_forward(const sc_conv_config *cfg, int act_dtype, co
     a.cin_g = (int)cfg->in_channels_per_group;
     a.cout_g = (int)cfg->out_channels_per_group;
     a.K = (int)K;
+    a.vec_out = (a.cout_g % 4 == 0) && (a.cout % 4 == 0) && ((uintptr_t)d_out % 16 == 0) &&
+                ((uintptr_t)d_residual % 16 == 0);
 
     const size_t asz = dtype_size(act_dtype);
     const int bk = kChunkBytes / (int)asz;
