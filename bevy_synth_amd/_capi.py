@@ -22,6 +22,7 @@ EXPORTED = (
     "sc_abi_version", "sc_status_string", "sc_last_error", "sc_validate_config",
     "sc_kernel_rows", "sc_kernel_offsets", "sc_neighbor_map_workspace_size",
     "sc_neighbor_map_build", "sc_neighbor_map_check", "sc_subm_conv_forward",
+    "sc_subm_conv_forward_fused",
     "sc_layer_norm", "sc_add", "sc_subdivision_workspace_size", "sc_subdivision_build",
     "sc_gather_rows", "sc_c2s_skip_add", "sc_convert",
 )
@@ -41,6 +42,19 @@ class ScConvConfig(ctypes.Structure):
         ("groups", ctypes.c_int64),
         ("axis_order", ctypes.c_int32 * 3),
         ("axis_sign", ctypes.c_int32 * 3),
+    ]
+
+
+class ScConvEpilogue(ctypes.Structure):
+    """sc_conv_epilogue: fused + bias -> LayerNorm -> SiLU -> + residual."""
+
+    _fields_ = [
+        ("residual", ctypes.c_void_p),
+        ("layer_norm", ctypes.c_int),
+        ("ln_weight", ctypes.c_void_p),
+        ("ln_bias", ctypes.c_void_p),
+        ("ln_eps", ctypes.c_float),
+        ("silu", ctypes.c_int),
     ]
 
 
@@ -81,6 +95,8 @@ def load() -> ctypes.CDLL:
     L.sc_neighbor_map_build.argtypes = [cfgp, P, i64, i64, P, P, ctypes.c_size_t, P]
     L.sc_neighbor_map_check.argtypes = [P, P]
     L.sc_subm_conv_forward.argtypes = [cfgp, i32, P, i64, P, i64, i32, P, P, P, P, i32, P, P]
+    L.sc_subm_conv_forward_fused.argtypes = [cfgp, i32, P, i64, P, i64, i32, P, P, P,
+                                             ctypes.POINTER(ScConvEpilogue), i32, P, P]
     L.sc_layer_norm.argtypes = [i32, P, i64, i64, P, P, ctypes.c_float, i32, i32, P, P]
     L.sc_add.argtypes = [i32, P, P, i64, P, P]
     L.sc_subdivision_workspace_size.argtypes = [i64, sizep]

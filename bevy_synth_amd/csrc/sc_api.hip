@@ -62,6 +62,30 @@ __global__ void convert_kernel(const Tin *__restrict__ in, Tout *__restrict__ ou
 }
 
 template <typename T>
+__global__ void silu_kernel(T *x, int64_t n)
+{
+    int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const float t = load_as_f32<T>(x, i);
+        store_from_f32<T>(x, i, t / (1.0f + expf(-t)));
+    }
+}
+
+int silu_inplace(int dtype, void *d, int64_t n, hipStream_t s)
+{
+    if (n <= 0) return SC_OK;
+    const unsigned g = grid_for(n, 256, 8192);
+    if (dtype == SC_DTYPE_F32)
+        silu_kernel<float><<<g, 256, 0, s>>>((float *)d, n);
+    else if (dtype == SC_DTYPE_BF16)
+        silu_kernel<uint16_t><<<g, 256, 0, s>>>((uint16_t *)d, n);
+    else
+        return fail(SC_ERR_DTYPE, "silu: dtype must be f32 or bf16");
+    SC_LAUNCH_CHECK("silu_kernel launch");
+    return SC_OK;
+}
+
+template <typename T>
 __global__ void add_kernel(const T *__restrict__ a, const T *__restrict__ b, T *out, int64_t n)
 {
     int64_t stride = (int64_t)gridDim.x * blockDim.x;

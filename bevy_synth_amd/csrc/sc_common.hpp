@@ -32,6 +32,8 @@ int hip_fail(hipError_t err, const char *what);
     } while (0)
 
 int validate_config(const sc_conv_config *cfg);
+// In-place x / (1 + exp(-x)) over n values (f32 or bf16); stream-ordered.
+int silu_inplace(int dtype, void *d, int64_t n, hipStream_t s);
 
 inline bool mul_ok(int64_t a, int64_t b, int64_t *out)
 {

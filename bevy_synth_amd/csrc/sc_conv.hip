@@ -54,6 +54,13 @@ struct ConvArgs {
     int cout_g;
     int K;
     int vec_out;      // 4-channel packed output stores allowed (counts and pointers aligned)
+    // Fused epilogue (order: + bias -> LayerNorm over the row -> SiLU -> + residual).
+    // LayerNorm needs every channel of a row in one workgroup (groups == 1, Cout <= 128).
+    int ln;
+    const float *ln_w;
+    const float *ln_b;
+    float ln_eps;
+    int silu;
 };
 
 // ------------------------------------------------------------ loaders
@@ -417,15 +424,69 @@ __global__ __launch_bounds__(kThreads, 2) void conv_mfma_kernel(ConvArgs args)
 
     // ---- epilogue.  32x32 MFMA result layout (transposed product): lane l,
     //      element e -> output channel 8*(e/4) + 4*(l/32) + e%4 of the block,
-    //      voxel row l%32.  Each run of 4 elements is 4 consecutive channels.
+    //      voxel row l%32.  Each run of 4 elements is 4 consecutive channels;
+    //      lanes l and l^32 together hold all channels of a row.
     TO *__restrict__ out = static_cast<TO *>(args.out);
     const TO *__restrict__ res = static_cast<const TO *>(args.residual);
     const bool vec_ok = args.vec_out != 0;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int r = wave * 64 + i * 32 + (lane & 31);
-        if (r >= nrows) continue;
+        if (r >= nrows) continue;  // lanes l and l^32 share r: both skip together
         const int64_t rowbase = (row0 + r) * args.cout + out_col0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int o = o0 + j * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
+                const bool ok = o < args.cout_g;
+                const float bias = (args.bias && ok) ? args.bias[out_col0 + o] : 0.f;
+                const float scale = (kI8 && args.w_scale && ok) ? args.w_scale[out_col0 + o] : 1.f;
+                acc[i][j][e] = ok ? (kI8 ? acc[i][j][e] * scale + bias : acc[i][j][e] + bias) : 0.f;
+            }
+        if (args.ln) {
+            // Two-pass f32 statistics over the row's Cout channels (the
+            // reference's layer_norm_row_stats, wgpu/ops.rs:162-187).
+            float s = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) s += acc[i][j][e];
+            s += __shfl_xor(s, 32, 64);
+            const float inv_c = 1.0f / (float)args.cout_g;
+            const float mean = s * inv_c;
+            float q = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int o = o0 + j * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
+                    const float d = acc[i][j][e] - mean;
+                    q += o < args.cout_g ? d * d : 0.f;
+                }
+            q += __shfl_xor(q, 32, 64);
+            const float inv_std = 1.0f / sqrtf(q * inv_c + args.ln_eps);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int o = o0 + j * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
+                    const bool ok = o < args.cout_g;
+                    float t = (acc[i][j][e] - mean) * inv_std;
+                    if (args.ln_w && ok) t *= args.ln_w[o];
+                    if (args.ln_b && ok) t += args.ln_b[o];
+                    acc[i][j][e] = t;
+                }
+        }
+        if (args.silu) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const float t = acc[i][j][e];
+                    acc[i][j][e] = t / (1.0f + expf(-t));
+                }
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -433,13 +494,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv_mfma_kernel(ConvArgs args)
                 const int oc = o0 + j * 32 + 8 * e4 + 4 * half;  // first of 4 channels
                 float v[4];
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const int o = oc + c;
-                    const float bias = (args.bias && o < args.cout_g) ? args.bias[out_col0 + o] : 0.f;
-                    const float scale = (kI8 && args.w_scale && o < args.cout_g) ? args.w_scale[out_col0 + o] : 1.f;
-                    const float a = acc[i][j][4 * e4 + c];
-                    v[c] = kI8 ? a * scale + bias : a + bias;
-                }
+                for (int c = 0; c < 4; ++c) v[c] = acc[i][j][4 * e4 + c];
                 if (vec_ok && oc + 3 < args.cout_g) {
                     typename Out4<TO>::V *dst = reinterpret_cast<typename Out4<TO>::V *>(out + rowbase + oc);
                     if (res) {
@@ -527,13 +582,29 @@ int launch_conv(const ConvArgs &a, int groups, bool mfma, hipStream_t s)
 
 using namespace sc;
 
-extern "C" int sc_subm_conv_forward(const sc_conv_config *cfg, int act_dtype, const void *d_input,
-                                    int64_t n_in, const int32_t *d_map, int64_t n_q, int w_dtype,
-                                    const void *d_weight, const float *d_w_scale,
-                                    const float *d_bias, const void *d_residual, int out_dtype,
-                                    void *d_out, sc_stream stream)
+static int launch_conv_typed(const ConvArgs &a, bool act_f32, int w_dtype, int out_dtype, int groups,
+                             bool mfma, hipStream_t s)
+{
+    if (act_f32) {
+        if (out_dtype == SC_DTYPE_F32) return launch_conv<float, float, float>(a, groups, mfma, s);
+        return launch_conv<float, float, uint16_t>(a, groups, mfma, s);
+    }
+    if (w_dtype == SC_DTYPE_BF16) {
+        if (out_dtype == SC_DTYPE_F32) return launch_conv<uint16_t, uint16_t, float>(a, groups, mfma, s);
+        return launch_conv<uint16_t, uint16_t, uint16_t>(a, groups, mfma, s);
+    }
+    if (out_dtype == SC_DTYPE_F32) return launch_conv<uint16_t, int8_t, float>(a, groups, mfma, s);
+    return launch_conv<uint16_t, int8_t, uint16_t>(a, groups, mfma, s);
+}
+
+static int conv_forward_impl(const sc_conv_config *cfg, int act_dtype, const void *d_input,
+                             int64_t n_in, const int32_t *d_map, int64_t n_q, int w_dtype,
+                             const void *d_weight, const float *d_w_scale, const float *d_bias,
+                             const sc_conv_epilogue *epi, int out_dtype, void *d_out,
+                             sc_stream stream)
 {
     clear_error();
+    const void *d_residual = epi ? epi->residual : nullptr;
     int rc = validate_config(cfg);
     if (rc) return rc;
     if (n_in < 0 || n_q < 0) return fail(SC_ERR_SHAPE, "negative row count");
@@ -578,6 +649,10 @@ extern "C" int sc_subm_conv_forward(const sc_conv_config *cfg, int act_dtype, co
     a.K = (int)K;
     a.vec_out = (a.cout_g % 4 == 0) && (a.cout % 4 == 0) && ((uintptr_t)d_out % 16 == 0) &&
                 ((uintptr_t)d_residual % 16 == 0);
+    a.ln = 0;
+    a.ln_w = a.ln_b = nullptr;
+    a.ln_eps = 0.f;
+    a.silu = 0;
 
     const size_t asz = dtype_size(act_dtype);
     const int bk = kChunkBytes / (int)asz;
@@ -591,14 +666,52 @@ extern "C" int sc_subm_conv_forward(const sc_conv_config *cfg, int act_dtype, co
                       in_bytes < (int64_t)1 << 31 && w_bytes < (int64_t)1 << 31;
     const int groups = (int)cfg->groups;
     hipStream_t s = as_stream(stream);
-    if (act_f32) {
-        if (out_dtype == SC_DTYPE_F32) return launch_conv<float, float, float>(a, groups, mfma, s);
-        return launch_conv<float, float, uint16_t>(a, groups, mfma, s);
+    const bool want_ln = epi && epi->layer_norm, want_silu = epi && epi->silu;
+    // In-kernel epilogue when one workgroup holds whole rows; otherwise the
+    // conv writes its output and LayerNorm/SiLU and the residual run after it.
+    const bool fuse = mfma && groups == 1 && a.cout_g <= kBN;
+    if (want_ln || want_silu) {
+        if (fuse) {
+            a.ln = want_ln;
+            a.ln_w = epi->ln_weight;
+            a.ln_b = epi->ln_bias;
+            a.ln_eps = epi->ln_eps;
+            a.silu = want_silu;
+        } else {
+            a.residual = nullptr;
+        }
     }
-    if (w_dtype == SC_DTYPE_BF16) {
-        if (out_dtype == SC_DTYPE_F32) return launch_conv<uint16_t, uint16_t, float>(a, groups, mfma, s);
-        return launch_conv<uint16_t, uint16_t, uint16_t>(a, groups, mfma, s);
-    }
-    if (out_dtype == SC_DTYPE_F32) return launch_conv<uint16_t, int8_t, float>(a, groups, mfma, s);
-    return launch_conv<uint16_t, int8_t, uint16_t>(a, groups, mfma, s);
+    int rc2 = launch_conv_typed(a, act_f32, w_dtype, out_dtype, groups, mfma, s);
+    if (rc2 != SC_OK || fuse || !(want_ln || want_silu)) return rc2;
+    if (want_ln)
+        rc2 = sc_layer_norm(out_dtype, d_out, n_q, cfg->out_channels, epi->ln_weight, epi->ln_bias,
+                            epi->ln_eps, want_silu, out_dtype, d_out, stream);
+    else
+        rc2 = silu_inplace(out_dtype, d_out, n_q * cfg->out_channels, s);
+    if (rc2 != SC_OK || !d_residual) return rc2;
+    return sc_add(out_dtype, d_out, d_residual, n_q * cfg->out_channels, d_out, stream);
+}
+
+
+extern "C" int sc_subm_conv_forward(const sc_conv_config *cfg, int act_dtype, const void *d_input,
+                                    int64_t n_in, const int32_t *d_map, int64_t n_q, int w_dtype,
+                                    const void *d_weight, const float *d_w_scale,
+                                    const float *d_bias, const void *d_residual, int out_dtype,
+                                    void *d_out, sc_stream stream)
+{
+    sc_conv_epilogue epi{};
+    epi.residual = d_residual;
+    return conv_forward_impl(cfg, act_dtype, d_input, n_in, d_map, n_q, w_dtype, d_weight, d_w_scale,
+                             d_bias, &epi, out_dtype, d_out, stream);
+}
+
+extern "C" int sc_subm_conv_forward_fused(const sc_conv_config *cfg, int act_dtype,
+                                          const void *d_input, int64_t n_in, const int32_t *d_map,
+                                          int64_t n_q, int w_dtype, const void *d_weight,
+                                          const float *d_w_scale, const float *d_bias,
+                                          const sc_conv_epilogue *epi, int out_dtype, void *d_out,
+                                          sc_stream stream)
+{
+    return conv_forward_impl(cfg, act_dtype, d_input, n_in, d_map, n_q, w_dtype, d_weight, d_w_scale,
+                             d_bias, epi, out_dtype, d_out, stream);
 }

@@ -38,9 +38,11 @@ class ConvLayer:
     w_scale: Optional[torch.Tensor] = None
 
     def __call__(self, x: torch.Tensor, nbr: torch.Tensor, out_dtype=None,
-                 residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+                 residual: Optional[torch.Tensor] = None, layer_norm: bool = False,
+                 silu: bool = False, ln_eps: float = LAYER_NORM32_EPS) -> torch.Tensor:
         return sparse_subm_conv_forward(self.cfg, x, nbr, self.weight, self.bias, self.w_scale,
-                                        residual=residual, out_dtype=out_dtype)
+                                        residual=residual, out_dtype=out_dtype,
+                                        layer_norm=layer_norm, ln_eps=ln_eps, silu=silu)
 
 
 @dataclass
@@ -50,8 +52,8 @@ class ResidualBlock:
     eps: float = LAYER_NORM32_EPS
 
     def __call__(self, x: torch.Tensor, nbr: torch.Tensor) -> torch.Tensor:
-        h = self.conv1(x, nbr, out_dtype=x.dtype)
-        h = layer_norm(h, eps=self.eps, silu=True, out=h)
+        # conv1 carries LayerNorm + SiLU in its epilogue; conv2 adds the residual.
+        h = self.conv1(x, nbr, out_dtype=x.dtype, layer_norm=True, silu=True, ln_eps=self.eps)
         return self.conv2(h, nbr, out_dtype=x.dtype, residual=x)
 
 

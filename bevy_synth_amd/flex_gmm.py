@@ -183,13 +183,18 @@ def sparse_subm_conv_forward(cfg: SparseSubmConvConfig, input: torch.Tensor,
                              w_scale: Optional[torch.Tensor] = None,
                              residual: Optional[torch.Tensor] = None,
                              out_dtype: Optional[torch.dtype] = None,
-                             out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                             out: Optional[torch.Tensor] = None,
+                             layer_norm: bool = False, ln_weight: Optional[torch.Tensor] = None,
+                             ln_bias: Optional[torch.Tensor] = None, ln_eps: float = 1e-6,
+                             silu: bool = False) -> torch.Tensor:
     """sparse_subm_conv_forward_wgpu (crates/burn_flex_gmm/src/wgpu/sparse_conv.rs:310-367).
 
     input [N_in, Cin] f32|bf16; neighbor_rows [N_q, K] int32 (N_q <= N_in);
     weight [Cout, KD, KH, KW, Cin_g] (or any view with that element count)
     f32 (f32 input), bf16 or int8 (+ w_scale [Cout] f32) (bf16 input);
     bias [Cout] f32 or None; residual [N_q, Cout] in the output dtype or None.
+    Optional fused epilogue: + bias -> LayerNorm over Cout (ln_weight / ln_bias
+    [Cout] f32 or None, ln_eps) -> SiLU -> + residual.
     Returns [N_q, Cout] in out_dtype (default: the input dtype)."""
     _require_cuda("input", input)
     _require_cuda("neighbor_rows", neighbor_rows)
@@ -226,6 +231,24 @@ def sparse_subm_conv_forward(cfg: SparseSubmConvConfig, input: torch.Tensor,
         _require_cuda("residual", residual)
         if residual.shape != (n_q, cfg.out_channels) or residual.dtype != od:
             raise SparseConvError(2, "residual must be [N_q, Cout] in the output dtype")
+    for name, t in (("ln_weight", ln_weight), ("ln_bias", ln_bias)):
+        if t is not None:
+            _require_cuda(name, t)
+            if t.dtype != torch.float32 or t.numel() != cfg.out_channels:
+                raise SparseConvError(2, f"{name} must be f32 [Cout]")
+    if layer_norm or silu:
+        epi = _capi.ScConvEpilogue()
+        epi.residual = None if residual is None else residual.data_ptr()
+        epi.layer_norm = int(layer_norm)
+        epi.ln_weight = None if ln_weight is None else ln_weight.data_ptr()
+        epi.ln_bias = None if ln_bias is None else ln_bias.data_ptr()
+        epi.ln_eps = float(ln_eps)
+        epi.silu = int(silu)
+        check(_capi.load().sc_subm_conv_forward_fused(
+            ctypes.byref(c), _dt(input), _ptr(input), input.shape[0], _ptr(neighbor_rows), n_q,
+            _dt(weight), _ptr(weight), _ptr(w_scale), _ptr(bias), ctypes.byref(epi), _dt(out),
+            _ptr(out), _stream()))
+        return out
     check(_capi.load().sc_subm_conv_forward(
         ctypes.byref(c), _dt(input), _ptr(input), input.shape[0], _ptr(neighbor_rows), n_q,
         _dt(weight), _ptr(weight), _ptr(w_scale), _ptr(bias), _ptr(residual), _dt(out),

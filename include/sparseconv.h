@@ -151,6 +151,35 @@ int sc_subm_conv_forward(const sc_conv_config *cfg, int act_dtype, const void *d
                          const void *d_weight, const float *d_w_scale, const float *d_bias,
                          const void *d_residual, int out_dtype, void *d_out, sc_stream stream);
 
+/*
+ * Epilogue fused into the conv (the block patterns of the decoder: conv ->
+ * LayerNorm -> SiLU, sparse_decoder_wgpu_ops.rs:1091-1161, and conv -> + x):
+ *   y = conv + bias;  if layer_norm: y = LN(y over the row's Cout channels)
+ *   [*ln_weight][+ln_bias] (two-pass f32, biased variance, ln_eps);  if silu:
+ *   y = y / (1 + exp(-y));  if residual: y += residual.
+ */
+typedef struct sc_conv_epilogue {
+    const void *residual;    /* [n_q][Cout] in out_dtype, or NULL */
+    int layer_norm;          /* 0 / 1 */
+    const float *ln_weight;  /* [Cout] or NULL */
+    const float *ln_bias;    /* [Cout] or NULL */
+    float ln_eps;
+    int silu;                /* 0 / 1 */
+} sc_conv_epilogue;
+
+/* sc_subm_conv_forward with a fused epilogue (same arguments, epi replaces
+ * d_residual; epi may be NULL).  The epilogue runs inside the conv kernel, on
+ * the f32 accumulators, when one workgroup holds whole rows (groups == 1,
+ * Cout <= 128, the MFMA tile); otherwise the conv stores its output in
+ * out_dtype and LayerNorm/SiLU and the residual run as separate
+ * stream-ordered kernels (for a bf16 output that is one more bf16 rounding,
+ * before the LayerNorm). */
+int sc_subm_conv_forward_fused(const sc_conv_config *cfg, int act_dtype, const void *d_input,
+                               int64_t n_in, const int32_t *d_map, int64_t n_q, int w_dtype,
+                               const void *d_weight, const float *d_w_scale, const float *d_bias,
+                               const sc_conv_epilogue *epi, int out_dtype, void *d_out,
+                               sc_stream stream);
+
 /* ------------------------------------------------------------ block ops */
 
 /*
