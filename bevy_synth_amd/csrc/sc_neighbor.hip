@@ -19,6 +19,11 @@
 //
 // Linear probing over a power-of-two table with >= 2 slots per row; every
 // probe loop is bounded by the table capacity.
+//
+// When the bbox holds at most 32 cells per row (and the workspace has room),
+// the "table" is a dense bbox-indexed grid of rows instead: the slot of a key
+// is the key itself, so insertion is one atomicMin on a distinct word and a
+// query one load, and the neighbours of nearby voxels share cache lines.
 #include <climits>
 
 #include "sc_common.hpp"
@@ -48,9 +53,18 @@ inline uint64_t table_capacity(int64_t n)
     return cap;
 }
 
+// Dense-grid budget: 32 cells per row (at least 2^16 cells).
+inline uint64_t dense_cells_for(int64_t n)
+{
+    const uint64_t c = (uint64_t)(n > 0 ? n : 0) * 32u;
+    return c < (1u << 16) ? (1u << 16) : c;
+}
+
 inline size_t workspace_bytes_for(int64_t n)
 {
-    return kHeaderBytes + (size_t)table_capacity(n) * 12u;
+    const size_t hash_bytes = (size_t)table_capacity(n) * 12u;
+    const size_t dense_bytes = (size_t)dense_cells_for(n) * 4u;
+    return kHeaderBytes + (hash_bytes > dense_bytes ? hash_bytes : dense_bytes);
 }
 
 // splitmix64 finaliser (Steele, Lea & Flood, OOPSLA 2014).
@@ -63,16 +77,18 @@ __device__ inline uint64_t mix64(uint64_t z)
 
 struct Plan {
     int mode;  // 0: no table (error), 1: 32-bit keys packed with rows, 2: 64-bit keys,
-               // 3: row-only table compared through the coords
+               // 3: row-only table compared through the coords, 4: dense grid
+    uint64_t total;  // bbox cells (valid for modes 1, 2, 4)
     int32_t lo[4];
     int32_t hi[4];
     uint64_t ext[4];
 };
 
-__device__ inline Plan make_plan(const NbrHeader *h)
+__device__ inline Plan make_plan(const NbrHeader *h, uint64_t dense_cells)
 {
     Plan p;
     p.mode = 0;
+    p.total = 0;
     for (int j = 0; j < 4; ++j) {
         p.lo[j] = h->bmin[j];
         p.hi[j] = h->bmax[j];
@@ -85,7 +101,8 @@ __device__ inline Plan make_plan(const NbrHeader *h)
         if (total != 0 && p.ext[j] > kEmpty64 / total) ovf = true;
         total *= p.ext[j];
     }
-    p.mode = ovf ? 3 : (total <= 0xffffffffull ? 1 : 2);
+    p.total = total;
+    p.mode = ovf ? 3 : (total <= dense_cells ? 4 : (total <= 0xffffffffull ? 1 : 2));
     return p;
 }
 
@@ -109,18 +126,26 @@ __device__ inline uint64_t pack_key(const Plan &p, int32_t b, int32_t x, int32_t
     return k;
 }
 
-__global__ void nm_init_kernel(NbrHeader *h, uint64_t *words, uint64_t n_words)
+__global__ void nm_header_init_kernel(NbrHeader *h)
 {
-    const uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (tid == 0) {
-        for (int j = 0; j < 4; ++j) {
-            h->bmin[j] = INT_MAX;
-            h->bmax[j] = INT_MIN;
-        }
-        h->status = 0;
+    for (int j = 0; j < 4; ++j) {
+        h->bmin[j] = INT_MAX;
+        h->bmax[j] = INT_MIN;
     }
+    h->status = 0;
+}
+
+// Fills the table region the plan uses with all-ones (EMPTY keys, EMPTY rows,
+// or -1 grid cells): cap*12 bytes for the hash modes, total*4 for the grid.
+__global__ void nm_table_init_kernel(const NbrHeader *h, uint64_t *words, uint64_t cap,
+                                     uint64_t dense_cells)
+{
+    const Plan p = make_plan(h, dense_cells);
+    if (p.mode == 0) return;
+    const uint64_t n_words = p.mode == 4 ? (p.total + 1) / 2 : cap + cap / 2;
     const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-    for (uint64_t i = tid; i < n_words; i += stride) words[i] = kEmpty64;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_words; i += stride)
+        words[i] = kEmpty64;
 }
 
 __global__ __launch_bounds__(256) void nm_bbox_kernel(const int4 *__restrict__ coords, int64_t n,
@@ -172,14 +197,20 @@ __global__ __launch_bounds__(256) void nm_bbox_kernel(const int4 *__restrict__ c
 
 __global__ __launch_bounds__(256) void nm_insert_kernel(const int4 *__restrict__ coords, int64_t n,
                                                         NbrHeader *h, uint64_t *keys, uint32_t *rows,
-                                                        uint64_t mask)
+                                                        uint64_t mask, uint64_t dense_cells)
 {
-    const Plan p = make_plan(h);
+    const Plan p = make_plan(h, dense_cells);
     const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (p.mode == 0) return;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    uint32_t *grid = reinterpret_cast<uint32_t *>(keys);
     for (int64_t r = tid; r < n; r += stride) {
         const int4 c = coords[r];
+        if (p.mode == 4) {
+            // cells start at 0xffffffff: the unsigned minimum keeps the lowest row
+            atomicMin(&grid[pack_key(p, c.x, c.y, c.z, c.w)], (uint32_t)r);
+            continue;
+        }
         if (p.mode == 3) {
             uint64_t s = hash_coord(c.x, c.y, c.z, c.w) & mask;
             for (uint64_t probe = 0; probe <= mask; ++probe) {
@@ -244,7 +275,8 @@ __global__ __launch_bounds__(256) void nm_query_kernel(const int4 *__restrict__ 
                                                        const NbrHeader *__restrict__ h,
                                                        const uint64_t *__restrict__ keys,
                                                        const uint32_t *__restrict__ rows,
-                                                       uint64_t mask, int32_t *__restrict__ map)
+                                                       uint64_t mask, uint64_t dense_cells,
+                                                       int32_t *__restrict__ map)
 {
     __shared__ int4 s_coord[kMaxStagedRows];
     __shared__ int s_off[kMaxStagedOffsets * 3];
@@ -255,7 +287,8 @@ __global__ __launch_bounds__(256) void nm_query_kernel(const int4 *__restrict__ 
     if (staged)
         for (int k = threadIdx.x; k < ks.K; k += blockDim.x) offset_of(ks, k, &s_off[3 * k]);
     __syncthreads();
-    const Plan p = make_plan(h);
+    const Plan p = make_plan(h, dense_cells);
+    const uint32_t *grid = reinterpret_cast<const uint32_t *>(keys);
     const int total = nrows * ks.K;
     int32_t *out = map + row0 * ks.K;
     for (int e = threadIdx.x; e < total; e += blockDim.x) {
@@ -274,8 +307,11 @@ __global__ __launch_bounds__(256) void nm_query_kernel(const int4 *__restrict__ 
         int32_t found = SC_INVALID_NEIGHBOR_ROW;
         // A negative neighbour is absent (crates/burn_flex_gmm/src/lib.rs:98-100);
         // so is any neighbour outside the bbox of the coord set.
-        if (p.mode != 0 && nx >= p.lo[1] && nx <= p.hi[1] && ny >= p.lo[2] && ny <= p.hi[2] &&
-            nz >= p.lo[3] && nz <= p.hi[3] && p.mode == 3) {
+        const bool inside = p.mode != 0 && nx >= p.lo[1] && nx <= p.hi[1] && ny >= p.lo[2] &&
+                            ny <= p.hi[2] && nz >= p.lo[3] && nz <= p.hi[3];
+        if (inside && p.mode == 4) {
+            found = (int32_t)grid[pack_key(p, c.x, (int32_t)nx, (int32_t)ny, (int32_t)nz)];
+        } else if (inside && p.mode == 3) {
             const int4 q = make_int4(c.x, (int32_t)nx, (int32_t)ny, (int32_t)nz);
             uint64_t s = hash_coord(q.x, q.y, q.z, q.w) & mask;
             for (uint64_t probe = 0; probe <= mask; ++probe) {
@@ -287,8 +323,7 @@ __global__ __launch_bounds__(256) void nm_query_kernel(const int4 *__restrict__ 
                 }
                 s = (s + 1) & mask;
             }
-        } else if (p.mode != 0 && nx >= p.lo[1] && nx <= p.hi[1] && ny >= p.lo[2] && ny <= p.hi[2] &&
-                   nz >= p.lo[3] && nz <= p.hi[3]) {
+        } else if (inside) {
             const uint64_t key = pack_key(p, c.x, (int32_t)nx, (int32_t)ny, (int32_t)nz);
             uint64_t s = mix64(key) & mask;
             if (p.mode == 1) {
@@ -365,15 +400,21 @@ int sc_neighbor_map_build(const sc_conv_config *cfg, const int32_t *d_coords, in
     const uint64_t cap = table_capacity(n_rows);
     uint64_t *keys = (uint64_t *)((char *)d_workspace + kHeaderBytes);
     uint32_t *rows = (uint32_t *)(keys + cap);
-    // Fill keys (cap u64) and rows (cap u32 = cap/2 u64) with all-ones.
-    const uint64_t words = cap + cap / 2;
-    nm_init_kernel<<<grid_for((int64_t)words, 256, 4096), 256, 0, s>>>(h, keys, n_rows ? words : 0);
-    SC_LAUNCH_CHECK("nm_init_kernel launch");
+    // Dense grid when the bbox fits the workspace's grid budget (decided on the
+    // device from the bbox; the budget never exceeds 32 cells per row).
+    uint64_t dense_cells = (workspace_bytes - kHeaderBytes) / 4u;
+    if (dense_cells > dense_cells_for(n_rows)) dense_cells = dense_cells_for(n_rows);
+    dense_cells &= ~1ull;  // even: the 8-byte fill of an odd cell count stays inside
+    nm_header_init_kernel<<<1, 1, 0, s>>>(h);
+    SC_LAUNCH_CHECK("nm_header_init_kernel launch");
     if (n_rows == 0) return SC_OK;
     const int4 *c4 = (const int4 *)d_coords;
     nm_bbox_kernel<<<grid_for(n_rows, 256, 512), 256, 0, s>>>(c4, n_rows, h);
     SC_LAUNCH_CHECK("nm_bbox_kernel launch");
-    nm_insert_kernel<<<grid_for(n_rows, 256, 65536), 256, 0, s>>>(c4, n_rows, h, keys, rows, cap - 1);
+    nm_table_init_kernel<<<4096, 256, 0, s>>>(h, keys, cap, dense_cells);
+    SC_LAUNCH_CHECK("nm_table_init_kernel launch");
+    nm_insert_kernel<<<grid_for(n_rows, 256, 65536), 256, 0, s>>>(c4, n_rows, h, keys, rows, cap - 1,
+                                                                  dense_cells);
     SC_LAUNCH_CHECK("nm_insert_kernel launch");
     if (query_rows == 0) return SC_OK;
     KernelShape ks;
@@ -391,7 +432,7 @@ int sc_neighbor_map_build(const sc_conv_config *cfg, const int32_t *d_coords, in
     const int64_t blocks = (query_rows + rpb - 1) / rpb;
     if (blocks > INT32_MAX) return fail(SC_ERR_OVERFLOW, "neighbor map grid overflow");
     nm_query_kernel<<<(unsigned)blocks, 256, 0, s>>>(c4, query_rows, ks, rpb, h, keys, rows, cap - 1,
-                                                     d_map);
+                                                     dense_cells, d_map);
     SC_LAUNCH_CHECK("nm_query_kernel launch");
     return SC_OK;
 }

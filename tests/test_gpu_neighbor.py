@@ -112,6 +112,26 @@ def test_wide_coordinates(oracle, scale_axes, lo, hi):
     assert np.array_equal(gpu_map(cfg, c), exp)
 
 
+def test_sparse_bbox_uses_hash_table(oracle):
+    """A bbox with far more than 32 cells per row takes the 32-bit-key hash
+    table instead of the dense grid."""
+    rng = np.random.default_rng(8)
+    n = 20000
+    c = np.zeros((n, 4), np.int32)
+    c[:, 0] = rng.integers(0, 2, n)
+    c[:, 1:] = rng.integers(0, 1000, (n, 3))
+    c[:2000, 1:] = c[2000:4000, 1:] + rng.integers(-1, 2, (2000, 3))  # planted neighbours
+    c[:2000, 0] = c[2000:4000, 0]
+    c[-50:] = c[-100:-50]                                              # duplicates
+    c[:, 1:] = np.maximum(c[:, 1:], 0)
+    cells = float(np.prod([c[:, j].max() - c[:, j].min() + 1 for j in range(4)]))
+    assert cells > 32 * n and cells < 2.0 ** 32
+    cfg = F.SparseSubmConvConfig(1, 1)
+    exp = oracle.build_neighbor_rows(ocfg(oracle, cfg), c)
+    assert (exp >= 0).sum() > n + 1000  # centre taps + planted pairs
+    assert np.array_equal(gpu_map(cfg, c), exp)
+
+
 def test_negative_coordinate_is_rejected():
     cfg = F.SparseSubmConvConfig(1, 1)
     c = line_coords(64)
