@@ -60,11 +60,13 @@ inline uint64_t dense_cells_for(int64_t n)
     return c < (1u << 16) ? (1u << 16) : c;
 }
 
+constexpr size_t kPartialBytes = 1024 * 9 * 4;  // bbox partials (kBboxBlocks x 9 ints)
+
 inline size_t workspace_bytes_for(int64_t n)
 {
     const size_t hash_bytes = (size_t)table_capacity(n) * 12u;
     const size_t dense_bytes = (size_t)dense_cells_for(n) * 4u;
-    return kHeaderBytes + (hash_bytes > dense_bytes ? hash_bytes : dense_bytes);
+    return kHeaderBytes + kPartialBytes + (hash_bytes > dense_bytes ? hash_bytes : dense_bytes);
 }
 
 // splitmix64 finaliser (Steele, Lea & Flood, OOPSLA 2014).
@@ -148,8 +150,11 @@ __global__ void nm_table_init_kernel(const NbrHeader *h, uint64_t *words, uint64
         words[i] = kEmpty64;
 }
 
-__global__ __launch_bounds__(256) void nm_bbox_kernel(const int4 *__restrict__ coords, int64_t n,
-                                                      NbrHeader *h)
+// Per-block bbox partials (4 min, 4 max, negative flag), no atomics.
+constexpr int kBboxBlocks = 1024;
+
+__global__ __launch_bounds__(256) void nm_bbox_partial_kernel(const int4 *__restrict__ coords, int64_t n,
+                                                              int32_t *__restrict__ partials)
 {
     int mn[4] = {INT_MAX, INT_MAX, INT_MAX, INT_MAX};
     int mx[4] = {INT_MIN, INT_MIN, INT_MIN, INT_MIN};
@@ -186,12 +191,51 @@ __global__ __launch_bounds__(256) void nm_bbox_kernel(const int4 *__restrict__ c
         const int nw = blockDim.x >> 6;
         int v = s_red[0][j];
         for (int w = 1; w < nw; ++w) v = j < 4 ? min(v, s_red[w][j]) : max(v, s_red[w][j]);
+        partials[blockIdx.x * 9 + j] = v;
+    }
+}
+
+// One block: reduces the partials and writes the header (bbox + status).
+__global__ __launch_bounds__(256) void nm_bbox_final_kernel(const int32_t *__restrict__ partials,
+                                                            int nblocks, NbrHeader *h)
+{
+    int mn[4] = {INT_MAX, INT_MAX, INT_MAX, INT_MAX};
+    int mx[4] = {INT_MIN, INT_MIN, INT_MIN, INT_MIN};
+    int neg = 0;
+    for (int b = threadIdx.x; b < nblocks; b += blockDim.x) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            mn[j] = min(mn[j], partials[b * 9 + j]);
+            mx[j] = max(mx[j], partials[b * 9 + 4 + j]);
+        }
+        neg |= partials[b * 9 + 8];
+    }
+    __shared__ int s_red[4][9];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        mn[j] = wave_min_i32(mn[j]);
+        mx[j] = wave_max_i32(mx[j]);
+    }
+    neg = wave_max_i32(neg);
+    if (lane == 0) {
+        for (int j = 0; j < 4; ++j) {
+            s_red[wave][j] = mn[j];
+            s_red[wave][4 + j] = mx[j];
+        }
+        s_red[wave][8] = neg;
+    }
+    __syncthreads();
+    if (threadIdx.x < 9) {
+        const int j = threadIdx.x;
+        int v = s_red[0][j];
+        for (int w = 1; w < (int)(blockDim.x >> 6); ++w) v = j < 4 ? min(v, s_red[w][j]) : max(v, s_red[w][j]);
         if (j < 4)
-            atomicMin(&h->bmin[j], v);
+            h->bmin[j] = v;
         else if (j < 8)
-            atomicMax(&h->bmax[j - 4], v);
-        else if (v)
-            atomicOr(&h->status, kStatusNegative);
+            h->bmax[j - 4] = v;
+        else
+            h->status = v ? kStatusNegative : 0u;
     }
 }
 
@@ -269,6 +313,45 @@ __device__ inline void offset_of(const KernelShape &ks, int k, int o[3])
     o[ks.order[2]] = d[2];
 }
 
+// Dense-grid query: a row's neighbour at offset k is cell base[r] + delta[k]
+// (32-bit mixed-radix strides), valid when the neighbour lies in the bbox.
+// Entries (r, k) are walked incrementally (no division), four loads in
+// flight per lane before their stores.
+__device__ inline void query_dense(const int4 *s_coord, const int *s_off, const uint32_t *s_base,
+                                   const int *s_delta, int nrows, int K, const Plan &p,
+                                   const uint32_t *__restrict__ grid, int32_t *__restrict__ out)
+{
+    const int total = nrows * K;
+    const int step_r = (int)blockDim.x / K, step_k = (int)blockDim.x % K;
+    int r = (int)threadIdx.x / K, k = (int)threadIdx.x % K;
+    for (int e0 = threadIdx.x; e0 < total; e0 += 4 * (int)blockDim.x) {
+        int32_t v[4];
+        int idx[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int e = e0 + u * (int)blockDim.x;
+            idx[u] = e;
+            v[u] = SC_INVALID_NEIGHBOR_ROW;
+            if (e < total) {
+                const int4 c = s_coord[r];
+                const int nx = c.y + s_off[3 * k], ny = c.z + s_off[3 * k + 1], nz = c.w + s_off[3 * k + 2];
+                if (nx >= p.lo[1] && nx <= p.hi[1] && ny >= p.lo[2] && ny <= p.hi[2] && nz >= p.lo[3] &&
+                    nz <= p.hi[3])
+                    v[u] = (int32_t)grid[s_base[r] + (uint32_t)s_delta[k]];
+            }
+            r += step_r;
+            k += step_k;
+            if (k >= K) {
+                k -= K;
+                ++r;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (idx[u] < total) out[idx[u]] = v[u];
+    }
+}
+
 __global__ __launch_bounds__(256) void nm_query_kernel(const int4 *__restrict__ coords,
                                                        int64_t q_rows, KernelShape ks,
                                                        int rows_per_block,
@@ -279,18 +362,34 @@ __global__ __launch_bounds__(256) void nm_query_kernel(const int4 *__restrict__ 
                                                        int32_t *__restrict__ map)
 {
     __shared__ int4 s_coord[kMaxStagedRows];
+    __shared__ uint32_t s_base[kMaxStagedRows];
     __shared__ int s_off[kMaxStagedOffsets * 3];
+    __shared__ int s_delta[kMaxStagedOffsets];
     const int64_t row0 = (int64_t)blockIdx.x * rows_per_block;
     const int nrows = (int)min<int64_t>(rows_per_block, q_rows - row0);
-    for (int i = threadIdx.x; i < nrows; i += blockDim.x) s_coord[i] = coords[row0 + i];
-    const bool staged = ks.K <= kMaxStagedOffsets;
-    if (staged)
-        for (int k = threadIdx.x; k < ks.K; k += blockDim.x) offset_of(ks, k, &s_off[3 * k]);
-    __syncthreads();
     const Plan p = make_plan(h, dense_cells);
+    const bool staged = ks.K <= kMaxStagedOffsets;
+    for (int i = threadIdx.x; i < nrows; i += blockDim.x) {
+        const int4 c = coords[row0 + i];
+        s_coord[i] = c;
+        if (p.mode == 4) s_base[i] = (uint32_t)pack_key(p, c.x, c.y, c.z, c.w);
+    }
+    if (staged)
+        for (int k = threadIdx.x; k < ks.K; k += blockDim.x) {
+            offset_of(ks, k, &s_off[3 * k]);
+            // 32-bit cell delta of the offset (wraps; only used inside the bbox)
+            s_delta[k] = (int)((uint32_t)s_off[3 * k] * (uint32_t)(p.ext[2] * p.ext[3]) +
+                               (uint32_t)s_off[3 * k + 1] * (uint32_t)p.ext[3] + (uint32_t)s_off[3 * k + 2]);
+        }
+    __syncthreads();
+    int32_t *out = map + row0 * ks.K;
+    if (p.mode == 4 && staged) {
+        query_dense(s_coord, s_off, s_base, s_delta, nrows, ks.K, p,
+                    reinterpret_cast<const uint32_t *>(keys), out);
+        return;
+    }
     const uint32_t *grid = reinterpret_cast<const uint32_t *>(keys);
     const int total = nrows * ks.K;
-    int32_t *out = map + row0 * ks.K;
     for (int e = threadIdx.x; e < total; e += blockDim.x) {
         const int r = e / ks.K, k = e - r * ks.K;
         int o[3];
@@ -396,21 +495,29 @@ int sc_neighbor_map_build(const sc_conv_config *cfg, const int32_t *d_coords, in
     if (!mul_ok(query_rows, K, &map_elems)) return fail(SC_ERR_OVERFLOW, "neighbor map size overflow");
 
     hipStream_t s = as_stream(stream);
+    // Workspace: [header 256 B][bbox partials][table or grid].
     NbrHeader *h = (NbrHeader *)d_workspace;
+    int32_t *partials = (int32_t *)((char *)d_workspace + kHeaderBytes);
     const uint64_t cap = table_capacity(n_rows);
-    uint64_t *keys = (uint64_t *)((char *)d_workspace + kHeaderBytes);
+    uint64_t *keys = (uint64_t *)((char *)d_workspace + kHeaderBytes + kPartialBytes);
     uint32_t *rows = (uint32_t *)(keys + cap);
     // Dense grid when the bbox fits the workspace's grid budget (decided on the
     // device from the bbox; the budget never exceeds 32 cells per row).
-    uint64_t dense_cells = (workspace_bytes - kHeaderBytes) / 4u;
+    uint64_t dense_cells = (workspace_bytes - kHeaderBytes - kPartialBytes) / 4u;
     if (dense_cells > dense_cells_for(n_rows)) dense_cells = dense_cells_for(n_rows);
     dense_cells &= ~1ull;  // even: the 8-byte fill of an odd cell count stays inside
-    nm_header_init_kernel<<<1, 1, 0, s>>>(h);
-    SC_LAUNCH_CHECK("nm_header_init_kernel launch");
-    if (n_rows == 0) return SC_OK;
+    if (dense_cells > 0xffffffffull) dense_cells = 0xfffffffeull;  // 32-bit grid keys
+    if (n_rows == 0) {
+        nm_header_init_kernel<<<1, 1, 0, s>>>(h);
+        SC_LAUNCH_CHECK("nm_header_init_kernel launch");
+        return SC_OK;
+    }
     const int4 *c4 = (const int4 *)d_coords;
-    nm_bbox_kernel<<<grid_for(n_rows, 256, 512), 256, 0, s>>>(c4, n_rows, h);
-    SC_LAUNCH_CHECK("nm_bbox_kernel launch");
+    const unsigned bb = grid_for(n_rows, 256, kBboxBlocks);
+    nm_bbox_partial_kernel<<<bb, 256, 0, s>>>(c4, n_rows, partials);
+    SC_LAUNCH_CHECK("nm_bbox_partial_kernel launch");
+    nm_bbox_final_kernel<<<1, 256, 0, s>>>(partials, (int)bb, h);
+    SC_LAUNCH_CHECK("nm_bbox_final_kernel launch");
     nm_table_init_kernel<<<4096, 256, 0, s>>>(h, keys, cap, dense_cells);
     SC_LAUNCH_CHECK("nm_table_init_kernel launch");
     nm_insert_kernel<<<grid_for(n_rows, 256, 65536), 256, 0, s>>>(c4, n_rows, h, keys, rows, cap - 1,
