@@ -31,6 +31,7 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kTileRows = 256;  // query rows per workgroup (64 per wave)
 constexpr int kBN = 128;        // output channels per workgroup
@@ -64,21 +65,6 @@ struct ConvArgs {
 };
 
 // ------------------------------------------------------------ loaders
-
-template <typename TA>
-__device__ inline uint4 load_a_chunk(const TA *input, int64_t cin, int32_t nbr, int64_t col_elem)
-{
-    if (nbr < 0) return make_uint4(0, 0, 0, 0);  // absent neighbour (or out of range)
-    return *reinterpret_cast<const uint4 *>(input + (int64_t)nbr * cin + col_elem);
-}
-
-// bf16 / f32 weights: 16 bytes of w[o, k, c0 .. ].
-template <typename TW>
-__device__ inline uint4 load_w_chunk(const TW *w, int64_t row_elem, bool valid)
-{
-    if (!valid) return make_uint4(0, 0, 0, 0);
-    return *reinterpret_cast<const uint4 *>(w + row_elem);
-}
 
 // int8 -> two bf16 words.  |q| <= 128 is exact in bf16.
 __device__ inline uint32_t i8pair_to_bf16x2(uint32_t word, int shift)
@@ -259,6 +245,29 @@ __device__ inline int build_offset_list(const int32_t *map_tile, int nrows, int 
     return *s_nk;
 }
 
+
+// LDS table of the byte offsets (in the input) of the neighbour rows of the
+// tile: s_aoff[ki][r] for used offset ki and tile row r (thread r fills row r);
+// kOobOffset for an absent neighbour or a row past the end.
+__device__ inline void fill_row_offsets(const int32_t *map_tile, int nrows, int K, int64_t n_in,
+                                        uint32_t row_bytes, const int16_t *s_klist, int nk,
+                                        uint32_t (*s_aoff)[kTileRows])
+{
+    const int r = threadIdx.x;  // kThreads == kTileRows
+    const int32_t *mrow = map_tile + (int64_t)min(r, nrows - 1) * K;
+    for (int k0 = 0; k0 < nk; k0 += 8) {
+        int32_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = k0 + u < nk ? mrow[s_klist[k0 + u]] : -1;
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (k0 + u < nk)
+                s_aoff[k0 + u][r] =
+                    (r < nrows && v[u] >= 0 && v[u] < n_in) ? (uint32_t)v[u] * row_bytes : kOobOffset;
+    }
+    __syncthreads();
+}
+
 // Tile = 256 query rows x 128 output channels of one group; 4 waves, wave w
 // owns rows [64w, 64w+64) x all 128 channels (2 x 4 MFMA 32x32 blocks, 128
 // f32 accumulators per lane).  CB = bytes of a row's reduction slice per
@@ -309,22 +318,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv_mfma_kernel(ConvArgs args)
     const uint32_t row_bytes = (uint32_t)(args.cin * (int64_t)sizeof(TA));
 
     const int nk = build_offset_list(map_tile, nrows, K, n_in, s_kmask, s_klist, &s_nk);
-    // Row-offset table: thread r fills row r for every used offset.
-    {
-        const int r = tid;  // kThreads == kRows
-        const int32_t *mrow = map_tile + (int64_t)min(r, nrows - 1) * K;
-        for (int k0 = 0; k0 < nk; k0 += 8) {
-            int32_t v[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = k0 + u < nk ? mrow[s_klist[k0 + u]] : -1;
-#pragma unroll
-            for (int u = 0; u < 8; ++u)
-                if (k0 + u < nk)
-                    s_aoff[k0 + u][r] = (r < nrows && v[u] >= 0 && v[u] < n_in)
-                                            ? (uint32_t)v[u] * row_bytes : kOobOffset;
-        }
-    }
-    __syncthreads();
+    fill_row_offsets(map_tile, nrows, K, n_in, row_bytes, s_klist, nk, s_aoff);
 
     const int nkc = args.cin_g / kBK;  // chunks per offset
     const int S = nk * nkc;
@@ -517,6 +511,248 @@ __global__ __launch_bounds__(kThreads, 2) void conv_mfma_kernel(ConvArgs args)
     }
 }
 
+
+// bf16 activations: the same tile and pipeline on v_mfma_f32_16x16x32_bf16.
+// Wave w owns rows [64w, 64w+64) x 128 channels = 4 x 8 blocks of 16x16 (128
+// f32 accumulators per lane).  With 16-row MFMA blocks, the four lanes l,
+// l+16, l+32, l+48 hold one row: each A load instruction reads 16 rows x 64
+// contiguous bytes (the 32x32 layout reads 32 rows x 32 bytes).  Product
+// transposed as in the f32 kernel: lane l ends with channels 4*(l/16)+e of
+// row l%16 of each block.
+template <typename TW, typename TO, int CB>
+__global__ __launch_bounds__(kThreads, 2) void conv_mfma16_kernel(ConvArgs args)
+{
+    typedef uint16_t TA;
+    constexpr int kBK = CB / 2;                 // bf16 elements per stage
+    constexpr int KS = CB / 64;                 // 32-element MFMA k-steps per stage
+    constexpr bool kI8 = sizeof(TW) == 1;
+    constexpr int kRows = kTileRows;
+    constexpr int kStride = CB + 16;            // LDS pitch of one output channel
+    constexpr int kWBytes = kBK * (int)sizeof(TW);
+    constexpr int kWPieces = kWBytes / 16;
+    constexpr int kBPerThread = kBN * kWPieces / kThreads;
+    static_assert(kBPerThread >= 1, "weight pieces per thread");
+
+    __shared__ __attribute__((aligned(16))) unsigned char s_b[2][kBN * kStride];
+    __shared__ uint32_t s_aoff[kMaxTableK][kRows];
+    __shared__ uint32_t s_kmask[kMaxTableK / 32 + 1];
+    __shared__ int16_t s_klist[kMaxTableK];
+    __shared__ int s_nk;
+
+    const TA *input = static_cast<const TA *>(args.input);
+    const TW *weight = static_cast<const TW *>(args.weight);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, q4 = lane >> 4;
+    const int K = args.K;
+
+    const int tile = tile_for_block(blockIdx.x, gridDim.x);
+    const int64_t row0 = (int64_t)tile * kRows;
+    const int o0 = blockIdx.y * kBN;
+    const int g = blockIdx.z;
+    const int64_t in_col0 = (int64_t)g * args.cin_g;
+    const int64_t out_col0 = (int64_t)g * args.cout_g;
+    const int nrows = (int)min<int64_t>(kRows, args.n_q - row0);
+    const int32_t *map_tile = args.map + row0 * K;
+    const int64_t n_in = args.n_in;
+    const uint32_t row_bytes = (uint32_t)(args.cin * (int64_t)sizeof(TA));
+
+    const int nk = build_offset_list(map_tile, nrows, K, n_in, s_kmask, s_klist, &s_nk);
+    fill_row_offsets(map_tile, nrows, K, n_in, row_bytes, s_klist, nk, s_aoff);
+
+    const int nkc = args.cin_g / kBK;
+    const int S = nk * nkc;
+
+    f32x4 acc[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[i][j][e] = 0.f;
+
+    if (S > 0) {
+        const __amdgpu_buffer_rsrc_t a_rsrc =
+            make_rsrc(input + in_col0, (uint32_t)(n_in * row_bytes - in_col0 * (int64_t)sizeof(TA)));
+        const __amdgpu_buffer_rsrc_t w_rsrc =
+            make_rsrc(weight, (uint32_t)(args.cout * (int64_t)K * args.cin_g * (int64_t)sizeof(TW)));
+        uint32_t w_base[kBPerThread];
+#pragma unroll
+        for (int i = 0; i < kBPerThread; ++i) {
+            const int idx = tid + kThreads * i;
+            const int ch = idx / kWPieces, pc = idx % kWPieces;
+            w_base[i] = o0 + ch < args.cout_g
+                            ? (uint32_t)((out_col0 + o0 + ch) * (int64_t)K * args.cin_g * (int64_t)sizeof(TW)) + pc * 16
+                            : kOobOffset;
+        }
+        const uint32_t w_k_bytes = (uint32_t)(args.cin_g * (int64_t)sizeof(TW));
+        const int a_piece = q4 * 16;  // byte offset of this lane's 8 elements in a 64-byte k-step
+        uint4 rb[kBPerThread];
+        // Weights run one stage ahead (registers -> double-buffered LDS); the
+        // gathered rows run two stages ahead in a ring of three register sets.
+        auto load_b = [&](int t) {
+            const bool live = t < S;
+            const int tt = live ? t : 0;
+            const int ki = tt / nkc, kc = tt - ki * nkc;
+            const uint32_t wk = (uint32_t)s_klist[ki] * w_k_bytes + (uint32_t)(kc * kWBytes);
+#pragma unroll
+            for (int i = 0; i < kBPerThread; ++i) rb[i] = bload16(w_rsrc, live ? w_base[i] + wk : kOobOffset);
+        };
+        auto load_a = [&](int t, APiece<4 * KS> &f) {
+            const bool live = t < S;
+            const int tt = live ? t : 0;
+            const int ki = tt / nkc, kc = tt - ki * nkc;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t ro = live ? s_aoff[ki][wave * 64 + i * 16 + l16] : kOobOffset;
+#pragma unroll
+                for (int q = 0; q < KS; ++q)
+                    f.p[i * KS + q] = bload16(a_rsrc, ro + (uint32_t)(kc * CB + q * 64 + a_piece));
+            }
+        };
+        auto store_b = [&](int buf) {
+            unsigned char *b = s_b[buf];
+#pragma unroll
+            for (int i = 0; i < kBPerThread; ++i) {
+                const int idx = tid + kThreads * i;
+                const int ch = idx / kWPieces, pc = idx % kWPieces;
+                if constexpr (kI8) {
+                    uint4 w0, w1;
+                    widen_i8x16(rb[i], w0, w1);
+                    *reinterpret_cast<uint4 *>(b + ch * kStride + pc * 32) = w0;
+                    *reinterpret_cast<uint4 *>(b + ch * kStride + pc * 32 + 16) = w1;
+                } else {
+                    *reinterpret_cast<uint4 *>(b + ch * kStride + pc * 16) = rb[i];
+                }
+            }
+        };
+        auto compute = [&](int buf, const APiece<4 * KS> &c) {
+            const unsigned char *b = s_b[buf];
+#pragma unroll
+            for (int q = 0; q < KS; ++q)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint4 w = *reinterpret_cast<const uint4 *>(b + (j * 16 + l16) * kStride + q * 64 + a_piece);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            __builtin_bit_cast(bf16x8, w), __builtin_bit_cast(bf16x8, c.p[i * KS + q]), acc[i][j], 0, 0, 0);
+                }
+        };
+        // stage t: weights of t+1 -> registers, rows of t+2 -> set (t+2)%3,
+        // MFMAs of t, weights of t+1 -> LDS, barrier.
+        auto stage = [&](int t, const APiece<4 * KS> &cur, APiece<4 * KS> &ahead2) {
+            load_b(t + 1);
+            load_a(t + 2, ahead2);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(t & 1, cur);
+            store_b((t + 1) & 1);
+            __syncthreads();
+        };
+
+        APiece<4 * KS> x0, x1, x2;
+        load_b(0);
+        load_a(0, x0);
+        load_a(1, x1);
+        store_b(0);
+        __syncthreads();
+        const int S3 = ((S + 2) / 3) * 3;  // padded stages have zero weights
+        for (int t = 0; t < S3; t += 3) {
+            stage(t, x0, x2);
+            stage(t + 1, x1, x0);
+            stage(t + 2, x2, x1);
+        }
+    }
+
+    // ---- epilogue: lane l holds channels j*16 + 4*(l/16) + e (e = 0..3) of row
+    //      i*16 + l%16; lanes l%16 + 16m (m = 0..3) together hold a whole row.
+    TO *__restrict__ out = static_cast<TO *>(args.out);
+    const TO *__restrict__ res = static_cast<const TO *>(args.residual);
+    const bool vec_ok = args.vec_out != 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = wave * 64 + i * 16 + l16;
+        if (r >= nrows) continue;  // the 4 lanes of a row skip together
+        const int64_t rowbase = (row0 + r) * args.cout + out_col0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int o = o0 + j * 16 + 4 * q4 + e;
+                const bool ok = o < args.cout_g;
+                const float bias = (args.bias && ok) ? args.bias[out_col0 + o] : 0.f;
+                const float scale = (kI8 && args.w_scale && ok) ? args.w_scale[out_col0 + o] : 1.f;
+                acc[i][j][e] = ok ? (kI8 ? acc[i][j][e] * scale + bias : acc[i][j][e] + bias) : 0.f;
+            }
+        if (args.ln) {
+            float sum = 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) sum += acc[i][j][e];
+            sum += __shfl_xor(sum, 16, 64);
+            sum += __shfl_xor(sum, 32, 64);
+            const float inv_c = 1.0f / (float)args.cout_g;
+            const float mean = sum * inv_c;
+            float qv = 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int o = o0 + j * 16 + 4 * q4 + e;
+                    const float d = acc[i][j][e] - mean;
+                    qv += o < args.cout_g ? d * d : 0.f;
+                }
+            qv += __shfl_xor(qv, 16, 64);
+            qv += __shfl_xor(qv, 32, 64);
+            const float inv_std = 1.0f / sqrtf(qv * inv_c + args.ln_eps);
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int o = o0 + j * 16 + 4 * q4 + e;
+                    const bool ok = o < args.cout_g;
+                    float t = (acc[i][j][e] - mean) * inv_std;
+                    if (args.ln_w && ok) t *= args.ln_w[o];
+                    if (args.ln_b && ok) t += args.ln_b[o];
+                    acc[i][j][e] = t;
+                }
+        }
+        if (args.silu) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float t = acc[i][j][e];
+                    acc[i][j][e] = t / (1.0f + expf(-t));
+                }
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int oc = o0 + j * 16 + 4 * q4;
+            float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+            if (vec_ok && oc + 3 < args.cout_g) {
+                typename Out4<TO>::V *dst = reinterpret_cast<typename Out4<TO>::V *>(out + rowbase + oc);
+                if (res) {
+                    float rv[4];
+                    Out4<TO>::unpack(*reinterpret_cast<const typename Out4<TO>::V *>(res + rowbase + oc), rv);
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) v[c] += rv[c];
+                }
+                *dst = Out4<TO>::pack(v);
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    if (oc + c >= args.cout_g) continue;
+                    float t = v[c];
+                    if (res) t += load_as_f32<TO>(res, rowbase + oc + c);
+                    store_from_f32<TO>(out, rowbase + oc + c, t);
+                }
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------ scalar path
 
 template <typename TA, typename TW, typename TO>
@@ -565,10 +801,14 @@ int launch_conv(const ConvArgs &a, int groups, bool mfma, hipStream_t s)
         if (tiles > INT32_MAX || ntile > 65535 || groups > 65535)
             return fail(SC_ERR_OVERFLOW, "sparse conv grid overflow");
         dim3 grid((unsigned)tiles, (unsigned)ntile, (unsigned)groups);
-        if (wide)
-            conv_mfma_kernel<TA, TW, TO, 128><<<grid, kThreads, 0, s>>>(a);
-        else
-            conv_mfma_kernel<TA, TW, TO, 64><<<grid, kThreads, 0, s>>>(a);
+        if constexpr (sizeof(TA) == 2) {
+            conv_mfma16_kernel<TW, TO, 64><<<grid, kThreads, 0, s>>>(a);
+        } else {
+            if (wide)
+                conv_mfma_kernel<TA, TW, TO, 128><<<grid, kThreads, 0, s>>>(a);
+            else
+                conv_mfma_kernel<TA, TW, TO, 64><<<grid, kThreads, 0, s>>>(a);
+        }
         SC_LAUNCH_CHECK("conv_mfma_kernel launch");
     } else {
         conv_scalar_kernel<TA, TW, TO><<<grid_for(a.n_q * a.cout, 256, 65536), 256, 0, s>>>(a);
