@@ -2,9 +2,12 @@
 
 Workload: 256^3 grid, 1,040,679 active voxels (shell
 of a seeded union of 8 ellipsoids), C = 128, bf16 activations and weights
-with f32 accumulation.  One step = neighbour-map build for the coords +
-conv3x3x3 -> LayerNorm -> SiLU (fused into the first conv's epilogue) ->
-conv3x3x3 -> + x (fused into the second conv's epilogue).  Inputs are resident in HBM before timing.
+with f32 accumulation.  One step = neighbour-map build for the coords + conv
+plan build (row order and per-tile halo tables of the map) + conv3x3x3 ->
+LayerNorm -> SiLU (fused into the first conv's epilogue) -> conv3x3x3 -> + x
+(fused into the second conv's epilogue), both convs halo-staged.  Inputs are
+resident in HBM before timing; the weights are packed once beforehand (layer
+constants, as the reference's decoder caches its weights per layer).
 
 Prints one JSON line: value = voxels/s of the whole step; roofline = the
 dominant kernel (the MFMA conv) at its useful FLOPs 2*P*Cin*Cout per launch
@@ -34,7 +37,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cpu-sample", type=int, default=262144,
                     help="query rows of the CPU baseline sample (0 = skip)")
-    ap.add_argument("--only", choices=["map", "conv", "ln"], default=None,
+    ap.add_argument("--only", choices=["map", "plan", "conv", "ln"], default=None,
                     help="run just this part of the step --steps times (for rocprofv3) and exit")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 1 GiB device-to-device copy (the known-size kernel that "
@@ -127,24 +130,32 @@ def main():
     cfg = F.SparseSubmConvConfig(C, C)
     nbr = torch.empty((n, 27), dtype=torch.int32, device=dev)
     ws = F.NeighborMapWorkspace(dev).get(n)
+    plan_buf = torch.empty(F.conv_plan_bytes(n, 27), dtype=torch.uint8, device=dev)
     h = torch.empty((n, C), dtype=torch.bfloat16, device=dev)
     out = torch.empty((n, C), dtype=torch.bfloat16, device=dev)
+    w1_p, w2_p = F.pack_conv_weight(cfg, w1_d), F.pack_conv_weight(cfg, w2_d)
+    plan = F.ConvPlan(plan_buf, n, n, 27)
 
     def map_build():
         F.neighbor_map_build_into(cfg, coords_d, nbr, ws)
 
+    def plan_build():
+        F.conv_plan_build_into(cfg, coords_d, nbr, plan_buf)
+
     def conv1():  # conv -> LayerNorm -> SiLU, fused in the conv epilogue
         F.sparse_subm_conv_forward(cfg, x, nbr, w1_d, bias, out=h, layer_norm=True, ln_eps=1e-6,
-                                   silu=True)
+                                   silu=True, plan=plan, packed_weight=w1_p)
 
     def ln_silu():  # the unfused LayerNorm + SiLU kernel, timed for reference only
         F.layer_norm(h, eps=1e-6, silu=True, out=h)
 
     def conv2():  # conv -> + x, fused
-        F.sparse_subm_conv_forward(cfg, h, nbr, w2_d, bias, residual=x, out=out)
+        F.sparse_subm_conv_forward(cfg, h, nbr, w2_d, bias, residual=x, out=out, plan=plan,
+                                   packed_weight=w2_p)
 
     def step():
         map_build()
+        plan_build()
         conv1()
         conv2()
 
@@ -159,7 +170,8 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     if args.only:
-        part = {"map": map_build, "conv": lambda: (conv1(), conv2()), "ln": ln_silu}[args.only]
+        part = {"map": map_build, "plan": plan_build, "conv": lambda: (conv1(), conv2()),
+                "ln": ln_silu}[args.only]
         ms = events_ms(part, args.steps)
         print(f"[bench] only={args.only} {ms:.3f} ms per call", file=sys.stderr, flush=True)
         return
@@ -170,10 +182,12 @@ def main():
     ms_step = events_ms(step, args.steps)
     # Per-kernel launch durations (HIP events on the launch stream).
     ms_map = events_ms(map_build, args.steps)
+    ms_plan = events_ms(plan_build, args.steps)
     # both convs of the block are the same kernel; average one launch over the pair
     ms_conv = events_ms(lambda: (conv1(), conv2()), args.steps) / 2.0
     ms_ln = events_ms(ln_silu, args.steps)
-    print(f"[bench] step {ms_step:.3f} ms  map {ms_map:.3f}  conv {ms_conv:.3f}  ln {ms_ln:.3f}",
+    print(f"[bench] step {ms_step:.3f} ms  map {ms_map:.3f}  plan {ms_plan:.3f}  conv {ms_conv:.3f}  "
+          f"ln {ms_ln:.3f}",
           file=sys.stderr, flush=True)
 
     flops = 2.0 * P * C * C
@@ -184,7 +198,7 @@ def main():
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get("conv_mfma_kernel/config3", None)
+            traffic = json.load(f).get("conv_halo_kernel/config3", None)
 
     cpu = None
     if args.cpu_sample > 0:
@@ -204,15 +218,16 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": "config3 sparse residual block (map build + conv3x3x3 -> LN -> SiLU "
-                               "-> conv3x3x3 -> +x), 256^3 ellipsoid-union shell",
+        "config": {"workload": "config3 sparse residual block (map build + conv plan + conv3x3x3 -> LN "
+                               "-> SiLU -> conv3x3x3 -> +x), 256^3 ellipsoid-union shell",
                    "voxels": n, "channels": C, "kernel": "3x3x3", "valid_pairs": P,
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "kernel": "conv_mfma_kernel<bf16,bf16,bf16>",
+        "roofline": {"bound": "mfma", "kernel": "conv_halo_kernel<bf16,bf16>",
                      "achieved": conv_tflops, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": conv_tflops / PEAK_BF16_TFLOPS, "traffic": traffic},
         "components": {
-            "map_build_ms": ms_map, "conv_ms": ms_conv, "unfused_ln_silu_ms": ms_ln,
+            "map_build_ms": ms_map, "plan_build_ms": ms_plan, "conv_ms": ms_conv,
+            "unfused_ln_silu_ms": ms_ln,
             "map_build_gbps": map_gbps, "map_build_frac_hbm": map_gbps / PEAK_HBM_GBPS,
             "conv_useful_tflops": conv_tflops,
             "conv_issued_tflops_dense27": 2.0 * n * 27 * C * C / (ms_conv * 1e-3) / 1e12,

@@ -25,6 +25,8 @@ EXPORTED = (
     "sc_subm_conv_forward_fused",
     "sc_layer_norm", "sc_add", "sc_subdivision_workspace_size", "sc_subdivision_build",
     "sc_gather_rows", "sc_c2s_skip_add", "sc_convert",
+    "sc_conv_plan_size", "sc_conv_plan_build", "sc_subm_conv_forward_planned",
+    "sc_conv_weight_pack_size", "sc_conv_weight_pack",
 )
 
 
@@ -97,6 +99,12 @@ def load() -> ctypes.CDLL:
     L.sc_subm_conv_forward.argtypes = [cfgp, i32, P, i64, P, i64, i32, P, P, P, P, i32, P, P]
     L.sc_subm_conv_forward_fused.argtypes = [cfgp, i32, P, i64, P, i64, i32, P, P, P,
                                              ctypes.POINTER(ScConvEpilogue), i32, P, P]
+    L.sc_conv_plan_size.argtypes = [i64, i64, sizep]
+    L.sc_conv_plan_build.argtypes = [cfgp, P, i64, P, i64, P, ctypes.c_size_t, P]
+    L.sc_subm_conv_forward_planned.argtypes = [cfgp, i32, P, i64, P, i64, i32, P, P, P, P,
+                                               ctypes.POINTER(ScConvEpilogue), i32, P, P, P]
+    L.sc_conv_weight_pack_size.argtypes = [cfgp, i32, sizep]
+    L.sc_conv_weight_pack.argtypes = [cfgp, i32, P, P, P]
     L.sc_layer_norm.argtypes = [i32, P, i64, i64, P, P, ctypes.c_float, i32, i32, P, P]
     L.sc_add.argtypes = [i32, P, P, i64, P, P]
     L.sc_subdivision_workspace_size.argtypes = [i64, sizep]

@@ -25,6 +25,7 @@
 // take (channel counts that are not multiples of the 64-byte chunk, K > 32,
 // unaligned pointers, tensors of 2 GiB or more).
 #include "sc_common.hpp"
+#include "sc_plan.hpp"
 
 namespace sc {
 namespace {
@@ -38,6 +39,7 @@ constexpr int kBN = 128;        // output channels per workgroup
 constexpr int kThreads = 256;
 constexpr int kChunkBytes = 64;   // smallest per-stage reduction slice of a row (bytes)
 constexpr int kMaxTableK = 32;    // MFMA tile: kernels with at most 32 offsets
+constexpr int kSubTiles = kPlanTileRows / kTileRows;  // direct tiles per plan tile
 
 struct ConvArgs {
     const void *input;
@@ -62,6 +64,14 @@ struct ConvArgs {
     const float *ln_b;
     float ln_eps;
     int silu;
+    // Optional row order (a permutation of [0, n_q), padded with -1 to whole
+    // tiles): tile row p computes query row perm[p].
+    const int32_t *perm;
+    // Optional tile list: workgroup b takes tile tile_list[b] if b < *tile_count.
+    const int32_t *tile_list;
+    const int32_t *tile_count;
+    // Weights packed by sc_conv_weight_pack (the halo-staged kernel's layout).
+    const void *wpack;
 };
 
 // ------------------------------------------------------------ loaders
@@ -753,6 +763,792 @@ __global__ __launch_bounds__(kThreads, 2) void conv_mfma16_kernel(ConvArgs args)
     }
 }
 
+// ------------------------------------------------------ bf16 tile, v2
+//
+// Same tile as conv_mfma16_kernel (256 rows x 128 output channels, 4 waves,
+// wave w owns rows [64w, 64w+64) as 4 x 8 blocks of v_mfma_f32_16x16x32_bf16),
+// restructured around what limits the first version on gfx950:
+//  * a stage is one used offset x CB bytes of the input row (CB = 128: two
+//    MFMA k-steps, half the barriers of 64-byte stages);
+//  * bf16 weights go global -> LDS by buffer_load ... lds (no staging
+//    registers, no ds_write); int8 weights are widened through registers;
+//  * LDS weight slices are XOR-swizzled per 16-byte piece, so the MFMA
+//    operand reads (16 channels x 16 bytes per 16 lanes) hit distinct banks;
+//  * offsets are walked by scalar bit cursors over the tile's offset mask,
+//    and the gathered-row byte offsets of the next A stage are read from LDS
+//    one stage before the loads that use them;
+//  * optional row permutation (args.perm) and per-16-row-block skipping of
+//    MFMAs for offsets no row of the block uses (BSKIP): with rows grouped by
+//    neighbour mask, this removes most MFMA work on absent neighbours.
+// The stage loop keeps a static number of vector loads per stage, so the
+// explicit vmcnt waits below are exact: W(t) and A(t) have landed when
+// stage t starts.
+
+template <int N>
+__device__ inline void wait_vmcnt()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Physical 16-byte slot of logical piece p of channel c's CB-byte slice.
+template <int CB>
+__device__ inline int wslot(int c, int p)
+{
+    if constexpr (CB == 128)
+        return p ^ (c & 7);
+    else
+        return p ^ (((c >> 1) ^ (c >> 2)) & 3);
+}
+
+// Scalar cursor over (used offset, input chunk) stages.
+struct StageCursor {
+    uint32_t rem;  // offsets not yet finished (bit k = offset k); 0 = past the end
+    int k;         // current offset
+    int kc;        // current input chunk
+    __device__ inline void init(uint32_t mask)
+    {
+        rem = mask;
+        k = mask ? __builtin_ctz(mask) : 0;
+        kc = 0;
+    }
+    __device__ inline void next(int nkc)
+    {
+        if (++kc == nkc) {
+            kc = 0;
+            rem &= rem - 1u;
+            k = rem ? __builtin_ctz(rem) : 0;
+        }
+    }
+    __device__ inline bool live() const { return rem != 0u; }
+};
+
+template <typename TW, typename TO, int CB, int DIST, bool PERM, bool BSKIP>
+__global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
+{
+    typedef uint16_t TA;
+    constexpr bool kI8 = sizeof(TW) == 1;
+    constexpr bool kDMA = !kI8;              // bf16 weights: direct global -> LDS
+    constexpr int KS = CB / 64;              // 32-element MFMA k-steps per stage
+    constexpr int NP = CB / 16;              // 16-byte pieces per channel per stage
+    constexpr int NSET = DIST + 1;           // register sets of gathered rows
+    constexpr int NA = 4 * KS;               // A load instructions per stage
+    constexpr int kRows = kTileRows;
+    constexpr int kWStage = kBN * CB;        // LDS bytes of one weight stage
+    constexpr int kDmaPerWave = kWStage / 1024 / 4;  // 1 KB per DMA instruction
+    constexpr int kWBytesCh = kI8 ? CB / 2 : CB;     // weight bytes per channel per stage
+    constexpr int kRegPieces = kBN * (kWBytesCh / 16) / kThreads;  // staged 16 B loads/thread
+    constexpr int NW = kDMA ? kDmaPerWave : kRegPieces;  // weight load instructions per stage
+    static_assert(!kDMA || kDmaPerWave >= 1, "DMA pieces");
+    static_assert(DIST == 1 || DIST == 2, "prefetch distance");
+    static_assert(kDMA || kRegPieces >= 1, "staged pieces");
+
+    // Two weight buffers as separate LDS objects: the compiler then sees that
+    // the MFMA operand reads of one buffer cannot alias the DMA into the
+    // other, and does not wait for that DMA before them.
+    __shared__ __attribute__((aligned(16))) unsigned char s_b0[kWStage];
+    __shared__ __attribute__((aligned(16))) unsigned char s_b1[kWStage];
+    __shared__ uint32_t s_aoff[kMaxTableK][kRows];
+    __shared__ int32_t s_qrow[kRows];
+    __shared__ uint32_t s_tmask;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, q4 = lane >> 4;
+    const int K = args.K;
+
+    int tile;
+    if (args.tile_list) {
+        // plan tile tile_list[b / kSubTiles], part b % kSubTiles
+        const int b = (int)blockIdx.x / kSubTiles;
+        if (b >= *args.tile_count) return;
+        tile = args.tile_list[b] * kSubTiles + (int)blockIdx.x % kSubTiles;
+    } else {
+        tile = tile_for_block(blockIdx.x, gridDim.x);
+    }
+    const int64_t row0 = (int64_t)tile * kRows;
+    const int o0 = blockIdx.y * kBN;
+    const int g = blockIdx.z;
+    const int64_t in_col0 = (int64_t)g * args.cin_g;
+    const int64_t out_col0 = (int64_t)g * args.cout_g;
+    const int64_t n_in = args.n_in;
+    const uint32_t row_bytes = (uint32_t)(args.cin * (int64_t)sizeof(TA));
+
+    // ---- prologue: row ids, neighbour byte offsets, masks.
+    if (tid == 0) s_tmask = 0u;
+    uint32_t m = 0;
+    {
+        const int64_t q = row0 + tid;
+        bool rv = q < args.n_q;
+        int64_t qrow = q;
+        if constexpr (PERM) {
+            // the order is padded to whole tiles with -1
+            const int32_t pq = args.perm[q];
+            qrow = pq;
+            rv = pq >= 0 && pq < args.n_q;
+        }
+        s_qrow[tid] = rv ? (int32_t)qrow : -1;
+        const int32_t *mrow = args.map + (rv ? qrow : 0) * K;
+        int32_t v[kMaxTableK];
+#pragma unroll
+        for (int k = 0; k < kMaxTableK; ++k) v[k] = (rv && k < K) ? mrow[k] : -1;
+#pragma unroll
+        for (int k = 0; k < kMaxTableK; ++k) {
+            const bool ok = v[k] >= 0 && v[k] < n_in;
+            if (k < K) s_aoff[k][tid] = ok ? (uint32_t)v[k] * row_bytes : kOobOffset;
+            m |= (uint32_t)ok << k;
+        }
+    }
+    // Per-16-row-block masks (wave-uniform) and the tile's offset mask.
+    uint32_t bm = m;
+    bm |= __shfl_xor(bm, 1, 64);
+    bm |= __shfl_xor(bm, 2, 64);
+    bm |= __shfl_xor(bm, 4, 64);
+    bm |= __shfl_xor(bm, 8, 64);
+    const uint32_t bm0 = __builtin_amdgcn_readlane(bm, 0), bm1 = __builtin_amdgcn_readlane(bm, 16);
+    const uint32_t bm2 = __builtin_amdgcn_readlane(bm, 32), bm3 = __builtin_amdgcn_readlane(bm, 48);
+    __syncthreads();
+    if (lane == 0) atomicOr(&s_tmask, bm0 | bm1 | bm2 | bm3);
+    __syncthreads();
+    const uint32_t tmask = __builtin_amdgcn_readfirstlane(s_tmask);
+
+    f32x4 acc[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[i][j][e] = 0.f;
+
+    const int nkc = args.cin_g / (CB / 2);
+    if (tmask != 0u) {
+        const TA *input = static_cast<const TA *>(args.input);
+        const __amdgpu_buffer_rsrc_t a_rsrc =
+            make_rsrc(input + in_col0, (uint32_t)(n_in * row_bytes - in_col0 * (int64_t)sizeof(TA)));
+        const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(
+            args.weight, (uint32_t)(args.cout * (int64_t)K * args.cin_g * (int64_t)sizeof(TW)));
+        const uint32_t w_k_bytes = (uint32_t)(args.cin_g * (int64_t)sizeof(TW));
+        const uint32_t w_ch_bytes = (uint32_t)K * w_k_bytes;
+
+        // Weight piece(s) this thread moves per stage: channel, logical piece, LDS slot.
+        uint32_t w_gbase[NW];
+        uint32_t w_lds[NW];
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+            int c, p;
+            if constexpr (kDMA) {
+                // DMA instruction i of this wave fills LDS bytes [1 KB * (wave*NW + i), +1 KB):
+                // lane l writes slot l -> channel c, physical piece l % NP.
+                c = (wave * NW + i) * (1024 / CB) + lane / NP;
+                const int phys = lane % NP;
+                p = wslot<CB>(c, phys);  // logical piece stored at that slot
+                w_lds[i] = (uint32_t)((wave * NW + i) * 1024);
+            } else {
+                const int idx = tid + kThreads * i;
+                constexpr int pcs = kWBytesCh / 16;  // 16-byte global pieces per channel
+                c = idx / pcs;
+                p = idx % pcs;
+                w_lds[i] = 0;
+            }
+            w_gbase[i] = (o0 + c < args.cout_g)
+                             ? (uint32_t)((out_col0 + o0 + c) * (int64_t)w_ch_bytes) + (uint32_t)(p * 16)
+                             : kOobOffset;
+        }
+        uint4 rb[kDMA ? 1 : NW];
+        // buf is a compile-time constant wherever this is called (unrolled loops)
+        auto wbuf = [&](int buf) -> unsigned char * { return buf ? s_b1 : s_b0; };
+
+        auto load_w = [&](const StageCursor &c, int buf) {
+            const bool live = c.live();
+            const uint32_t wk = (uint32_t)c.k * w_k_bytes + (uint32_t)(c.kc * kWBytesCh);
+#pragma unroll
+            for (int i = 0; i < NW; ++i) {
+                // an out-of-range base stays out of range: w_gbase + wk < 2^32
+                const uint32_t off = live ? w_gbase[i] + wk : kOobOffset;
+                if constexpr (kDMA) {
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                        w_rsrc, (__attribute__((address_space(3))) void *)(wbuf(buf) + w_lds[i]), 16, off, 0, 0,
+                        0);
+                } else {
+                    rb[i] = bload16(w_rsrc, off);
+                }
+            }
+        };
+        auto store_w = [&](int buf) {  // staged (int8) path only
+            if constexpr (!kDMA) {
+                unsigned char *b = wbuf(buf);
+#pragma unroll
+                for (int i = 0; i < NW; ++i) {
+                    const int idx = tid + kThreads * i;
+                    constexpr int pcs = kWBytesCh / 16;
+                    const int c = idx / pcs, p = idx % pcs;
+                    uint4 w0, w1;
+                    widen_i8x16(rb[i], w0, w1);
+                    *reinterpret_cast<uint4 *>(b + c * CB + wslot<CB>(c, 2 * p) * 16) = w0;
+                    *reinterpret_cast<uint4 *>(b + c * CB + wslot<CB>(c, 2 * p + 1) * 16) = w1;
+                }
+            }
+        };
+        auto read_offsets = [&](const StageCursor &c, uint32_t (&ro)[4]) {
+            const int k = c.live() ? c.k : 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ro[i] = s_aoff[k][wave * 64 + i * 16 + l16];
+        };
+        auto load_a = [&](const StageCursor &c, const uint32_t (&ro)[4], uint4 (&f)[4][KS]) {
+            const bool live = c.live();
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t base = live ? ro[i] : kOobOffset;
+#pragma unroll
+                for (int q = 0; q < KS; ++q)
+                    f[i][q] = bload16(a_rsrc, base + (uint32_t)(c.kc * CB + q * 64 + q4 * 16));
+            }
+        };
+        auto compute = [&](const StageCursor &c, int buf, const uint4 (&f)[4][KS]) {
+            if (!c.live()) return;
+            const unsigned char *b = wbuf(buf);
+            uint32_t use = 0xFu;
+            if constexpr (BSKIP)
+                use = ((bm0 >> c.k) & 1u) | (((bm1 >> c.k) & 1u) << 1) | (((bm2 >> c.k) & 1u) << 2) |
+                      (((bm3 >> c.k) & 1u) << 3);
+#pragma unroll
+            for (int q = 0; q < KS; ++q) {
+                uint4 w[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int ch = j * 16 + l16;
+                    w[j] = *reinterpret_cast<const uint4 *>(b + ch * CB + wslot<CB>(ch, q * 4 + q4) * 16);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if (BSKIP && !((use >> i) & 1u)) continue;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            __builtin_bit_cast(bf16x8, w[j]), __builtin_bit_cast(bf16x8, f[i][q]), acc[i][j], 0,
+                            0, 0);
+                }
+            }
+        };
+        // LDS-only barrier: the waits above it are explicit (vmcnt for the
+        // DMA'd weights, lgkmcnt for ds ops).
+        auto barrier = [&]() {
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0) (vmcnt, expcnt untouched)
+            __builtin_amdgcn_s_barrier();
+        };
+
+        uint4 fa[NSET][4][KS];
+        uint32_t ro[4];
+        StageCursor cc, ca, co;  // compute (t), A loads (t + DIST), offsets (t + DIST + 1)
+        cc.init(tmask);
+        ca.init(tmask);
+        co.init(tmask);
+        // Prologue: W(0), A(0..DIST-1), offsets of stage DIST.
+        read_offsets(co, ro);
+        co.next(nkc);
+        load_w(cc, 0);
+        store_w(0);  // staged weights only (the compiler waits for rb)
+#pragma unroll
+        for (int d = 0; d < DIST; ++d) {
+            load_a(ca, ro, fa[d]);
+            ca.next(nkc);
+            read_offsets(co, ro);
+            co.next(nkc);
+        }
+
+        // Stage t (weight buffer t & 1, register set t % NSET):
+        //   wait until W(t) and A(t) have landed; barrier; issue W(t+1) into
+        //   buffer (t+1) & 1 (its last readers finished stage t-1 before the
+        //   barrier) and A(t+DIST) into set (t+DIST) % NSET; read the row
+        //   offsets of stage t+DIST+1; MFMAs of stage t.
+        // Loads are issued in the order W(t+1), A(t+DIST), so at the top of
+        // stage t+1 only A(t+DIST) (DIST >= 2) may still be in flight.
+        // The body covers lcm(2, NSET) stages so parities and sets are static.
+        constexpr int kUnroll = (NSET % 2 == 0) ? NSET : 2 * NSET;
+        constexpr int kInFlight = DIST >= 2 ? NA : 0;
+        while (cc.live()) {
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                const int buf = u & 1;
+                wait_vmcnt<kInFlight>();
+                barrier();
+                __builtin_amdgcn_sched_barrier(0);
+                StageCursor cn = cc;
+                cn.next(nkc);
+                load_w(cn, buf ^ 1);
+                load_a(ca, ro, fa[(u + DIST) % NSET]);
+                ca.next(nkc);
+                read_offsets(co, ro);
+                co.next(nkc);
+                __builtin_amdgcn_sched_barrier(0);
+                compute(cc, buf, fa[u % NSET]);
+                // staged weights: W(t+1) registers -> buffer buf ^ 1
+                store_w(buf ^ 1);
+                cc = cn;
+            }
+        }
+        wait_vmcnt<0>();
+    }
+
+    // ---- epilogue: lane l holds channels j*16 + 4*(l/16) + e (e = 0..3) of
+    //      tile row i*16 + l%16; the 4 lanes of a row skip together.
+    TO *__restrict__ out = static_cast<TO *>(args.out);
+    const TO *__restrict__ res = static_cast<const TO *>(args.residual);
+    const bool vec_ok = args.vec_out != 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int32_t qrow = s_qrow[wave * 64 + i * 16 + l16];
+        if (qrow < 0) continue;
+        const int64_t rowbase = (int64_t)qrow * args.cout + out_col0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int o = o0 + j * 16 + 4 * q4 + e;
+                const bool ok = o < args.cout_g;
+                const float bias = (args.bias && ok) ? args.bias[out_col0 + o] : 0.f;
+                const float scale = (kI8 && args.w_scale && ok) ? args.w_scale[out_col0 + o] : 1.f;
+                acc[i][j][e] = ok ? (kI8 ? acc[i][j][e] * scale + bias : acc[i][j][e] + bias) : 0.f;
+            }
+        if (args.ln) {
+            float sum = 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) sum += acc[i][j][e];
+            sum += __shfl_xor(sum, 16, 64);
+            sum += __shfl_xor(sum, 32, 64);
+            const float inv_c = 1.0f / (float)args.cout_g;
+            const float mean = sum * inv_c;
+            float qv = 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int o = o0 + j * 16 + 4 * q4 + e;
+                    const float d = acc[i][j][e] - mean;
+                    qv += o < args.cout_g ? d * d : 0.f;
+                }
+            qv += __shfl_xor(qv, 16, 64);
+            qv += __shfl_xor(qv, 32, 64);
+            const float inv_std = 1.0f / sqrtf(qv * inv_c + args.ln_eps);
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int o = o0 + j * 16 + 4 * q4 + e;
+                    const bool ok = o < args.cout_g;
+                    float t = (acc[i][j][e] - mean) * inv_std;
+                    if (args.ln_w && ok) t *= args.ln_w[o];
+                    if (args.ln_b && ok) t += args.ln_b[o];
+                    acc[i][j][e] = t;
+                }
+        }
+        if (args.silu) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float t = acc[i][j][e];
+                    acc[i][j][e] = t / (1.0f + expf(-t));
+                }
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int oc = o0 + j * 16 + 4 * q4;
+            float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+            if (vec_ok && oc + 3 < args.cout_g) {
+                typename Out4<TO>::V *dst = reinterpret_cast<typename Out4<TO>::V *>(out + rowbase + oc);
+                if (res) {
+                    float rv[4];
+                    Out4<TO>::unpack(*reinterpret_cast<const typename Out4<TO>::V *>(res + rowbase + oc), rv);
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) v[c] += rv[c];
+                }
+                *dst = Out4<TO>::pack(v);
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    if (oc + c >= args.cout_g) continue;
+                    float t = v[c];
+                    if (res) t += load_as_f32<TO>(res, rowbase + oc + c);
+                    store_from_f32<TO>(out, rowbase + oc + c, t);
+                }
+            }
+        }
+    }
+}
+
+// ------------------------------------------------- bf16 tile, halo-staged
+//
+// Reads a conv plan (sc_plan.hpp).  For 256-row tile t (rows order[t*256..]
+// in brick order), the U distinct input rows its neighbours touch (the halo,
+// U <= kPlanHaloMax, numbered in increasing row order) are staged into LDS
+// once per 32-channel chunk by buffer_load ... lds (16 rows x 64 B per
+// instruction, coalesced), and every (row, offset) operand is read from LDS
+// through the local map lmap[k][row].  Global gather traffic drops from one
+// row per valid (row, offset) pair (~21 per output row at config 3) to ~2.
+//
+// Tile = 256 rows x 128 output channels, 4 waves, two workgroups per CU;
+// wave w owns rows [64w, 64w+64) x all 128 channels as 4 x 8 blocks of
+// v_mfma_f32_16x16x32_bf16 (transposed product: lane l ends with channels
+// 4*(l/16)+e of row l%16 of each block).  Stage = (32-channel chunk c, used
+// offset k), chunk-major.  Per stage a wave reads 4 operand fragments from
+// the LDS halo (each feeds 8 MFMAs) and loads its 8 weight fragments
+// w[o, k, 32c..32c+32) from L2 straight into registers one stage ahead (the
+// 4 waves of a workgroup share them through L1), so stages need no barrier:
+// the workgroup synchronises only when the halo moves to the next chunk, and
+// the other workgroup on the CU computes meanwhile.  Absent neighbours read
+// a zero row.  Per-row accumulation order is fixed (chunk-major, offsets
+// ascending).
+//
+// LDS: halo (960 + 1) x 64 B + source offsets 960 x 4 B + lmap 27 x 256 x 2 B
+// = 77 KB.
+constexpr int kHaloK = 27;
+
+__device__ inline int hslot(int j, int p) { return p ^ (((j >> 1) ^ (j >> 2)) & 3); }
+
+__device__ inline uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    return make_uint2(v.x, v.y);
+}
+
+// 8 int8 (two words) -> 8 bf16 (exact: |q| <= 128).
+__device__ inline uint4 widen_i8x8(uint2 q)
+{
+    return make_uint4(i8pair_to_bf16x2(q.x, 0), i8pair_to_bf16x2(q.x, 16), i8pair_to_bf16x2(q.y, 0),
+                      i8pair_to_bf16x2(q.y, 16));
+}
+
+template <bool kI8>
+struct WFrag;
+template <>
+struct WFrag<false> {
+    uint4 v;
+    __device__ inline void load(__amdgpu_buffer_rsrc_t r, uint32_t off) { v = bload16(r, off); }
+    __device__ inline uint4 bf16() const { return v; }
+};
+template <>
+struct WFrag<true> {
+    uint2 v;
+    __device__ inline void load(__amdgpu_buffer_rsrc_t r, uint32_t off) { v = bload8(r, off); }
+    __device__ inline uint4 bf16() const { return widen_i8x8(v); }
+};
+
+template <typename TW, typename TO, bool kLN>
+__global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, PlanView plan)
+{
+    constexpr int CB = 64;  // bytes of an input row per chunk (32 bf16 = one MFMA k-step)
+    constexpr bool kI8 = sizeof(TW) == 1;
+    constexpr int kWChunk = kI8 ? 32 : 64;      // weight bytes per channel per chunk
+    constexpr int kWLane = kI8 ? 8 : 16;        // weight bytes per lane per fragment
+    constexpr int kZeroRow = kPlanHaloMax;
+    constexpr int kHaloPerWave = (kPlanHaloMax / 16 + 3) / 4;  // 16-row DMA instructions per wave
+    constexpr int kWS = 2;                      // weight register sets: stages t, t+1
+    static_assert(kPlanTileRows == kTileRows, "plan tile = 256 rows");
+
+    __shared__ __attribute__((aligned(16))) unsigned char s_halo[(kPlanHaloMax + 1) * CB];
+    __shared__ __attribute__((aligned(16))) uint16_t s_lmap[kHaloK][kPlanTileRows];
+    __shared__ uint32_t s_hoff[kPlanHaloMax];
+    __shared__ uint32_t s_tmask;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, q4 = lane >> 4;
+    const int K = args.K;
+
+    const int tile = tile_for_block(blockIdx.x, gridDim.x);
+    const int U = plan.tile_u[tile];
+    if (U > kPlanHaloMax) return;  // listed in plan.overflow; the direct kernel takes it
+    const int o0 = blockIdx.y * kBN;
+    const int g = blockIdx.z;
+    const int64_t in_col0 = (int64_t)g * args.cin_g;
+    const int64_t out_col0 = (int64_t)g * args.cout_g;
+    const uint32_t row_bytes = (uint32_t)(args.cin * (int64_t)sizeof(uint16_t));
+
+    // ---- prologue: local map, zero row, halo source offsets, offset mask.
+    {
+        const int4 *src = reinterpret_cast<const int4 *>(plan.lmap + (int64_t)tile * K * kPlanTileRows);
+        int4 *dst = reinterpret_cast<int4 *>(&s_lmap[0][0]);
+        const int n16 = K * kPlanTileRows * 2 / 16;
+        for (int i = tid; i < n16; i += kThreads) dst[i] = src[i];
+        if (tid < CB / 16) reinterpret_cast<uint4 *>(s_halo + kZeroRow * CB)[tid] = make_uint4(0, 0, 0, 0);
+        if (tid == 0) s_tmask = 0u;
+        const int32_t *hrows = plan.halo + (int64_t)tile * kPlanHaloMax;
+        for (int j = tid; j < U; j += kThreads) s_hoff[j] = (uint32_t)hrows[j] * row_bytes;
+    }
+    __syncthreads();
+    {
+        uint32_t m = 0;
+        for (int k = 0; k < K; ++k) m |= (uint32_t)(s_lmap[k][tid] != kPlanAbsent) << k;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) m |= __shfl_xor(m, off, 64);
+        if (lane == 0) atomicOr(&s_tmask, m);
+    }
+    __syncthreads();
+    const uint32_t tmask = __builtin_amdgcn_readfirstlane(s_tmask);
+
+    f32x4 acc[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[i][j][e] = 0.f;
+
+    const int nkc = args.cin_g / (CB / 2);
+    if (tmask != 0u && nkc > 0) {
+        const uint16_t *input = static_cast<const uint16_t *>(args.input);
+        const __amdgpu_buffer_rsrc_t a_rsrc =
+            make_rsrc(input + in_col0, (uint32_t)(args.n_in * row_bytes - in_col0 * (int64_t)sizeof(uint16_t)));
+        const int n_ot = (args.cout_g + kBN - 1) / kBN;
+        // Packed weights (sc_conv_weight_pack): per (group, 128-channel tile)
+        // a block of K x nkc x 8 fragments; fragment (k, c, jj) is 64 lanes x
+        // kWLane bytes, lane (l16, q4) holding w[tile*128 + 16 jj + l16, k,
+        // 32c + 8 q4 .. +8]: one contiguous load per fragment and wave.
+        constexpr uint32_t kFrag = 64u * kWLane;
+        const uint32_t w_tile_bytes = (uint32_t)K * (uint32_t)nkc * 8u * kFrag;
+        const __amdgpu_buffer_rsrc_t w_rsrc =
+            make_rsrc(args.wpack, (uint32_t)((int64_t)args.cin / args.cin_g * n_ot) * w_tile_bytes);
+        const uint32_t w_lane = (uint32_t)(g * n_ot + (int)blockIdx.y) * w_tile_bytes + (uint32_t)(lane * kWLane);
+        const int n_halo_instr = (U + 15) >> 4;
+
+        struct Cursor {
+            uint32_t rem;
+            int k, c;
+        };
+        auto cur_init = [&](Cursor &u) {
+            u.rem = tmask;
+            u.k = __builtin_ctz(tmask);
+            u.c = 0;
+        };
+        auto cur_next = [&](Cursor &u) {
+            u.rem &= u.rem - 1u;
+            if (u.rem == 0u) {
+                u.rem = tmask;
+                ++u.c;
+            }
+            u.k = __builtin_ctz(u.rem);
+        };
+        WFrag<kI8> wf[kWS][8];
+        auto load_w = [&](const Cursor &u, WFrag<kI8>(&f)[8]) {
+            const bool live = u.c < nkc;
+            const uint32_t wk = w_lane + (uint32_t)((u.k * nkc + u.c) * 8) * kFrag;
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) f[jj].load(w_rsrc, live ? wk + (uint32_t)jj * kFrag : kOobOffset);
+        };
+        // Halo DMA: instruction wave + 4*ii fills halo rows 16*(wave + 4*ii) + lane/4;
+        // the lane moves logical piece hslot(j, lane%4) of row j.
+        auto load_halo = [&](int c) {
+            const uint32_t cb = (uint32_t)(c * CB) + (uint32_t)(hslot(lane >> 2, lane & 3) * 16);
+#pragma unroll
+            for (int ii = 0; ii < kHaloPerWave; ++ii) {
+                const int instr = wave + 4 * ii;
+                if (instr < n_halo_instr) {
+                    const int j = 16 * instr + (lane >> 2);
+                    const uint32_t off = j < U ? s_hoff[j] + cb : kOobOffset;
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                        a_rsrc, (__attribute__((address_space(3))) void *)(s_halo + instr * 1024), 16, off, 0,
+                        0, 0);
+                }
+            }
+        };
+        auto barrier = [&]() {
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+            __builtin_amdgcn_s_barrier();
+        };
+        auto compute = [&](int k, const WFrag<kI8>(&f)[8]) {
+            uint4 x[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                int j = s_lmap[k][wave * 64 + 16 * i + l16];
+                j = j == kPlanAbsent ? kZeroRow : j;
+                x[i] = *reinterpret_cast<const uint4 *>(s_halo + j * CB + hslot(j, q4) * 16);
+            }
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+                const uint4 w = f[jj].bf16();
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        __builtin_bit_cast(bf16x8, w), __builtin_bit_cast(bf16x8, x[i]), acc[i][jj], 0, 0, 0);
+            }
+        };
+
+        Cursor cur, pre;
+        cur_init(cur);
+        cur_init(pre);
+        load_w(pre, wf[0]);
+        cur_next(pre);
+        load_halo(0);
+        wait_vmcnt<0>();
+        barrier();
+        // Stage t uses weight set t % 2 and issues the loads of stage t + 1
+        // into the other set; the body covers two stages so the sets are
+        // compile-time constants.
+        int prev_c = 0;
+        while (true) {
+            bool done = false;
+#pragma unroll
+            for (int u = 0; u < kWS; ++u) {
+                if (!done && cur.c >= nkc) done = true;
+                if (!done) {
+                    if (cur.c != prev_c) {  // next chunk: every wave is done with the halo
+                        barrier();
+                        load_halo(cur.c);
+                        wait_vmcnt<0>();
+                        barrier();
+                    }
+                    load_w(pre, wf[(u + 1) % kWS]);
+                    cur_next(pre);
+                    compute(cur.k, wf[u]);
+                    prev_c = cur.c;
+                    cur_next(cur);
+                }
+            }
+            if (done) break;
+        }
+        wait_vmcnt<0>();
+    }
+
+    // ---- epilogue: lane l holds channels o0 + 16 j + 4 q4 + e of tile row
+    //      64 wave + 16 i + l16; the 4 lanes l16 + 16 m hold the whole row.
+    TO *__restrict__ out = static_cast<TO *>(args.out);
+    const TO *__restrict__ res = static_cast<const TO *>(args.residual);
+    const bool vec_ok = args.vec_out != 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int o = o0 + j * 16 + 4 * q4 + e;
+            const bool ok = o < args.cout_g;
+            const float bias = (args.bias && ok) ? args.bias[out_col0 + o] : 0.f;
+            const float scale = (kI8 && args.w_scale && ok) ? args.w_scale[out_col0 + o] : 1.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                acc[i][j][e] = ok ? (kI8 ? acc[i][j][e] * scale + bias : acc[i][j][e] + bias) : 0.f;
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    if constexpr (kLN) {
+        // Two-pass f32 statistics over the row's Cout channels (the
+        // reference's layer_norm_row_stats, wgpu/ops.rs:162-187).
+        const float inv_c = 1.0f / (float)args.cout_g;
+        float mean[4], inv_std[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float sum = 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) sum += acc[i][j][e];
+            sum += __shfl_xor(sum, 16, 64);
+            sum += __shfl_xor(sum, 32, 64);
+            mean[i] = sum * inv_c;
+            float qv = 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int o = o0 + j * 16 + 4 * q4 + e;
+                    const float d = acc[i][j][e] - mean[i];
+                    qv += o < args.cout_g ? d * d : 0.f;
+                }
+            qv += __shfl_xor(qv, 16, 64);
+            qv += __shfl_xor(qv, 32, 64);
+            inv_std[i] = 1.0f / sqrtf(qv * inv_c + args.ln_eps);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int o = o0 + j * 16 + 4 * q4 + e;
+                const bool ok = o < args.cout_g;
+                const float lw = (args.ln_w && ok) ? args.ln_w[o] : 1.f;
+                const float lb = (args.ln_b && ok) ? args.ln_b[o] : 0.f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[i][j][e] = (acc[i][j][e] - mean[i]) * inv_std[i] * lw + lb;
+                __builtin_amdgcn_sched_barrier(0);
+            }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int32_t qrow = plan.order[(int64_t)tile * kPlanTileRows + wave * 64 + 16 * i + l16];
+        if (qrow < 0) continue;
+        const int64_t rowbase = (int64_t)qrow * args.cout + out_col0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int oc = o0 + j * 16 + 4 * q4;
+            float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+            if (args.silu) {
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc) v[cc] = v[cc] / (1.0f + expf(-v[cc]));
+            }
+            if (vec_ok && oc + 3 < args.cout_g) {
+                typename Out4<TO>::V *dst = reinterpret_cast<typename Out4<TO>::V *>(out + rowbase + oc);
+                if (res) {
+                    float rv[4];
+                    Out4<TO>::unpack(*reinterpret_cast<const typename Out4<TO>::V *>(res + rowbase + oc), rv);
+#pragma unroll
+                    for (int cc = 0; cc < 4; ++cc) v[cc] += rv[cc];
+                }
+                *dst = Out4<TO>::pack(v);
+            } else {
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc) {
+                    if (oc + cc >= args.cout_g) continue;
+                    float t = v[cc];
+                    if (res) t += load_as_f32<TO>(res, rowbase + oc + cc);
+                    store_from_f32<TO>(out, rowbase + oc + cc, t);
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// --------------------------------------------------------- weight packing
+//
+// The halo-staged kernel's weight layout: per (group g, 128-channel output
+// tile ot, offset k, 32-channel input chunk c, 16-channel block jj) one
+// fragment of 64 lanes; lane (l16, q4) holds the 8 weights
+// w[g, ot*128 + 16 jj + l16, k, 32c + 8 q4 .. +8] (bf16: 16 B, int8: 8 B),
+// zero for channels beyond Cout_g.  Same role as the reference's
+// pack_flex_weight (crates/burn_flex_gmm/src/lib.rs:377-426): a one-time
+// per-layer reorder so that the conv's weight reads are contiguous.
+template <typename TW>
+__global__ void pack_weights_kernel(const TW *__restrict__ w, TW *__restrict__ dst, int groups, int cout_g,
+                                    int cin_g, int K)
+{
+    const int nkc = cin_g / 32, n_ot = (cout_g + kBN - 1) / kBN;
+    const int64_t pieces = (int64_t)groups * n_ot * K * nkc * 8 * 64;
+    for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < pieces;
+         p += (int64_t)gridDim.x * blockDim.x) {
+        const int lane = (int)(p & 63);
+        int64_t r = p >> 6;
+        const int jj = (int)(r % 8);
+        r /= 8;
+        const int c = (int)(r % nkc);
+        r /= nkc;
+        const int k = (int)(r % K);
+        r /= K;
+        const int ot = (int)(r % n_ot);
+        const int g = (int)(r / n_ot);
+        const int o = ot * kBN + 16 * jj + (lane & 15);
+        const int i0 = 32 * c + 8 * (lane >> 4);
+        TW *d = dst + p * 8;
+        if (o < cout_g) {
+            const TW *s = w + (((int64_t)g * cout_g + o) * K + k) * cin_g + i0;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) d[e] = s[e];
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) d[e] = 0;
+        }
+    }
+}
+
 // ------------------------------------------------------------ scalar path
 
 template <typename TA, typename TW, typename TO>
@@ -791,8 +1587,19 @@ __global__ __launch_bounds__(256) void conv_scalar_kernel(ConvArgs args)
     }
 }
 
+// bf16 activations through the v2 tile: 128-byte stages when the group's
+// input channels allow it, else 64-byte stages with a deeper A prefetch.
+template <typename TW, typename TO, bool PERM>
+void launch_v2(const ConvArgs &a, dim3 grid, hipStream_t s)
+{
+    if (sizeof(TW) == 2 && a.cin_g % 64 == 0)
+        conv_v2_kernel<TW, TO, 128, 1, PERM, false><<<grid, kThreads, 0, s>>>(a);
+    else
+        conv_v2_kernel<TW, TO, 64, 2, PERM, false><<<grid, kThreads, 0, s>>>(a);
+}
+
 template <typename TA, typename TW, typename TO>
-int launch_conv(const ConvArgs &a, int groups, bool mfma, hipStream_t s)
+int launch_conv(const ConvArgs &a, int groups, bool mfma, const void *plan, hipStream_t s)
 {
     if (mfma) {
         const bool wide = a.cin_g % (128 / (int)sizeof(TA)) == 0;
@@ -802,7 +1609,27 @@ int launch_conv(const ConvArgs &a, int groups, bool mfma, hipStream_t s)
             return fail(SC_ERR_OVERFLOW, "sparse conv grid overflow");
         dim3 grid((unsigned)tiles, (unsigned)ntile, (unsigned)groups);
         if constexpr (sizeof(TA) == 2) {
-            conv_mfma16_kernel<TW, TO, 64><<<grid, kThreads, 0, s>>>(a);
+            if (plan && a.wpack) {
+                // Halo-staged tiles, then the tiles whose halo overflowed
+                // (listed by the plan) through the direct kernel in plan
+                // order, each plan tile as kPlanTileRows / kTileRows tiles.
+                const PlanLayout L = plan_layout(a.n_q, a.K);
+                const PlanView pv = plan_view(plan, L);
+                dim3 hgrid((unsigned)L.n_tiles, (unsigned)ntile, (unsigned)groups);
+                if (a.ln)
+                    conv_halo_kernel<TW, TO, true><<<hgrid, kThreads, 0, s>>>(a, pv);
+                else
+                    conv_halo_kernel<TW, TO, false><<<hgrid, kThreads, 0, s>>>(a, pv);
+                SC_LAUNCH_CHECK("conv_halo_kernel launch");
+                ConvArgs b = a;
+                b.perm = pv.order;
+                b.tile_list = pv.overflow;
+                b.tile_count = &pv.hdr->n_overflow;
+                dim3 fgrid((unsigned)(L.n_tiles * kSubTiles), (unsigned)ntile, (unsigned)groups);
+                launch_v2<TW, TO, true>(b, fgrid, s);
+            } else {
+                launch_v2<TW, TO, false>(a, grid, s);
+            }
         } else {
             if (wide)
                 conv_mfma_kernel<TA, TW, TO, 128><<<grid, kThreads, 0, s>>>(a);
@@ -823,25 +1650,25 @@ int launch_conv(const ConvArgs &a, int groups, bool mfma, hipStream_t s)
 using namespace sc;
 
 static int launch_conv_typed(const ConvArgs &a, bool act_f32, int w_dtype, int out_dtype, int groups,
-                             bool mfma, hipStream_t s)
+                             bool mfma, const void *plan, hipStream_t s)
 {
     if (act_f32) {
-        if (out_dtype == SC_DTYPE_F32) return launch_conv<float, float, float>(a, groups, mfma, s);
-        return launch_conv<float, float, uint16_t>(a, groups, mfma, s);
+        if (out_dtype == SC_DTYPE_F32) return launch_conv<float, float, float>(a, groups, mfma, nullptr, s);
+        return launch_conv<float, float, uint16_t>(a, groups, mfma, nullptr, s);
     }
     if (w_dtype == SC_DTYPE_BF16) {
-        if (out_dtype == SC_DTYPE_F32) return launch_conv<uint16_t, uint16_t, float>(a, groups, mfma, s);
-        return launch_conv<uint16_t, uint16_t, uint16_t>(a, groups, mfma, s);
+        if (out_dtype == SC_DTYPE_F32) return launch_conv<uint16_t, uint16_t, float>(a, groups, mfma, plan, s);
+        return launch_conv<uint16_t, uint16_t, uint16_t>(a, groups, mfma, plan, s);
     }
-    if (out_dtype == SC_DTYPE_F32) return launch_conv<uint16_t, int8_t, float>(a, groups, mfma, s);
-    return launch_conv<uint16_t, int8_t, uint16_t>(a, groups, mfma, s);
+    if (out_dtype == SC_DTYPE_F32) return launch_conv<uint16_t, int8_t, float>(a, groups, mfma, plan, s);
+    return launch_conv<uint16_t, int8_t, uint16_t>(a, groups, mfma, plan, s);
 }
 
 static int conv_forward_impl(const sc_conv_config *cfg, int act_dtype, const void *d_input,
                              int64_t n_in, const int32_t *d_map, int64_t n_q, int w_dtype,
                              const void *d_weight, const float *d_w_scale, const float *d_bias,
                              const sc_conv_epilogue *epi, int out_dtype, void *d_out,
-                             sc_stream stream)
+                             const void *d_plan, const void *d_wpack, sc_stream stream)
 {
     clear_error();
     const void *d_residual = epi ? epi->residual : nullptr;
@@ -893,6 +1720,10 @@ static int conv_forward_impl(const sc_conv_config *cfg, int act_dtype, const voi
     a.ln_w = a.ln_b = nullptr;
     a.ln_eps = 0.f;
     a.silu = 0;
+    a.perm = nullptr;
+    a.tile_list = nullptr;
+    a.tile_count = nullptr;
+    a.wpack = d_wpack;
 
     const size_t asz = dtype_size(act_dtype);
     const int bk = kChunkBytes / (int)asz;
@@ -921,7 +1752,14 @@ static int conv_forward_impl(const sc_conv_config *cfg, int act_dtype, const voi
             a.residual = nullptr;
         }
     }
-    int rc2 = launch_conv_typed(a, act_f32, w_dtype, out_dtype, groups, mfma, s);
+    // The halo-staged path (bf16 activations, up to 27 offsets) reads the
+    // plan; other shapes ignore it.
+    if (d_plan && (uintptr_t)d_plan % 256 != 0)
+        return fail(SC_ERR_WORKSPACE, "conv plan must be 256-byte aligned");
+    if (d_wpack && (uintptr_t)d_wpack % 16 != 0)
+        return fail(SC_ERR_SHAPE, "packed weights must be 16-byte aligned");
+    const void *plan = (d_plan && act_bf16 && mfma && K <= kHaloK) ? d_plan : nullptr;
+    int rc2 = launch_conv_typed(a, act_f32, w_dtype, out_dtype, groups, mfma, plan, s);
     if (rc2 != SC_OK || fuse || !(want_ln || want_silu)) return rc2;
     if (want_ln)
         rc2 = sc_layer_norm(out_dtype, d_out, n_q, cfg->out_channels, epi->ln_weight, epi->ln_bias,
@@ -942,7 +1780,7 @@ extern "C" int sc_subm_conv_forward(const sc_conv_config *cfg, int act_dtype, co
     sc_conv_epilogue epi{};
     epi.residual = d_residual;
     return conv_forward_impl(cfg, act_dtype, d_input, n_in, d_map, n_q, w_dtype, d_weight, d_w_scale,
-                             d_bias, &epi, out_dtype, d_out, stream);
+                             d_bias, &epi, out_dtype, d_out, nullptr, nullptr, stream);
 }
 
 extern "C" int sc_subm_conv_forward_fused(const sc_conv_config *cfg, int act_dtype,
@@ -953,5 +1791,67 @@ extern "C" int sc_subm_conv_forward_fused(const sc_conv_config *cfg, int act_dty
                                           sc_stream stream)
 {
     return conv_forward_impl(cfg, act_dtype, d_input, n_in, d_map, n_q, w_dtype, d_weight, d_w_scale,
-                             d_bias, epi, out_dtype, d_out, stream);
+                             d_bias, epi, out_dtype, d_out, nullptr, nullptr, stream);
+}
+
+extern "C" int sc_subm_conv_forward_planned(const sc_conv_config *cfg, int act_dtype,
+                                            const void *d_input, int64_t n_in, const int32_t *d_map,
+                                            int64_t n_q, int w_dtype, const void *d_weight,
+                                            const void *d_packed_weight, const float *d_w_scale,
+                                            const float *d_bias, const sc_conv_epilogue *epi,
+                                            int out_dtype, void *d_out, const void *d_plan,
+                                            sc_stream stream)
+{
+    return conv_forward_impl(cfg, act_dtype, d_input, n_in, d_map, n_q, w_dtype, d_weight, d_w_scale,
+                             d_bias, epi, out_dtype, d_out, d_plan, d_packed_weight, stream);
+}
+
+static int weight_pack_bytes(const sc_conv_config *cfg, int w_dtype, size_t *bytes)
+{
+    int rc = validate_config(cfg);
+    if (rc) return rc;
+    if (w_dtype != SC_DTYPE_BF16 && w_dtype != SC_DTYPE_I8)
+        return fail(SC_ERR_DTYPE, "weight packing takes bf16 or int8 weights");
+    if (cfg->in_channels_per_group % 32 != 0)
+        return fail(SC_ERR_UNSUPPORTED, "weight packing needs input channels per group divisible by 32");
+    const int64_t K = cfg->kernel_d * cfg->kernel_h * cfg->kernel_w;
+    const int64_t n_ot = (cfg->out_channels_per_group + kBN - 1) / kBN;
+    const long double b = (long double)cfg->groups * n_ot * kBN * K * cfg->in_channels_per_group *
+                          (long double)dtype_size(w_dtype);
+    if (b >= (long double)((int64_t)1 << 31))
+        return fail(SC_ERR_OVERFLOW, "packed weights must stay below 2 GiB");
+    *bytes = (size_t)b;
+    return SC_OK;
+}
+
+extern "C" int sc_conv_weight_pack_size(const sc_conv_config *cfg, int w_dtype, size_t *bytes)
+{
+    clear_error();
+    if (!bytes) return fail(SC_ERR_NULL, "bytes out-pointer is NULL");
+    return weight_pack_bytes(cfg, w_dtype, bytes);
+}
+
+extern "C" int sc_conv_weight_pack(const sc_conv_config *cfg, int w_dtype, const void *d_weight,
+                                   void *d_packed, sc_stream stream)
+{
+    clear_error();
+    size_t bytes = 0;
+    int rc = weight_pack_bytes(cfg, w_dtype, &bytes);
+    if (rc) return rc;
+    if (bytes == 0) return SC_OK;
+    if (!d_weight || !d_packed) return fail(SC_ERR_NULL, "weight packing: NULL pointer");
+    if ((uintptr_t)d_packed % 16 != 0) return fail(SC_ERR_SHAPE, "packed weights must be 16-byte aligned");
+    const int groups = (int)cfg->groups, cout_g = (int)cfg->out_channels_per_group,
+              cin_g = (int)cfg->in_channels_per_group;
+    const int K = (int)(cfg->kernel_d * cfg->kernel_h * cfg->kernel_w);
+    const int64_t pieces = (int64_t)(bytes / (8 * dtype_size(w_dtype)));
+    hipStream_t s = as_stream(stream);
+    if (w_dtype == SC_DTYPE_BF16)
+        pack_weights_kernel<uint16_t><<<grid_for(pieces, 256, 16384), 256, 0, s>>>(
+            static_cast<const uint16_t *>(d_weight), static_cast<uint16_t *>(d_packed), groups, cout_g, cin_g, K);
+    else
+        pack_weights_kernel<int8_t><<<grid_for(pieces, 256, 16384), 256, 0, s>>>(
+            static_cast<const int8_t *>(d_weight), static_cast<int8_t *>(d_packed), groups, cout_g, cin_g, K);
+    SC_LAUNCH_CHECK("pack_weights_kernel launch");
+    return SC_OK;
 }

@@ -1,0 +1,526 @@
+// Conv plan builder (layout in sc_plan.hpp).
+//
+// The halo-staged conv stages, per 256-row tile, every distinct input row the
+// tile's neighbours touch into LDS once, instead of gathering a row from
+// global memory for every (row, offset) pair: at config 3 each input row is
+// gathered ~21 times by the direct kernel, but a tile of spatially compact
+// rows touches only ~2 distinct input rows per output row.  The plan holds
+// what that kernel needs and is built once per neighbour map:
+//
+//   1. init    : header, brick counts := 0, padding rows of `order` := -1
+//   2. bbox    : min/max of the query coords (wave64 + one atomic per block)
+//   3. count   : brick edge 2^s (smallest s >= 3 with at most brick_cap bricks
+//                in the bbox), per-brick row counts (atomics)
+//   4. scan    : exclusive scan of the counts (per 1024-entry block, then the
+//                block totals by one block)
+//   5. scatter : order[off[brick] + rank] = row  -> rows grouped by brick,
+//                bricks in (batch, x, y, z) order (ranks from wave-aggregated
+//                atomics: one atomic per distinct brick in a wave)
+//   6. segsort : each brick's rows sorted by row index (one workgroup per
+//                brick, rank = number of smaller rows), so the order is
+//                deterministic and, for lexicographically sorted coords,
+//                lexicographic within a brick
+//   7. tiles   : one workgroup per 256-row tile: the distinct neighbour rows
+//                through an LDS hash table, then sorted, numbered in
+//                increasing row order -> halo[] and the u16 local map
+//                lmap[k][row].  Rows stay in brick order within a tile, so
+//                the neighbours of 16 consecutive tile rows at one offset are
+//                mostly consecutive halo entries (distinct LDS banks).
+#include <climits>
+
+#include "sc_common.hpp"
+#include "sc_plan.hpp"
+
+namespace sc {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kTileThreads = kPlanTileRows;  // plan_tiles_kernel: one thread per tile row
+constexpr int kHashBits = 13;
+constexpr int kHashSlots = 1 << kHashBits;  // > 27 * 256 distinct neighbours of a tile
+constexpr int kSegLds = 2048;                // brick segments sorted in LDS up to this size
+
+struct PlanArgs {
+    const int4 *coords;
+    const int32_t *map;
+    int64_t n_q;
+    int64_t n_in;
+    int K;
+    PlanHeader *hdr;
+    int32_t *order;
+    int32_t *tile_u;
+    int32_t *overflow;
+    int32_t *halo;
+    uint16_t *lmap;
+    int32_t *counts;
+    int32_t *offsets;
+    int32_t *bsum;
+    int64_t n_tiles;
+    int64_t brick_cap;
+    int64_t n_bsum;
+};
+
+__global__ void plan_init_kernel(PlanArgs a)
+{
+    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    if (tid == 0) {
+        PlanHeader *h = a.hdr;
+        h->n_q = a.n_q;
+        h->n_in = a.n_in;
+        h->n_tiles = (int32_t)a.n_tiles;
+        h->K = a.K;
+        h->brick_shift = -1;
+        h->n_overflow = 0;
+        for (int j = 0; j < 4; ++j) {
+            h->bmin[j] = INT_MAX;
+            h->bmax[j] = INT_MIN;
+        }
+        h->n_bricks = 0;
+        h->status = 0;
+    }
+    for (int64_t i = tid; i < a.brick_cap; i += stride) a.counts[i] = 0;
+    for (int64_t i = a.n_q + tid; i < a.n_tiles * kPlanTileRows; i += stride) a.order[i] = -1;
+}
+
+__global__ __launch_bounds__(kThreads) void plan_bbox_kernel(PlanArgs a)
+{
+    __shared__ int s_mn[4][4], s_mx[4][4];
+    int mn[4] = {INT_MAX, INT_MAX, INT_MAX, INT_MAX}, mx[4] = {INT_MIN, INT_MIN, INT_MIN, INT_MIN};
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n_q;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int4 c = a.coords[i];
+        const int v[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            mn[j] = min(mn[j], v[j]);
+            mx[j] = max(mx[j], v[j]);
+        }
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        mn[j] = wave_min_i32(mn[j]);
+        mx[j] = wave_max_i32(mx[j]);
+        if (lane == 0) {
+            s_mn[wave][j] = mn[j];
+            s_mx[wave][j] = mx[j];
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < 4) {
+        const int j = threadIdx.x;
+        int lo = INT_MAX, hi = INT_MIN;
+        for (int w = 0; w < (int)blockDim.x / 64; ++w) {
+            lo = min(lo, s_mn[w][j]);
+            hi = max(hi, s_mx[w][j]);
+        }
+        atomicMin(&a.hdr->bmin[j], lo);
+        atomicMax(&a.hdr->bmax[j], hi);
+    }
+}
+
+// Groups the active lanes of a wave by key: for each distinct key the lowest
+// lane calls fn(key, count, lane) once; every lane of the group receives the
+// leader's return value plus its rank among the group's lanes (lane order).
+template <typename F>
+__device__ inline int wave_runs(bool active, uint32_t key, F fn)
+{
+    const int lane = threadIdx.x & 63;
+    uint64_t pending = __ballot(active);
+    int mine = 0;
+    while (pending) {
+        const int leader = __builtin_ctzll(pending);
+        const uint32_t k = __builtin_amdgcn_readlane(key, leader);
+        const uint64_t same = __ballot(active && key == k) & pending;
+        int r = 0;
+        if (lane == leader) r = fn(k, __builtin_popcountll(same), lane);
+        r = __builtin_amdgcn_readlane(r, leader);
+        if ((same >> lane) & 1ull) mine = r + __builtin_popcountll(same & ((1ull << lane) - 1ull));
+        pending &= ~same;
+    }
+    return mine;
+}
+
+struct BrickGrid {
+    int shift;  // -1: no brick order fits the budget
+    int64_t lo[4];
+    int64_t nb[4];  // bricks per dimension (batch: one per batch index)
+    uint64_t total;
+};
+
+__device__ inline BrickGrid brick_grid(const PlanHeader *h, int64_t cap)
+{
+    BrickGrid g;
+    g.shift = -1;
+    g.total = 0;
+    int64_t ext[4];
+    for (int j = 0; j < 4; ++j) {
+        g.lo[j] = h->bmin[j];
+        ext[j] = (int64_t)h->bmax[j] - (int64_t)h->bmin[j] + 1;
+        g.nb[j] = 1;
+    }
+    if (ext[0] <= 0) return g;  // no rows
+    for (int s = 3; s < 32; ++s) {
+        double tot = (double)ext[0];
+        int64_t nb[4] = {ext[0], 0, 0, 0};
+        for (int j = 1; j < 4; ++j) {
+            nb[j] = ((ext[j] - 1) >> s) + 1;
+            tot *= (double)nb[j];
+        }
+        if (tot <= (double)cap) {
+            g.shift = s;
+            g.total = (uint64_t)nb[0] * (uint64_t)nb[1] * (uint64_t)nb[2] * (uint64_t)nb[3];
+            for (int j = 0; j < 4; ++j) g.nb[j] = nb[j];
+            return g;
+        }
+    }
+    return g;
+}
+
+__device__ inline int64_t brick_of(const BrickGrid &g, int4 c)
+{
+    const int64_t b = (int64_t)c.x - g.lo[0];
+    const int64_t x = ((int64_t)c.y - g.lo[1]) >> g.shift;
+    const int64_t y = ((int64_t)c.z - g.lo[2]) >> g.shift;
+    const int64_t z = ((int64_t)c.w - g.lo[3]) >> g.shift;
+    return ((b * g.nb[1] + x) * g.nb[2] + y) * g.nb[3] + z;
+}
+
+__global__ __launch_bounds__(kThreads) void plan_count_kernel(PlanArgs a)
+{
+    const BrickGrid g = brick_grid(a.hdr, a.brick_cap);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        a.hdr->brick_shift = g.shift;
+        a.hdr->n_bricks = g.total;
+    }
+    if (g.shift < 0) return;
+    for (int64_t base = (int64_t)blockIdx.x * blockDim.x; base < a.n_q; base += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t i = base + threadIdx.x;
+        const bool act = i < a.n_q;
+        const uint32_t br = act ? (uint32_t)brick_of(g, a.coords[i]) : 0u;
+        wave_runs(act, br, [&](uint32_t key, int n, int) {
+            atomicAdd(&a.counts[key], n);
+            return 0;
+        });
+    }
+}
+
+// Block-wide exclusive scan of one int per thread (256 threads).
+__device__ inline int block_scan_excl(int x, int *s_wave, int &total)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int inc = x;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(inc, off, 64);
+        if (lane >= off) inc += y;
+    }
+    __syncthreads();
+    if (lane == 63) s_wave[wave] = inc;
+    __syncthreads();
+    int before = 0;
+    total = 0;
+    for (int w = 0; w < kThreads / 64; ++w) {
+        if (w < wave) before += s_wave[w];
+        total += s_wave[w];
+    }
+    return before + inc - x;
+}
+
+// Exclusive scan of counts within blocks of 1024 entries; block totals -> bsum.
+__global__ __launch_bounds__(kThreads) void plan_scan_blocks_kernel(PlanArgs a)
+{
+    __shared__ int s_wave[kThreads / 64];
+    const int64_t base = (int64_t)blockIdx.x * kPlanScanBlock + threadIdx.x * 4;
+    const int4 c = *reinterpret_cast<const int4 *>(a.counts + base);
+    int total;
+    const int ex = block_scan_excl(c.x + c.y + c.z + c.w, s_wave, total);
+    int4 o;
+    o.x = ex;
+    o.y = ex + c.x;
+    o.z = o.y + c.y;
+    o.w = o.z + c.z;
+    *reinterpret_cast<int4 *>(a.offsets + base) = o;
+    if (threadIdx.x == 0) a.bsum[blockIdx.x] = total;
+}
+
+// Exclusive scan of the block totals (one block, carried over 1024-entry chunks).
+__global__ __launch_bounds__(kThreads) void plan_scan_top_kernel(PlanArgs a)
+{
+    __shared__ int s_wave[kThreads / 64];
+    int carry = 0;
+    for (int64_t base = 0; base < a.n_bsum; base += kThreads * 4) {
+        int v[4];
+        int sum = 0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t i = base + threadIdx.x * 4 + u;
+            v[u] = i < a.n_bsum ? a.bsum[i] : 0;
+            sum += v[u];
+        }
+        int total;
+        int ex = block_scan_excl(sum, s_wave, total);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t i = base + threadIdx.x * 4 + u;
+            if (i < a.n_bsum) a.bsum[i] = carry + ex;
+            ex += v[u];
+        }
+        carry += total;
+    }
+}
+
+__device__ inline int64_t brick_start(const PlanArgs &a, uint32_t br)
+{
+    return (int64_t)a.offsets[br] + a.bsum[br / kPlanScanBlock];
+}
+
+__global__ __launch_bounds__(kThreads) void plan_scatter_kernel(PlanArgs a)
+{
+    const int shift = a.hdr->brick_shift;
+    BrickGrid g;
+    if (shift >= 0) g = brick_grid(a.hdr, a.brick_cap);
+    for (int64_t base = (int64_t)blockIdx.x * blockDim.x; base < a.n_q; base += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t i = base + threadIdx.x;
+        const bool act = i < a.n_q;
+        if (shift < 0) {  // no brick order: rows stay in their own order
+            if (act) a.order[i] = (int32_t)i;
+            continue;
+        }
+        const uint32_t br = act ? (uint32_t)brick_of(g, a.coords[i]) : 0u;
+        // counts[br] counts down: the group takes ranks [old - n, old)
+        const int rank = wave_runs(act, br, [&](uint32_t key, int n, int) { return atomicSub(&a.counts[key], n) - n; });
+        if (act) a.order[brick_start(a, br) + rank] = (int32_t)i;
+    }
+}
+
+// Sorts each brick's segment of `order` by row index: one workgroup per
+// brick (grid-stride), rank of a row = number of smaller rows in the segment.
+__global__ __launch_bounds__(kThreads) void plan_segsort_kernel(PlanArgs a)
+{
+    __shared__ int32_t s_seg[kSegLds];
+    if (a.hdr->brick_shift < 0) return;
+    const uint64_t nb = a.hdr->n_bricks;
+    for (uint64_t br = blockIdx.x; br < nb; br += gridDim.x) {
+        const int64_t start = brick_start(a, (uint32_t)br);
+        const int64_t end = br + 1 < nb ? brick_start(a, (uint32_t)(br + 1)) : a.n_q;
+        const int n = (int)(end - start);
+        if (n <= 1) continue;
+        int32_t *seg = a.order + start;
+        if (n <= kSegLds) {
+            for (int e = threadIdx.x; e < n; e += kThreads) s_seg[e] = seg[e];
+            __syncthreads();
+            int32_t mine[kSegLds / kThreads];
+            int rank[kSegLds / kThreads];
+#pragma unroll
+            for (int u = 0; u < kSegLds / kThreads; ++u) {
+                const int e = threadIdx.x + u * kThreads;
+                mine[u] = e < n ? s_seg[e] : INT_MAX;
+                rank[u] = 0;
+            }
+            for (int f = 0; f < n; ++f) {
+                const int32_t v = s_seg[f];
+#pragma unroll
+                for (int u = 0; u < kSegLds / kThreads; ++u) rank[u] += v < mine[u];
+            }
+#pragma unroll
+            for (int u = 0; u < kSegLds / kThreads; ++u)
+                if (threadIdx.x + u * kThreads < n) seg[rank[u]] = mine[u];
+            __syncthreads();
+        }
+        // Larger segments (only with heavily duplicated coords) keep the
+        // scatter's order.
+    }
+}
+
+__device__ inline uint32_t slot_hash(int32_t v)
+{
+    return ((uint32_t)v * 0x9E3779B1u) >> (32 - kHashBits);
+}
+
+__global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
+{
+    __shared__ int32_t s_key[kHashSlots];
+    __shared__ uint64_t s_list[kPlanHaloMax];
+    __shared__ int s_wave[kTileThreads / 64];
+    const int64_t t = blockIdx.x;
+    const int p = threadIdx.x;
+    const int K = a.K;
+    const int64_t n_in = a.n_in;
+
+    for (int i = p; i < kHashSlots; i += kTileThreads) s_key[i] = -1;
+    const int32_t q = a.order[t * kPlanTileRows + p];
+    __syncthreads();
+
+    // Distinct neighbour rows through the LDS hash table (linear probing; at
+    // most 27 * 256 keys in 8192 slots, so every probe ends).  A slot is read
+    // before it is claimed: most neighbours are shared by several rows of the
+    // tile and are found without an atomic.  Each neighbour's slot is kept.
+    int32_t v[32];
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+        int32_t x = -1;
+        if (k < K && q >= 0) x = a.map[(int64_t)q * K + k];
+        v[k] = (x >= 0 && x < n_in) ? x : -1;
+    }
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+        if (v[k] < 0) continue;
+        uint32_t h = slot_hash(v[k]);
+        for (int probe = 0; probe < kHashSlots; ++probe) {
+            int32_t cur = s_key[h];
+            if (cur == -1) cur = atomicCAS(&s_key[h], -1, v[k]);
+            if (cur == -1 || cur == v[k]) break;
+            h = (h + 1) & (kHashSlots - 1);
+        }
+        v[k] = (int32_t)h;  // present neighbour: its slot (absent stays -1)
+    }
+    __syncthreads();
+
+    // Compact the occupied slots (slot order) into s_list as (row << 32 | slot).
+    constexpr int kPer = kHashSlots / kTileThreads;
+    int cnt = 0;
+    for (int i = 0; i < kPer; ++i) cnt += s_key[p * kPer + i] >= 0;
+    int U, id;
+    {
+        const int lane = p & 63, wave = p >> 6;
+        int inc = cnt;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int y = __shfl_up(inc, off, 64);
+            if (lane >= off) inc += y;
+        }
+        if (lane == 63) s_wave[wave] = inc;
+        __syncthreads();
+        int before = 0;
+        U = 0;
+        for (int w = 0; w < kTileThreads / 64; ++w) {
+            if (w < wave) before += s_wave[w];
+            U += s_wave[w];
+        }
+        id = before + inc - cnt;
+    }
+    if (p == 0) {
+        a.tile_u[t] = U;
+        if (U > kPlanHaloMax) a.overflow[atomicAdd(&a.hdr->n_overflow, 1)] = (int32_t)t;
+    }
+    if (U > kPlanHaloMax) return;  // handled by the direct-gather kernel
+    for (int i = 0; i < kPer; ++i) {
+        const int slot = p * kPer + i;
+        const int32_t key = s_key[slot];
+        if (key >= 0) s_list[id++] = ((uint64_t)(uint32_t)key << 32) | (uint32_t)slot;
+    }
+    // Pad to a power of two and sort by row (bitonic); the rank is the halo index.
+    int n2 = 1;
+    while (n2 < U) n2 <<= 1;
+    for (int i = U + p; i < n2; i += kTileThreads) s_list[i] = ~0ull;
+    __syncthreads();
+    for (int size = 2; size <= n2; size <<= 1)
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int e = p; e < n2; e += kTileThreads) {
+                const int partner = e ^ stride;
+                if (partner > e) {
+                    const bool up = (e & size) == 0;
+                    const uint64_t x = s_list[e], y = s_list[partner];
+                    if ((x > y) == up) {
+                        s_list[e] = y;
+                        s_list[partner] = x;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    int32_t *halo = a.halo + t * kPlanHaloMax;
+    for (int e = p; e < U; e += kTileThreads) {
+        const uint64_t kv = s_list[e];
+        halo[e] = (int32_t)(kv >> 32);
+        s_key[(uint32_t)kv & (kHashSlots - 1)] = e;
+    }
+    __syncthreads();
+
+    uint16_t *lm = a.lmap + t * K * kPlanTileRows + p;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+        if (k >= K) break;
+        lm[k * kPlanTileRows] = v[k] >= 0 ? (uint16_t)s_key[v[k] & (kHashSlots - 1)] : kPlanAbsent;
+    }
+}
+
+}  // namespace
+}  // namespace sc
+
+using namespace sc;
+
+extern "C" int sc_conv_plan_size(int64_t n_q, int64_t kernel_rows, size_t *bytes)
+{
+    clear_error();
+    if (!bytes) return fail(SC_ERR_NULL, "bytes out-pointer is NULL");
+    if (n_q < 0 || n_q > INT32_MAX) return fail(SC_ERR_SHAPE, "conv plan row count must be in [0, i32::MAX]");
+    if (kernel_rows < 1 || kernel_rows > 32)
+        return fail(SC_ERR_UNSUPPORTED, "conv plan supports kernels of 1..32 offsets");
+    *bytes = plan_layout(n_q, kernel_rows).total;
+    return SC_OK;
+}
+
+extern "C" int sc_conv_plan_build(const sc_conv_config *cfg, const int32_t *d_coords, int64_t n_in,
+                                  const int32_t *d_map, int64_t n_q, void *d_plan, size_t plan_bytes,
+                                  sc_stream stream)
+{
+    clear_error();
+    int rc = validate_config(cfg);
+    if (rc) return rc;
+    const int64_t K = cfg->kernel_d * cfg->kernel_h * cfg->kernel_w;
+    if (K > 32) return fail(SC_ERR_UNSUPPORTED, "conv plan supports kernels of 1..32 offsets");
+    if (n_in < 0 || n_in > INT32_MAX || n_q < 0 || n_q > n_in)
+        return fail(SC_ERR_SHAPE, "conv plan needs 0 <= n_q <= n_in <= i32::MAX");
+    if (!d_plan) return fail(SC_ERR_NULL, "conv plan buffer is NULL");
+    if ((uintptr_t)d_plan % 256 != 0) return fail(SC_ERR_WORKSPACE, "conv plan buffer must be 256-byte aligned");
+    const PlanLayout L = plan_layout(n_q, K);
+    if (plan_bytes < L.total)
+        return fail(SC_ERR_WORKSPACE, "conv plan buffer too small: got " + std::to_string(plan_bytes) + " need " +
+                                          std::to_string(L.total));
+    if (n_q > 0 && (!d_coords || !d_map)) return fail(SC_ERR_NULL, "conv plan: coords or map is NULL");
+    if ((uintptr_t)d_coords % 16 != 0) return fail(SC_ERR_SHAPE, "coords must be 16-byte aligned");
+
+    char *b = static_cast<char *>(d_plan);
+    PlanArgs a;
+    a.coords = reinterpret_cast<const int4 *>(d_coords);
+    a.map = d_map;
+    a.n_q = n_q;
+    a.n_in = n_in;
+    a.K = (int)K;
+    a.hdr = reinterpret_cast<PlanHeader *>(b);
+    a.order = reinterpret_cast<int32_t *>(b + L.order);
+    a.tile_u = reinterpret_cast<int32_t *>(b + L.tile_u);
+    a.overflow = reinterpret_cast<int32_t *>(b + L.overflow);
+    a.halo = reinterpret_cast<int32_t *>(b + L.halo);
+    a.lmap = reinterpret_cast<uint16_t *>(b + L.lmap);
+    a.counts = reinterpret_cast<int32_t *>(b + L.counts);
+    a.offsets = reinterpret_cast<int32_t *>(b + L.offsets);
+    a.bsum = reinterpret_cast<int32_t *>(b + L.bsum);
+    a.n_tiles = L.n_tiles;
+    a.brick_cap = L.brick_cap;
+    a.n_bsum = L.n_bsum;
+
+    hipStream_t s = as_stream(stream);
+    plan_init_kernel<<<grid_for(L.brick_cap, kThreads, 4096), kThreads, 0, s>>>(a);
+    SC_LAUNCH_CHECK("plan_init_kernel launch");
+    if (n_q == 0) return SC_OK;
+    plan_bbox_kernel<<<grid_for(n_q, kThreads, 1024), kThreads, 0, s>>>(a);
+    SC_LAUNCH_CHECK("plan_bbox_kernel launch");
+    plan_count_kernel<<<grid_for(n_q, kThreads, 8192), kThreads, 0, s>>>(a);
+    SC_LAUNCH_CHECK("plan_count_kernel launch");
+    plan_scan_blocks_kernel<<<(unsigned)L.n_bsum, kThreads, 0, s>>>(a);
+    SC_LAUNCH_CHECK("plan_scan_blocks_kernel launch");
+    plan_scan_top_kernel<<<1, kThreads, 0, s>>>(a);
+    SC_LAUNCH_CHECK("plan_scan_top_kernel launch");
+    plan_scatter_kernel<<<grid_for(n_q, kThreads, 8192), kThreads, 0, s>>>(a);
+    SC_LAUNCH_CHECK("plan_scatter_kernel launch");
+    plan_segsort_kernel<<<grid_for(L.brick_cap, 1, 4096), kThreads, 0, s>>>(a);
+    SC_LAUNCH_CHECK("plan_segsort_kernel launch");
+    if (L.n_tiles > INT32_MAX) return fail(SC_ERR_OVERFLOW, "conv plan tile count overflow");
+    plan_tiles_kernel<<<(unsigned)L.n_tiles, kTileThreads, 0, s>>>(a);
+    SC_LAUNCH_CHECK("plan_tiles_kernel launch");
+    return SC_OK;
+}

@@ -1,0 +1,107 @@
+// Conv plan: the row order and per-tile halo tables that the halo-staged
+// submanifold conv (conv_halo_kernel) reads.  Built on the device from the
+// coords and the neighbour map by sc_conv_plan_build (sc_plan.hip); shared by
+// every conv that uses the same map.
+//
+//   order   [n_tiles * 256] i32   tile row p of tile t computes query row
+//                                 order[t*256 + p] (-1 = padding)
+//   tile_u  [n_tiles]       i32   number of distinct input rows (the halo)
+//                                 the tile's neighbours touch
+//   overflow[n_tiles]       i32   tiles whose halo exceeds kPlanHaloMax
+//                                 (first header.n_overflow entries)
+//   halo    [n_tiles][kPlanHaloMax] i32  input row of local index u, increasing
+//   lmap    [n_tiles][K][256] u16  local index of neighbour (p, k), or
+//                                 kPlanAbsent
+//   brick counts / offsets / block sums: scratch of the build's counting sort
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+
+namespace sc {
+
+constexpr int kPlanTileRows = 256;
+// Halo rows of one tile held in LDS at 64 bytes each (one 32-channel bf16
+// slice) plus a 4-byte source offset: 960 x 68 B = 64 KB, so that two
+// workgroups fit a CU's 160 KB.
+constexpr int kPlanHaloMax = 960;
+constexpr uint16_t kPlanAbsent = 0xFFFFu;
+constexpr int kPlanScanBlock = 1024;  // entries per block of the brick-count scan
+
+struct alignas(16) PlanHeader {
+    int64_t n_q;
+    int64_t n_in;
+    int32_t n_tiles;
+    int32_t K;
+    int32_t brick_shift;  // log2 of the brick edge used for the row order
+    int32_t n_overflow;   // tiles listed in `overflow`
+    int32_t bmin[4];
+    int32_t bmax[4];
+    uint64_t n_bricks;
+    uint32_t status;
+    uint32_t pad[45];
+};
+static_assert(sizeof(PlanHeader) == 256, "plan header size");
+
+struct PlanLayout {
+    int64_t n_tiles;
+    int64_t brick_cap;  // brick-count entries (multiple of kPlanScanBlock)
+    int64_t n_bsum;     // scan block sums
+    size_t order, tile_u, overflow, halo, lmap, counts, offsets, bsum, total;
+};
+
+inline size_t plan_align(size_t x) { return (x + 255) & ~(size_t)255; }
+
+inline PlanLayout plan_layout(int64_t n_q, int64_t K)
+{
+    PlanLayout L;
+    L.n_tiles = (n_q + kPlanTileRows - 1) / kPlanTileRows;
+    int64_t cap = 2 * n_q;
+    if (cap < 4096) cap = 4096;
+    L.brick_cap = (cap + kPlanScanBlock - 1) / kPlanScanBlock * kPlanScanBlock;
+    L.n_bsum = L.brick_cap / kPlanScanBlock;
+    size_t o = plan_align(sizeof(PlanHeader));
+    L.order = o;
+    o = plan_align(o + (size_t)L.n_tiles * kPlanTileRows * 4);
+    L.tile_u = o;
+    o = plan_align(o + (size_t)L.n_tiles * 4);
+    L.overflow = o;
+    o = plan_align(o + (size_t)L.n_tiles * 4);
+    L.halo = o;
+    o = plan_align(o + (size_t)L.n_tiles * kPlanHaloMax * 4);
+    L.lmap = o;
+    o = plan_align(o + (size_t)L.n_tiles * (size_t)K * kPlanTileRows * 2);
+    L.counts = o;
+    o = plan_align(o + (size_t)L.brick_cap * 4);
+    L.offsets = o;
+    o = plan_align(o + (size_t)L.brick_cap * 4);
+    L.bsum = o;
+    o = plan_align(o + (size_t)L.n_bsum * 4);
+    L.total = o;
+    return L;
+}
+
+// Device view of a built plan.
+struct PlanView {
+    const PlanHeader *hdr;
+    const int32_t *order;
+    const int32_t *tile_u;
+    const int32_t *overflow;
+    const int32_t *halo;
+    const uint16_t *lmap;
+};
+
+inline PlanView plan_view(const void *plan, const PlanLayout &L)
+{
+    const char *b = static_cast<const char *>(plan);
+    PlanView v;
+    v.hdr = reinterpret_cast<const PlanHeader *>(b);
+    v.order = reinterpret_cast<const int32_t *>(b + L.order);
+    v.tile_u = reinterpret_cast<const int32_t *>(b + L.tile_u);
+    v.overflow = reinterpret_cast<const int32_t *>(b + L.overflow);
+    v.halo = reinterpret_cast<const int32_t *>(b + L.halo);
+    v.lmap = reinterpret_cast<const uint16_t *>(b + L.lmap);
+    return v;
+}
+
+}  // namespace sc

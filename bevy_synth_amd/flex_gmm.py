@@ -177,6 +177,112 @@ def neighbor_rows_tensor_from_coords_tensor(
     return out
 
 
+def conv_plan_bytes(n_q: int, kernel_rows_: int) -> int:
+    out = ctypes.c_size_t()
+    check(_capi.load().sc_conv_plan_size(int(n_q), int(kernel_rows_), ctypes.byref(out)))
+    return out.value
+
+
+# Plan layout constants of bevy_synth_amd/csrc/sc_plan.hpp.
+PLAN_TILE_ROWS = 256
+PLAN_HALO_MAX = 960
+PLAN_ABSENT = 0xFFFF
+
+
+def conv_plan_layout(n_q: int, K: int) -> dict:
+    """Byte offsets of the plan sections (mirror of plan_layout in sc_plan.hpp;
+    tests check the total against sc_conv_plan_size)."""
+    def al(x):
+        return (x + 255) & ~255
+    nt = (n_q + PLAN_TILE_ROWS - 1) // PLAN_TILE_ROWS
+    cap = max(2 * n_q, 4096)
+    cap = (cap + 1023) // 1024 * 1024
+    L = {"n_tiles": nt}
+    o = al(256)
+    for name, size in (("order", nt * PLAN_TILE_ROWS * 4), ("tile_u", nt * 4), ("overflow", nt * 4),
+                       ("halo", nt * PLAN_HALO_MAX * 4), ("lmap", nt * K * PLAN_TILE_ROWS * 2),
+                       ("counts", cap * 4), ("offsets", cap * 4), ("bsum", cap // 1024 * 4)):
+        L[name] = o
+        o = al(o + size)
+    L["total"] = o
+    return L
+
+
+class ConvPlan:
+    """Row order + per-tile halo tables of one neighbour map (sc_conv_plan_build).
+
+    Built once per map and passed to every conv on that map, the role the
+    reference's neighbour cache plays for its decoder
+    (crates/burn_flex_gmm/src/wgpu.rs:349-382).  ``buf`` is the device buffer;
+    n_in / n_q / K record the map it was built from."""
+
+    def __init__(self, buf: torch.Tensor, n_in: int, n_q: int, K: int):
+        self.buf, self.n_in, self.n_q, self.K = buf, n_in, n_q, K
+
+    def to_host(self) -> dict:
+        """Reads the plan back (syncs): header fields and the per-tile tables
+        as numpy arrays, for inspection and tests."""
+        L = conv_plan_layout(self.n_q, self.K)
+        nt = L["n_tiles"]
+        b = self.buf.cpu().numpy()
+
+        def sec(name, count, dt):
+            return b[L[name]:L[name] + count * np.dtype(dt).itemsize].view(dt)
+        hdr = b[:256].view(np.int32)
+        n_over = int(hdr[7])
+        return {
+            "n_tiles": int(hdr[4]), "K": int(hdr[5]), "brick_shift": int(hdr[6]), "n_overflow": n_over,
+            "order": sec("order", nt * PLAN_TILE_ROWS, np.int32).reshape(nt, PLAN_TILE_ROWS),
+            "tile_u": sec("tile_u", nt, np.int32),
+            "overflow": np.sort(sec("overflow", nt, np.int32)[:n_over]),
+            "halo": sec("halo", nt * PLAN_HALO_MAX, np.int32).reshape(nt, PLAN_HALO_MAX),
+            "lmap": sec("lmap", nt * self.K * PLAN_TILE_ROWS, np.uint16).reshape(nt, self.K, PLAN_TILE_ROWS),
+        }
+
+
+def conv_plan_build_into(cfg: SparseSubmConvConfig, coords: torch.Tensor, neighbor_rows: torch.Tensor,
+                         buf: torch.Tensor) -> ConvPlan:
+    """Stream-ordered plan build into a preallocated 256-byte aligned uint8 buffer."""
+    n_in, n_q, K = coords.shape[0], neighbor_rows.shape[0], kernel_rows(cfg)
+    check(_capi.load().sc_conv_plan_build(
+        ctypes.byref(cfg.to_c()), _ptr(coords), n_in, _ptr(neighbor_rows), n_q, _ptr(buf),
+        buf.numel(), _stream()))
+    return ConvPlan(buf, n_in, n_q, K)
+
+
+def build_conv_plan(cfg: SparseSubmConvConfig, coords: torch.Tensor,
+                    neighbor_rows: torch.Tensor) -> ConvPlan:
+    """Allocates and builds the conv plan of ``neighbor_rows`` (built from ``coords``)."""
+    _require_cuda("coords", coords)
+    _require_cuda("neighbor_rows", neighbor_rows)
+    K = kernel_rows(cfg)
+    if neighbor_rows.dtype != torch.int32 or neighbor_rows.dim() != 2 or neighbor_rows.shape[1] != K:
+        raise SparseConvError(2, f"conv plan: neighbor rows must be int32 [N_q, {K}]")
+    buf = torch.empty(conv_plan_bytes(neighbor_rows.shape[0], K), dtype=torch.uint8,
+                      device=coords.device)
+    return conv_plan_build_into(cfg, coords, neighbor_rows, buf)
+
+
+def conv_weight_pack_bytes(cfg: SparseSubmConvConfig, w_dtype: torch.dtype) -> int:
+    out = ctypes.c_size_t()
+    dt = {torch.bfloat16: _capi.SC_DTYPE_BF16, torch.int8: _capi.SC_DTYPE_I8}.get(w_dtype)
+    if dt is None:
+        raise SparseConvError(3, "weight packing takes bf16 or int8 weights")
+    check(_capi.load().sc_conv_weight_pack_size(ctypes.byref(cfg.to_c()), dt, ctypes.byref(out)))
+    return out.value
+
+
+def pack_conv_weight(cfg: SparseSubmConvConfig, weight: torch.Tensor) -> torch.Tensor:
+    """The planned conv's weight layout (sc_conv_weight_pack); a one-time
+    per-layer reorder, the role pack_flex_weight plays for the reference's CPU
+    path (crates/burn_flex_gmm/src/lib.rs:377-426)."""
+    _require_cuda("weight", weight)
+    buf = torch.empty(conv_weight_pack_bytes(cfg, weight.dtype), dtype=torch.uint8, device=weight.device)
+    check(_capi.load().sc_conv_weight_pack(ctypes.byref(cfg.to_c()), _dt(weight), _ptr(weight), _ptr(buf),
+                                           _stream()))
+    return buf
+
+
 def sparse_subm_conv_forward(cfg: SparseSubmConvConfig, input: torch.Tensor,
                              neighbor_rows: torch.Tensor, weight: torch.Tensor,
                              bias: Optional[torch.Tensor] = None,
@@ -186,7 +292,8 @@ def sparse_subm_conv_forward(cfg: SparseSubmConvConfig, input: torch.Tensor,
                              out: Optional[torch.Tensor] = None,
                              layer_norm: bool = False, ln_weight: Optional[torch.Tensor] = None,
                              ln_bias: Optional[torch.Tensor] = None, ln_eps: float = 1e-6,
-                             silu: bool = False) -> torch.Tensor:
+                             silu: bool = False, plan: Optional[ConvPlan] = None,
+                             packed_weight: Optional[torch.Tensor] = None) -> torch.Tensor:
     """sparse_subm_conv_forward_wgpu (crates/burn_flex_gmm/src/wgpu/sparse_conv.rs:310-367).
 
     input [N_in, Cin] f32|bf16; neighbor_rows [N_q, K] int32 (N_q <= N_in);
@@ -195,6 +302,9 @@ def sparse_subm_conv_forward(cfg: SparseSubmConvConfig, input: torch.Tensor,
     bias [Cout] f32 or None; residual [N_q, Cout] in the output dtype or None.
     Optional fused epilogue: + bias -> LayerNorm over Cout (ln_weight / ln_bias
     [Cout] f32 or None, ln_eps) -> SiLU -> + residual.
+    With ``plan`` (a ConvPlan of this map) and ``packed_weight``
+    (pack_conv_weight of ``weight``) bf16 convs take the halo-staged kernel
+    (same result up to the fixed f32 summation order).
     Returns [N_q, Cout] in out_dtype (default: the input dtype)."""
     _require_cuda("input", input)
     _require_cuda("neighbor_rows", neighbor_rows)
@@ -236,7 +346,10 @@ def sparse_subm_conv_forward(cfg: SparseSubmConvConfig, input: torch.Tensor,
             _require_cuda(name, t)
             if t.dtype != torch.float32 or t.numel() != cfg.out_channels:
                 raise SparseConvError(2, f"{name} must be f32 [Cout]")
-    if layer_norm or silu:
+    if plan is not None and (plan.n_q != n_q or plan.n_in != input.shape[0] or plan.K != K):
+        raise SparseConvError(2, f"conv plan was built for n_in={plan.n_in} n_q={plan.n_q} K={plan.K}, "
+                                 f"got n_in={input.shape[0]} n_q={n_q} K={K}")
+    if layer_norm or silu or plan is not None:
         epi = _capi.ScConvEpilogue()
         epi.residual = None if residual is None else residual.data_ptr()
         epi.layer_norm = int(layer_norm)
@@ -244,6 +357,12 @@ def sparse_subm_conv_forward(cfg: SparseSubmConvConfig, input: torch.Tensor,
         epi.ln_bias = None if ln_bias is None else ln_bias.data_ptr()
         epi.ln_eps = float(ln_eps)
         epi.silu = int(silu)
+        if plan is not None:
+            check(_capi.load().sc_subm_conv_forward_planned(
+                ctypes.byref(c), _dt(input), _ptr(input), input.shape[0], _ptr(neighbor_rows), n_q,
+                _dt(weight), _ptr(weight), _ptr(packed_weight), _ptr(w_scale), _ptr(bias), ctypes.byref(epi),
+                _dt(out), _ptr(out), _ptr(plan.buf), _stream()))
+            return out
         check(_capi.load().sc_subm_conv_forward_fused(
             ctypes.byref(c), _dt(input), _ptr(input), input.shape[0], _ptr(neighbor_rows), n_q,
             _dt(weight), _ptr(weight), _ptr(w_scale), _ptr(bias), ctypes.byref(epi), _dt(out),

@@ -180,6 +180,67 @@ int sc_subm_conv_forward_fused(const sc_conv_config *cfg, int act_dtype, const v
                                const sc_conv_epilogue *epi, int out_dtype, void *d_out,
                                sc_stream stream);
 
+/* ----------------------------------------------------------- conv plan */
+
+/*
+ * Conv plan: a row order and per-tile halo tables derived from one
+ * neighbour map, which the planned conv reads.  It has no counterpart in the
+ * reference's API: it plays the role of the reference's neighbour cache
+ * (the decoder reuses one map for every conv at a resolution,
+ * crates/burn_flex_gmm/src/wgpu.rs:349-382, sparse_decoder.rs:1057-1136):
+ * build it once per map, right after sc_neighbor_map_build, and pass it to
+ * every sc_subm_conv_forward_planned call on that map.
+ *
+ * Rows are grouped by 8^3 bricks (coarser if the coords' bounding box has
+ * more than 2*n_q bricks) into tiles of 256 rows, sorted by neighbour mask
+ * within a tile; for each tile the plan lists the distinct input rows its
+ * neighbours touch and a 16-bit local index per (row, offset).
+ *
+ * sc_conv_plan_size: bytes of the plan buffer for n_q query rows and a kernel
+ * of kernel_rows offsets (1..32).
+ * sc_conv_plan_build: d_coords [n_in][4] i32 (the coords the map was built
+ * from), d_map [n_q][K] i32 (sc_neighbor_map_build's output for query rows
+ * [0, n_q)); d_plan 256-byte aligned, plan_bytes >= sc_conv_plan_size.
+ * Stream-ordered, no sync, no allocation.  The plan is valid for that map
+ * (same n_in, n_q, K) until the map changes.
+ */
+int sc_conv_plan_size(int64_t n_q, int64_t kernel_rows, size_t *bytes);
+int sc_conv_plan_build(const sc_conv_config *cfg, const int32_t *d_coords, int64_t n_in,
+                       const int32_t *d_map, int64_t n_q, void *d_plan, size_t plan_bytes,
+                       sc_stream stream);
+
+/*
+ * Weights packed for the planned conv: per (group, 128-output-channel tile,
+ * offset k, 32-input-channel chunk, 16-channel block) one contiguous
+ * fragment in MFMA operand order.  It has no counterpart in the reference's
+ * device API; it plays the role of pack_flex_weight
+ * (crates/burn_flex_gmm/src/lib.rs:377-426), a one-time per-layer reorder
+ * (the decoder caches its weights per layer, sparse_decoder.rs:757-844).
+ * w_dtype bf16 or i8 (scales stay [Cout] f32, unpacked); Cin per group must
+ * be a multiple of 32.  d_weight is the reference layout [Cout][KD][KH][KW]
+ * [Cin_g]; d_packed is 16-byte aligned, sc_conv_weight_pack_size bytes.
+ */
+int sc_conv_weight_pack_size(const sc_conv_config *cfg, int w_dtype, size_t *bytes);
+int sc_conv_weight_pack(const sc_conv_config *cfg, int w_dtype, const void *d_weight, void *d_packed,
+                        sc_stream stream);
+
+/*
+ * sc_subm_conv_forward_fused reading a plan of the same map and the packed
+ * copy of the weights (both may be NULL).  With both, bf16 activations and at
+ * most 27 offsets take the halo-staged kernel; d_weight (reference layout)
+ * is still required for tiles whose halo exceeds the kernel's LDS budget and
+ * for shapes the halo kernel does not take.  Same result as
+ * sc_subm_conv_forward_fused up to f32 summation order: the halo kernel sums
+ * each row's (32-channel chunk, offset) products chunk-major instead of
+ * offset-major, in a fixed order, so results are bit-identical run to run.
+ */
+int sc_subm_conv_forward_planned(const sc_conv_config *cfg, int act_dtype, const void *d_input,
+                                 int64_t n_in, const int32_t *d_map, int64_t n_q, int w_dtype,
+                                 const void *d_weight, const void *d_packed_weight,
+                                 const float *d_w_scale, const float *d_bias,
+                                 const sc_conv_epilogue *epi, int out_dtype, void *d_out,
+                                 const void *d_plan, sc_stream stream);
+
 /* ------------------------------------------------------------ block ops */
 
 /*

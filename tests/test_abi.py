@@ -7,6 +7,7 @@ import re
 
 import numpy as np
 import pytest
+import torch
 
 from bevy_synth_amd import _capi
 from bevy_synth_amd import flex_gmm as F
@@ -69,8 +70,10 @@ def test_validate_config_errors(cfg, msg, oracle):
 def test_workspace_sizes():
     n = 1_040_679
     b = F.neighbor_map_workspace_bytes(n)
+    # header 256 B + bbox partials (1024 blocks x 9 i32) +
     # max(hash table: 2..4 slots x 12 B, dense grid: 32 cells x 4 B) per row
-    assert 256 + 128 * n <= b <= 256 + max(128 * n, 12 * 4 * n)
+    fixed = 256 + 1024 * 9 * 4
+    assert fixed + 128 * n <= b <= fixed + max(128 * n, 12 * 4 * n)
     assert F.neighbor_map_workspace_bytes(0) > 256
     with pytest.raises(_capi.SparseConvError):
         F.neighbor_map_workspace_bytes(-1)
@@ -109,3 +112,19 @@ def test_argument_errors_before_device_work():
     assert L.sc_subm_conv_forward(ctypes.byref(cfg), 0, None, 0, None, 0, 0, None, None, None, None,
                                   0, None, None) == 0
     assert L.sc_add(0, None, None, 0, None, None) == 0
+
+
+def test_plan_size_matches_layout():
+    """sc_conv_plan_size equals the section layout the Python reader mirrors."""
+    for n_q, K in ((0, 27), (1, 27), (1000, 27), (1040679, 27), (4097, 1), (300, 8)):
+        assert F.conv_plan_bytes(n_q, K) == F.conv_plan_layout(n_q, K)["total"]
+    with pytest.raises(_capi.SparseConvError):
+        F.conv_plan_bytes(100, 33)
+
+
+def test_weight_pack_size():
+    cfg = F.SparseSubmConvConfig(128, 200)
+    assert F.conv_weight_pack_bytes(cfg, torch.bfloat16) == 2 * 128 * 27 * 128 * 2
+    assert F.conv_weight_pack_bytes(cfg, torch.int8) == 2 * 128 * 27 * 128
+    with pytest.raises(_capi.SparseConvError):
+        F.conv_weight_pack_bytes(F.SparseSubmConvConfig(48, 64), torch.bfloat16)

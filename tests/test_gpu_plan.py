@@ -1,0 +1,297 @@
+"""GPU tests of the conv plan (sc_conv_plan_build), the weight packing
+(sc_conv_weight_pack) and the planned, halo-staged conv
+(sc_subm_conv_forward_planned).
+
+The plan is checked structurally against the map it was built from (every
+(row, offset) entry resolves to the same input row); the planned conv against
+the fp64 definition on the same bf16-rounded operands (1e-2, f32 output 2e-5),
+including tiles whose halo overflows the LDS budget and take the direct
+kernel."""
+import numpy as np
+import pytest
+import torch
+
+from bevy_synth_amd import flex_gmm as F
+from bevy_synth_amd import synth
+from tests.tolerance import TOL_BF16, assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def bf16_dev(x_f32):
+    return dev(synth.bf16_bits(x_f32).view(np.int16)).view(torch.bfloat16)
+
+
+def rbf(a):
+    return synth.bf16_to_f32(synth.bf16_bits(np.asarray(a, np.float32)))
+
+
+def ocfg(oracle, cfg):
+    return oracle.OracleConfig(cfg.in_channels, cfg.out_channels, cfg.kernel_d, cfg.kernel_h,
+                               cfg.kernel_w, groups=cfg.groups, axis_order=cfg.axis_order,
+                               axis_sign=cfg.axis_sign)
+
+
+def cluster_coords(n_centres, spacing=3):
+    """Centres on a lattice of the given spacing, each followed later by its 26
+    neighbours: with the centres as query rows, every neighbour is distinct, so
+    a 256-row tile touches 27 * 256 input rows (its halo overflows)."""
+    side = int(np.ceil(n_centres ** (1 / 3)))
+    g = np.stack(np.meshgrid(*[np.arange(side)] * 3, indexing="ij"), -1).reshape(-1, 3)[:n_centres]
+    centres = 1 + spacing * g
+    offs = np.stack(np.meshgrid(*[np.arange(-1, 2)] * 3, indexing="ij"), -1).reshape(-1, 3)
+    offs = offs[np.any(offs != 0, axis=1)]
+    nb = (centres[:, None, :] + offs[None]).reshape(-1, 3)
+    xyz = np.concatenate([centres, nb])
+    out = np.zeros((len(xyz), 4), np.int32)
+    out[:, 1:] = xyz
+    return out
+
+
+def check_plan(plan, nbr, n_in):
+    h = plan.to_host()
+    n_q, K = nbr.shape
+    order, tile_u, halo, lmap = h["order"], h["tile_u"], h["halo"], h["lmap"]
+    assert h["n_tiles"] == (n_q + 255) // 256 and h["K"] == K
+    flat = order.ravel()
+    rows = flat[flat >= 0]
+    assert len(rows) == n_q and np.array_equal(np.sort(rows), np.arange(n_q)), "order is not a permutation"
+    assert np.all(flat[n_q:] == -1), "padding rows are not at the end"
+    over = set(np.nonzero(tile_u > F.PLAN_HALO_MAX)[0].tolist())
+    assert over == set(h["overflow"].tolist())
+    for t in range(h["n_tiles"]):
+        if t in over:
+            continue
+        U = tile_u[t]
+        hl = halo[t, :U]
+        assert np.all(np.diff(hl) > 0), "halo not strictly increasing"
+        r = order[t]
+        valid = r >= 0
+        m = nbr[r[valid]]                       # [rows, K]
+        lm = lmap[t][:, valid].T                # [rows, K]
+        present = (m >= 0) & (m < n_in)
+        assert np.all((lm == F.PLAN_ABSENT) == ~present)
+        assert np.array_equal(hl[lm[present]], m[present])
+        assert len(np.unique(m[present])) == U
+    return h
+
+
+@pytest.mark.parametrize("which", ["config1", "random_batches", "clusters", "query_subset"])
+def test_plan_structure(which):
+    rng = np.random.default_rng(11)
+    cfg = F.SparseSubmConvConfig(32, 32)
+    q = None
+    if which == "config1":
+        coords = synth.config1_coords()
+    elif which == "random_batches":
+        c = rng.integers(0, 40, size=(20000, 4)).astype(np.int32)
+        c[:, 0] = rng.integers(0, 3, 20000)
+        coords = np.unique(c, axis=0)
+        coords = coords[rng.permutation(len(coords))]  # unsorted input order
+    elif which == "clusters":
+        coords = cluster_coords(600)
+        q = 600
+    else:
+        coords = synth.config1_coords()
+        q = 9000
+    cd = dev(coords)
+    nbr = F.neighbor_rows_tensor_from_coords_tensor(cfg, cd, query_rows=q)
+    plan = F.build_conv_plan(cfg, cd, nbr)
+    h = check_plan(plan, nbr.cpu().numpy(), len(coords))
+    if which == "clusters":
+        assert h["n_overflow"] == h["n_tiles"]
+    # deterministic: a second build gives the same tables (entries past a
+    # tile's halo count, and the tables of overflowing tiles, are not written)
+    h2 = F.build_conv_plan(cfg, cd, nbr).to_host()
+    for key in ("order", "tile_u", "overflow"):
+        assert np.array_equal(h[key], h2[key]), key
+    for t in range(h["n_tiles"]):
+        U = h["tile_u"][t]
+        if U <= F.PLAN_HALO_MAX:
+            assert np.array_equal(h["halo"][t, :U], h2["halo"][t, :U])
+            assert np.array_equal(h["lmap"][t], h2["lmap"][t])
+
+
+@pytest.mark.parametrize("cin,cout,groups,wdt", [(64, 128, 1, "bf16"), (96, 200, 1, "bf16"),
+                                                  (64, 64, 2, "bf16"), (128, 64, 1, "i8")])
+def test_weight_pack_layout(cin, cout, groups, wdt):
+    rng = np.random.default_rng(cin + cout)
+    cfg = F.SparseSubmConvConfig(cin, cout, groups=groups)
+    cin_g, cout_g, K = cin // groups, cout // groups, 27
+    if wdt == "bf16":
+        w = rbf(synth.normal_f32(rng, (cout, K, cin_g)))
+        wd = bf16_dev(w)
+        wh = synth.bf16_bits(w).astype(np.int64)
+    else:
+        q, _ = synth.int8_weight(rng, cout, K, cin_g)
+        wd = dev(q)
+        wh = q.astype(np.int64)
+    packed = F.pack_conv_weight(cfg, wd).cpu().numpy()
+    packed = packed.view(np.uint16 if wdt == "bf16" else np.int8).astype(np.int64)
+    n_ot, nkc = (cout_g + 127) // 128, cin_g // 32
+    exp = np.zeros((groups, n_ot, K, nkc, 8, 64, 8), np.int64)
+    for g in range(groups):
+        for ot in range(n_ot):
+            for jj in range(8):
+                for lane in range(64):
+                    o = ot * 128 + 16 * jj + (lane & 15)
+                    if o >= cout_g:
+                        continue
+                    for c in range(nkc):
+                        i0 = 32 * c + 8 * (lane >> 4)
+                        exp[g, ot, :, c, jj, lane, :] = wh[g * cout_g + o, :, i0:i0 + 8]
+    assert np.array_equal(packed.reshape(exp.shape), exp)
+
+
+def planned(cfg, coords, x, w, b, *, wdt="bf16", w_scale=None, q=None, **kw):
+    cd = dev(coords)
+    nbr = F.neighbor_rows_tensor_from_coords_tensor(cfg, cd, query_rows=q)
+    plan = F.build_conv_plan(cfg, cd, nbr)
+    wd = bf16_dev(w) if wdt == "bf16" else dev(w)
+    pw = F.pack_conv_weight(cfg, wd)
+    out = F.sparse_subm_conv_forward(cfg, bf16_dev(x), nbr, wd, dev(b),
+                                     w_scale=None if w_scale is None else dev(w_scale),
+                                     plan=plan, packed_weight=pw, **kw)
+    return out, nbr.cpu().numpy(), plan
+
+
+@pytest.mark.parametrize("cin,cout,groups", [(32, 32, 1), (64, 96, 1), (128, 128, 1), (256, 64, 1),
+                                             (64, 64, 2), (96, 200, 1)])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_planned_conv_shapes(oracle, cin, cout, groups, out_dtype):
+    coords = synth.config1_coords()
+    rng = np.random.default_rng(cin * 7 + cout + groups)
+    n = len(coords)
+    x = rbf(synth.normal_f32(rng, (n, cin)))
+    w = rbf(synth.conv_weight(rng, cout, 27, cin // groups, 1.0 / np.sqrt(27 * cin)))
+    b = synth.normal_f32(rng, cout, 0.1)
+    cfg = F.SparseSubmConvConfig(cin, cout, groups=groups)
+    out, nbr, _ = planned(cfg, coords, x, w, b, out_dtype=out_dtype)
+    exp = oracle.conv_ref_f64(ocfg(oracle, cfg), w, b, x, nbr)
+    assert_close(out.float().cpu().numpy(), exp, TOL_BF16 if out_dtype == torch.bfloat16 else 2e-5,
+                 "planned conv")
+
+
+def test_planned_int8_weights(oracle):
+    coords = synth.config1_coords()
+    rng = np.random.default_rng(5)
+    n, cin, cout = len(coords), 128, 64
+    x = rbf(synth.normal_f32(rng, (n, cin)))
+    q, scale = synth.int8_weight(rng, cout, 27, cin)
+    b = synth.normal_f32(rng, cout, 0.1)
+    cfg = F.SparseSubmConvConfig(cin, cout)
+    out, nbr, _ = planned(cfg, coords, x, q, b, wdt="i8", w_scale=scale, out_dtype=torch.float32)
+    exp = oracle.conv_ref_f64(ocfg(oracle, cfg), q.astype(np.float32), b, x, nbr, w_scale=scale)
+    assert_close(out.cpu().numpy(), exp, 2e-5, "planned int8 conv")
+
+
+@pytest.mark.parametrize("affine", [False, True])
+def test_planned_ln_silu_and_residual(oracle, affine):
+    coords = synth.config1_coords()
+    rng = np.random.default_rng(21)
+    n, c = len(coords), 128
+    x = rbf(synth.normal_f32(rng, (n, c)))
+    w = rbf(synth.conv_weight(rng, c, 27, c, 1 / np.sqrt(27 * c)))
+    b = synth.normal_f32(rng, c, 0.1)
+    lw = synth.normal_f32(rng, c) if affine else None
+    lb = synth.normal_f32(rng, c) if affine else None
+    res = rbf(synth.normal_f32(rng, (n, c)))
+    cfg = F.SparseSubmConvConfig(c, c)
+    out, nbr, _ = planned(cfg, coords, x, w, b, residual=bf16_dev(res), layer_norm=True,
+                          ln_weight=None if lw is None else dev(lw), ln_bias=None if lb is None else dev(lb),
+                          ln_eps=1e-6, silu=True)
+    conv = oracle.conv_ref_f64(oracle.OracleConfig(c, c), w, b, x, nbr).astype(np.float32)
+    exp = oracle.silu(oracle.layer_norm(conv, lw, lb, 1e-6)) + res
+    assert_close(out.float().cpu().numpy(), exp, TOL_BF16, "planned LN/SiLU/residual")
+    # conv -> + residual only (the second conv of the residual block)
+    out2, _, _ = planned(cfg, coords, x, w, b, residual=dev(res), out_dtype=torch.float32)
+    exp2 = oracle.conv_ref_f64(oracle.OracleConfig(c, c), w, b, x, nbr) + res
+    assert_close(out2.cpu().numpy(), exp2, 2e-5, "planned residual")
+
+
+def test_planned_overflow_tiles_and_query_subset(oracle):
+    """Cluster centres as query rows: every tile's halo overflows, so the whole
+    conv runs through the direct kernel in plan order."""
+    coords = cluster_coords(700)
+    rng = np.random.default_rng(8)
+    n, c = len(coords), 64
+    x = rbf(synth.normal_f32(rng, (n, c)))
+    w = rbf(synth.conv_weight(rng, c, 27, c, 0.05))
+    b = synth.normal_f32(rng, c, 0.1)
+    cfg = F.SparseSubmConvConfig(c, c)
+    out, nbr, plan = planned(cfg, coords, x, w, b, q=700, out_dtype=torch.float32)
+    h = plan.to_host()
+    assert h["n_overflow"] == h["n_tiles"] == 3
+    exp = oracle.conv_ref_f64(ocfg(oracle, cfg), w, b, x, nbr)
+    assert_close(out.cpu().numpy(), exp, 2e-5, "overflow tiles")
+
+
+def test_planned_mixed_overflow(oracle):
+    """Some tiles overflow, others take the halo kernel, in one call."""
+    a = synth.config1_coords()[:3000]
+    cl = cluster_coords(300)
+    cl[:, 1:] += 200
+    # query rows: the shell, then the cluster centres; the cluster neighbours last
+    coords = np.concatenate([a, cl[:300], cl[300:]])
+    q = 3300
+    rng = np.random.default_rng(9)
+    n, c = len(coords), 32
+    x = rbf(synth.normal_f32(rng, (n, c)))
+    w = rbf(synth.conv_weight(rng, c, 27, c, 0.05))
+    b = synth.normal_f32(rng, c, 0.1)
+    cfg = F.SparseSubmConvConfig(c, c)
+    out, nbr, plan = planned(cfg, coords, x, w, b, q=q, out_dtype=torch.float32)
+    h = plan.to_host()
+    assert 0 < h["n_overflow"] < h["n_tiles"]
+    exp = oracle.conv_ref_f64(ocfg(oracle, cfg), w, b, x, nbr)
+    assert_close(out.cpu().numpy(), exp, 2e-5, "mixed overflow")
+
+
+def test_planned_config3_sampled_and_deterministic(oracle):
+    """Config 3 (1.04M voxels, C=128, bf16): plan structure, sampled rows
+    against the fp64 definition, bit-identical reruns, and agreement with the
+    unplanned conv within the bf16 bar."""
+    coords = synth.config3_coords()
+    n, c = len(coords), 128
+    rng = np.random.default_rng(3)
+    x = rbf(synth.normal_f32(rng, (n, c)))
+    w = rbf(synth.conv_weight(rng, c, 27, c, 1.0 / np.sqrt(27 * c)))
+    b = np.zeros(c, np.float32)
+    cfg = F.SparseSubmConvConfig(c, c)
+    cd = dev(coords)
+    nbr = F.neighbor_rows_tensor_from_coords_tensor(cfg, cd)
+    plan = F.build_conv_plan(cfg, cd, nbr)
+    nb = nbr.cpu().numpy()
+    h = check_plan(plan, nb, n)
+    assert h["brick_shift"] == 3
+    xd, wd, bd = bf16_dev(x), bf16_dev(w), dev(b)
+    pw = F.pack_conv_weight(cfg, wd)
+    o1 = F.sparse_subm_conv_forward(cfg, xd, nbr, wd, bd, plan=plan, packed_weight=pw)
+    o2 = F.sparse_subm_conv_forward(cfg, xd, nbr, wd, bd, plan=plan, packed_weight=pw)
+    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
+    sample = np.sort(np.random.default_rng(0).choice(n, 3000, replace=False))
+    exp = oracle.conv_ref_f64(ocfg(oracle, cfg), w, b, x, nb[sample])
+    assert_close(o1.float().cpu().numpy()[sample], exp, TOL_BF16, "config3 planned sampled")
+    unplanned = F.sparse_subm_conv_forward(cfg, xd, nbr, wd, bd)
+    d = (o1.float() - unplanned.float()).abs().max().item()
+    assert d <= 2.0 ** -5, d  # one bf16 ulp at |y| < 4 at most
+
+
+def test_plan_argument_errors():
+    cfg = F.SparseSubmConvConfig(64, 64)
+    coords = dev(synth.config1_coords()[:1000])
+    nbr = F.neighbor_rows_tensor_from_coords_tensor(cfg, coords)
+    plan = F.build_conv_plan(cfg, coords, nbr)
+    x = torch.zeros((1000, 64), dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros((64, 27, 64), dtype=torch.bfloat16, device="cuda")
+    nbr_short = nbr[:500].contiguous()
+    with pytest.raises(F.SparseConvError):
+        F.sparse_subm_conv_forward(cfg, x, nbr_short, w, plan=plan, packed_weight=F.pack_conv_weight(cfg, w))
+    small = torch.empty(16, dtype=torch.uint8, device="cuda")
+    with pytest.raises(F.SparseConvError) as e:
+        F.conv_plan_build_into(cfg, coords, nbr, small)
+    assert e.value.status == 5
