@@ -52,13 +52,18 @@ struct PlanArgs {
     int32_t *overflow;
     int32_t *halo;
     uint16_t *lmap;
+    uint32_t *grid;
+    int32_t *gsum;
     int32_t *counts;
     int32_t *offsets;
     int32_t *bsum;
     int64_t n_tiles;
     int64_t brick_cap;
     int64_t n_bsum;
+    int64_t grid_cap;
 };
+
+constexpr uint32_t kGridEmpty = 0xFFFFFFFFu;
 
 __global__ void plan_init_kernel(PlanArgs a)
 {
@@ -78,10 +83,17 @@ __global__ void plan_init_kernel(PlanArgs a)
         }
         h->n_bricks = 0;
         h->status = 0;
+        h->grid_mode = 0;
+        h->n_unique = 0;
+        h->n_extras = 0;
     }
-    for (int64_t i = tid; i < a.brick_cap; i += stride) a.counts[i] = 0;
     for (int64_t i = a.n_q + tid; i < a.n_tiles * kPlanTileRows; i += stride) a.order[i] = -1;
 }
+
+// Per-block min/max of the query coords -> partials (in the brick-offset
+// array, which the scan overwrites later); plan_bbox_final_kernel reduces them
+// (one atomic-free pass instead of thousands of same-address atomics).
+constexpr int kBboxBlocks = 512;
 
 __global__ __launch_bounds__(kThreads) void plan_bbox_kernel(PlanArgs a)
 {
@@ -115,8 +127,38 @@ __global__ __launch_bounds__(kThreads) void plan_bbox_kernel(PlanArgs a)
             lo = min(lo, s_mn[w][j]);
             hi = max(hi, s_mx[w][j]);
         }
-        atomicMin(&a.hdr->bmin[j], lo);
-        atomicMax(&a.hdr->bmax[j], hi);
+        a.offsets[blockIdx.x * 8 + j] = lo;
+        a.offsets[blockIdx.x * 8 + 4 + j] = hi;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void plan_bbox_final_kernel(PlanArgs a, int nblocks)
+{
+    __shared__ int s_v[8][kThreads / 64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = j < 4 ? INT_MAX : INT_MIN;
+    for (int b = threadIdx.x; b < nblocks; b += blockDim.x)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v[j] = min(v[j], a.offsets[b * 8 + j]);
+            v[4 + j] = max(v[4 + j], a.offsets[b * 8 + 4 + j]);
+        }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        v[j] = j < 4 ? wave_min_i32(v[j]) : wave_max_i32(v[j]);
+        if (lane == 0) s_v[j][wave] = v[j];
+    }
+    __syncthreads();
+    if (threadIdx.x < 8) {
+        const int j = threadIdx.x;
+        int r = s_v[j][0];
+        for (int w = 1; w < (int)blockDim.x / 64; ++w) r = j < 4 ? min(r, s_v[j][w]) : max(r, s_v[j][w]);
+        if (j < 4)
+            a.hdr->bmin[j] = r;
+        else
+            a.hdr->bmax[j - 4] = r;
     }
 }
 
@@ -187,14 +229,82 @@ __device__ inline int64_t brick_of(const BrickGrid &g, int4 c)
     return ((b * g.nb[1] + x) * g.nb[2] + y) * g.nb[3] + z;
 }
 
-__global__ __launch_bounds__(kThreads) void plan_count_kernel(PlanArgs a)
+// Occupancy-grid geometry: 8^3 bricks over the bounding box; a cell's index
+// is brick * 512 + its lexicographic position inside the brick, bricks in
+// (batch, x, y, z) order.  Valid when the cells fit the plan's grid.
+struct GridGeom {
+    bool ok;
+    int64_t lo[4];
+    int64_t nb[4];
+    int64_t cells;
+};
+
+__device__ inline GridGeom grid_geom(const PlanHeader *h, int64_t grid_cap)
 {
+    GridGeom g;
+    g.ok = false;
+    g.cells = 0;
+    double tot = 512.0;
+    for (int j = 0; j < 4; ++j) {
+        g.lo[j] = h->bmin[j];
+        const int64_t ext = (int64_t)h->bmax[j] - (int64_t)h->bmin[j] + 1;
+        if (ext <= 0) return g;
+        g.nb[j] = j == 0 ? ext : ((ext - 1) >> 3) + 1;
+        tot *= (double)g.nb[j];
+    }
+    if (tot > (double)grid_cap) return g;
+    g.ok = true;
+    g.cells = g.nb[0] * g.nb[1] * g.nb[2] * g.nb[3] * 512;
+    return g;
+}
+
+__device__ inline int64_t grid_cell(const GridGeom &g, int4 c)
+{
+    const int64_t b = (int64_t)c.x - g.lo[0];
+    const int64_t x = (int64_t)c.y - g.lo[1], y = (int64_t)c.z - g.lo[2], z = (int64_t)c.w - g.lo[3];
+    const int64_t brick = ((b * g.nb[1] + (x >> 3)) * g.nb[2] + (y >> 3)) * g.nb[3] + (z >> 3);
+    return brick * 512 + ((x & 7) * 64 + (y & 7) * 8 + (z & 7));
+}
+
+// Chooses the ordering mode; grid mode: grid := EMPTY; fallback: brick counts := 0.
+__global__ __launch_bounds__(kThreads) void plan_prep_kernel(PlanArgs a)
+{
+    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const GridGeom gg = grid_geom(a.hdr, a.grid_cap);
+    if (gg.ok) {
+        if (tid == 0) {
+            a.hdr->grid_mode = 1;
+            a.hdr->brick_shift = 3;
+            a.hdr->n_bricks = (uint64_t)(gg.cells / 512);
+        }
+        for (int64_t i = tid; i < gg.cells; i += stride) a.grid[i] = kGridEmpty;
+        return;
+    }
     const BrickGrid g = brick_grid(a.hdr, a.brick_cap);
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
+    if (tid == 0) {
         a.hdr->brick_shift = g.shift;
         a.hdr->n_bricks = g.total;
     }
-    if (g.shift < 0) return;
+    for (int64_t i = tid; i < a.brick_cap; i += stride) a.counts[i] = 0;
+}
+
+// Grid mode: each query row claims its cell (the lowest row of a duplicated
+// coord keeps it, the others go to the extras list); fallback: brick counts.
+__global__ __launch_bounds__(kThreads) void plan_place_kernel(PlanArgs a)
+{
+    if (a.hdr->grid_mode) {
+        const GridGeom gg = grid_geom(a.hdr, a.grid_cap);
+        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n_q;
+             i += (int64_t)gridDim.x * blockDim.x) {
+            const uint32_t old = atomicMin(&a.grid[grid_cell(gg, a.coords[i])], (uint32_t)i);
+            if (old != kGridEmpty) a.counts[atomicAdd(&a.hdr->n_extras, 1)] = (int32_t)max(old, (uint32_t)i);
+        }
+        return;
+    }
+    const int shift = a.hdr->brick_shift;
+    if (shift < 0) return;
+    const BrickGrid g = brick_grid(a.hdr, a.brick_cap);
     for (int64_t base = (int64_t)blockIdx.x * blockDim.x; base < a.n_q; base += (int64_t)gridDim.x * blockDim.x) {
         const int64_t i = base + threadIdx.x;
         const bool act = i < a.n_q;
@@ -228,10 +338,29 @@ __device__ inline int block_scan_excl(int x, int *s_wave, int &total)
     return before + inc - x;
 }
 
-// Exclusive scan of counts within blocks of 1024 entries; block totals -> bsum.
-__global__ __launch_bounds__(kThreads) void plan_scan_blocks_kernel(PlanArgs a)
+// Grid mode: occupied cells per 2048-cell block -> gsum; fallback: exclusive
+// scan of the brick counts within 1024-entry blocks, block totals -> bsum.
+__global__ __launch_bounds__(kThreads) void plan_scan1_kernel(PlanArgs a)
 {
     __shared__ int s_wave[kThreads / 64];
+    if (a.hdr->grid_mode) {
+        const int64_t nblk = a.grid_cap / kPlanGridBlock;
+        if ((int64_t)blockIdx.x >= nblk) return;
+        const GridGeom gg = grid_geom(a.hdr, a.grid_cap);
+        const int64_t base = (int64_t)blockIdx.x * kPlanGridBlock + threadIdx.x * 8;
+        int cnt = 0;
+        if (base < gg.cells) {
+            const uint4 *g4 = reinterpret_cast<const uint4 *>(a.grid + base);
+            const uint4 u0 = g4[0], u1 = g4[1];
+            cnt = (u0.x != kGridEmpty) + (u0.y != kGridEmpty) + (u0.z != kGridEmpty) + (u0.w != kGridEmpty) +
+                  (u1.x != kGridEmpty) + (u1.y != kGridEmpty) + (u1.z != kGridEmpty) + (u1.w != kGridEmpty);
+        }
+        int total;
+        block_scan_excl(cnt, s_wave, total);
+        if (threadIdx.x == 0) a.gsum[blockIdx.x] = total;
+        return;
+    }
+    if ((int64_t)blockIdx.x >= a.n_bsum || a.hdr->brick_shift < 0) return;
     const int64_t base = (int64_t)blockIdx.x * kPlanScanBlock + threadIdx.x * 4;
     const int4 c = *reinterpret_cast<const int4 *>(a.counts + base);
     int total;
@@ -245,18 +374,23 @@ __global__ __launch_bounds__(kThreads) void plan_scan_blocks_kernel(PlanArgs a)
     if (threadIdx.x == 0) a.bsum[blockIdx.x] = total;
 }
 
-// Exclusive scan of the block totals (one block, carried over 1024-entry chunks).
-__global__ __launch_bounds__(kThreads) void plan_scan_top_kernel(PlanArgs a)
+// Exclusive scan of the block totals (gsum or bsum; one block, carried over
+// 1024-entry chunks).  Grid mode: the total (distinct coords) -> n_unique.
+__global__ __launch_bounds__(kThreads) void plan_scan2_kernel(PlanArgs a)
 {
     __shared__ int s_wave[kThreads / 64];
+    const bool grid = a.hdr->grid_mode != 0;
+    if (!grid && a.hdr->brick_shift < 0) return;
+    int32_t *arr = grid ? a.gsum : a.bsum;
+    const int64_t n = grid ? a.grid_cap / kPlanGridBlock : a.n_bsum;
     int carry = 0;
-    for (int64_t base = 0; base < a.n_bsum; base += kThreads * 4) {
+    for (int64_t base = 0; base < n; base += kThreads * 4) {
         int v[4];
         int sum = 0;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int64_t i = base + threadIdx.x * 4 + u;
-            v[u] = i < a.n_bsum ? a.bsum[i] : 0;
+            v[u] = i < n ? arr[i] : 0;
             sum += v[u];
         }
         int total;
@@ -264,11 +398,12 @@ __global__ __launch_bounds__(kThreads) void plan_scan_top_kernel(PlanArgs a)
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int64_t i = base + threadIdx.x * 4 + u;
-            if (i < a.n_bsum) a.bsum[i] = carry + ex;
+            if (i < n) arr[i] = carry + ex;
             ex += v[u];
         }
         carry += total;
     }
+    if (grid && threadIdx.x == 0) a.hdr->n_unique = carry;
 }
 
 __device__ inline int64_t brick_start(const PlanArgs &a, uint32_t br)
@@ -276,15 +411,44 @@ __device__ inline int64_t brick_start(const PlanArgs &a, uint32_t br)
     return (int64_t)a.offsets[br] + a.bsum[br / kPlanScanBlock];
 }
 
-__global__ __launch_bounds__(kThreads) void plan_scatter_kernel(PlanArgs a)
+// Grid mode: the rows of the occupied cells in cell order -> order (brick
+// order, lexicographic within a brick).  Fallback: rows to their brick's
+// segment (ranks from wave-aggregated atomics), or row order when no brick
+// grid fits.
+__global__ __launch_bounds__(kThreads) void plan_emit_kernel(PlanArgs a)
 {
+    __shared__ int s_wave[kThreads / 64];
+    if (a.hdr->grid_mode) {
+        const int64_t nblk = a.grid_cap / kPlanGridBlock;
+        if ((int64_t)blockIdx.x >= nblk) return;
+        const GridGeom gg = grid_geom(a.hdr, a.grid_cap);
+        const int64_t base = (int64_t)blockIdx.x * kPlanGridBlock + threadIdx.x * 8;
+        uint32_t r[8];
+        int cnt = 0;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) r[u] = kGridEmpty;
+        if (base < gg.cells) {
+            const uint4 *g4 = reinterpret_cast<const uint4 *>(a.grid + base);
+            const uint4 u0 = g4[0], u1 = g4[1];
+            r[0] = u0.x; r[1] = u0.y; r[2] = u0.z; r[3] = u0.w;
+            r[4] = u1.x; r[5] = u1.y; r[6] = u1.z; r[7] = u1.w;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) cnt += r[u] != kGridEmpty;
+        }
+        int total;
+        int pos = a.gsum[blockIdx.x] + block_scan_excl(cnt, s_wave, total);
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (r[u] != kGridEmpty) a.order[pos++] = (int32_t)r[u];
+        return;
+    }
     const int shift = a.hdr->brick_shift;
     BrickGrid g;
     if (shift >= 0) g = brick_grid(a.hdr, a.brick_cap);
     for (int64_t base = (int64_t)blockIdx.x * blockDim.x; base < a.n_q; base += (int64_t)gridDim.x * blockDim.x) {
         const int64_t i = base + threadIdx.x;
         const bool act = i < a.n_q;
-        if (shift < 0) {  // no brick order: rows stay in their own order
+        if (shift < 0) {
             if (act) a.order[i] = (int32_t)i;
             continue;
         }
@@ -295,42 +459,59 @@ __global__ __launch_bounds__(kThreads) void plan_scatter_kernel(PlanArgs a)
     }
 }
 
-// Sorts each brick's segment of `order` by row index: one workgroup per
-// brick (grid-stride), rank of a row = number of smaller rows in the segment.
-__global__ __launch_bounds__(kThreads) void plan_segsort_kernel(PlanArgs a)
+// Grid mode: rows of duplicated coords after the distinct ones.  Fallback:
+// each brick's segment sorted by row index (one wave per brick, rank = number
+// of smaller rows), so the order is deterministic; segments longer than
+// kSegWave (only with duplicated coords) keep the scatter's order.
+constexpr int kSegWave = 512;
+
+__global__ __launch_bounds__(kThreads) void plan_fix_kernel(PlanArgs a)
 {
-    __shared__ int32_t s_seg[kSegLds];
+    __shared__ __attribute__((aligned(16))) int32_t s_seg[kThreads / 64][kSegWave];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (a.hdr->grid_mode) {
+        const int n_unique = a.hdr->n_unique, n_extras = a.hdr->n_extras;
+        for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < n_extras;
+             j += (int64_t)gridDim.x * blockDim.x)
+            a.order[n_unique + j] = a.counts[j];
+        return;
+    }
     if (a.hdr->brick_shift < 0) return;
     const uint64_t nb = a.hdr->n_bricks;
-    for (uint64_t br = blockIdx.x; br < nb; br += gridDim.x) {
+    int32_t *seg_lds = s_seg[wave];
+    for (uint64_t br = (uint64_t)blockIdx.x * (kThreads / 64) + wave; br < nb;
+         br += (uint64_t)gridDim.x * (kThreads / 64)) {
         const int64_t start = brick_start(a, (uint32_t)br);
         const int64_t end = br + 1 < nb ? brick_start(a, (uint32_t)(br + 1)) : a.n_q;
         const int n = (int)(end - start);
-        if (n <= 1) continue;
+        if (n <= 1 || n > kSegWave) continue;
         int32_t *seg = a.order + start;
-        if (n <= kSegLds) {
-            for (int e = threadIdx.x; e < n; e += kThreads) s_seg[e] = seg[e];
-            __syncthreads();
-            int32_t mine[kSegLds / kThreads];
-            int rank[kSegLds / kThreads];
+        const int n4 = (n + 3) & ~3;
+        constexpr int kPer = kSegWave / 64;
+        int32_t mine[kPer];
+        int rank[kPer];
 #pragma unroll
-            for (int u = 0; u < kSegLds / kThreads; ++u) {
-                const int e = threadIdx.x + u * kThreads;
-                mine[u] = e < n ? s_seg[e] : INT_MAX;
-                rank[u] = 0;
-            }
-            for (int f = 0; f < n; ++f) {
-                const int32_t v = s_seg[f];
-#pragma unroll
-                for (int u = 0; u < kSegLds / kThreads; ++u) rank[u] += v < mine[u];
-            }
-#pragma unroll
-            for (int u = 0; u < kSegLds / kThreads; ++u)
-                if (threadIdx.x + u * kThreads < n) seg[rank[u]] = mine[u];
-            __syncthreads();
+        for (int u = 0; u < kPer; ++u) {
+            const int e = lane + 64 * u;
+            mine[u] = e < n ? seg[e] : INT_MAX;
+            rank[u] = 0;
+            if (e < n4) seg_lds[e] = mine[u];
         }
-        // Larger segments (only with heavily duplicated coords) keep the
-        // scatter's order.
+        // the wave's own LDS writes are visible to its later reads once lgkmcnt drains
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_wave_barrier();
+        const int4 *s4 = reinterpret_cast<const int4 *>(seg_lds);
+        for (int f = 0; f < n4 / 4; ++f) {
+            const int4 v = s4[f];
+#pragma unroll
+            for (int u = 0; u < kPer; ++u)
+                rank[u] += (v.x < mine[u]) + (v.y < mine[u]) + (v.z < mine[u]) + (v.w < mine[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < kPer; ++u)
+            if (lane + 64 * u < n) seg[rank[u]] = mine[u];
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_wave_barrier();
     }
 }
 
@@ -339,31 +520,131 @@ __device__ inline uint32_t slot_hash(int32_t v)
     return ((uint32_t)v * 0x9E3779B1u) >> (32 - kHashBits);
 }
 
+// Block-wide exclusive scan for plan_tiles_kernel (kTileThreads threads).
+__device__ inline int tile_scan_excl(int x, int *s_wave, int &total)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int inc = x;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(inc, off, 64);
+        if (lane >= off) inc += y;
+    }
+    __syncthreads();
+    if (lane == 63) s_wave[wave] = inc;
+    __syncthreads();
+    int before = 0;
+    total = 0;
+    for (int w = 0; w < kTileThreads / 64; ++w) {
+        if (w < wave) before += s_wave[w];
+        total += s_wave[w];
+    }
+    return before + inc - x;
+}
+
+// Halo numbering: the rank of a row among the tile's distinct neighbour rows.
+//  * bitmap path (the neighbours span at most kBitmapBits row indices, the
+//    usual case for brick-ordered rows): one bit per row index in LDS, then
+//    a per-word prefix of popcounts; rank = prefix + popcount below the bit.
+//  * otherwise: an LDS hash table of the distinct rows, sorted (bitonic).
+constexpr int kBitmapWords = kHashSlots;  // 8192 words = 262144 row indices
+constexpr int kBitmapBits = kBitmapWords * 32;
+
 __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
 {
-    __shared__ int32_t s_key[kHashSlots];
-    __shared__ uint64_t s_list[kPlanHaloMax];
+    __shared__ uint32_t s_bits[kHashSlots];        // bitmap, or the hash table's keys
+    __shared__ __attribute__((aligned(16))) uint16_t s_pre[kBitmapWords];  // word prefix (bitmap path)
     __shared__ int s_wave[kTileThreads / 64];
+    __shared__ int s_mm[2][kTileThreads / 64];
+    int32_t *s_key = reinterpret_cast<int32_t *>(s_bits);
+    uint64_t *s_list = reinterpret_cast<uint64_t *>(s_pre);  // kPlanHaloMax entries (8 KB <= 16 KB)
+    static_assert(kPlanHaloMax * 8 <= kBitmapWords * 2, "sort list fits the prefix array");
     const int64_t t = blockIdx.x;
     const int p = threadIdx.x;
+    const int lane = p & 63, wave = p >> 6;
     const int K = a.K;
     const int64_t n_in = a.n_in;
-
-    for (int i = p; i < kHashSlots; i += kTileThreads) s_key[i] = -1;
     const int32_t q = a.order[t * kPlanTileRows + p];
-    __syncthreads();
 
-    // Distinct neighbour rows through the LDS hash table (linear probing; at
-    // most 27 * 256 keys in 8192 slots, so every probe ends).  A slot is read
-    // before it is claimed: most neighbours are shared by several rows of the
-    // tile and are found without an atomic.  Each neighbour's slot is kept.
     int32_t v[32];
+    int lo = INT_MAX, hi = INT_MIN;
 #pragma unroll
     for (int k = 0; k < 32; ++k) {
         int32_t x = -1;
         if (k < K && q >= 0) x = a.map[(int64_t)q * K + k];
         v[k] = (x >= 0 && x < n_in) ? x : -1;
+        if (v[k] >= 0) {
+            lo = min(lo, v[k]);
+            hi = max(hi, v[k]);
+        }
     }
+    lo = wave_min_i32(lo);
+    hi = wave_max_i32(hi);
+    if (lane == 0) {
+        s_mm[0][wave] = lo;
+        s_mm[1][wave] = hi;
+    }
+    __syncthreads();
+    for (int w = 0; w < kTileThreads / 64; ++w) {
+        lo = min(lo, s_mm[0][w]);
+        hi = max(hi, s_mm[1][w]);
+    }
+    int32_t *halo = a.halo + t * kPlanHaloMax;
+    uint16_t *lm = a.lmap + t * K * kPlanTileRows + p;
+    const bool bitmap = hi < lo || (int64_t)hi - lo < (int64_t)kBitmapBits;
+
+    if (bitmap) {
+        // Only words [0, nw) can hold bits.
+        const int nw = hi < lo ? 0 : (int)(((int64_t)hi - lo) >> 5) + 1;
+        for (int i = p; i < nw; i += kTileThreads) s_bits[i] = 0u;
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 32; ++k)
+            if (v[k] >= 0) atomicOr(&s_bits[(v[k] - lo) >> 5], 1u << ((v[k] - lo) & 31));
+        __syncthreads();
+        // Thread p owns `chunk` consecutive words, chunk odd so that the lanes
+        // of a wave (stride chunk words) hit distinct LDS banks; first the
+        // popcounts, then, after the scan, the ranks in word order.
+        int chunk = (nw + kTileThreads - 1) / kTileThreads;
+        chunk |= 1;
+        const int w0 = p * chunk, w1 = min(w0 + chunk, nw);
+        int cnt = 0;
+        for (int w = w0; w < w1; ++w) cnt += __builtin_popcount(s_bits[w]);
+        int U;
+        int run = tile_scan_excl(cnt, s_wave, U);
+        for (int w = w0; w < w1; ++w) {
+            uint32_t bits = s_bits[w];
+            s_pre[w] = (uint16_t)run;
+            while (bits) {
+                if (run < kPlanHaloMax) halo[run] = lo + 32 * w + __builtin_ctz(bits);
+                ++run;
+                bits &= bits - 1u;
+            }
+        }
+        if (p == 0) {
+            a.tile_u[t] = U;
+            if (U > kPlanHaloMax) a.overflow[atomicAdd(&a.hdr->n_overflow, 1)] = (int32_t)t;
+        }
+        if (U > kPlanHaloMax) return;  // handled by the direct-gather kernel
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 32; ++k) {
+            if (k >= K) break;
+            uint16_t out = kPlanAbsent;
+            if (v[k] >= 0) {
+                const int d = v[k] - lo, w = d >> 5;
+                out = (uint16_t)(s_pre[w] + __builtin_popcount(s_bits[w] & ((1u << (d & 31)) - 1u)));
+            }
+            lm[k * kPlanTileRows] = out;
+        }
+        return;
+    }
+
+    // ---- wide neighbour range: LDS hash table of the distinct rows (linear
+    // probing; at most 27 * 256 keys in 8192 slots, so every probe ends).  A
+    // slot is read before it is claimed; each neighbour's slot is kept.
+    for (int i = p; i < kHashSlots; i += kTileThreads) s_key[i] = -1;
+    __syncthreads();
 #pragma unroll
     for (int k = 0; k < 32; ++k) {
         if (v[k] < 0) continue;
@@ -377,35 +658,16 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
         v[k] = (int32_t)h;  // present neighbour: its slot (absent stays -1)
     }
     __syncthreads();
-
-    // Compact the occupied slots (slot order) into s_list as (row << 32 | slot).
     constexpr int kPer = kHashSlots / kTileThreads;
     int cnt = 0;
     for (int i = 0; i < kPer; ++i) cnt += s_key[p * kPer + i] >= 0;
-    int U, id;
-    {
-        const int lane = p & 63, wave = p >> 6;
-        int inc = cnt;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const int y = __shfl_up(inc, off, 64);
-            if (lane >= off) inc += y;
-        }
-        if (lane == 63) s_wave[wave] = inc;
-        __syncthreads();
-        int before = 0;
-        U = 0;
-        for (int w = 0; w < kTileThreads / 64; ++w) {
-            if (w < wave) before += s_wave[w];
-            U += s_wave[w];
-        }
-        id = before + inc - cnt;
-    }
+    int U;
+    int id = tile_scan_excl(cnt, s_wave, U);
     if (p == 0) {
         a.tile_u[t] = U;
         if (U > kPlanHaloMax) a.overflow[atomicAdd(&a.hdr->n_overflow, 1)] = (int32_t)t;
     }
-    if (U > kPlanHaloMax) return;  // handled by the direct-gather kernel
+    if (U > kPlanHaloMax) return;
     for (int i = 0; i < kPer; ++i) {
         const int slot = p * kPer + i;
         const int32_t key = s_key[slot];
@@ -431,15 +693,12 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
             }
             __syncthreads();
         }
-    int32_t *halo = a.halo + t * kPlanHaloMax;
     for (int e = p; e < U; e += kTileThreads) {
         const uint64_t kv = s_list[e];
         halo[e] = (int32_t)(kv >> 32);
         s_key[(uint32_t)kv & (kHashSlots - 1)] = e;
     }
     __syncthreads();
-
-    uint16_t *lm = a.lmap + t * K * kPlanTileRows + p;
 #pragma unroll
     for (int k = 0; k < 32; ++k) {
         if (k >= K) break;
@@ -496,29 +755,44 @@ extern "C" int sc_conv_plan_build(const sc_conv_config *cfg, const int32_t *d_co
     a.overflow = reinterpret_cast<int32_t *>(b + L.overflow);
     a.halo = reinterpret_cast<int32_t *>(b + L.halo);
     a.lmap = reinterpret_cast<uint16_t *>(b + L.lmap);
+    a.grid = reinterpret_cast<uint32_t *>(b + L.grid);
+    a.gsum = reinterpret_cast<int32_t *>(b + L.gsum);
     a.counts = reinterpret_cast<int32_t *>(b + L.counts);
     a.offsets = reinterpret_cast<int32_t *>(b + L.offsets);
     a.bsum = reinterpret_cast<int32_t *>(b + L.bsum);
     a.n_tiles = L.n_tiles;
     a.brick_cap = L.brick_cap;
     a.n_bsum = L.n_bsum;
+    a.grid_cap = L.grid_cap;
 
     hipStream_t s = as_stream(stream);
-    plan_init_kernel<<<grid_for(L.brick_cap, kThreads, 4096), kThreads, 0, s>>>(a);
+    plan_init_kernel<<<grid_for(L.n_tiles * kPlanTileRows, kThreads, 1024), kThreads, 0, s>>>(a);
     SC_LAUNCH_CHECK("plan_init_kernel launch");
     if (n_q == 0) return SC_OK;
-    plan_bbox_kernel<<<grid_for(n_q, kThreads, 1024), kThreads, 0, s>>>(a);
+    const unsigned nbb = grid_for(n_q, kThreads, kBboxBlocks);
+    plan_bbox_kernel<<<nbb, kThreads, 0, s>>>(a);
     SC_LAUNCH_CHECK("plan_bbox_kernel launch");
-    plan_count_kernel<<<grid_for(n_q, kThreads, 8192), kThreads, 0, s>>>(a);
-    SC_LAUNCH_CHECK("plan_count_kernel launch");
-    plan_scan_blocks_kernel<<<(unsigned)L.n_bsum, kThreads, 0, s>>>(a);
-    SC_LAUNCH_CHECK("plan_scan_blocks_kernel launch");
-    plan_scan_top_kernel<<<1, kThreads, 0, s>>>(a);
-    SC_LAUNCH_CHECK("plan_scan_top_kernel launch");
-    plan_scatter_kernel<<<grid_for(n_q, kThreads, 8192), kThreads, 0, s>>>(a);
-    SC_LAUNCH_CHECK("plan_scatter_kernel launch");
-    plan_segsort_kernel<<<grid_for(L.brick_cap, 1, 4096), kThreads, 0, s>>>(a);
-    SC_LAUNCH_CHECK("plan_segsort_kernel launch");
+    plan_bbox_final_kernel<<<1, kThreads, 0, s>>>(a, (int)nbb);
+    SC_LAUNCH_CHECK("plan_bbox_final_kernel launch");
+    // The ordering mode (occupancy grid or counting sort) is chosen on the
+    // device from the bounding box; every launch below covers both.
+    const int64_t grid_blocks = L.grid_cap / kPlanGridBlock;
+    plan_prep_kernel<<<grid_for(L.grid_cap > L.brick_cap ? L.grid_cap : L.brick_cap, kThreads, 8192), kThreads, 0,
+                       s>>>(a);
+    SC_LAUNCH_CHECK("plan_prep_kernel launch");
+    plan_place_kernel<<<grid_for(n_q, kThreads, 8192), kThreads, 0, s>>>(a);
+    SC_LAUNCH_CHECK("plan_place_kernel launch");
+    if (grid_blocks > INT32_MAX) return fail(SC_ERR_OVERFLOW, "conv plan grid overflow");
+    plan_scan1_kernel<<<(unsigned)(grid_blocks > L.n_bsum ? grid_blocks : L.n_bsum), kThreads, 0, s>>>(a);
+    SC_LAUNCH_CHECK("plan_scan1_kernel launch");
+    plan_scan2_kernel<<<1, kThreads, 0, s>>>(a);
+    SC_LAUNCH_CHECK("plan_scan2_kernel launch");
+    const unsigned emit_blocks = grid_for(n_q, kThreads, 8192);
+    plan_emit_kernel<<<(unsigned)grid_blocks > emit_blocks ? (unsigned)grid_blocks : emit_blocks, kThreads, 0, s>>>(
+        a);
+    SC_LAUNCH_CHECK("plan_emit_kernel launch");
+    plan_fix_kernel<<<grid_for(L.brick_cap, kThreads / 64, 2048), kThreads, 0, s>>>(a);
+    SC_LAUNCH_CHECK("plan_fix_kernel launch");
     if (L.n_tiles > INT32_MAX) return fail(SC_ERR_OVERFLOW, "conv plan tile count overflow");
     plan_tiles_kernel<<<(unsigned)L.n_tiles, kTileThreads, 0, s>>>(a);
     SC_LAUNCH_CHECK("plan_tiles_kernel launch");

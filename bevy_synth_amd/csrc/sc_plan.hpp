@@ -12,7 +12,14 @@
 //   halo    [n_tiles][kPlanHaloMax] i32  input row of local index u, increasing
 //   lmap    [n_tiles][K][256] u16  local index of neighbour (p, k), or
 //                                 kPlanAbsent
-//   brick counts / offsets / block sums: scratch of the build's counting sort
+//   grid    [grid_cap] u32        row of each cell of the coords' bounding
+//                                 box, cells in brick-major order (8^3
+//                                 bricks, lexicographic inside a brick)
+//   gsum    [grid_cap / 2048] i32 occupied cells per compaction block
+//   brick counts / offsets / block sums: scratch of the counting-sort
+//                                 fallback (bounding box too large for the
+//                                 grid); counts also hold the rows of
+//                                 duplicated coords in grid mode
 #pragma once
 
 #include <cstddef>
@@ -27,6 +34,8 @@ constexpr int kPlanTileRows = 256;
 constexpr int kPlanHaloMax = 960;
 constexpr uint16_t kPlanAbsent = 0xFFFFu;
 constexpr int kPlanScanBlock = 1024;  // entries per block of the brick-count scan
+constexpr int kPlanGridBlock = 2048;  // grid cells per compaction block
+constexpr int kPlanGridPerRow = 16;   // grid budget: cells per query row
 
 struct alignas(16) PlanHeader {
     int64_t n_q;
@@ -39,7 +48,10 @@ struct alignas(16) PlanHeader {
     int32_t bmax[4];
     uint64_t n_bricks;
     uint32_t status;
-    uint32_t pad[45];
+    int32_t grid_mode;  // 1: occupancy-grid order, 0: counting-sort fallback
+    int32_t n_unique;   // grid mode: occupied cells (distinct coords)
+    int32_t n_extras;   // grid mode: rows of duplicated coords
+    uint32_t pad[42];
 };
 static_assert(sizeof(PlanHeader) == 256, "plan header size");
 
@@ -47,7 +59,8 @@ struct PlanLayout {
     int64_t n_tiles;
     int64_t brick_cap;  // brick-count entries (multiple of kPlanScanBlock)
     int64_t n_bsum;     // scan block sums
-    size_t order, tile_u, overflow, halo, lmap, counts, offsets, bsum, total;
+    int64_t grid_cap;   // grid cells (multiple of kPlanGridBlock)
+    size_t order, tile_u, overflow, halo, lmap, grid, gsum, counts, offsets, bsum, total;
 };
 
 inline size_t plan_align(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -60,6 +73,9 @@ inline PlanLayout plan_layout(int64_t n_q, int64_t K)
     if (cap < 4096) cap = 4096;
     L.brick_cap = (cap + kPlanScanBlock - 1) / kPlanScanBlock * kPlanScanBlock;
     L.n_bsum = L.brick_cap / kPlanScanBlock;
+    int64_t gcap = kPlanGridPerRow * n_q;
+    if (gcap < (1 << 20)) gcap = 1 << 20;
+    L.grid_cap = (gcap + kPlanGridBlock - 1) / kPlanGridBlock * kPlanGridBlock;
     size_t o = plan_align(sizeof(PlanHeader));
     L.order = o;
     o = plan_align(o + (size_t)L.n_tiles * kPlanTileRows * 4);
@@ -71,6 +87,10 @@ inline PlanLayout plan_layout(int64_t n_q, int64_t K)
     o = plan_align(o + (size_t)L.n_tiles * kPlanHaloMax * 4);
     L.lmap = o;
     o = plan_align(o + (size_t)L.n_tiles * (size_t)K * kPlanTileRows * 2);
+    L.grid = o;
+    o = plan_align(o + (size_t)L.grid_cap * 4);
+    L.gsum = o;
+    o = plan_align(o + (size_t)(L.grid_cap / kPlanGridBlock) * 4);
     L.counts = o;
     o = plan_align(o + (size_t)L.brick_cap * 4);
     L.offsets = o;

@@ -197,10 +197,13 @@ def conv_plan_layout(n_q: int, K: int) -> dict:
     nt = (n_q + PLAN_TILE_ROWS - 1) // PLAN_TILE_ROWS
     cap = max(2 * n_q, 4096)
     cap = (cap + 1023) // 1024 * 1024
+    gcap = max(16 * n_q, 1 << 20)
+    gcap = (gcap + 2047) // 2048 * 2048
     L = {"n_tiles": nt}
     o = al(256)
     for name, size in (("order", nt * PLAN_TILE_ROWS * 4), ("tile_u", nt * 4), ("overflow", nt * 4),
                        ("halo", nt * PLAN_HALO_MAX * 4), ("lmap", nt * K * PLAN_TILE_ROWS * 2),
+                       ("grid", gcap * 4), ("gsum", gcap // 2048 * 4),
                        ("counts", cap * 4), ("offsets", cap * 4), ("bsum", cap // 1024 * 4)):
         L[name] = o
         o = al(o + size)
@@ -232,6 +235,7 @@ class ConvPlan:
         n_over = int(hdr[7])
         return {
             "n_tiles": int(hdr[4]), "K": int(hdr[5]), "brick_shift": int(hdr[6]), "n_overflow": n_over,
+            "grid_mode": int(hdr[19]), "n_unique": int(hdr[20]), "n_extras": int(hdr[21]),
             "order": sec("order", nt * PLAN_TILE_ROWS, np.int32).reshape(nt, PLAN_TILE_ROWS),
             "tile_u": sec("tile_u", nt, np.int32),
             "overflow": np.sort(sec("overflow", nt, np.int32)[:n_over]),
