@@ -67,7 +67,7 @@ __global__ void silu_kernel(T *x, int64_t n)
     int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
         const float t = load_as_f32<T>(x, i);
-        store_from_f32<T>(x, i, t / (1.0f + expf(-t)));
+        store_from_f32<T>(x, i, silu_f32(t));
     }
 }
 
@@ -126,7 +126,7 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const Tin *in, int64_t 
         q += j < channels ? d * d : 0.f;
     }
     const float var = wave_sum(q) * inv_c;
-    const float inv_std = 1.0f / sqrtf(var + eps);
+    const float inv_std = rsqrt_f32(var + eps);
     Tout *y = out + row * channels;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
@@ -135,7 +135,7 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const Tin *in, int64_t 
             float t = (v[i] - mean) * inv_std;
             if (w) t *= w[j];
             if (b) t += b[j];
-            if (apply_silu) t = t / (1.0f + expf(-t));
+            if (apply_silu) t = silu_f32(t);
             store_from_f32<Tout>(y, j, t);
         }
     }
@@ -208,7 +208,7 @@ __global__ __launch_bounds__(256) void layer_norm_vec_kernel(const Tin *in, int6
             const float d = v[i][e] - mean;
             q += d * d;
         }
-    const float inv_std = 1.0f / sqrtf(seg_sum<LPR>(q) * inv_c + eps);
+    const float inv_std = rsqrt_f32(seg_sum<LPR>(q) * inv_c + eps);
     if (!live) return;
     Tout *y = out + row * channels;
 #pragma unroll
@@ -220,7 +220,7 @@ __global__ __launch_bounds__(256) void layer_norm_vec_kernel(const Tin *in, int6
             float z = (v[i][e] - mean) * inv_std;
             if (w) z *= w[c0 + e];
             if (b) z += b[c0 + e];
-            if (apply_silu) z = z / (1.0f + expf(-z));
+            if (apply_silu) z = silu_f32(z);
             t[e] = z;
         }
         if constexpr (sizeof(Tout) == 2) {
@@ -267,13 +267,13 @@ __global__ __launch_bounds__(256) void layer_norm_wide_kernel(const Tin *in, int
         float d = load_as_f32<Tin>(x, j) - mean;
         q += d * d;
     }
-    const float inv_std = 1.0f / sqrtf(wave_sum(q) * inv_c + eps);
+    const float inv_std = rsqrt_f32(wave_sum(q) * inv_c + eps);
     Tout *y = out + row * channels;
     for (int j = lane; j < channels; j += 64) {
         float t = (load_as_f32<Tin>(x, j) - mean) * inv_std;
         if (w) t *= w[j];
         if (b) t += b[j];
-        if (apply_silu) t = t / (1.0f + expf(-t));
+        if (apply_silu) t = silu_f32(t);
         store_from_f32<Tout>(y, j, t);
     }
 }

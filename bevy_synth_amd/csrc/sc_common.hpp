@@ -92,6 +92,21 @@ template <> __device__ inline void store_from_f32<uint16_t>(uint16_t *p, int64_t
     p[i] = f32_to_bf16(v);
 }
 
+// ---------------------------------------------------- activations
+// SiLU x * sigmoid(x) = x / (1 + e^-x) on the hardware exponential and
+// reciprocal (v_exp_f32 computes 2^y, so e^-x = 2^(-x log2 e); each is
+// accurate to about 1 ulp, far below the bf16 / f32 tolerances of the path).
+// Large negative x: 2^y overflows to +inf, the reciprocal gives 0 and the
+// result -0; large positive x: 2^y underflows to 0 and the result is x.
+__device__ inline float silu_f32(float x)
+{
+    constexpr float kLog2e = 1.4426950408889634f;
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * kLog2e));
+}
+
+// 1 / sqrt(x) on the hardware reciprocal square root (about 1 ulp).
+__device__ inline float rsqrt_f32(float x) { return __builtin_amdgcn_rsqf(x); }
+
 // ---------------------------------------------------- wave64 reductions
 __device__ inline float wave_sum(float v)
 {

@@ -469,7 +469,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv_mfma_kernel(ConvArgs args)
                     q += o < args.cout_g ? d * d : 0.f;
                 }
             q += __shfl_xor(q, 32, 64);
-            const float inv_std = 1.0f / sqrtf(q * inv_c + args.ln_eps);
+            const float inv_std = rsqrt_f32(q * inv_c + args.ln_eps);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -488,7 +488,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv_mfma_kernel(ConvArgs args)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const float t = acc[i][j][e];
-                    acc[i][j][e] = t / (1.0f + expf(-t));
+                    acc[i][j][e] = silu_f32(t);
                 }
         }
 #pragma unroll
@@ -715,7 +715,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv_mfma16_kernel(ConvArgs args)
                 }
             qv += __shfl_xor(qv, 16, 64);
             qv += __shfl_xor(qv, 32, 64);
-            const float inv_std = 1.0f / sqrtf(qv * inv_c + args.ln_eps);
+            const float inv_std = rsqrt_f32(qv * inv_c + args.ln_eps);
 #pragma unroll
             for (int j = 0; j < 8; ++j)
 #pragma unroll
@@ -734,7 +734,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv_mfma16_kernel(ConvArgs args)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const float t = acc[i][j][e];
-                    acc[i][j][e] = t / (1.0f + expf(-t));
+                    acc[i][j][e] = silu_f32(t);
                 }
         }
 #pragma unroll
@@ -1131,7 +1131,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
                 }
             qv += __shfl_xor(qv, 16, 64);
             qv += __shfl_xor(qv, 32, 64);
-            const float inv_std = 1.0f / sqrtf(qv * inv_c + args.ln_eps);
+            const float inv_std = rsqrt_f32(qv * inv_c + args.ln_eps);
 #pragma unroll
             for (int j = 0; j < 8; ++j)
 #pragma unroll
@@ -1150,7 +1150,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const float t = acc[i][j][e];
-                    acc[i][j][e] = t / (1.0f + expf(-t));
+                    acc[i][j][e] = silu_f32(t);
                 }
         }
 #pragma unroll
@@ -1190,21 +1190,26 @@ __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
 // row per valid (row, offset) pair (~21 per output row at config 3) to ~2.
 //
 // Tile = 256 rows x 128 output channels, 4 waves, two workgroups per CU;
-// wave w owns rows [64w, 64w+64) x all 128 channels as 4 x 8 blocks of
-// v_mfma_f32_16x16x32_bf16 (transposed product: lane l ends with channels
-// 4*(l/16)+e of row l%16 of each block).  Stage = (32-channel chunk c, used
-// offset k), chunk-major.  Per stage a wave reads 4 operand fragments from
-// the LDS halo (each feeds 8 MFMAs) and loads its 8 weight fragments
+// wave w owns rows [128 (w/2), +128) x channels [64 (w%2), +64) as 8 x 4
+// blocks of v_mfma_f32_16x16x32_bf16 (transposed product: lane l ends with
+// channels 4*(l/16)+e of row l%16 of each block).  Stage = (32-channel chunk
+// c, used offset k), chunk-major.  Per stage a wave reads 8 operand fragments
+// from the LDS halo (each feeds 4 MFMAs) and loads its 4 weight fragments
 // w[o, k, 32c..32c+32) from L2 straight into registers one stage ahead (the
-// 4 waves of a workgroup share them through L1), so stages need no barrier:
-// the workgroup synchronises only when the halo moves to the next chunk, and
-// the other workgroup on the CU computes meanwhile.  Absent neighbours read
-// a zero row.  Per-row accumulation order is fixed (chunk-major, offsets
-// ascending).
+// two waves of a column half share them through L1), so stages need no
+// barrier: the workgroup synchronises only when the halo moves to the next
+// chunk, and the other workgroup on the CU computes meanwhile.  The 2 x 2
+// split halves the vector-memory weight traffic of a 1 x 4 row split (the
+// texture path, not the MFMAs, bounds that form) for twice the LDS operand
+// reads.  Absent neighbours read a zero row.  Per-row accumulation order is
+// fixed (chunk-major, offsets ascending).
 //
 // LDS: halo (960 + 1) x 64 B + source offsets 960 x 4 B + lmap 27 x 256 x 2 B
 // = 77 KB.
 constexpr int kHaloK = 27;
+#ifndef SC_HALO_WS
+#define SC_HALO_WS 2
+#endif
 
 __device__ inline int hslot(int j, int p) { return p ^ (((j >> 1) ^ (j >> 2)) & 3); }
 
@@ -1246,17 +1251,23 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
     constexpr int kWLane = kI8 ? 8 : 16;        // weight bytes per lane per fragment
     constexpr int kZeroRow = kPlanHaloMax;
     constexpr int kHaloPerWave = (kPlanHaloMax / 16 + 3) / 4;  // 16-row DMA instructions per wave
-    constexpr int kWS = 2;                      // weight register sets: stages t, t+1
+    static_assert(kHaloPerWave * 64 == kPlanHaloMax, "4 waves x 16 rows tile the halo exactly");
+    constexpr int kWS = SC_HALO_WS;             // weight register sets: stages t .. t+kWS-1
     static_assert(kPlanTileRows == kTileRows, "plan tile = 256 rows");
 
     __shared__ __attribute__((aligned(16))) unsigned char s_halo[(kPlanHaloMax + 1) * CB];
-    __shared__ __attribute__((aligned(16))) uint16_t s_lmap[kHaloK][kPlanTileRows];
+    // s_lmap[k][rh][l16][i]: LDS byte offset of the halo row feeding tile row
+    // 128 rh + 16 i + l16 at offset k, pre-swizzled (j*64 + 16*s(j), so that
+    // XOR with 16 q4 gives the lane's piece); absent -> the zero row.  One
+    // 16-byte read hands a lane its 8 operand rows of a stage.
+    __shared__ __attribute__((aligned(16))) uint16_t s_lmap[kHaloK][2][16][8];
     __shared__ uint32_t s_hoff[kPlanHaloMax];
-    __shared__ uint32_t s_tmask;
+    __shared__ uint32_t s_wmask[kThreads / 64];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, q4 = lane >> 4;
+    const int rh = wave >> 1, ch = wave & 1;  // row half, channel half
     const int K = args.K;
 
     const int tile = tile_for_block(blockIdx.x, gridDim.x);
@@ -1268,33 +1279,33 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
     const int64_t out_col0 = (int64_t)g * args.cout_g;
     const uint32_t row_bytes = (uint32_t)(args.cin * (int64_t)sizeof(uint16_t));
 
-    // ---- prologue: local map, zero row, halo source offsets, offset mask.
+    // ---- prologue: local map (as LDS offsets, thread = tile row), zero
+    //      row, halo source offsets, mask of the offsets the tile uses.
     {
-        const int4 *src = reinterpret_cast<const int4 *>(plan.lmap + (int64_t)tile * K * kPlanTileRows);
-        int4 *dst = reinterpret_cast<int4 *>(&s_lmap[0][0]);
-        const int n16 = K * kPlanTileRows * 2 / 16;
-        for (int i = tid; i < n16; i += kThreads) dst[i] = src[i];
+        const uint16_t *src = plan.lmap + (int64_t)tile * K * kPlanTileRows + tid;
+        uint16_t *dst = &s_lmap[0][tid >> 7][tid & 15][(tid >> 4) & 7];
+        uint32_t m = 0;
+        for (int k = 0; k < K; ++k) {
+            const int j = src[k * kPlanTileRows];
+            m |= (uint32_t)(j != kPlanAbsent) << k;
+            dst[k * kPlanTileRows] =
+                (uint16_t)(j == kPlanAbsent ? kZeroRow * CB : j * CB + 16 * (((j >> 1) ^ (j >> 2)) & 3));
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) m |= __shfl_xor(m, off, 64);
+        if (lane == 0) s_wmask[wave] = m;
         if (tid < CB / 16) reinterpret_cast<uint4 *>(s_halo + kZeroRow * CB)[tid] = make_uint4(0, 0, 0, 0);
-        if (tid == 0) s_tmask = 0u;
         const int32_t *hrows = plan.halo + (int64_t)tile * kPlanHaloMax;
         for (int j = tid; j < U; j += kThreads) s_hoff[j] = (uint32_t)hrows[j] * row_bytes;
     }
     __syncthreads();
-    {
-        uint32_t m = 0;
-        for (int k = 0; k < K; ++k) m |= (uint32_t)(s_lmap[k][tid] != kPlanAbsent) << k;
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) m |= __shfl_xor(m, off, 64);
-        if (lane == 0) atomicOr(&s_tmask, m);
-    }
-    __syncthreads();
-    const uint32_t tmask = __builtin_amdgcn_readfirstlane(s_tmask);
+    const uint32_t tmask = __builtin_amdgcn_readfirstlane(s_wmask[0] | s_wmask[1] | s_wmask[2] | s_wmask[3]);
 
-    f32x4 acc[4][8];
+    f32x4 acc[8][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int e = 0; e < 4; ++e) acc[i][j][e] = 0.f;
 
@@ -1312,7 +1323,8 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
         const uint32_t w_tile_bytes = (uint32_t)K * (uint32_t)nkc * 8u * kFrag;
         const __amdgpu_buffer_rsrc_t w_rsrc =
             make_rsrc(args.wpack, (uint32_t)((int64_t)args.cin / args.cin_g * n_ot) * w_tile_bytes);
-        const uint32_t w_lane = (uint32_t)(g * n_ot + (int)blockIdx.y) * w_tile_bytes + (uint32_t)(lane * kWLane);
+        const uint32_t w_lane = (uint32_t)(g * n_ot + (int)blockIdx.y) * w_tile_bytes +
+                                (uint32_t)(4 * ch) * kFrag + (uint32_t)(lane * kWLane);
         const int n_halo_instr = (U + 15) >> 4;
 
         struct Cursor {
@@ -1332,23 +1344,28 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
             }
             u.k = __builtin_ctz(u.rem);
         };
-        WFrag<kI8> wf[kWS][8];
-        auto load_w = [&](const Cursor &u, WFrag<kI8>(&f)[8]) {
+        WFrag<kI8> wf[kWS][4];
+        auto load_w = [&](const Cursor &u, WFrag<kI8>(&f)[4]) {
             const bool live = u.c < nkc;
             const uint32_t wk = w_lane + (uint32_t)((u.k * nkc + u.c) * 8) * kFrag;
 #pragma unroll
-            for (int jj = 0; jj < 8; ++jj) f[jj].load(w_rsrc, live ? wk + (uint32_t)jj * kFrag : kOobOffset);
+            for (int jj = 0; jj < 4; ++jj) f[jj].load(w_rsrc, live ? wk + (uint32_t)jj * kFrag : kOobOffset);
         };
         // Halo DMA: instruction wave + 4*ii fills halo rows 16*(wave + 4*ii) + lane/4;
         // the lane moves logical piece hslot(j, lane%4) of row j.
         auto load_halo = [&](int c) {
             const uint32_t cb = (uint32_t)(c * CB) + (uint32_t)(hslot(lane >> 2, lane & 3) * 16);
+            // All source offsets first (rows < kPlanHaloMax, in bounds; those
+            // past U are not used), so the LDS reads overlap.
+            uint32_t hv[kHaloPerWave];
+#pragma unroll
+            for (int ii = 0; ii < kHaloPerWave; ++ii) hv[ii] = s_hoff[16 * (wave + 4 * ii) + (lane >> 2)];
 #pragma unroll
             for (int ii = 0; ii < kHaloPerWave; ++ii) {
                 const int instr = wave + 4 * ii;
                 if (instr < n_halo_instr) {
                     const int j = 16 * instr + (lane >> 2);
-                    const uint32_t off = j < U ? s_hoff[j] + cb : kOobOffset;
+                    const uint32_t off = j < U ? hv[ii] + cb : kOobOffset;
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(
                         a_rsrc, (__attribute__((address_space(3))) void *)(s_halo + instr * 1024), 16, off, 0,
                         0, 0);
@@ -1359,19 +1376,21 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
             __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
             __builtin_amdgcn_s_barrier();
         };
-        auto compute = [&](int k, const WFrag<kI8>(&f)[8]) {
-            uint4 x[4];
+        auto read_lm = [&](int k) { return *reinterpret_cast<const uint4 *>(&s_lmap[k][rh][l16][0]); };
+        auto compute = [&](const uint4 &lm, const WFrag<kI8>(&f)[4]) {
+            const uint32_t lw[4] = {lm.x, lm.y, lm.z, lm.w};
+            const uint32_t qx = (uint32_t)q4 << 4;
+            uint4 x[8];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                int j = s_lmap[k][wave * 64 + 16 * i + l16];
-                j = j == kPlanAbsent ? kZeroRow : j;
-                x[i] = *reinterpret_cast<const uint4 *>(s_halo + j * CB + hslot(j, q4) * 16);
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t off = ((i & 1) ? (lw[i >> 1] >> 16) : (lw[i >> 1] & 0xFFFFu)) ^ qx;
+                x[i] = *reinterpret_cast<const uint4 *>(s_halo + off);
             }
 #pragma unroll
-            for (int jj = 0; jj < 8; ++jj) {
+            for (int jj = 0; jj < 4; ++jj) {
                 const uint4 w = f[jj].bf16();
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < 8; ++i)
                     acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                         __builtin_bit_cast(bf16x8, w), __builtin_bit_cast(bf16x8, x[i]), acc[i][jj], 0, 0, 0);
             }
@@ -1380,8 +1399,13 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
         Cursor cur, pre;
         cur_init(cur);
         cur_init(pre);
-        load_w(pre, wf[0]);
-        cur_next(pre);
+        uint4 lm[kWS];
+#pragma unroll
+        for (int s0 = 0; s0 < kWS - 1; ++s0) {
+            load_w(pre, wf[s0]);
+            lm[s0] = read_lm(pre.k);
+            cur_next(pre);
+        }
         load_halo(0);
         wait_vmcnt<0>();
         barrier();
@@ -1401,9 +1425,10 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
                         wait_vmcnt<0>();
                         barrier();
                     }
-                    load_w(pre, wf[(u + 1) % kWS]);
+                    load_w(pre, wf[(u + kWS - 1) % kWS]);
+                    lm[(u + kWS - 1) % kWS] = read_lm(pre.k);
                     cur_next(pre);
-                    compute(cur.k, wf[u]);
+                    compute(lm[u], wf[u]);
                     prev_c = cur.c;
                     cur_next(cur);
                 }
@@ -1413,94 +1438,138 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
         wait_vmcnt<0>();
     }
 
-    // ---- epilogue: lane l holds channels o0 + 16 j + 4 q4 + e of tile row
-    //      64 wave + 16 i + l16; the 4 lanes l16 + 16 m hold the whole row.
+    // ---- epilogue: lane l holds channels oc0 + 16 j + 4 q4 + e of tile row
+    //      128 rh + 16 i + l16; the lanes l16 + 16 m of the two waves of a row
+    //      half hold the whole row.
     TO *__restrict__ out = static_cast<TO *>(args.out);
     const TO *__restrict__ res = static_cast<const TO *>(args.residual);
     const bool vec_ok = args.vec_out != 0;
+    const int oc0 = o0 + 64 * ch;
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const int o = o0 + j * 16 + 4 * q4 + e;
+            const int o = oc0 + j * 16 + 4 * q4 + e;
             const bool ok = o < args.cout_g;
             const float bias = (args.bias && ok) ? args.bias[out_col0 + o] : 0.f;
             const float scale = (kI8 && args.w_scale && ok) ? args.w_scale[out_col0 + o] : 1.f;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < 8; ++i)
                 acc[i][j][e] = ok ? (kI8 ? acc[i][j][e] * scale + bias : acc[i][j][e] + bias) : 0.f;
             __builtin_amdgcn_sched_barrier(0);
         }
     if constexpr (kLN) {
         // Two-pass f32 statistics over the row's Cout channels (the
-        // reference's layer_norm_row_stats, wgpu/ops.rs:162-187).
+        // reference's layer_norm_row_stats, wgpu/ops.rs:162-187).  Each wave
+        // reduces its 64 channels; the two halves meet in LDS (the halo's
+        // first 2 KB, free once every wave has left the main loop) and are
+        // added in a fixed order, so both waves hold the same statistics.
+        float *red = reinterpret_cast<float *>(s_halo);  // [channel half][256 tile rows]
         const float inv_c = 1.0f / (float)args.cout_g;
-        float mean[4], inv_std[4];
+        float mean[8], inv_std[8];
+        __syncthreads();
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 8; ++i) {
             float sum = 0.f;
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
+            for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) sum += acc[i][j][e];
             sum += __shfl_xor(sum, 16, 64);
             sum += __shfl_xor(sum, 32, 64);
-            mean[i] = sum * inv_c;
+            if (q4 == 0) red[ch * kPlanTileRows + rh * 128 + 16 * i + l16] = sum;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = rh * 128 + 16 * i + l16;
+            mean[i] = (red[r] + red[kPlanTileRows + r]) * inv_c;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
             float qv = 0.f;
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
+            for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const int o = o0 + j * 16 + 4 * q4 + e;
+                    const int o = oc0 + j * 16 + 4 * q4 + e;
                     const float d = acc[i][j][e] - mean[i];
                     qv += o < args.cout_g ? d * d : 0.f;
                 }
             qv += __shfl_xor(qv, 16, 64);
             qv += __shfl_xor(qv, 32, 64);
-            inv_std[i] = 1.0f / sqrtf(qv * inv_c + args.ln_eps);
+            if (q4 == 0) red[ch * kPlanTileRows + rh * 128 + 16 * i + l16] = qv;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = rh * 128 + 16 * i + l16;
+            inv_std[i] = rsqrt_f32((red[r] + red[kPlanTileRows + r]) * inv_c + args.ln_eps);
         }
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int o = o0 + j * 16 + 4 * q4 + e;
+                const int o = oc0 + j * 16 + 4 * q4 + e;
                 const bool ok = o < args.cout_g;
                 const float lw = (args.ln_w && ok) ? args.ln_w[o] : 1.f;
                 const float lb = (args.ln_b && ok) ? args.ln_b[o] : 0.f;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) acc[i][j][e] = (acc[i][j][e] - mean[i]) * inv_std[i] * lw + lb;
+                for (int i = 0; i < 8; ++i) acc[i][j][e] = (acc[i][j][e] - mean[i]) * inv_std[i] * lw + lb;
                 __builtin_amdgcn_sched_barrier(0);
             }
     }
+    // Stores: the residual of kRG row blocks (4 for bf16, 2 for f32 outputs)
+    // is fetched before any of them is written, so its latency overlaps
+    // instead of serialising per block.
+    constexpr int kRG = sizeof(TO) == 2 ? 4 : 2;
+    int32_t qrow[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int32_t qrow = plan.order[(int64_t)tile * kPlanTileRows + wave * 64 + 16 * i + l16];
-        if (qrow < 0) continue;
-        const int64_t rowbase = (int64_t)qrow * args.cout + out_col0;
+    for (int i = 0; i < 8; ++i) qrow[i] = plan.order[(int64_t)tile * kPlanTileRows + rh * 128 + 16 * i + l16];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int oc = o0 + j * 16 + 4 * q4;
-            float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
-            if (args.silu) {
+    for (int ih = 0; ih < 8; ih += kRG) {
+        typename Out4<TO>::V rv[kRG][4];
+        if (res && vec_ok) {
 #pragma unroll
-                for (int cc = 0; cc < 4; ++cc) v[cc] = v[cc] / (1.0f + expf(-v[cc]));
-            }
-            if (vec_ok && oc + 3 < args.cout_g) {
-                typename Out4<TO>::V *dst = reinterpret_cast<typename Out4<TO>::V *>(out + rowbase + oc);
-                if (res) {
-                    float rv[4];
-                    Out4<TO>::unpack(*reinterpret_cast<const typename Out4<TO>::V *>(res + rowbase + oc), rv);
+            for (int ii = 0; ii < kRG; ++ii)
 #pragma unroll
-                    for (int cc = 0; cc < 4; ++cc) v[cc] += rv[cc];
+                for (int j = 0; j < 4; ++j) {
+                    const int oc = oc0 + j * 16 + 4 * q4;
+                    if (qrow[ih + ii] >= 0 && oc + 3 < args.cout_g)
+                        rv[ii][j] = *reinterpret_cast<const typename Out4<TO>::V *>(
+                            res + (int64_t)qrow[ih + ii] * args.cout + out_col0 + oc);
                 }
-                *dst = Out4<TO>::pack(v);
-            } else {
+        }
 #pragma unroll
-                for (int cc = 0; cc < 4; ++cc) {
-                    if (oc + cc >= args.cout_g) continue;
-                    float t = v[cc];
-                    if (res) t += load_as_f32<TO>(res, rowbase + oc + cc);
-                    store_from_f32<TO>(out, rowbase + oc + cc, t);
+        for (int ii = 0; ii < kRG; ++ii) {
+            const int i = ih + ii;
+            if (qrow[i] < 0) continue;
+            const int64_t rowbase = (int64_t)qrow[i] * args.cout + out_col0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int oc = oc0 + j * 16 + 4 * q4;
+                float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+                if (args.silu) {
+#pragma unroll
+                    for (int cc = 0; cc < 4; ++cc) v[cc] = silu_f32(v[cc]);
+                }
+                if (vec_ok && oc + 3 < args.cout_g) {
+                    if (res) {
+                        float r4[4];
+                        Out4<TO>::unpack(rv[ii][j], r4);
+#pragma unroll
+                        for (int cc = 0; cc < 4; ++cc) v[cc] += r4[cc];
+                    }
+                    *reinterpret_cast<typename Out4<TO>::V *>(out + rowbase + oc) = Out4<TO>::pack(v);
+                } else {
+#pragma unroll
+                    for (int cc = 0; cc < 4; ++cc) {
+                        if (oc + cc >= args.cout_g) continue;
+                        float t = v[cc];
+                        if (res) t += load_as_f32<TO>(res, rowbase + oc + cc);
+                        store_from_f32<TO>(out, rowbase + oc + cc, t);
+                    }
                 }
             }
         }
