@@ -92,6 +92,25 @@ template <> __device__ inline void store_from_f32<uint16_t>(uint16_t *p, int64_t
     p[i] = f32_to_bf16(v);
 }
 
+// ---------------------------------------------------- buffer loads
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer loads: an offset at or beyond the descriptor's byte count reads as
+// zero, which is how absent neighbours, rows outside the input and channels
+// beyond Cout contribute nothing without a branch.
+constexpr uint32_t kOobOffset = 0xC0000000u;
+
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ inline uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // ---------------------------------------------------- activations
 // SiLU x * sigmoid(x) = x / (1 + e^-x) on the hardware exponential and
 // reciprocal (v_exp_f32 computes 2^y, so e^-x = 2^(-x log2 e); each is

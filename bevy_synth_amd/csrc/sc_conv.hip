@@ -5,25 +5,25 @@
 // (crates/burn_flex_gmm/src/wgpu/sparse_conv_kernels.rs K9-K17: one lane per
 // output value re-reading K*Cin inputs and weights from global memory).
 //
-// Tile = 256 query rows x 128 output channels of one group, 256 threads
-// (4 waves; wave w owns 64 rows x 128 channels = 2x4 MFMA 32x32 blocks).  The
-// reduction runs over (kernel offset k, input-channel chunk of 64 bytes):
-//   A stage: each lane gathers its MFMA A fragments (neighbour rows
-//            map[r, k], 64-byte slices; zero where map = -1) directly into
-//            registers, one stage ahead -- A is private to a wave;
-//   B stage: w[o, k, chunk] for the tile's 128 output channels, read in the
-//            reference layout [Cout][K][Cin_g] (Cin-contiguous = the MFMA B
-//            operand's K-contiguous column), int8 widened to bf16 exactly,
-//            staged through double-buffered LDS (shared by the 4 waves).
-// Offsets that no row of the tile uses are skipped (a per-tile bitmask built
-// from the map block before the main loop).  One barrier per stage;
-// neighbour indices are prefetched one offset ahead.
-// bf16 uses v_mfma_f32_32x32x16_bf16, f32 uses v_mfma_f32_32x32x2_f32; both
-// accumulate in f32.  Epilogue: * scale[o] (int8) + bias[o] (+ residual).
-//
-// A scalar kernel (one lane per output value) covers shapes the tile cannot
-// take (channel counts that are not multiples of the 64-byte chunk, K > 32,
-// unaligned pointers, tensors of 2 GiB or more).
+// Every MFMA kernel here computes a tile of 256 query rows x 128 output
+// channels of one group with 4 waves, reduces over (used kernel offset,
+// input-channel chunk) stages, skips offsets no row of the tile uses, and
+// fuses the epilogue (* int8 scale + bias, optional LayerNorm / SiLU over the
+// row, optional residual).  Kernels, by the path that takes them:
+//   conv_halo_kernel  bf16 activations with a conv plan (sc_plan.hpp) and
+//                     packed weights: the tile's distinct neighbour rows are
+//                     staged in LDS once per 32-channel chunk and every
+//                     operand is read from there (v_mfma_f32_16x16x32_bf16);
+//   conv_v2_kernel    bf16 activations without a plan, and the plan tiles
+//                     whose halo exceeds the LDS budget: neighbour rows
+//                     gathered from global memory per (row, offset), weights
+//                     staged in LDS;
+//   conv_mfma_kernel  f32 activations (v_mfma_f32_32x32x2_f32);
+//   conv_scalar_kernel  shapes no tile takes (channel counts that are not
+//                     multiples of the chunk, K > 32, unaligned pointers,
+//                     tensors of 2 GiB or more): one lane per output value.
+// All accumulate in f32 in a fixed order, so results are bit-identical run to
+// run.
 #include "sc_common.hpp"
 #include "sc_plan.hpp"
 
@@ -112,23 +112,6 @@ __device__ inline int piece_offset(int q, int half)
     return kF32 ? half * (CB / 2) + q * 16 : q * 32 + half * 16;
 }
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-// Buffer loads: an offset at or beyond the descriptor's byte count reads as
-// zero, which is how absent neighbours, rows outside the input and channels
-// beyond Cout contribute nothing without a branch.
-constexpr uint32_t kOobOffset = 0xC0000000u;
-
-__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes)
-{
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
-}
-
-__device__ inline uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off)
-{
-    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
 
 template <bool kF32, int CB>
 __device__ inline APiece<CB / 32> load_a_pieces(__amdgpu_buffer_rsrc_t r, uint32_t row_off, int kc,
@@ -522,252 +505,12 @@ __global__ __launch_bounds__(kThreads, 2) void conv_mfma_kernel(ConvArgs args)
 }
 
 
-// bf16 activations: the same tile and pipeline on v_mfma_f32_16x16x32_bf16.
-// Wave w owns rows [64w, 64w+64) x 128 channels = 4 x 8 blocks of 16x16 (128
-// f32 accumulators per lane).  With 16-row MFMA blocks, the four lanes l,
-// l+16, l+32, l+48 hold one row: each A load instruction reads 16 rows x 64
-// contiguous bytes (the 32x32 layout reads 32 rows x 32 bytes).  Product
-// transposed as in the f32 kernel: lane l ends with channels 4*(l/16)+e of
-// row l%16 of each block.
-template <typename TW, typename TO, int CB>
-__global__ __launch_bounds__(kThreads, 2) void conv_mfma16_kernel(ConvArgs args)
-{
-    typedef uint16_t TA;
-    constexpr int kBK = CB / 2;                 // bf16 elements per stage
-    constexpr int KS = CB / 64;                 // 32-element MFMA k-steps per stage
-    constexpr bool kI8 = sizeof(TW) == 1;
-    constexpr int kRows = kTileRows;
-    constexpr int kStride = CB + 16;            // LDS pitch of one output channel
-    constexpr int kWBytes = kBK * (int)sizeof(TW);
-    constexpr int kWPieces = kWBytes / 16;
-    constexpr int kBPerThread = kBN * kWPieces / kThreads;
-    static_assert(kBPerThread >= 1, "weight pieces per thread");
-
-    __shared__ __attribute__((aligned(16))) unsigned char s_b[2][kBN * kStride];
-    __shared__ uint32_t s_aoff[kMaxTableK][kRows];
-    __shared__ uint32_t s_kmask[kMaxTableK / 32 + 1];
-    __shared__ int16_t s_klist[kMaxTableK];
-    __shared__ int s_nk;
-
-    const TA *input = static_cast<const TA *>(args.input);
-    const TW *weight = static_cast<const TW *>(args.weight);
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int l16 = lane & 15, q4 = lane >> 4;
-    const int K = args.K;
-
-    const int tile = tile_for_block(blockIdx.x, gridDim.x);
-    const int64_t row0 = (int64_t)tile * kRows;
-    const int o0 = blockIdx.y * kBN;
-    const int g = blockIdx.z;
-    const int64_t in_col0 = (int64_t)g * args.cin_g;
-    const int64_t out_col0 = (int64_t)g * args.cout_g;
-    const int nrows = (int)min<int64_t>(kRows, args.n_q - row0);
-    const int32_t *map_tile = args.map + row0 * K;
-    const int64_t n_in = args.n_in;
-    const uint32_t row_bytes = (uint32_t)(args.cin * (int64_t)sizeof(TA));
-
-    const int nk = build_offset_list(map_tile, nrows, K, n_in, s_kmask, s_klist, &s_nk);
-    fill_row_offsets(map_tile, nrows, K, n_in, row_bytes, s_klist, nk, s_aoff);
-
-    const int nkc = args.cin_g / kBK;
-    const int S = nk * nkc;
-
-    f32x4 acc[4][8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[i][j][e] = 0.f;
-
-    if (S > 0) {
-        const __amdgpu_buffer_rsrc_t a_rsrc =
-            make_rsrc(input + in_col0, (uint32_t)(n_in * row_bytes - in_col0 * (int64_t)sizeof(TA)));
-        const __amdgpu_buffer_rsrc_t w_rsrc =
-            make_rsrc(weight, (uint32_t)(args.cout * (int64_t)K * args.cin_g * (int64_t)sizeof(TW)));
-        uint32_t w_base[kBPerThread];
-#pragma unroll
-        for (int i = 0; i < kBPerThread; ++i) {
-            const int idx = tid + kThreads * i;
-            const int ch = idx / kWPieces, pc = idx % kWPieces;
-            w_base[i] = o0 + ch < args.cout_g
-                            ? (uint32_t)((out_col0 + o0 + ch) * (int64_t)K * args.cin_g * (int64_t)sizeof(TW)) + pc * 16
-                            : kOobOffset;
-        }
-        const uint32_t w_k_bytes = (uint32_t)(args.cin_g * (int64_t)sizeof(TW));
-        const int a_piece = q4 * 16;  // byte offset of this lane's 8 elements in a 64-byte k-step
-        uint4 rb[kBPerThread];
-        // Weights run one stage ahead (registers -> double-buffered LDS); the
-        // gathered rows run two stages ahead in a ring of three register sets.
-        auto load_b = [&](int t) {
-            const bool live = t < S;
-            const int tt = live ? t : 0;
-            const int ki = tt / nkc, kc = tt - ki * nkc;
-            const uint32_t wk = (uint32_t)s_klist[ki] * w_k_bytes + (uint32_t)(kc * kWBytes);
-#pragma unroll
-            for (int i = 0; i < kBPerThread; ++i) rb[i] = bload16(w_rsrc, live ? w_base[i] + wk : kOobOffset);
-        };
-        auto load_a = [&](int t, APiece<4 * KS> &f) {
-            const bool live = t < S;
-            const int tt = live ? t : 0;
-            const int ki = tt / nkc, kc = tt - ki * nkc;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t ro = live ? s_aoff[ki][wave * 64 + i * 16 + l16] : kOobOffset;
-#pragma unroll
-                for (int q = 0; q < KS; ++q)
-                    f.p[i * KS + q] = bload16(a_rsrc, ro + (uint32_t)(kc * CB + q * 64 + a_piece));
-            }
-        };
-        auto store_b = [&](int buf) {
-            unsigned char *b = s_b[buf];
-#pragma unroll
-            for (int i = 0; i < kBPerThread; ++i) {
-                const int idx = tid + kThreads * i;
-                const int ch = idx / kWPieces, pc = idx % kWPieces;
-                if constexpr (kI8) {
-                    uint4 w0, w1;
-                    widen_i8x16(rb[i], w0, w1);
-                    *reinterpret_cast<uint4 *>(b + ch * kStride + pc * 32) = w0;
-                    *reinterpret_cast<uint4 *>(b + ch * kStride + pc * 32 + 16) = w1;
-                } else {
-                    *reinterpret_cast<uint4 *>(b + ch * kStride + pc * 16) = rb[i];
-                }
-            }
-        };
-        auto compute = [&](int buf, const APiece<4 * KS> &c) {
-            const unsigned char *b = s_b[buf];
-#pragma unroll
-            for (int q = 0; q < KS; ++q)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const uint4 w = *reinterpret_cast<const uint4 *>(b + (j * 16 + l16) * kStride + q * 64 + a_piece);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            __builtin_bit_cast(bf16x8, w), __builtin_bit_cast(bf16x8, c.p[i * KS + q]), acc[i][j], 0, 0, 0);
-                }
-        };
-        // stage t: weights of t+1 -> registers, rows of t+2 -> set (t+2)%3,
-        // MFMAs of t, weights of t+1 -> LDS, barrier.
-        auto stage = [&](int t, const APiece<4 * KS> &cur, APiece<4 * KS> &ahead2) {
-            load_b(t + 1);
-            load_a(t + 2, ahead2);
-            __builtin_amdgcn_sched_barrier(0);
-            compute(t & 1, cur);
-            store_b((t + 1) & 1);
-            __syncthreads();
-        };
-
-        APiece<4 * KS> x0, x1, x2;
-        load_b(0);
-        load_a(0, x0);
-        load_a(1, x1);
-        store_b(0);
-        __syncthreads();
-        const int S3 = ((S + 2) / 3) * 3;  // padded stages have zero weights
-        for (int t = 0; t < S3; t += 3) {
-            stage(t, x0, x2);
-            stage(t + 1, x1, x0);
-            stage(t + 2, x2, x1);
-        }
-    }
-
-    // ---- epilogue: lane l holds channels j*16 + 4*(l/16) + e (e = 0..3) of row
-    //      i*16 + l%16; lanes l%16 + 16m (m = 0..3) together hold a whole row.
-    TO *__restrict__ out = static_cast<TO *>(args.out);
-    const TO *__restrict__ res = static_cast<const TO *>(args.residual);
-    const bool vec_ok = args.vec_out != 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int r = wave * 64 + i * 16 + l16;
-        if (r >= nrows) continue;  // the 4 lanes of a row skip together
-        const int64_t rowbase = (row0 + r) * args.cout + out_col0;
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int o = o0 + j * 16 + 4 * q4 + e;
-                const bool ok = o < args.cout_g;
-                const float bias = (args.bias && ok) ? args.bias[out_col0 + o] : 0.f;
-                const float scale = (kI8 && args.w_scale && ok) ? args.w_scale[out_col0 + o] : 1.f;
-                acc[i][j][e] = ok ? (kI8 ? acc[i][j][e] * scale + bias : acc[i][j][e] + bias) : 0.f;
-            }
-        if (args.ln) {
-            float sum = 0.f;
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) sum += acc[i][j][e];
-            sum += __shfl_xor(sum, 16, 64);
-            sum += __shfl_xor(sum, 32, 64);
-            const float inv_c = 1.0f / (float)args.cout_g;
-            const float mean = sum * inv_c;
-            float qv = 0.f;
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int o = o0 + j * 16 + 4 * q4 + e;
-                    const float d = acc[i][j][e] - mean;
-                    qv += o < args.cout_g ? d * d : 0.f;
-                }
-            qv += __shfl_xor(qv, 16, 64);
-            qv += __shfl_xor(qv, 32, 64);
-            const float inv_std = rsqrt_f32(qv * inv_c + args.ln_eps);
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int o = o0 + j * 16 + 4 * q4 + e;
-                    const bool ok = o < args.cout_g;
-                    float t = (acc[i][j][e] - mean) * inv_std;
-                    if (args.ln_w && ok) t *= args.ln_w[o];
-                    if (args.ln_b && ok) t += args.ln_b[o];
-                    acc[i][j][e] = t;
-                }
-        }
-        if (args.silu) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float t = acc[i][j][e];
-                    acc[i][j][e] = silu_f32(t);
-                }
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int oc = o0 + j * 16 + 4 * q4;
-            float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
-            if (vec_ok && oc + 3 < args.cout_g) {
-                typename Out4<TO>::V *dst = reinterpret_cast<typename Out4<TO>::V *>(out + rowbase + oc);
-                if (res) {
-                    float rv[4];
-                    Out4<TO>::unpack(*reinterpret_cast<const typename Out4<TO>::V *>(res + rowbase + oc), rv);
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) v[c] += rv[c];
-                }
-                *dst = Out4<TO>::pack(v);
-            } else {
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    if (oc + c >= args.cout_g) continue;
-                    float t = v[c];
-                    if (res) t += load_as_f32<TO>(res, rowbase + oc + c);
-                    store_from_f32<TO>(out, rowbase + oc + c, t);
-                }
-            }
-        }
-    }
-}
-
 // ------------------------------------------------------ bf16 tile, v2
 //
-// Same tile as conv_mfma16_kernel (256 rows x 128 output channels, 4 waves,
-// wave w owns rows [64w, 64w+64) as 4 x 8 blocks of v_mfma_f32_16x16x32_bf16),
-// restructured around what limits the first version on gfx950:
+// 256 rows x 128 output channels, 4 waves; wave w owns rows [64w, 64w+64) as
+// 4 x 8 blocks of v_mfma_f32_16x16x32_bf16 (transposed product: lane l ends
+// with channels 4*(l/16)+e of row l%16 of each block).  The neighbour rows are
+// gathered from global memory per (row, offset):
 //  * a stage is one used offset x CB bytes of the input row (CB = 128: two
 //    MFMA k-steps, half the barriers of 64-byte stages);
 //  * bf16 weights go global -> LDS by buffer_load ... lds (no staging
@@ -777,9 +520,9 @@ __global__ __launch_bounds__(kThreads, 2) void conv_mfma16_kernel(ConvArgs args)
 //  * offsets are walked by scalar bit cursors over the tile's offset mask,
 //    and the gathered-row byte offsets of the next A stage are read from LDS
 //    one stage before the loads that use them;
-//  * optional row permutation (args.perm) and per-16-row-block skipping of
-//    MFMAs for offsets no row of the block uses (BSKIP): with rows grouped by
-//    neighbour mask, this removes most MFMA work on absent neighbours.
+//  * optional row permutation (args.perm, a plan's row order) and tile list
+//    (args.tile_list: the plan tiles whose halo overflowed the halo kernel's
+//    LDS budget).
 // The stage loop keeps a static number of vector loads per stage, so the
 // explicit vmcnt waits below are exact: W(t) and A(t) have landed when
 // stage t starts.
@@ -823,7 +566,7 @@ struct StageCursor {
     __device__ inline bool live() const { return rem != 0u; }
 };
 
-template <typename TW, typename TO, int CB, int DIST, bool PERM, bool BSKIP>
+template <typename TW, typename TO, int CB, int DIST, bool PERM>
 __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
 {
     typedef uint16_t TA;
@@ -1007,10 +750,6 @@ __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
         auto compute = [&](const StageCursor &c, int buf, const uint4 (&f)[4][KS]) {
             if (!c.live()) return;
             const unsigned char *b = wbuf(buf);
-            uint32_t use = 0xFu;
-            if constexpr (BSKIP)
-                use = ((bm0 >> c.k) & 1u) | (((bm1 >> c.k) & 1u) << 1) | (((bm2 >> c.k) & 1u) << 2) |
-                      (((bm3 >> c.k) & 1u) << 3);
 #pragma unroll
             for (int q = 0; q < KS; ++q) {
                 uint4 w[8];
@@ -1021,7 +760,6 @@ __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
                 }
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    if (BSKIP && !((use >> i) & 1u)) continue;
 #pragma unroll
                     for (int j = 0; j < 8; ++j)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
@@ -1247,7 +985,6 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
 {
     constexpr int CB = 64;  // bytes of an input row per chunk (32 bf16 = one MFMA k-step)
     constexpr bool kI8 = sizeof(TW) == 1;
-    constexpr int kWChunk = kI8 ? 32 : 64;      // weight bytes per channel per chunk
     constexpr int kWLane = kI8 ? 8 : 16;        // weight bytes per lane per fragment
     constexpr int kZeroRow = kPlanHaloMax;
     constexpr int kHaloPerWave = (kPlanHaloMax / 16 + 3) / 4;  // 16-row DMA instructions per wave
@@ -1662,9 +1399,9 @@ template <typename TW, typename TO, bool PERM>
 void launch_v2(const ConvArgs &a, dim3 grid, hipStream_t s)
 {
     if (sizeof(TW) == 2 && a.cin_g % 64 == 0)
-        conv_v2_kernel<TW, TO, 128, 1, PERM, false><<<grid, kThreads, 0, s>>>(a);
+        conv_v2_kernel<TW, TO, 128, 1, PERM><<<grid, kThreads, 0, s>>>(a);
     else
-        conv_v2_kernel<TW, TO, 64, 2, PERM, false><<<grid, kThreads, 0, s>>>(a);
+        conv_v2_kernel<TW, TO, 64, 2, PERM><<<grid, kThreads, 0, s>>>(a);
 }
 
 template <typename TA, typename TW, typename TO>

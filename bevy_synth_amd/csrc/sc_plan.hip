@@ -5,27 +5,36 @@
 // global memory for every (row, offset) pair: at config 3 each input row is
 // gathered ~21 times by the direct kernel, but a tile of spatially compact
 // rows touches only ~2 distinct input rows per output row.  The plan holds
-// what that kernel needs and is built once per neighbour map:
+// what that kernel needs and is built once per neighbour map.
 //
-//   1. init    : header, brick counts := 0, padding rows of `order` := -1
-//   2. bbox    : min/max of the query coords (wave64 + one atomic per block)
-//   3. count   : brick edge 2^s (smallest s >= 3 with at most brick_cap bricks
-//                in the bbox), per-brick row counts (atomics)
-//   4. scan    : exclusive scan of the counts (per 1024-entry block, then the
-//                block totals by one block)
-//   5. scatter : order[off[brick] + rank] = row  -> rows grouped by brick,
-//                bricks in (batch, x, y, z) order (ranks from wave-aggregated
-//                atomics: one atomic per distinct brick in a wave)
-//   6. segsort : each brick's rows sorted by row index (one workgroup per
-//                brick, rank = number of smaller rows), so the order is
-//                deterministic and, for lexicographically sorted coords,
-//                lexicographic within a brick
-//   7. tiles   : one workgroup per 256-row tile: the distinct neighbour rows
-//                through an LDS hash table, then sorted, numbered in
-//                increasing row order -> halo[] and the u16 local map
-//                lmap[k][row].  Rows stay in brick order within a tile, so
-//                the neighbours of 16 consecutive tile rows at one offset are
-//                mostly consecutive halo entries (distinct LDS banks).
+// Row order (tiles of 256 consecutive entries of `order`):
+//   1. init    : header, padding entries of `order` := -1
+//   2. bbox    : min/max of the query coords (per-block partials, then one
+//                block reduces them; no atomics)
+//   3. prep    : grid mode when the bounding box, cut into 8^3 bricks, has
+//                at most grid_cap cells: the occupancy grid := EMPTY
+//   4. place   : each row atomicMin's its row index into its cell (cells in
+//                brick-major order, lexicographic inside a brick); the row
+//                displaced from a cell (a duplicated coord) goes to a list
+//   5. scan1/2 : occupied cells per 2048-cell block, then one block scans
+//                the block totals
+//   6. emit    : the occupied cells' rows compacted in cell order -> order
+//   7. fix     : rows of duplicated coords appended after the distinct ones
+// The order is a pure function of the coords (no sort, no atomics whose
+// interleaving shows): bricks in (batch, x, y, z) order, lexicographic inside
+// a brick.  A bounding box too large for the grid falls back to a counting
+// sort by brick (brick edge 2^s, the smallest s >= 3 with at most brick_cap
+// bricks): count, scan, scatter with wave-aggregated atomics, then each
+// brick's segment sorted by row index so that the order is deterministic.
+//
+// Halo tables:
+//   8. tiles   : one workgroup per tile, one thread per tile row; the
+//                distinct neighbour rows are numbered in increasing row
+//                order -> halo[] and the u16 local map lmap[k][row], through
+//                an LDS bitmap over the tile's neighbour row range (the usual
+//                case) or, for a wide range, an LDS hash table and a bitonic
+//                sort.  Tiles whose halo exceeds kPlanHaloMax are listed in
+//                `overflow` for the direct kernel.
 #include <climits>
 
 #include "sc_common.hpp"
@@ -38,7 +47,6 @@ constexpr int kThreads = 256;
 constexpr int kTileThreads = kPlanTileRows;  // plan_tiles_kernel: one thread per tile row
 constexpr int kHashBits = 13;
 constexpr int kHashSlots = 1 << kHashBits;  // > 27 * 256 distinct neighbours of a tile
-constexpr int kSegLds = 2048;                // brick segments sorted in LDS up to this size
 
 struct PlanArgs {
     const int4 *coords;
@@ -566,18 +574,48 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
     const int64_t n_in = a.n_in;
     const int32_t q = a.order[t * kPlanTileRows + p];
 
+    // The thread's map row (K dwords at dword K*q, rows in brick order, so
+    // scattered across lanes): 16-byte loads from the aligned-down address,
+    // then a shift by the row's dword offset within 16 bytes (s).  Maps of 3
+    // GiB or more take one 4-byte load per entry.
     int32_t v[32];
+    const int64_t map_bytes = a.n_q * (int64_t)K * 4;
+    if (map_bytes + 256 <= (int64_t)kOobOffset) {
+        const __amdgpu_buffer_rsrc_t r = make_rsrc(a.map, (uint32_t)map_bytes);
+        const int64_t d0 = q >= 0 ? (int64_t)q * K : 0;
+        const int s = (int)(d0 & 3);
+        const uint32_t base = q >= 0 ? (uint32_t)((d0 & ~(int64_t)3) * 4) : kOobOffset;
+        const int nl = (K + 6) >> 2;  // loads covering s + K dwords for every s
+        uint32_t w[36];
+#pragma unroll
+        for (int i = 0; i < 9; ++i) {
+            uint4 x = make_uint4(0u, 0u, 0u, 0u);
+            if (i < nl) x = bload16(r, base + 16u * i);
+            w[4 * i] = x.x;
+            w[4 * i + 1] = x.y;
+            w[4 * i + 2] = x.z;
+            w[4 * i + 3] = x.w;
+        }
+#pragma unroll
+        for (int k = 0; k < 32; ++k) {
+            const int32_t x = (int32_t)(s == 0 ? w[k] : s == 1 ? w[k + 1] : s == 2 ? w[k + 2] : w[k + 3]);
+            v[k] = (k < K && q >= 0 && x >= 0 && x < n_in) ? x : -1;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 32; ++k) {
+            int32_t x = -1;
+            if (k < K && q >= 0) x = a.map[(int64_t)q * K + k];
+            v[k] = (x >= 0 && x < n_in) ? x : -1;
+        }
+    }
     int lo = INT_MAX, hi = INT_MIN;
 #pragma unroll
-    for (int k = 0; k < 32; ++k) {
-        int32_t x = -1;
-        if (k < K && q >= 0) x = a.map[(int64_t)q * K + k];
-        v[k] = (x >= 0 && x < n_in) ? x : -1;
+    for (int k = 0; k < 32; ++k)
         if (v[k] >= 0) {
             lo = min(lo, v[k]);
             hi = max(hi, v[k]);
         }
-    }
     lo = wave_min_i32(lo);
     hi = wave_max_i32(hi);
     if (lane == 0) {

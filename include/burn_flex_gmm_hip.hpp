@@ -234,10 +234,75 @@ inline Result<DeviceTensor> neighbor_rows_tensor_from_coords_tensor(const Sparse
     return out;
 }
 
+// Conv plan: row order and per-tile halo tables of one neighbour map.  No
+// counterpart in the reference's API; it plays the role of its neighbour
+// cache (wgpu.rs:349-382): build it once per map and pass it to every conv on
+// that map (ConvOptions::plan).
+struct ConvPlan {
+    DeviceTensor buf;
+    size_t n_in = 0, n_q = 0, kernel_rows = 0;
+};
+
+inline Result<ConvPlan> build_conv_plan(const SparseSubmConvConfig &config, const DeviceTensor &coords,
+                                        const DeviceTensor &neighbor_rows, hipStream_t stream = nullptr)
+{
+    using R = Result<ConvPlan>;
+    if (coords.dtype() != DType::I32 || coords.dims().size() != 2 || coords.dims()[1] != 4)
+        return R::err("conv plan coords must be an i32 [N, 4] tensor");
+    auto k = kernel_rows(config);
+    if (k.is_err()) return R::err(k.error());
+    if (neighbor_rows.dtype() != DType::I32 || neighbor_rows.dims().size() != 2 ||
+        neighbor_rows.dims()[1] != k.value())
+        return R::err("conv plan neighbor_rows must be an i32 [N_q, K] tensor");
+    ConvPlan plan;
+    plan.n_in = coords.dims()[0];
+    plan.n_q = neighbor_rows.dims()[0];
+    plan.kernel_rows = k.value();
+    size_t bytes = 0;
+    int rc = sc_conv_plan_size((int64_t)plan.n_q, (int64_t)plan.kernel_rows, &bytes);
+    if (rc != SC_OK) return R::err(detail::status_message(rc));
+    auto buf = DeviceTensor::empty({bytes}, DType::U8);
+    if (buf.is_err()) return R::err(buf.error());
+    plan.buf = buf.take();
+    const sc_conv_config c = config.to_c();
+    rc = sc_conv_plan_build(&c, (const int32_t *)coords.data(), (int64_t)plan.n_in,
+                            (const int32_t *)neighbor_rows.data(), (int64_t)plan.n_q, plan.buf.data(), bytes,
+                            stream);
+    if (rc != SC_OK) return R::err(detail::status_message(rc));
+    return R::ok(std::move(plan));
+}
+
+// Weights packed for the planned conv.  No device counterpart in the
+// reference; the role of pack_flex_weight (lib.rs:377-426): once per layer.
+// weight [Cout, KD, KH, KW, Cin_g] bf16 | i8 -> packed bytes.
+inline Result<DeviceTensor> pack_conv_weight(const SparseSubmConvConfig &config, const DeviceTensor &weight,
+                                             hipStream_t stream = nullptr)
+{
+    using R = Result<DeviceTensor>;
+    size_t bytes = 0;
+    const sc_conv_config c = config.to_c();
+    int rc = sc_conv_weight_pack_size(&c, to_sc_dtype(weight.dtype()), &bytes);
+    if (rc != SC_OK) return R::err(detail::status_message(rc));
+    auto out = DeviceTensor::empty({bytes}, DType::U8);
+    if (out.is_err()) return out;
+    rc = sc_conv_weight_pack(&c, to_sc_dtype(weight.dtype()), weight.data(), out.value().data(), stream);
+    if (rc != SC_OK) return R::err(detail::status_message(rc));
+    return out;
+}
+
 struct ConvOptions {
     std::optional<DType> out_dtype;         // default: the input dtype
     const DeviceTensor *w_scale = nullptr;  // [Cout] f32, int8 weights only
     const DeviceTensor *residual = nullptr; // [N_q, Cout] in the output dtype
+    // Block epilogue (the decoder's conv -> LayerNorm -> SiLU, + residual):
+    bool layer_norm = false;
+    const DeviceTensor *ln_weight = nullptr;  // [Cout] f32 or none
+    const DeviceTensor *ln_bias = nullptr;    // [Cout] f32 or none
+    float ln_eps = 1e-6f;
+    bool silu = false;
+    // Fast path: a plan of this map and the packed weights (both or neither).
+    const ConvPlan *plan = nullptr;
+    const DeviceTensor *packed_weight = nullptr;
 };
 
 // sparse_subm_conv_forward_wgpu, wgpu/sparse_conv.rs:310-367 (same shape rules,
@@ -276,12 +341,31 @@ inline Result<DeviceTensor> sparse_subm_conv_forward_hip(const SparseSubmConvCon
     const size_t n_q = neighbor_rows.dims()[0];
     auto out = DeviceTensor::empty({n_q, config.out_channels}, od);
     if (out.is_err()) return out;
+    if ((opt.plan == nullptr) != (opt.packed_weight == nullptr))
+        return R::err("sparse conv: a plan and packed weights go together");
+    if (opt.plan && (opt.plan->n_q != n_q || opt.plan->n_in != input.dims()[0] ||
+                     opt.plan->kernel_rows != k.value()))
+        return R::err("sparse conv: the plan was built for another neighbour map");
     const sc_conv_config c = config.to_c();
-    const int rc = sc_subm_conv_forward(
-        &c, to_sc_dtype(input.dtype()), input.data(), (int64_t)input.dims()[0],
-        (const int32_t *)neighbor_rows.data(), (int64_t)n_q, to_sc_dtype(weight.dtype()), weight.data(),
-        opt.w_scale ? (const float *)opt.w_scale->data() : nullptr, (const float *)bias.data(),
-        opt.residual ? opt.residual->data() : nullptr, to_sc_dtype(od), out.value().data(), stream);
+    sc_conv_epilogue epi{};
+    epi.residual = opt.residual ? opt.residual->data() : nullptr;
+    epi.layer_norm = opt.layer_norm ? 1 : 0;
+    epi.ln_weight = opt.ln_weight ? (const float *)opt.ln_weight->data() : nullptr;
+    epi.ln_bias = opt.ln_bias ? (const float *)opt.ln_bias->data() : nullptr;
+    epi.ln_eps = opt.ln_eps;
+    epi.silu = opt.silu ? 1 : 0;
+    const float *scale = opt.w_scale ? (const float *)opt.w_scale->data() : nullptr;
+    const int rc =
+        opt.plan ? sc_subm_conv_forward_planned(
+                       &c, to_sc_dtype(input.dtype()), input.data(), (int64_t)input.dims()[0],
+                       (const int32_t *)neighbor_rows.data(), (int64_t)n_q, to_sc_dtype(weight.dtype()),
+                       weight.data(), opt.packed_weight->data(), scale, (const float *)bias.data(), &epi,
+                       to_sc_dtype(od), out.value().data(), opt.plan->buf.data(), stream)
+                 : sc_subm_conv_forward_fused(&c, to_sc_dtype(input.dtype()), input.data(),
+                                              (int64_t)input.dims()[0], (const int32_t *)neighbor_rows.data(),
+                                              (int64_t)n_q, to_sc_dtype(weight.dtype()), weight.data(), scale,
+                                              (const float *)bias.data(), &epi, to_sc_dtype(od),
+                                              out.value().data(), stream);
     if (rc != SC_OK) return R::err(detail::status_message(rc));
     return out;
 }

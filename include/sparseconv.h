@@ -191,10 +191,14 @@ int sc_subm_conv_forward_fused(const sc_conv_config *cfg, int act_dtype, const v
  * build it once per map, right after sc_neighbor_map_build, and pass it to
  * every sc_subm_conv_forward_planned call on that map.
  *
- * Rows are grouped by 8^3 bricks (coarser if the coords' bounding box has
- * more than 2*n_q bricks) into tiles of 256 rows, sorted by neighbour mask
- * within a tile; for each tile the plan lists the distinct input rows its
- * neighbours touch and a 16-bit local index per (row, offset).
+ * Rows are ordered by 8^3 bricks of the coords' bounding box (bricks in
+ * (batch, x, y, z) order, lexicographic inside a brick; coarser bricks when
+ * the box is too large for the plan's occupancy grid) and cut into tiles of
+ * 256 rows; for each tile the plan lists the distinct input rows its
+ * neighbours touch (at most 960, else the tile is listed for the direct
+ * kernel) and a 16-bit local index per (row, offset).  The row order and
+ * the tables are a pure function of the coords and the map: a rebuild gives
+ * the same plan.
  *
  * sc_conv_plan_size: bytes of the plan buffer for n_q query rows and a kernel
  * of kernel_rows offsets (1..32).

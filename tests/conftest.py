@@ -14,6 +14,14 @@ def pytest_configure(config):
 
 
 @pytest.fixture(scope="session")
+def kats():
+    """Known-answer vectors of the reference's tests (tests/golden/reference_kats.json)."""
+    import json
+    with open(os.path.join(ROOT, "tests", "golden", "reference_kats.json")) as f:
+        return json.load(f)
+
+
+@pytest.fixture(scope="session")
 def oracle():
     from oracle import oracle as O
     O.build()

@@ -140,6 +140,45 @@ int main()
                 max_err = std::max(max_err, std::fabs(o[i] - ref[i]) / std::max(std::fabs(ref[i]), rms));
             CHECK(max_err <= 1e-4, "bf16 conv rel err %g", max_err);
             std::printf("device conv rel err %.3g\n", max_err);
+
+            // the planned conv (plan + packed weights) against the same loop,
+            // then with the LayerNorm + SiLU epilogue against the unplanned one
+            auto plan = build_conv_plan(c, dc.value(), map.value());
+            CHECK(plan.is_ok(), "%s", plan.error().c_str());
+            auto wp = pack_conv_weight(c, dw.value());
+            CHECK(wp.is_ok(), "%s", wp.error().c_str());
+            if (plan.is_ok() && wp.is_ok()) {
+                ConvOptions po = opt;
+                po.plan = &plan.value();
+                po.packed_weight = &wp.value();
+                auto pout = sparse_subm_conv_forward_hip(c, dx.value(), map.value(), dw.value(), dbias.value(), po);
+                CHECK(pout.is_ok(), "%s", pout.error().c_str());
+                if (pout.is_ok()) {
+                    auto p = pout.value().to_vec<float>().take();
+                    double perr = 0;
+                    for (size_t i = 0; i < ref.size(); ++i)
+                        perr = std::max(perr, std::fabs(p[i] - ref[i]) / std::max(std::fabs(ref[i]), rms));
+                    CHECK(perr <= 1e-4, "planned conv rel err %g", perr);
+                    std::printf("planned conv rel err %.3g\n", perr);
+                }
+                ConvOptions lo = opt, plo = po;
+                lo.layer_norm = plo.layer_norm = true;
+                lo.silu = plo.silu = true;
+                auto a = sparse_subm_conv_forward_hip(c, dx.value(), map.value(), dw.value(), dbias.value(), lo);
+                auto b2 = sparse_subm_conv_forward_hip(c, dx.value(), map.value(), dw.value(), dbias.value(), plo);
+                CHECK(a.is_ok() && b2.is_ok(), "fused convs");
+                if (a.is_ok() && b2.is_ok()) {
+                    auto av = a.value().to_vec<float>().take(), bv = b2.value().to_vec<float>().take();
+                    double d = 0;
+                    for (size_t i = 0; i < av.size(); ++i) d = std::max(d, (double)std::fabs(av[i] - bv[i]));
+                    CHECK(d <= 1e-4, "planned LN+SiLU vs unplanned: max abs diff %g", d);
+                    std::printf("planned LN+SiLU max diff %.3g\n", d);
+                }
+                ConvOptions bad = po;
+                bad.packed_weight = nullptr;
+                auto e = sparse_subm_conv_forward_hip(c, dx.value(), map.value(), dw.value(), dbias.value(), bad);
+                CHECK(e.is_err() && e.error().find("go together") != std::string::npos, "plan without packed weights");
+            }
         }
     }
     if (failures) {

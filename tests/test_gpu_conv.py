@@ -40,13 +40,13 @@ def run_f32(cfg, coords, x, w, b, **kw):
     return out.cpu().numpy(), nbr.cpu().numpy()
 
 
-def test_kat_conv_uses_neighbor_voxels():
+def test_kat_conv_uses_neighbor_voxels(kats):
     """sparse_decoder_tests.rs:190-236 -> [201, 12]."""
-    cfg = F.SparseSubmConvConfig(1, 1, 3, 1, 1)
-    out, _ = run_f32(cfg, np.array([[0, 0, 0, 0], [0, 1, 0, 0]], np.int32),
-                     np.array([[1.0], [2.0]], np.float32), np.array([10.0, 1.0, 100.0], np.float32),
-                     np.zeros(1, np.float32))
-    assert abs(out[0, 0] - 201.0) < 1e-5 and abs(out[1, 0] - 12.0) < 1e-5
+    g = kats["conv_uses_neighbor_voxels"]
+    cfg = F.SparseSubmConvConfig(1, 1, *g["config"]["kernel"])
+    out, _ = run_f32(cfg, np.array(g["coords"], np.int32), np.array(g["input"], np.float32),
+                     np.array(g["weight"], np.float32), np.array(g["bias"], np.float32))
+    assert np.abs(out - np.array(g["expected_output"], np.float32)).max() < g["tolerance"]
 
 
 @pytest.mark.parametrize("cin,cout,dims,groups,n,seed", [

@@ -33,13 +33,14 @@ def line_coords(n):
     return c
 
 
-def test_kat_query_chunks(oracle):
+def test_kat_query_chunks(oracle, kats):
     """sparse_decoder_tests.rs:239-292."""
-    cfg = F.SparseSubmConvConfig(1, 1, 3, 1, 1)
-    coords = np.array([[0, 0, 0, 0], [0, 1, 0, 0]], np.int32)
-    assert gpu_map(cfg, coords).reshape(-1).tolist() == [-1, 0, 1, 0, 1, -1]
-    assert gpu_map(cfg, coords[:1]).reshape(-1).tolist() == [-1, 0, -1]
-    assert gpu_map(cfg, coords, query_rows=1).reshape(-1).tolist() == [-1, 0, 1]
+    g = kats["query_chunks_keep_global_neighbors"]
+    cfg = F.SparseSubmConvConfig(1, 1, *g["config"]["kernel"])
+    coords = np.array(g["coords"], np.int32)
+    assert gpu_map(cfg, coords).tolist() == g["expected_full_map"]
+    assert gpu_map(cfg, coords[:1]).tolist() == g["expected_chunk_map_first_row_only"]
+    assert gpu_map(cfg, coords, query_rows=1).tolist() == g["expected_query_rows_1_map"]
 
 
 @pytest.mark.parametrize("dims,n", [((3, 3, 1), 192), ((9, 9, 9), 256), ((9, 9, 9), 512),

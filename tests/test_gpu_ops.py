@@ -61,15 +61,17 @@ def test_add():
     assert np.array_equal(F.add(dev(a), dev(b)).cpu().numpy(), a + b)
 
 
-def test_subdivision_kat_child_expand():
+def test_subdivision_kat_child_expand(kats):
     """sparse_decoder_tests.rs:37-124: mask with (0,0),(0,3),(1,7) set."""
-    parents = np.array([[0, 0, 0, 0], [0, 1, 0, 0]], np.int32)
-    mask = np.zeros((2, 8), np.uint8)
-    mask[0, 0] = mask[0, 3] = mask[1, 7] = 1
+    g = kats["subdivision_child_expand"]
+    parents = np.array(g["parent_coords"], np.int32)
+    mask = np.zeros((len(parents), 8), np.uint8)
+    for p_, c_ in g["active_pairs"]:
+        mask[p_, c_] = 1
     cc, li, pairs = F.subdivision_build(dev(parents), mask=dev(mask))
-    assert cc.cpu().numpy().reshape(-1).tolist() == [0, 0, 0, 0, 0, 1, 1, 0, 0, 3, 1, 1]
-    assert li.cpu().numpy().tolist() == [0, 3, 15]
-    assert pairs.cpu().numpy().reshape(-1).tolist() == [0, 0, 0, 3, 1, 7]
+    assert cc.cpu().numpy().tolist() == g["expected_child_coords"]
+    assert li.cpu().numpy().tolist() == g["expected_linear_idx"]
+    assert pairs.cpu().numpy().tolist() == g["active_pairs"]
 
 
 @pytest.mark.parametrize("P", [1, 5, 1023, 1024, 1025, 70000])

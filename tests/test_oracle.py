@@ -26,45 +26,49 @@ def checkerboard(nx, ny, nz):
 
 # --------------------------------------------------------------- KATs
 
-def test_kat_conv_uses_neighbor_voxels(oracle):
+def test_kat_conv_uses_neighbor_voxels(oracle, kats):
     """sparse_decoder_tests.rs:190-236: x=0,1; in [1,2]; w [10,1,100] (3x1x1) -> [201, 12]."""
-    cfg = oracle.OracleConfig(1, 1, 3, 1, 1)
-    coords = [[0, 0, 0, 0], [0, 1, 0, 0]]
-    w = np.array([10.0, 1.0, 100.0], np.float32)
-    b = np.zeros(1, np.float32)
-    x = np.array([[1.0], [2.0]], np.float32)
-    for out in (oracle.conv_flex(cfg, w, b, coords, x), oracle.conv_legacy(cfg, w, b, coords, x)):
-        assert abs(out[0, 0] - 201.0) < 1e-5 and abs(out[1, 0] - 12.0) < 1e-5
+    g = kats["conv_uses_neighbor_voxels"]
+    cfg = oracle.OracleConfig(1, 1, *g["config"]["kernel"])
+    x = np.array(g["input"], np.float32)
+    w = np.array(g["weight"], np.float32)
+    b = np.array(g["bias"], np.float32)
+    want = np.array(g["expected_output"], np.float32)
+    for out in (oracle.conv_flex(cfg, w, b, g["coords"], x), oracle.conv_legacy(cfg, w, b, g["coords"], x)):
+        assert np.abs(out - want).max() < g["tolerance"]
 
 
-def test_kat_query_chunks_keep_global_neighbors(oracle):
+def test_kat_query_chunks_keep_global_neighbors(oracle, kats):
     """sparse_decoder_tests.rs:239-292: full map [-1,0,1]; chunk rebuild [-1,0,-1];
     the query-row conv on the full input equals the full conv's row 0."""
-    cfg = oracle.OracleConfig(1, 1, 3, 1, 1)
-    coords = np.array([[0, 0, 0, 0], [0, 1, 0, 0]], np.uint32)
+    g = kats["query_chunks_keep_global_neighbors"]
+    cfg = oracle.OracleConfig(1, 1, *g["config"]["kernel"])
+    coords = np.array(g["coords"], np.uint32)
     full = oracle.build_neighbor_rows(cfg, coords)
     chunk = oracle.build_neighbor_rows(cfg, coords[:1])
-    assert full.reshape(-1).tolist() == [-1, 0, 1, 0, 1, -1]
-    assert chunk.reshape(-1).tolist() == [-1, 0, -1]
+    assert full.tolist() == g["expected_full_map"]
+    assert chunk.tolist() == g["expected_chunk_map_first_row_only"]
     q = oracle.build_neighbor_rows(cfg, coords, query_rows=1)
-    assert q.reshape(-1).tolist() == [-1, 0, 1]
-    w = np.array([10.0, 1.0, 100.0], np.float32)
-    b = np.zeros(1, np.float32)
-    x = np.array([[1.0], [2.0]], np.float32)
+    assert q.tolist() == g["expected_query_rows_1_map"]
+    c = kats["conv_uses_neighbor_voxels"]
+    w = np.array(c["weight"], np.float32)
+    b = np.array(c["bias"], np.float32)
+    x = np.array(c["input"], np.float32)
     fo = oracle.conv_flex_precomputed(cfg, w, b, x, full)
     qo = oracle.conv_flex_precomputed(cfg, w, b, x, full[:1])
     assert np.array_equal(qo, fo[:1])
 
 
-def test_kat_subdivision_child_expand(oracle):
+def test_kat_subdivision_child_expand(oracle, kats):
     """decoder_guide_subdivision_tensor_handoff_parity, sparse_decoder_tests.rs:37-124:
     parents (0,0,0),(1,0,0); active (0,0),(0,3),(1,7) -> child coords
     [0,0,0,0],[0,1,1,0],[0,3,1,1], linear idx [0,3,15]."""
-    parents = np.array([[0, 0, 0, 0], [0, 1, 0, 0]], np.uint32)
-    pairs = np.array([[0, 0], [0, 3], [1, 7]], np.int32)
+    g = kats["subdivision_child_expand"]
+    parents = np.array(g["parent_coords"], np.uint32)
+    pairs = np.array(g["active_pairs"], np.int32)
     cc, li = oracle.subdivide_expand(parents, pairs)
-    assert cc.reshape(-1).tolist() == [0, 0, 0, 0, 0, 1, 1, 0, 0, 3, 1, 1]
-    assert li.tolist() == [0, 3, 15]
+    assert cc.tolist() == g["expected_child_coords"]
+    assert li.tolist() == g["expected_linear_idx"]
 
 
 # ------------------------------------------- reference cross-impl tests
