@@ -92,6 +92,43 @@ template <> __device__ inline void store_from_f32<uint16_t>(uint16_t *p, int64_t
     p[i] = f32_to_bf16(v);
 }
 
+// ---------------------------------------------------- kernel offsets
+// Offset k of a KD x KH x KW kernel: k = (kd*KH + kh)*KW + kw, deltas
+// sign_j * (idx_j - dim_j/2) written to axis order[j]
+// (crates/burn_flex_gmm/src/lib.rs:727-752).
+struct KernelShape {
+    int K, KD, KH, KW;
+    int order[3];
+    int sign[3];
+};
+
+inline KernelShape kernel_shape(const sc_conv_config *cfg)
+{
+    KernelShape ks;
+    ks.KD = (int)cfg->kernel_d;
+    ks.KH = (int)cfg->kernel_h;
+    ks.KW = (int)cfg->kernel_w;
+    ks.K = ks.KD * ks.KH * ks.KW;
+    for (int j = 0; j < 3; ++j) {
+        ks.order[j] = cfg->axis_order[j];
+        ks.sign[j] = cfg->axis_sign[j];
+    }
+    return ks;
+}
+
+__device__ inline void offset_of(const KernelShape &ks, int k, int o[3])
+{
+    const int hw = ks.KH * ks.KW;
+    const int kd = k / hw, rem = k - kd * hw;
+    const int kh = rem / ks.KW, kw = rem - kh * ks.KW;
+    const int d[3] = {ks.sign[0] * (kd - ks.KD / 2), ks.sign[1] * (kh - ks.KH / 2),
+                      ks.sign[2] * (kw - ks.KW / 2)};
+    o[0] = o[1] = o[2] = 0;
+    o[ks.order[0]] = d[0];
+    o[ks.order[1]] = d[1];
+    o[ks.order[2]] = d[2];
+}
+
 // ---------------------------------------------------- buffer loads
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 

@@ -294,25 +294,6 @@ __global__ __launch_bounds__(256) void nm_insert_kernel(const int4 *__restrict__
     }
 }
 
-struct KernelShape {
-    int K, KD, KH, KW;
-    int order[3];
-    int sign[3];
-};
-
-__device__ inline void offset_of(const KernelShape &ks, int k, int o[3])
-{
-    const int hw = ks.KH * ks.KW;
-    const int kd = k / hw, rem = k - kd * hw;
-    const int kh = rem / ks.KW, kw = rem - kh * ks.KW;
-    const int d[3] = {ks.sign[0] * (kd - ks.KD / 2), ks.sign[1] * (kh - ks.KH / 2),
-                      ks.sign[2] * (kw - ks.KW / 2)};
-    o[0] = o[1] = o[2] = 0;
-    o[ks.order[0]] = d[0];
-    o[ks.order[1]] = d[1];
-    o[ks.order[2]] = d[2];
-}
-
 // Dense-grid query: a row's neighbour at offset k is cell base[r] + delta[k]
 // (32-bit mixed-radix strides), valid when the neighbour lies in the bbox.
 // Entries (r, k) are walked incrementally (no division), four loads in
@@ -524,15 +505,7 @@ int sc_neighbor_map_build(const sc_conv_config *cfg, const int32_t *d_coords, in
                                                                   dense_cells);
     SC_LAUNCH_CHECK("nm_insert_kernel launch");
     if (query_rows == 0) return SC_OK;
-    KernelShape ks;
-    ks.K = (int)K;
-    ks.KD = (int)cfg->kernel_d;
-    ks.KH = (int)cfg->kernel_h;
-    ks.KW = (int)cfg->kernel_w;
-    for (int j = 0; j < 3; ++j) {
-        ks.order[j] = cfg->axis_order[j];
-        ks.sign[j] = cfg->axis_sign[j];
-    }
+    const KernelShape ks = kernel_shape(cfg);
     int rpb = (int)(2048 / K);
     if (rpb < 1) rpb = 1;
     if (rpb > kMaxStagedRows) rpb = kMaxStagedRows;

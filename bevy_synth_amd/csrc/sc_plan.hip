@@ -306,7 +306,7 @@ __global__ __launch_bounds__(kThreads) void plan_place_kernel(PlanArgs a)
         for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n_q;
              i += (int64_t)gridDim.x * blockDim.x) {
             const uint32_t old = atomicMin(&a.grid[grid_cell(gg, a.coords[i])], (uint32_t)i);
-            if (old != kGridEmpty) a.counts[atomicAdd(&a.hdr->n_extras, 1)] = (int32_t)max(old, (uint32_t)i);
+            if (old != kGridEmpty) atomicAdd(&a.hdr->n_extras, 1);
         }
         return;
     }
@@ -346,15 +346,41 @@ __device__ inline int block_scan_excl(int x, int *s_wave, int &total)
     return before + inc - x;
 }
 
-// Grid mode: occupied cells per 2048-cell block -> gsum; fallback: exclusive
+// Grid mode, duplicated coords: query rows whose cell holds a lower row.
+// 2048-row blocks, 8 consecutive rows per thread; returns the thread's count
+// and (optionally) its rows as bits.
+__device__ inline int64_t row_blocks(const PlanArgs &a) { return (a.n_q + kPlanGridBlock - 1) / kPlanGridBlock; }
+
+__device__ inline int extras_in(const PlanArgs &a, const GridGeom &gg, int64_t rb, uint32_t *flags = nullptr)
+{
+    const int64_t r0 = rb * kPlanGridBlock + threadIdx.x * 8;
+    uint32_t f = 0;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const int64_t i = r0 + u;
+        if (i < a.n_q && a.grid[grid_cell(gg, a.coords[i])] != (uint32_t)i) f |= 1u << u;
+    }
+    if (flags) *flags = f;
+    return __builtin_popcount(f);
+}
+
+// Grid mode: occupied cells per 2048-cell block -> gsum, and with duplicated
+// coords the extra rows per 2048-row block -> bsum; fallback: exclusive
 // scan of the brick counts within 1024-entry blocks, block totals -> bsum.
 __global__ __launch_bounds__(kThreads) void plan_scan1_kernel(PlanArgs a)
 {
     __shared__ int s_wave[kThreads / 64];
     if (a.hdr->grid_mode) {
         const int64_t nblk = a.grid_cap / kPlanGridBlock;
-        if ((int64_t)blockIdx.x >= nblk) return;
         const GridGeom gg = grid_geom(a.hdr, a.grid_cap);
+        if ((int64_t)blockIdx.x >= nblk) {  // rows of duplicated coords per 2048-row block
+            const int64_t rb = (int64_t)blockIdx.x - nblk;
+            if (a.hdr->n_extras == 0 || rb >= row_blocks(a)) return;
+            int total;
+            block_scan_excl(extras_in(a, gg, rb), s_wave, total);
+            if (threadIdx.x == 0) a.bsum[rb] = total;
+            return;
+        }
         const int64_t base = (int64_t)blockIdx.x * kPlanGridBlock + threadIdx.x * 8;
         int cnt = 0;
         if (base < gg.cells) {
@@ -412,6 +438,29 @@ __global__ __launch_bounds__(kThreads) void plan_scan2_kernel(PlanArgs a)
         carry += total;
     }
     if (grid && threadIdx.x == 0) a.hdr->n_unique = carry;
+    if (grid && a.hdr->n_extras > 0) {
+        const int64_t nr = row_blocks(a);
+        carry = 0;
+        for (int64_t base = 0; base < nr; base += kThreads * 4) {
+            int v[4];
+            int sum = 0;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int64_t i = base + threadIdx.x * 4 + u;
+                v[u] = i < nr ? a.bsum[i] : 0;
+                sum += v[u];
+            }
+            int total;
+            int ex = block_scan_excl(sum, s_wave, total);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int64_t i = base + threadIdx.x * 4 + u;
+                if (i < nr) a.bsum[i] = carry + ex;
+                ex += v[u];
+            }
+            carry += total;
+        }
+    }
 }
 
 __device__ inline int64_t brick_start(const PlanArgs &a, uint32_t br)
@@ -428,8 +477,20 @@ __global__ __launch_bounds__(kThreads) void plan_emit_kernel(PlanArgs a)
     __shared__ int s_wave[kThreads / 64];
     if (a.hdr->grid_mode) {
         const int64_t nblk = a.grid_cap / kPlanGridBlock;
-        if ((int64_t)blockIdx.x >= nblk) return;
         const GridGeom gg = grid_geom(a.hdr, a.grid_cap);
+        if ((int64_t)blockIdx.x >= nblk) {  // rows of duplicated coords, in row order
+            const int64_t rb = (int64_t)blockIdx.x - nblk;
+            if (a.hdr->n_extras == 0 || rb >= row_blocks(a)) return;
+            uint32_t flags;
+            const int cnt = extras_in(a, gg, rb, &flags);
+            int total;
+            int64_t pos = (int64_t)a.hdr->n_unique + a.bsum[rb] + block_scan_excl(cnt, s_wave, total);
+            const int64_t r0 = rb * kPlanGridBlock + threadIdx.x * 8;
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if ((flags >> u) & 1u) a.order[pos++] = (int32_t)(r0 + u);
+            return;
+        }
         const int64_t base = (int64_t)blockIdx.x * kPlanGridBlock + threadIdx.x * 8;
         uint32_t r[8];
         int cnt = 0;
@@ -467,23 +528,17 @@ __global__ __launch_bounds__(kThreads) void plan_emit_kernel(PlanArgs a)
     }
 }
 
-// Grid mode: rows of duplicated coords after the distinct ones.  Fallback:
-// each brick's segment sorted by row index (one wave per brick, rank = number
-// of smaller rows), so the order is deterministic; segments longer than
-// kSegWave (only with duplicated coords) keep the scatter's order.
+// Fallback mode: each brick's segment sorted by row index (one wave per
+// brick, rank = number of smaller rows), so the order is deterministic;
+// segments longer than kSegWave (only with duplicated coords) keep the
+// scatter's order.  (Grid mode needs no fix-up: emit places everything.)
 constexpr int kSegWave = 512;
 
 __global__ __launch_bounds__(kThreads) void plan_fix_kernel(PlanArgs a)
 {
     __shared__ __attribute__((aligned(16))) int32_t s_seg[kThreads / 64][kSegWave];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (a.hdr->grid_mode) {
-        const int n_unique = a.hdr->n_unique, n_extras = a.hdr->n_extras;
-        for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < n_extras;
-             j += (int64_t)gridDim.x * blockDim.x)
-            a.order[n_unique + j] = a.counts[j];
-        return;
-    }
+    if (a.hdr->grid_mode) return;
     if (a.hdr->brick_shift < 0) return;
     const uint64_t nb = a.hdr->n_bricks;
     int32_t *seg_lds = s_seg[wave];
@@ -821,13 +876,18 @@ extern "C" int sc_conv_plan_build(const sc_conv_config *cfg, const int32_t *d_co
     plan_place_kernel<<<grid_for(n_q, kThreads, 8192), kThreads, 0, s>>>(a);
     SC_LAUNCH_CHECK("plan_place_kernel launch");
     if (grid_blocks > INT32_MAX) return fail(SC_ERR_OVERFLOW, "conv plan grid overflow");
-    plan_scan1_kernel<<<(unsigned)(grid_blocks > L.n_bsum ? grid_blocks : L.n_bsum), kThreads, 0, s>>>(a);
+    // grid mode uses grid_blocks cell blocks + row_blocks duplicate-row blocks
+    const int64_t row_blocks = (n_q + kPlanGridBlock - 1) / kPlanGridBlock;
+    const int64_t scan_blocks = grid_blocks + row_blocks > L.n_bsum ? grid_blocks + row_blocks : L.n_bsum;
+    if (scan_blocks > INT32_MAX) return fail(SC_ERR_OVERFLOW, "conv plan grid overflow");
+    plan_scan1_kernel<<<(unsigned)scan_blocks, kThreads, 0, s>>>(a);
     SC_LAUNCH_CHECK("plan_scan1_kernel launch");
     plan_scan2_kernel<<<1, kThreads, 0, s>>>(a);
     SC_LAUNCH_CHECK("plan_scan2_kernel launch");
     const unsigned emit_blocks = grid_for(n_q, kThreads, 8192);
-    plan_emit_kernel<<<(unsigned)grid_blocks > emit_blocks ? (unsigned)grid_blocks : emit_blocks, kThreads, 0, s>>>(
-        a);
+    plan_emit_kernel<<<(unsigned)(grid_blocks + row_blocks) > emit_blocks ? (unsigned)(grid_blocks + row_blocks)
+                                                                          : emit_blocks,
+                       kThreads, 0, s>>>(a);
     SC_LAUNCH_CHECK("plan_emit_kernel launch");
     plan_fix_kernel<<<grid_for(L.brick_cap, kThreads / 64, 2048), kThreads, 0, s>>>(a);
     SC_LAUNCH_CHECK("plan_fix_kernel launch");

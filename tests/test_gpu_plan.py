@@ -80,7 +80,7 @@ def check_plan(plan, nbr, n_in):
     return h
 
 
-@pytest.mark.parametrize("which", ["config1", "random_batches", "clusters", "query_subset"])
+@pytest.mark.parametrize("which", ["config1", "random_batches", "clusters", "query_subset", "duplicates"])
 def test_plan_structure(which):
     rng = np.random.default_rng(11)
     cfg = F.SparseSubmConvConfig(32, 32)
@@ -95,6 +95,13 @@ def test_plan_structure(which):
     elif which == "clusters":
         coords = cluster_coords(600)
         q = 600
+    elif which == "duplicates":
+        # 3,000 extra rows repeating existing coords, in shuffled order: the
+        # plan lists every row once, and the rows of duplicated coords come
+        # after the distinct ones in increasing row order (deterministic)
+        base = synth.config1_coords()
+        coords = np.concatenate([base, base[rng.integers(0, len(base), 3000)]])
+        coords = coords[rng.permutation(len(coords))]
     else:
         coords = synth.config1_coords()
         q = 9000
