@@ -9,9 +9,11 @@ LayerNorm -> SiLU (fused into the first conv's epilogue) -> conv3x3x3 -> + x
 resident in HBM before timing; the weights are packed once beforehand (layer
 constants, as the reference's decoder caches its weights per layer).
 
-Prints one JSON line: value = voxels/s of the whole step; roofline = the
+Prints one JSON line: value = voxels/s of the whole step (W untimed steps,
+then K steps timed with HIP events, no host work in between); roofline = the
 dominant kernel (the MFMA conv) at its useful FLOPs 2*P*Cin*Cout per launch
-(P = valid (row, offset) pairs), timed with HIP events on the launch stream;
+(P = valid (row, offset) pairs) over its mean launch duration, measured with
+HIP events on the launch stream between the parts of K further steps;
 cpu_baseline = the oracle's restatement of the reference CPU flex path
 (HashMap map + im2col + single-thread sgemm) timed on this host over a
 bounded sample of query rows.
@@ -34,7 +36,8 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=25,
+                    help="untimed steps right before the timed ones (the GPU's clocks need ~20 steps)")
     ap.add_argument("--cpu-sample", type=int, default=262144,
                     help="query rows of the CPU baseline sample (0 = skip)")
     ap.add_argument("--only", choices=["map", "plan", "conv", "ln"], default=None,
@@ -45,8 +48,10 @@ def parse():
     return ap.parse_args()
 
 
-def events_ms(fn, iters):
+def events_ms(fn, iters, warmup=0):
     import torch
+    for _ in range(warmup):
+        fn()
     s = torch.cuda.Event(enable_timing=True)
     e = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -159,9 +164,13 @@ def main():
         conv1()
         conv2()
 
-    for _ in range(max(args.warmup, 1)):
-        step()
+    # One untimed step, then everything that needs the host (the map status
+    # check, the pair count, the calibration copy), so that the W warmup
+    # steps lead straight into the K timed steps: a host-side gap between them
+    # idles the GPU, its clocks drop, and the first timed steps run ~7 % slow.
+    step()
     F.neighbor_map_check(ws)
+    P = int((nbr >= 0).sum().item())
     if args.calibrate_copy:
         src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
@@ -172,22 +181,40 @@ def main():
     if args.only:
         part = {"map": map_build, "plan": plan_build, "conv": lambda: (conv1(), conv2()),
                 "ln": ln_silu}[args.only]
+        for _ in range(max(args.warmup, 1)):
+            part()
         ms = events_ms(part, args.steps)
         print(f"[bench] only={args.only} {ms:.3f} ms per call", file=sys.stderr, flush=True)
         return
-    P = int((nbr >= 0).sum().item())
-    print(f"[bench] config3 voxels={n} pairs={P} warmup done", file=sys.stderr, flush=True)
+    print(f"[bench] config3 voxels={n} pairs={P}", file=sys.stderr, flush=True)
 
-    torch.cuda.synchronize()
+    for _ in range(max(args.warmup, 1)):
+        step()
     ms_step = events_ms(step, args.steps)
-    # Per-kernel launch durations (HIP events on the launch stream).
-    ms_map = events_ms(map_build, args.steps)
-    ms_plan = events_ms(plan_build, args.steps)
-    # both convs of the block are the same kernel; average one launch over the pair
-    ms_conv = events_ms(lambda: (conv1(), conv2()), args.steps) / 2.0
-    ms_ln = events_ms(ln_silu, args.steps)
-    print(f"[bench] step {ms_step:.3f} ms  map {ms_map:.3f}  plan {ms_plan:.3f}  conv {ms_conv:.3f}  "
-          f"ln {ms_ln:.3f}",
+    # Per-part launch durations inside the step: K more steps with HIP events
+    # recorded on the launch stream between the parts (a separate pass, so the
+    # timed steps above carry no extra events).  The conv's duration in the
+    # roofline is its mean over conv1 and conv2 there, under the step's own
+    # mix of memory-bound and MFMA-bound kernels.
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    for e in ev:
+        e[0].record()
+        map_build()
+        e[1].record()
+        plan_build()
+        e[2].record()
+        conv1()
+        e[3].record()
+        conv2()
+        e[4].record()
+    torch.cuda.synchronize()
+    part = [sum(e[j].elapsed_time(e[j + 1]) for e in ev) / args.steps for j in range(4)]
+    ms_map, ms_plan, ms_conv1, ms_conv2 = part
+    ms_conv = (ms_conv1 + ms_conv2) / 2.0
+    ms_ln = events_ms(ln_silu, args.steps, max(args.warmup, 1))
+    print(f"[bench] step {ms_step:.3f} ms  map {ms_map:.3f}  plan {ms_plan:.3f}  conv1 {ms_conv1:.3f}  "
+          f"conv2 {ms_conv2:.3f}  (unfused ln {ms_ln:.3f})",
           file=sys.stderr, flush=True)
 
     flops = 2.0 * P * C * C
@@ -227,6 +254,7 @@ def main():
                      "frac": conv_tflops / PEAK_BF16_TFLOPS, "traffic": traffic},
         "components": {
             "map_build_ms": ms_map, "plan_build_ms": ms_plan, "conv_ms": ms_conv,
+            "conv1_ln_silu_ms": ms_conv1, "conv2_residual_ms": ms_conv2,
             "unfused_ln_silu_ms": ms_ln,
             "map_build_gbps": map_gbps, "map_build_frac_hbm": map_gbps / PEAK_HBM_GBPS,
             "conv_useful_tflops": conv_tflops,
