@@ -12,37 +12,82 @@
                         coords -> + channel-repeated parent skip.
 * ``transposed_upsample``: a stride-2 2x2x2 transposed sparse conv, which the
                         reference expresses as C2S with a 1x1x1 conv1 + select.
+* ``Neighborhood``    : one coord set's neighbour map and conv plan, built once
+                        per resolution and shared by every 3x3x3 conv there.
+* ``DecoderStack``    : config 5's decoder-shaped stack: per stage, residual
+                        blocks then a C2S 2x upsample, int8 weights, bf16
+                        activations.
 """
 from __future__ import annotations
 
-from dataclasses import dataclass
-from typing import Optional, Sequence, Tuple
+from dataclasses import dataclass, field
+from typing import List, Optional, Sequence, Tuple, Union
 
 import torch
 
-from .flex_gmm import (NeighborMapWorkspace, SparseSubmConvConfig, c2s_skip_add, gather_rows,
-                       layer_norm, neighbor_rows_tensor_from_coords_tensor,
+from .flex_gmm import (ConvPlan, NeighborMapWorkspace, SparseSubmConvConfig, build_conv_plan,
+                       c2s_skip_add, gather_rows, kernel_rows, layer_norm,
+                       neighbor_rows_tensor_from_coords_tensor, pack_conv_weight,
                        sparse_subm_conv_forward, subdivision_build)
 
 LAYER_NORM32_EPS = 1e-6  # sparse_decoder.rs:43
 
 
 @dataclass
+class Neighborhood:
+    """The neighbour map of one coord set and the conv plan built from it, made
+    once per resolution and passed to every conv there (the reference decoder
+    builds its map once per resolution and reuses it, sparse_decoder.rs
+    :1057-1136, through its neighbour cache, crates/burn_flex_gmm/src/
+    wgpu.rs:349-382)."""
+
+    coords: torch.Tensor
+    nbr: torch.Tensor
+    plan: Optional[ConvPlan] = None
+
+    @classmethod
+    def build(cls, cfg: SparseSubmConvConfig, coords: torch.Tensor,
+              workspace: Optional[NeighborMapWorkspace] = None, with_plan: bool = True
+              ) -> "Neighborhood":
+        nbr = neighbor_rows_tensor_from_coords_tensor(cfg, coords, workspace=workspace)
+        plan = build_conv_plan(cfg, coords, nbr) if with_plan and kernel_rows(cfg) <= 32 else None
+        return cls(coords, nbr, plan)
+
+
+@dataclass
 class ConvLayer:
     """One submanifold conv: weight [Cout, K, Cin_g] (bf16/f32/int8), bias f32,
-    optional per-output-channel scale for int8 weights."""
+    optional per-output-channel scale for int8 weights.  Given a Neighborhood
+    with a plan, bf16 activations take the halo-staged kernel on weights
+    packed once, on first use (the role of the reference's per-layer
+    pack_flex_weight, crates/burn_flex_gmm/src/lib.rs:377-426)."""
 
     cfg: SparseSubmConvConfig
     weight: torch.Tensor
     bias: Optional[torch.Tensor] = None
     w_scale: Optional[torch.Tensor] = None
+    packed: Optional[torch.Tensor] = field(default=None, repr=False)
 
-    def __call__(self, x: torch.Tensor, nbr: torch.Tensor, out_dtype=None,
+    def packed_weight(self) -> Optional[torch.Tensor]:
+        cin_g = self.cfg.to_c().in_channels_per_group
+        if (self.packed is None and self.weight.dtype in (torch.bfloat16, torch.int8)
+                and cin_g % 32 == 0):
+            self.packed = pack_conv_weight(self.cfg, self.weight)
+        return self.packed
+
+    def __call__(self, x: torch.Tensor, nbr: Union[torch.Tensor, Neighborhood], out_dtype=None,
                  residual: Optional[torch.Tensor] = None, layer_norm: bool = False,
                  silu: bool = False, ln_eps: float = LAYER_NORM32_EPS) -> torch.Tensor:
+        plan, packed = None, None
+        if isinstance(nbr, Neighborhood):
+            if nbr.plan is not None and x.dtype == torch.bfloat16:
+                packed = self.packed_weight()
+                plan = nbr.plan if packed is not None else None
+            nbr = nbr.nbr
         return sparse_subm_conv_forward(self.cfg, x, nbr, self.weight, self.bias, self.w_scale,
                                         residual=residual, out_dtype=out_dtype,
-                                        layer_norm=layer_norm, ln_eps=ln_eps, silu=silu)
+                                        layer_norm=layer_norm, ln_eps=ln_eps, silu=silu,
+                                        plan=plan, packed_weight=packed)
 
 
 @dataclass
@@ -51,7 +96,7 @@ class ResidualBlock:
     conv2: ConvLayer
     eps: float = LAYER_NORM32_EPS
 
-    def __call__(self, x: torch.Tensor, nbr: torch.Tensor) -> torch.Tensor:
+    def __call__(self, x: torch.Tensor, nbr: Union[torch.Tensor, Neighborhood]) -> torch.Tensor:
         # conv1 carries LayerNorm + SiLU in its epilogue; conv2 adds the residual.
         h = self.conv1(x, nbr, out_dtype=x.dtype, layer_norm=True, silu=True, ln_eps=self.eps)
         return self.conv2(h, nbr, out_dtype=x.dtype, residual=x)
@@ -73,21 +118,33 @@ class C2SUpsampleBlock:
                  parent_nbr: Optional[torch.Tensor] = None,
                  workspace: Optional[NeighborMapWorkspace] = None
                  ) -> Tuple[torch.Tensor, torch.Tensor]:
-        dt = parent_feats.dtype
-        child_coords, linear_idx, _ = subdivision_build(parent_coords, logits=logits, mask=mask,
-                                                        thresholds=thresholds, with_pairs=False)
         if parent_nbr is None:
-            parent_nbr = neighbor_rows_tensor_from_coords_tensor(self.conv1.cfg, parent_coords,
-                                                                 workspace=workspace)
+            parent_nb = Neighborhood.build(self.conv1.cfg, parent_coords, workspace)
+        else:
+            parent_nb = Neighborhood(parent_coords, parent_nbr)
+        child_nb, out = self.forward(parent_nb, parent_feats, logits=logits, mask=mask,
+                                     thresholds=thresholds, workspace=workspace)
+        return child_nb.coords, out
+
+    def forward(self, parent_nb: Neighborhood, parent_feats: torch.Tensor,
+                logits: Optional[torch.Tensor] = None, mask: Optional[torch.Tensor] = None,
+                thresholds: Optional[Sequence[float]] = None,
+                workspace: Optional[NeighborMapWorkspace] = None
+                ) -> Tuple[Neighborhood, torch.Tensor]:
+        """The block on a parent Neighborhood; returns the children's
+        Neighborhood (map + plan, for the next stage's convs) and features."""
+        dt = parent_feats.dtype
+        child_coords, linear_idx, _ = subdivision_build(parent_nb.coords, logits=logits, mask=mask,
+                                                        thresholds=thresholds, with_pairs=False)
         h = layer_norm(parent_feats, self.norm1_weight, self.norm1_bias, eps=self.eps, silu=True)
-        h1 = self.conv1(h, parent_nbr, out_dtype=dt)
+        h1 = self.conv1(h, parent_nb, out_dtype=dt)
         h_up = gather_rows(h1, 8, linear_idx)
         h_up = layer_norm(h_up, eps=self.eps, silu=True, out=h_up)
-        child_nbr = neighbor_rows_tensor_from_coords_tensor(self.conv2.cfg, child_coords,
-                                                            workspace=workspace)
-        out = self.conv2(h_up, child_nbr, out_dtype=dt)
+        child_nb = Neighborhood.build(self.conv2.cfg, child_coords, workspace,
+                                      with_plan=parent_nb.plan is not None)
+        out = self.conv2(h_up, child_nb, out_dtype=dt)
         c2s_skip_add(out, parent_feats, linear_idx)
-        return child_coords, out
+        return child_nb, out
 
 
 def transposed_upsample(parent_coords: torch.Tensor, parent_feats: torch.Tensor,
@@ -104,3 +161,77 @@ def transposed_upsample(parent_coords: torch.Tensor, parent_feats: torch.Tensor,
     ident = torch.arange(P, dtype=torch.int32, device=parent_coords.device).reshape(P, 1)
     h1 = conv1x1(parent_feats, ident, out_dtype=parent_feats.dtype)
     return child_coords, gather_rows(h1, 8, linear_idx), linear_idx
+
+
+@dataclass
+class DecoderStage:
+    blocks: List[ResidualBlock]
+    up: C2SUpsampleBlock
+
+
+@dataclass
+class DecoderStack:
+    """Config 5's decoder-shaped stack: per stage, residual blocks at the
+    stage's resolution, then a C2S 2x upsample (sparse_decoder_runtime_impl.rs
+    :758-1171) to the next resolution; one Neighborhood (map + plan) per
+    resolution, shared by the stage's convs and the next stage's."""
+
+    stages: List[DecoderStage]
+
+    def __call__(self, coords: torch.Tensor, feats: torch.Tensor, masks: Sequence[torch.Tensor],
+                 workspace: Optional[NeighborMapWorkspace] = None, with_plan: bool = True,
+                 trace: Optional[list] = None) -> Tuple[Neighborhood, torch.Tensor]:
+        """coords [N, 4] i32 and feats [N, C0] at the first resolution; masks[s]
+        [P_s, 8] u8 selects stage s's children.  ``trace`` (a list) receives
+        (stage, "block", Neighborhood, input, output, block) per residual block
+        and (stage, "up", parent Neighborhood, input, output, child
+        Neighborhood) per upsample, for tests."""
+        st0 = self.stages[0]
+        cfg0 = st0.blocks[0].conv1.cfg if st0.blocks else st0.up.conv1.cfg
+        nb = Neighborhood.build(cfg0, coords, workspace, with_plan=with_plan)
+        x = feats
+        for s, st in enumerate(self.stages):
+            for blk in st.blocks:
+                y = blk(x, nb)
+                if trace is not None:
+                    trace.append((s, "block", nb, x, y, blk))
+                x = y
+            child_nb, y = st.up.forward(nb, x, mask=masks[s], workspace=workspace)
+            if trace is not None:
+                trace.append((s, "up", nb, x, y, child_nb))
+            nb, x = child_nb, y
+        return nb, x
+
+
+def int8_stack(channels: Sequence[int], blocks_per_stage: int, seed: int,
+               device=None) -> DecoderStack:
+    """A random-weight stack shaped as config 5 (channels e.g. 512, 256, 128,
+    64): per stage ``blocks_per_stage`` residual blocks at channels[s] and a
+    C2S upsample channels[s] -> channels[s+1]; every conv 3x3x3 with
+    per-output-channel symmetric int8 weights (q ~ U{-127..127}, scale ~
+    U(0.5, 1.5)/127, so w = q * scale has std ~1/sqrt(3)); the scales are
+    divided by sqrt(27 * Cin) to keep activations O(1).  Zero conv biases;
+    norm1 affine ~ N(1, 0.1) / N(0, 0.1)."""
+    import numpy as np
+
+    from . import synth
+
+    dev = torch.device("cuda") if device is None else torch.device(device)
+    rng = np.random.default_rng(seed)
+
+    def layer(cin: int, cout: int) -> ConvLayer:
+        q, scale = synth.int8_weight(rng, cout, 27, cin)
+        scale = (scale / np.sqrt(27 * cin / 3.0)).astype(np.float32)
+        return ConvLayer(SparseSubmConvConfig(cin, cout), torch.from_numpy(q).to(dev),
+                         torch.zeros(cout, dtype=torch.float32, device=dev),
+                         torch.from_numpy(scale).to(dev))
+
+    stages = []
+    for s in range(len(channels) - 1):
+        c, c2 = channels[s], channels[s + 1]
+        blocks = [ResidualBlock(layer(c, c), layer(c, c)) for _ in range(blocks_per_stage)]
+        n1w = torch.from_numpy((1.0 + 0.1 * rng.standard_normal(c)).astype(np.float32)).to(dev)
+        n1b = torch.from_numpy((0.1 * rng.standard_normal(c)).astype(np.float32)).to(dev)
+        up = C2SUpsampleBlock(c, c2, n1w, n1b, layer(c, 8 * c2), layer(c2, c2))
+        stages.append(DecoderStage(blocks, up))
+    return DecoderStack(stages)

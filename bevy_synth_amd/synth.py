@@ -150,6 +150,57 @@ def config3_coords(seed: int = 13) -> np.ndarray:
     return EllipsoidShellGeometry(seed=seed).coords()
 
 
+def ellipsoid_shell_distance(geom: EllipsoidShellGeometry, pts: np.ndarray) -> np.ndarray:
+    """min_i |d_i(p)| over the union's ellipsoids, the first-order distance the
+    shell set uses, at arbitrary points (grid units of ``geom``)."""
+    a, c = geom.params()
+    p = np.asarray(pts, dtype=np.float64)
+    best = np.full(len(p), np.inf)
+    for i in range(geom.n_ellipsoids):
+        u = (p[:, 0] - c[i, 0]) / a[i, 0]
+        v = (p[:, 1] - c[i, 1]) / a[i, 1]
+        w = (p[:, 2] - c[i, 2]) / a[i, 2]
+        F = np.sqrt(u * u + v * v + w * w)
+        gn = np.sqrt((u / a[i, 0]) ** 2 + (v / a[i, 1]) ** 2 + (w / a[i, 2]) ** 2)
+        best = np.minimum(best, np.abs((F - 1.0) * F / np.maximum(gn, 1e-12)))
+    return best
+
+
+def child_expand(parent_coords: np.ndarray, mask: np.ndarray) -> np.ndarray:
+    """Children of the masked (parent, c) pairs in argwhere order (parent-major,
+    c ascending): (b, 2x + (c&1), 2y + (c>>1&1), 2z + (c>>2&1))."""
+    pairs = np.argwhere(mask)
+    p = parent_coords[pairs[:, 0]].astype(np.int64)
+    c = pairs[:, 1]
+    out = np.empty((len(pairs), 4), dtype=np.int32)
+    out[:, 0] = p[:, 0]
+    out[:, 1] = 2 * p[:, 1] + (c & 1)
+    out[:, 2] = 2 * p[:, 2] + ((c >> 1) & 1)
+    out[:, 3] = 2 * p[:, 3] + ((c >> 2) & 1)
+    return out
+
+
+def config5_stack_inputs(seed: int = 13, start_grid: int = 64, stages: int = 3):
+    """Config 5 geometry: the config-3 ellipsoid union scaled to each
+    resolution.  Returns the start coords (the shell set at ``start_grid``)
+    and, per stage, the [P, 8] u8 mask of the children of the stage's parents
+    that lie on the shell at twice the resolution (child centre within the
+    shell's half-width, in child grid units)."""
+    coords = EllipsoidShellGeometry(grid=start_grid, seed=seed).coords()
+    masks = []
+    parents = coords
+    for s in range(stages):
+        child = EllipsoidShellGeometry(grid=start_grid * 2 ** (s + 1), seed=seed)
+        mask = np.zeros((len(parents), 8), dtype=np.uint8)
+        base = 2.0 * parents[:, 1:4].astype(np.float64) + 0.5
+        for c in range(8):
+            off = np.array([c & 1, (c >> 1) & 1, (c >> 2) & 1], dtype=np.float64)
+            mask[:, c] = ellipsoid_shell_distance(child, base + off) <= child.half_width
+        masks.append(mask)
+        parents = child_expand(parents, mask)
+    return coords, masks
+
+
 def subdivision_mask_near_surface(parent_coords: np.ndarray, geom: ShellCubeGeometry,
                                   max_distance: float = 1.0) -> np.ndarray:
     """Config 4: [P, 8] u8 mask of children whose centre lies within
