@@ -951,41 +951,11 @@ constexpr int kHaloK = 27;
 
 __device__ inline int hslot(int j, int p) { return p ^ (((j >> 1) ^ (j >> 2)) & 3); }
 
-__device__ inline uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off)
-{
-    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
-    return make_uint2(v.x, v.y);
-}
-
-// 8 int8 (two words) -> 8 bf16 (exact: |q| <= 128).
-__device__ inline uint4 widen_i8x8(uint2 q)
-{
-    return make_uint4(i8pair_to_bf16x2(q.x, 0), i8pair_to_bf16x2(q.x, 16), i8pair_to_bf16x2(q.y, 0),
-                      i8pair_to_bf16x2(q.y, 16));
-}
-
-template <bool kI8>
-struct WFrag;
-template <>
-struct WFrag<false> {
-    uint4 v;
-    __device__ inline void load(__amdgpu_buffer_rsrc_t r, uint32_t off) { v = bload16(r, off); }
-    __device__ inline uint4 bf16() const { return v; }
-};
-template <>
-struct WFrag<true> {
-    uint2 v;
-    __device__ inline void load(__amdgpu_buffer_rsrc_t r, uint32_t off) { v = bload8(r, off); }
-    __device__ inline uint4 bf16() const { return widen_i8x8(v); }
-};
-
-template <typename TW, typename TO, bool kLN>
+template <typename TO, bool kLN>
 __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, PlanView plan)
 {
     constexpr int CB = 64;  // bytes of an input row per chunk (32 bf16 = one MFMA k-step)
-    constexpr bool kI8 = sizeof(TW) == 1;
-    constexpr int kWLane = kI8 ? 8 : 16;        // weight bytes per lane per fragment
+    constexpr int kWLane = 16;                  // weight bytes (8 bf16) per lane per fragment
     constexpr int kZeroRow = kPlanHaloMax;
     constexpr int kHaloPerWave = (kPlanHaloMax / 16 + 3) / 4;  // 16-row DMA instructions per wave
     static_assert(kHaloPerWave * 64 == kPlanHaloMax, "4 waves x 16 rows tile the halo exactly");
@@ -1081,12 +1051,12 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
             }
             u.k = __builtin_ctz(u.rem);
         };
-        WFrag<kI8> wf[kWS][4];
-        auto load_w = [&](const Cursor &u, WFrag<kI8>(&f)[4]) {
+        uint4 wf[kWS][4];
+        auto load_w = [&](const Cursor &u, uint4(&f)[4]) {
             const bool live = u.c < nkc;
             const uint32_t wk = w_lane + (uint32_t)((u.k * nkc + u.c) * 8) * kFrag;
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj) f[jj].load(w_rsrc, live ? wk + (uint32_t)jj * kFrag : kOobOffset);
+            for (int jj = 0; jj < 4; ++jj) f[jj] = bload16(w_rsrc, live ? wk + (uint32_t)jj * kFrag : kOobOffset);
         };
         // Halo DMA: instruction wave + 4*ii fills halo rows 16*(wave + 4*ii) + lane/4;
         // the lane moves logical piece hslot(j, lane%4) of row j.
@@ -1114,7 +1084,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
             __builtin_amdgcn_s_barrier();
         };
         auto read_lm = [&](int k) { return *reinterpret_cast<const uint4 *>(&s_lmap[k][rh][l16][0]); };
-        auto compute = [&](const uint4 &lm, const WFrag<kI8>(&f)[4]) {
+        auto compute = [&](const uint4 &lm, const uint4(&f)[4]) {
             const uint32_t lw[4] = {lm.x, lm.y, lm.z, lm.w};
             const uint32_t qx = (uint32_t)q4 << 4;
             uint4 x[8];
@@ -1125,7 +1095,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
             }
 #pragma unroll
             for (int jj = 0; jj < 4; ++jj) {
-                const uint4 w = f[jj].bf16();
+                const uint4 w = f[jj];
 #pragma unroll
                 for (int i = 0; i < 8; ++i)
                     acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
@@ -1189,10 +1159,10 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
             const int o = oc0 + j * 16 + 4 * q4 + e;
             const bool ok = o < args.cout_g;
             const float bias = (args.bias && ok) ? args.bias[out_col0 + o] : 0.f;
-            const float scale = (kI8 && args.w_scale && ok) ? args.w_scale[out_col0 + o] : 1.f;
+            const float scale = (args.w_scale && ok) ? args.w_scale[out_col0 + o] : 1.f;  // int8 weights
 #pragma unroll
             for (int i = 0; i < 8; ++i)
-                acc[i][j][e] = ok ? (kI8 ? acc[i][j][e] * scale + bias : acc[i][j][e] + bias) : 0.f;
+                acc[i][j][e] = ok ? acc[i][j][e] * scale + bias : 0.f;
             __builtin_amdgcn_sched_barrier(0);
         }
     if constexpr (kLN) {
@@ -1319,12 +1289,13 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
 // The halo-staged kernel's weight layout: per (group g, 128-channel output
 // tile ot, offset k, 32-channel input chunk c, 16-channel block jj) one
 // fragment of 64 lanes; lane (l16, q4) holds the 8 weights
-// w[g, ot*128 + 16 jj + l16, k, 32c + 8 q4 .. +8] (bf16: 16 B, int8: 8 B),
-// zero for channels beyond Cout_g.  Same role as the reference's
+// w[g, ot*128 + 16 jj + l16, k, 32c + 8 q4 .. +8] as bf16 (16 B; int8 weights
+// are widened exactly, their per-channel scales stay [Cout] f32 and are
+// applied in the conv's epilogue), zero for channels beyond Cout_g.  Same role as the reference's
 // pack_flex_weight (crates/burn_flex_gmm/src/lib.rs:377-426): a one-time
 // per-layer reorder so that the conv's weight reads are contiguous.
-template <typename TW>
-__global__ void pack_weights_kernel(const TW *__restrict__ w, TW *__restrict__ dst, int groups, int cout_g,
+template <typename TS>
+__global__ void pack_weights_kernel(const TS *__restrict__ w, uint16_t *__restrict__ dst, int groups, int cout_g,
                                     int cin_g, int K)
 {
     const int nkc = cin_g / 32, n_ot = (cout_g + kBN - 1) / kBN;
@@ -1343,11 +1314,16 @@ __global__ void pack_weights_kernel(const TW *__restrict__ w, TW *__restrict__ d
         const int g = (int)(r / n_ot);
         const int o = ot * kBN + 16 * jj + (lane & 15);
         const int i0 = 32 * c + 8 * (lane >> 4);
-        TW *d = dst + p * 8;
+        uint16_t *d = dst + p * 8;
         if (o < cout_g) {
-            const TW *s = w + (((int64_t)g * cout_g + o) * K + k) * cin_g + i0;
+            const TS *s = w + (((int64_t)g * cout_g + o) * K + k) * cin_g + i0;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) d[e] = s[e];
+            for (int e = 0; e < 8; ++e) {
+                if constexpr (sizeof(TS) == 1)
+                    d[e] = f32_to_bf16((float)s[e]);  // exact: |q| <= 128
+                else
+                    d[e] = s[e];
+            }
         } else {
 #pragma unroll
             for (int e = 0; e < 8; ++e) d[e] = 0;
@@ -1419,13 +1395,17 @@ int launch_conv(const ConvArgs &a, int groups, bool mfma, const void *plan, hipS
                 // Halo-staged tiles, then the tiles whose halo overflowed
                 // (listed by the plan) through the direct kernel in plan
                 // order, each plan tile as kPlanTileRows / kTileRows tiles.
+                // Packed weights are bf16 for either weight type; int8
+                // weights keep their per-channel scales for the epilogue.
                 const PlanLayout L = plan_layout(a.n_q, a.K);
                 const PlanView pv = plan_view(plan, L);
                 dim3 hgrid((unsigned)L.n_tiles, (unsigned)ntile, (unsigned)groups);
+                ConvArgs h = a;
+                if (sizeof(TW) != 1) h.w_scale = nullptr;
                 if (a.ln)
-                    conv_halo_kernel<TW, TO, true><<<hgrid, kThreads, 0, s>>>(a, pv);
+                    conv_halo_kernel<TO, true><<<hgrid, kThreads, 0, s>>>(h, pv);
                 else
-                    conv_halo_kernel<TW, TO, false><<<hgrid, kThreads, 0, s>>>(a, pv);
+                    conv_halo_kernel<TO, false><<<hgrid, kThreads, 0, s>>>(h, pv);
                 SC_LAUNCH_CHECK("conv_halo_kernel launch");
                 ConvArgs b = a;
                 b.perm = pv.order;
@@ -1622,8 +1602,7 @@ static int weight_pack_bytes(const sc_conv_config *cfg, int w_dtype, size_t *byt
         return fail(SC_ERR_UNSUPPORTED, "weight packing needs input channels per group divisible by 32");
     const int64_t K = cfg->kernel_d * cfg->kernel_h * cfg->kernel_w;
     const int64_t n_ot = (cfg->out_channels_per_group + kBN - 1) / kBN;
-    const long double b = (long double)cfg->groups * n_ot * kBN * K * cfg->in_channels_per_group *
-                          (long double)dtype_size(w_dtype);
+    const long double b = (long double)cfg->groups * n_ot * kBN * K * cfg->in_channels_per_group * 2.0L;
     if (b >= (long double)((int64_t)1 << 31))
         return fail(SC_ERR_OVERFLOW, "packed weights must stay below 2 GiB");
     *bytes = (size_t)b;
@@ -1650,14 +1629,14 @@ extern "C" int sc_conv_weight_pack(const sc_conv_config *cfg, int w_dtype, const
     const int groups = (int)cfg->groups, cout_g = (int)cfg->out_channels_per_group,
               cin_g = (int)cfg->in_channels_per_group;
     const int K = (int)(cfg->kernel_d * cfg->kernel_h * cfg->kernel_w);
-    const int64_t pieces = (int64_t)(bytes / (8 * dtype_size(w_dtype)));
+    const int64_t pieces = (int64_t)(bytes / 16);  // 8 bf16 per lane and fragment
     hipStream_t s = as_stream(stream);
     if (w_dtype == SC_DTYPE_BF16)
         pack_weights_kernel<uint16_t><<<grid_for(pieces, 256, 16384), 256, 0, s>>>(
             static_cast<const uint16_t *>(d_weight), static_cast<uint16_t *>(d_packed), groups, cout_g, cin_g, K);
     else
         pack_weights_kernel<int8_t><<<grid_for(pieces, 256, 16384), 256, 0, s>>>(
-            static_cast<const int8_t *>(d_weight), static_cast<int8_t *>(d_packed), groups, cout_g, cin_g, K);
+            static_cast<const int8_t *>(d_weight), static_cast<uint16_t *>(d_packed), groups, cout_g, cin_g, K);
     SC_LAUNCH_CHECK("pack_weights_kernel launch");
     return SC_OK;
 }

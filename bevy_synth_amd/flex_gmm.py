@@ -277,9 +277,11 @@ def conv_weight_pack_bytes(cfg: SparseSubmConvConfig, w_dtype: torch.dtype) -> i
 
 
 def pack_conv_weight(cfg: SparseSubmConvConfig, weight: torch.Tensor) -> torch.Tensor:
-    """The planned conv's weight layout (sc_conv_weight_pack); a one-time
-    per-layer reorder, the role pack_flex_weight plays for the reference's CPU
-    path (crates/burn_flex_gmm/src/lib.rs:377-426)."""
+    """The planned conv's weight layout (sc_conv_weight_pack): bf16 MFMA
+    fragments, int8 weights widened exactly (their scales are passed to the
+    conv as usual); a one-time per-layer reorder, the role pack_flex_weight
+    plays for the reference's CPU path (crates/burn_flex_gmm/src/lib.rs
+    :377-426)."""
     _require_cuda("weight", weight)
     buf = torch.empty(conv_weight_pack_bytes(cfg, weight.dtype), dtype=torch.uint8, device=weight.device)
     check(_capi.load().sc_conv_weight_pack(ctypes.byref(cfg.to_c()), _dt(weight), _ptr(weight), _ptr(buf),

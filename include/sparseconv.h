@@ -220,9 +220,12 @@ int sc_conv_plan_build(const sc_conv_config *cfg, const int32_t *d_coords, int64
  * device API; it plays the role of pack_flex_weight
  * (crates/burn_flex_gmm/src/lib.rs:377-426), a one-time per-layer reorder
  * (the decoder caches its weights per layer, sparse_decoder.rs:757-844).
- * w_dtype bf16 or i8 (scales stay [Cout] f32, unpacked); Cin per group must
- * be a multiple of 32.  d_weight is the reference layout [Cout][KD][KH][KW]
- * [Cin_g]; d_packed is 16-byte aligned, sc_conv_weight_pack_size bytes.
+ * w_dtype bf16 or i8; the fragments are bf16 either way (int8 weights are
+ * widened exactly, |q| <= 127, and their [Cout] f32 scales, passed to the
+ * conv as usual, are applied in its epilogue).  Cin per group must be a
+ * multiple of 32.  d_weight is the reference layout [Cout][KD][KH][KW]
+ * [Cin_g]; d_packed is 16-byte aligned, sc_conv_weight_pack_size bytes
+ * (2 bytes per weight of each 128-channel output tile).
  */
 int sc_conv_weight_pack_size(const sc_conv_config *cfg, int w_dtype, size_t *bytes);
 int sc_conv_weight_pack(const sc_conv_config *cfg, int w_dtype, const void *d_weight, void *d_packed,

@@ -125,6 +125,6 @@ def test_plan_size_matches_layout():
 def test_weight_pack_size():
     cfg = F.SparseSubmConvConfig(128, 200)
     assert F.conv_weight_pack_bytes(cfg, torch.bfloat16) == 2 * 128 * 27 * 128 * 2
-    assert F.conv_weight_pack_bytes(cfg, torch.int8) == 2 * 128 * 27 * 128
+    assert F.conv_weight_pack_bytes(cfg, torch.int8) == 2 * 128 * 27 * 128 * 2  # widened to bf16
     with pytest.raises(_capi.SparseConvError):
         F.conv_weight_pack_bytes(F.SparseSubmConvConfig(48, 64), torch.bfloat16)

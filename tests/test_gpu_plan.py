@@ -138,7 +138,9 @@ def test_weight_pack_layout(cin, cout, groups, wdt):
         wd = dev(q)
         wh = q.astype(np.int64)
     packed = F.pack_conv_weight(cfg, wd).cpu().numpy()
-    packed = packed.view(np.uint16 if wdt == "bf16" else np.int8).astype(np.int64)
+    packed = packed.view(np.uint16).astype(np.int64)        # bf16 fragments for either type
+    if wdt != "bf16":
+        wh = synth.bf16_bits(wh.astype(np.float32)).astype(np.int64)  # int8 widened exactly
     n_ot, nkc = (cout_g + 127) // 128, cin_g // 32
     exp = np.zeros((groups, n_ot, K, nkc, 8, 64, 8), np.int64)
     for g in range(groups):
