@@ -951,7 +951,7 @@ constexpr int kHaloK = 27;
 
 __device__ inline int hslot(int j, int p) { return p ^ (((j >> 1) ^ (j >> 2)) & 3); }
 
-template <typename TO, bool kLN>
+template <typename TO, bool kLN, int kNT>
 __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, PlanView plan)
 {
     constexpr int CB = 64;  // bytes of an input row per chunk (32 bf16 = one MFMA k-step)
@@ -961,6 +961,10 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
     static_assert(kHaloPerWave * 64 == kPlanHaloMax, "4 waves x 16 rows tile the halo exactly");
     constexpr int kWS = SC_HALO_WS;             // weight register sets: stages t .. t+kWS-1
     static_assert(kPlanTileRows == kTileRows, "plan tile = 256 rows");
+    // kNT = 128: waves 2 x 2 (128 rows x 64 channels each); kNT = 64 (layers
+    // of at most 64 output channels): waves 4 x 1 (64 rows x 64 channels).
+    static_assert(kNT == 128 || kNT == 64, "output tile of 128 or 64 channels");
+    constexpr int kI = kNT == 128 ? 8 : 4;      // 16-row MFMA blocks per wave
 
     __shared__ __attribute__((aligned(16))) unsigned char s_halo[(kPlanHaloMax + 1) * CB];
     // s_lmap[k][rh][l16][i]: LDS byte offset of the halo row feeding tile row
@@ -974,13 +978,15 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, q4 = lane >> 4;
-    const int rh = wave >> 1, ch = wave & 1;  // row half, channel half
+    const int rh = wave >> 1;                              // lmap half of the wave's rows
+    const int ch = kNT == 128 ? (wave & 1) : 0;            // channel half
+    const int row0 = kNT == 128 ? 128 * rh : 64 * wave;    // first tile row of the wave
     const int K = args.K;
 
     const int tile = tile_for_block(blockIdx.x, gridDim.x);
     const int U = plan.tile_u[tile];
     if (U > kPlanHaloMax) return;  // listed in plan.overflow; the direct kernel takes it
-    const int o0 = blockIdx.y * kBN;
+    const int o0 = blockIdx.y * kNT;
     const int g = blockIdx.z;
     const int64_t in_col0 = (int64_t)g * args.cin_g;
     const int64_t out_col0 = (int64_t)g * args.cout_g;
@@ -1008,9 +1014,9 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
     __syncthreads();
     const uint32_t tmask = __builtin_amdgcn_readfirstlane(s_wmask[0] | s_wmask[1] | s_wmask[2] | s_wmask[3]);
 
-    f32x4 acc[8][4];
+    f32x4 acc[kI][4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < kI; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -1021,7 +1027,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
         const uint16_t *input = static_cast<const uint16_t *>(args.input);
         const __amdgpu_buffer_rsrc_t a_rsrc =
             make_rsrc(input + in_col0, (uint32_t)(args.n_in * row_bytes - in_col0 * (int64_t)sizeof(uint16_t)));
-        const int n_ot = (args.cout_g + kBN - 1) / kBN;
+        const int n_ot = (args.cout_g + kBN - 1) / kBN;  // 128-channel tiles of the packing
         // Packed weights (sc_conv_weight_pack): per (group, 128-channel tile)
         // a block of K x nkc x 8 fragments; fragment (k, c, jj) is 64 lanes x
         // kWLane bytes, lane (l16, q4) holding w[tile*128 + 16 jj + l16, k,
@@ -1030,8 +1036,8 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
         const uint32_t w_tile_bytes = (uint32_t)K * (uint32_t)nkc * 8u * kFrag;
         const __amdgpu_buffer_rsrc_t w_rsrc =
             make_rsrc(args.wpack, (uint32_t)((int64_t)args.cin / args.cin_g * n_ot) * w_tile_bytes);
-        const uint32_t w_lane = (uint32_t)(g * n_ot + (int)blockIdx.y) * w_tile_bytes +
-                                (uint32_t)(4 * ch) * kFrag + (uint32_t)(lane * kWLane);
+        const uint32_t w_lane = (uint32_t)(g * n_ot + (o0 >> 7)) * w_tile_bytes +
+                                (uint32_t)((o0 & 127) / 16 + 4 * ch) * kFrag + (uint32_t)(lane * kWLane);
         const int n_halo_instr = (U + 15) >> 4;
 
         struct Cursor {
@@ -1083,13 +1089,20 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
             __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
             __builtin_amdgcn_s_barrier();
         };
-        auto read_lm = [&](int k) { return *reinterpret_cast<const uint4 *>(&s_lmap[k][rh][l16][0]); };
+        auto read_lm = [&](int k) {
+            if constexpr (kNT == 128) {
+                return *reinterpret_cast<const uint4 *>(&s_lmap[k][rh][l16][0]);
+            } else {
+                const uint2 v = *reinterpret_cast<const uint2 *>(&s_lmap[k][rh][l16][4 * (wave & 1)]);
+                return make_uint4(v.x, v.y, 0u, 0u);
+            }
+        };
         auto compute = [&](const uint4 &lm, const uint4(&f)[4]) {
             const uint32_t lw[4] = {lm.x, lm.y, lm.z, lm.w};
             const uint32_t qx = (uint32_t)q4 << 4;
-            uint4 x[8];
+            uint4 x[kI];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
+            for (int i = 0; i < kI; ++i) {
                 const uint32_t off = ((i & 1) ? (lw[i >> 1] >> 16) : (lw[i >> 1] & 0xFFFFu)) ^ qx;
                 x[i] = *reinterpret_cast<const uint4 *>(s_halo + off);
             }
@@ -1097,7 +1110,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
             for (int jj = 0; jj < 4; ++jj) {
                 const uint4 w = f[jj];
 #pragma unroll
-                for (int i = 0; i < 8; ++i)
+                for (int i = 0; i < kI; ++i)
                     acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                         __builtin_bit_cast(bf16x8, w), __builtin_bit_cast(bf16x8, x[i]), acc[i][jj], 0, 0, 0);
             }
@@ -1146,8 +1159,8 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
     }
 
     // ---- epilogue: lane l holds channels oc0 + 16 j + 4 q4 + e of tile row
-    //      128 rh + 16 i + l16; the lanes l16 + 16 m of the two waves of a row
-    //      half hold the whole row.
+    //      row0 + 16 i + l16; the lanes l16 + 16 m of the wave (kNT = 64) or
+    //      of the two waves of a row half (kNT = 128) hold the whole row.
     TO *__restrict__ out = static_cast<TO *>(args.out);
     const TO *__restrict__ res = static_cast<const TO *>(args.residual);
     const bool vec_ok = args.vec_out != 0;
@@ -1161,22 +1174,36 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
             const float bias = (args.bias && ok) ? args.bias[out_col0 + o] : 0.f;
             const float scale = (args.w_scale && ok) ? args.w_scale[out_col0 + o] : 1.f;  // int8 weights
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
+            for (int i = 0; i < kI; ++i)
                 acc[i][j][e] = ok ? acc[i][j][e] * scale + bias : 0.f;
             __builtin_amdgcn_sched_barrier(0);
         }
     if constexpr (kLN) {
         // Two-pass f32 statistics over the row's Cout channels (the
         // reference's layer_norm_row_stats, wgpu/ops.rs:162-187).  Each wave
-        // reduces its 64 channels; the two halves meet in LDS (the halo's
-        // first 2 KB, free once every wave has left the main loop) and are
-        // added in a fixed order, so both waves hold the same statistics.
+        // reduces its 64 channels over the 4 lanes of a row; with 128-channel
+        // tiles the two channel halves meet in LDS (the halo's first 2 KB,
+        // free once every wave has left the main loop) and are added in a
+        // fixed order, so both waves hold the same statistics.
         float *red = reinterpret_cast<float *>(s_halo);  // [channel half][256 tile rows]
-        const float inv_c = 1.0f / (float)args.cout_g;
-        float mean[8], inv_std[8];
-        __syncthreads();
+        auto row_total = [&](float(&part)[kI]) {
+            if constexpr (kNT == 128) {
+                __syncthreads();
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+                for (int i = 0; i < kI; ++i)
+                    if (q4 == 0) red[ch * kPlanTileRows + row0 + 16 * i + l16] = part[i];
+                __syncthreads();
+#pragma unroll
+                for (int i = 0; i < kI; ++i) {
+                    const int r = row0 + 16 * i + l16;
+                    part[i] = red[r] + red[kPlanTileRows + r];
+                }
+            }
+        };
+        const float inv_c = 1.0f / (float)args.cout_g;
+        float mean[kI], inv_std[kI], part[kI];
+#pragma unroll
+        for (int i = 0; i < kI; ++i) {
             float sum = 0.f;
 #pragma unroll
             for (int j = 0; j < 4; ++j)
@@ -1184,17 +1211,13 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
                 for (int e = 0; e < 4; ++e) sum += acc[i][j][e];
             sum += __shfl_xor(sum, 16, 64);
             sum += __shfl_xor(sum, 32, 64);
-            if (q4 == 0) red[ch * kPlanTileRows + rh * 128 + 16 * i + l16] = sum;
+            part[i] = sum;
         }
-        __syncthreads();
+        row_total(part);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int r = rh * 128 + 16 * i + l16;
-            mean[i] = (red[r] + red[kPlanTileRows + r]) * inv_c;
-        }
-        __syncthreads();
+        for (int i = 0; i < kI; ++i) mean[i] = part[i] * inv_c;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < kI; ++i) {
             float qv = 0.f;
 #pragma unroll
             for (int j = 0; j < 4; ++j)
@@ -1206,14 +1229,11 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
                 }
             qv += __shfl_xor(qv, 16, 64);
             qv += __shfl_xor(qv, 32, 64);
-            if (q4 == 0) red[ch * kPlanTileRows + rh * 128 + 16 * i + l16] = qv;
+            part[i] = qv;
         }
-        __syncthreads();
+        row_total(part);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int r = rh * 128 + 16 * i + l16;
-            inv_std[i] = rsqrt_f32((red[r] + red[kPlanTileRows + r]) * inv_c + args.ln_eps);
-        }
+        for (int i = 0; i < kI; ++i) inv_std[i] = rsqrt_f32(part[i] * inv_c + args.ln_eps);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -1223,7 +1243,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
                 const float lw = (args.ln_w && ok) ? args.ln_w[o] : 1.f;
                 const float lb = (args.ln_b && ok) ? args.ln_b[o] : 0.f;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) acc[i][j][e] = (acc[i][j][e] - mean[i]) * inv_std[i] * lw + lb;
+                for (int i = 0; i < kI; ++i) acc[i][j][e] = (acc[i][j][e] - mean[i]) * inv_std[i] * lw + lb;
                 __builtin_amdgcn_sched_barrier(0);
             }
     }
@@ -1231,11 +1251,11 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
     // is fetched before any of them is written, so its latency overlaps
     // instead of serialising per block.
     constexpr int kRG = sizeof(TO) == 2 ? 4 : 2;
-    int32_t qrow[8];
+    int32_t qrow[kI];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) qrow[i] = plan.order[(int64_t)tile * kPlanTileRows + rh * 128 + 16 * i + l16];
+    for (int i = 0; i < kI; ++i) qrow[i] = plan.order[(int64_t)tile * kPlanTileRows + row0 + 16 * i + l16];
 #pragma unroll
-    for (int ih = 0; ih < 8; ih += kRG) {
+    for (int ih = 0; ih < kI; ih += kRG) {
         typename Out4<TO>::V rv[kRG][4];
         if (res && vec_ok) {
 #pragma unroll
@@ -1402,10 +1422,17 @@ int launch_conv(const ConvArgs &a, int groups, bool mfma, const void *plan, hipS
                 dim3 hgrid((unsigned)L.n_tiles, (unsigned)ntile, (unsigned)groups);
                 ConvArgs h = a;
                 if (sizeof(TW) != 1) h.w_scale = nullptr;
-                if (a.ln)
-                    conv_halo_kernel<TO, true><<<hgrid, kThreads, 0, s>>>(h, pv);
-                else
-                    conv_halo_kernel<TO, false><<<hgrid, kThreads, 0, s>>>(h, pv);
+                if (a.cout_g <= 64) {  // 64-channel tiles: no half-empty MFMA tile
+                    hgrid.y = (unsigned)((a.cout_g + 63) / 64);
+                    if (a.ln)
+                        conv_halo_kernel<TO, true, 64><<<hgrid, kThreads, 0, s>>>(h, pv);
+                    else
+                        conv_halo_kernel<TO, false, 64><<<hgrid, kThreads, 0, s>>>(h, pv);
+                } else if (a.ln) {
+                    conv_halo_kernel<TO, true, 128><<<hgrid, kThreads, 0, s>>>(h, pv);
+                } else {
+                    conv_halo_kernel<TO, false, 128><<<hgrid, kThreads, 0, s>>>(h, pv);
+                }
                 SC_LAUNCH_CHECK("conv_halo_kernel launch");
                 ConvArgs b = a;
                 b.perm = pv.order;

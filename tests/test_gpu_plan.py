@@ -199,26 +199,28 @@ def test_planned_int8_weights(oracle):
 
 
 @pytest.mark.parametrize("affine", [False, True])
-def test_planned_ln_silu_and_residual(oracle, affine):
+@pytest.mark.parametrize("cin,cout", [(128, 128), (64, 64), (128, 40)])  # 128- and 64-channel tiles
+def test_planned_ln_silu_and_residual(oracle, affine, cin, cout):
     coords = synth.config1_coords()
     rng = np.random.default_rng(21)
-    n, c = len(coords), 128
-    x = rbf(synth.normal_f32(rng, (n, c)))
-    w = rbf(synth.conv_weight(rng, c, 27, c, 1 / np.sqrt(27 * c)))
-    b = synth.normal_f32(rng, c, 0.1)
-    lw = synth.normal_f32(rng, c) if affine else None
-    lb = synth.normal_f32(rng, c) if affine else None
-    res = rbf(synth.normal_f32(rng, (n, c)))
-    cfg = F.SparseSubmConvConfig(c, c)
+    n = len(coords)
+    x = rbf(synth.normal_f32(rng, (n, cin)))
+    w = rbf(synth.conv_weight(rng, cout, 27, cin, 1 / np.sqrt(27 * cin)))
+    b = synth.normal_f32(rng, cout, 0.1)
+    lw = synth.normal_f32(rng, cout) if affine else None
+    lb = synth.normal_f32(rng, cout) if affine else None
+    res = rbf(synth.normal_f32(rng, (n, cout)))
+    cfg = F.SparseSubmConvConfig(cin, cout)
+    ocfg_ = oracle.OracleConfig(cin, cout)
     out, nbr, _ = planned(cfg, coords, x, w, b, residual=bf16_dev(res), layer_norm=True,
                           ln_weight=None if lw is None else dev(lw), ln_bias=None if lb is None else dev(lb),
                           ln_eps=1e-6, silu=True)
-    conv = oracle.conv_ref_f64(oracle.OracleConfig(c, c), w, b, x, nbr).astype(np.float32)
+    conv = oracle.conv_ref_f64(ocfg_, w, b, x, nbr).astype(np.float32)
     exp = oracle.silu(oracle.layer_norm(conv, lw, lb, 1e-6)) + res
     assert_close(out.float().cpu().numpy(), exp, TOL_BF16, "planned LN/SiLU/residual")
     # conv -> + residual only (the second conv of the residual block)
     out2, _, _ = planned(cfg, coords, x, w, b, residual=dev(res), out_dtype=torch.float32)
-    exp2 = oracle.conv_ref_f64(oracle.OracleConfig(c, c), w, b, x, nbr) + res
+    exp2 = oracle.conv_ref_f64(ocfg_, w, b, x, nbr) + res
     assert_close(out2.cpu().numpy(), exp2, 2e-5, "planned residual")
 
 
