@@ -40,7 +40,7 @@ def parse():
                     help="untimed steps right before the timed ones (the GPU's clocks need ~20 steps)")
     ap.add_argument("--cpu-sample", type=int, default=262144,
                     help="query rows of the CPU baseline sample (0 = skip)")
-    ap.add_argument("--only", choices=["map", "plan", "conv", "ln"], default=None,
+    ap.add_argument("--only", choices=["map", "plan", "mapplan", "conv", "ln"], default=None,
                     help="run just this part of the step --steps times (for rocprofv3) and exit")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 1 GiB device-to-device copy (the known-size kernel that "
@@ -147,6 +147,10 @@ def main():
     def plan_build():
         F.conv_plan_build_into(cfg, coords_d, nbr, plan_buf)
 
+    def map_and_plan():
+        map_build()
+        plan_build()
+
     def conv1():  # conv -> LayerNorm -> SiLU, fused in the conv epilogue
         F.sparse_subm_conv_forward(cfg, x, nbr, w1_d, bias, out=h, layer_norm=True, ln_eps=1e-6,
                                    silu=True, plan=plan, packed_weight=w1_p)
@@ -179,8 +183,8 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     if args.only:
-        part = {"map": map_build, "plan": plan_build, "conv": lambda: (conv1(), conv2()),
-                "ln": ln_silu}[args.only]
+        part = {"map": map_build, "plan": plan_build, "mapplan": map_and_plan,
+                "conv": lambda: (conv1(), conv2()), "ln": ln_silu}[args.only]
         for _ in range(max(args.warmup, 1)):
             part()
         ms = events_ms(part, args.steps)
@@ -196,25 +200,27 @@ def main():
     # timed steps above carry no extra events).  The conv's duration in the
     # roofline is its mean over conv1 and conv2 there, under the step's own
     # mix of memory-bound and MFMA-bound kernels.
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
     torch.cuda.synchronize()
     for e in ev:
         e[0].record()
-        map_build()
+        map_and_plan()
         e[1].record()
-        plan_build()
-        e[2].record()
         conv1()
-        e[3].record()
+        e[2].record()
         conv2()
-        e[4].record()
+        e[3].record()
     torch.cuda.synchronize()
-    part = [sum(e[j].elapsed_time(e[j + 1]) for e in ev) / args.steps for j in range(4)]
-    ms_map, ms_plan, ms_conv1, ms_conv2 = part
+    part = [sum(e[j].elapsed_time(e[j + 1]) for e in ev) / args.steps for j in range(3)]
+    ms_map_plan, ms_conv1, ms_conv2 = part
     ms_conv = (ms_conv1 + ms_conv2) / 2.0
-    ms_ln = events_ms(ln_silu, args.steps, max(args.warmup, 1))
-    print(f"[bench] step {ms_step:.3f} ms  map {ms_map:.3f}  plan {ms_plan:.3f}  conv1 {ms_conv1:.3f}  "
-          f"conv2 {ms_conv2:.3f}  (unfused ln {ms_ln:.3f})",
+    # the map and the plan on their own (the map's GB/s), then the unfused LN
+    wu = max(args.warmup, 1)
+    ms_map = events_ms(map_build, args.steps, wu)
+    ms_plan = events_ms(plan_build, args.steps, wu)
+    ms_ln = events_ms(ln_silu, args.steps, wu)
+    print(f"[bench] step {ms_step:.3f} ms  map+plan {ms_map_plan:.3f}  conv1 {ms_conv1:.3f}  "
+          f"conv2 {ms_conv2:.3f}  (alone: map {ms_map:.3f}  plan {ms_plan:.3f}  unfused ln {ms_ln:.3f})",
           file=sys.stderr, flush=True)
 
     flops = 2.0 * P * C * C
@@ -253,7 +259,8 @@ def main():
                      "achieved": conv_tflops, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": conv_tflops / PEAK_BF16_TFLOPS, "traffic": traffic},
         "components": {
-            "map_build_ms": ms_map, "plan_build_ms": ms_plan, "conv_ms": ms_conv,
+            "map_and_plan_ms": ms_map_plan, "map_build_ms": ms_map, "plan_build_ms": ms_plan,
+            "conv_ms": ms_conv,
             "conv1_ln_silu_ms": ms_conv1, "conv2_residual_ms": ms_conv2,
             "unfused_ln_silu_ms": ms_ln,
             "map_build_gbps": map_gbps, "map_build_frac_hbm": map_gbps / PEAK_HBM_GBPS,

@@ -815,11 +815,14 @@ extern "C" int sc_conv_plan_size(int64_t n_q, int64_t kernel_rows, size_t *bytes
     return SC_OK;
 }
 
-extern "C" int sc_conv_plan_build(const sc_conv_config *cfg, const int32_t *d_coords, int64_t n_in,
-                                  const int32_t *d_map, int64_t n_q, void *d_plan, size_t plan_bytes,
-                                  sc_stream stream)
+namespace {
+
+// Validates a plan call and fills the kernel arguments (the map may be NULL
+// for the ordering half).
+int plan_args(const sc_conv_config *cfg, const int32_t *d_coords, int64_t n_in, const int32_t *d_map,
+              int64_t n_q, void *d_plan, size_t plan_bytes, bool need_coords, bool need_map, PlanArgs &a,
+              PlanLayout &L)
 {
-    clear_error();
     int rc = validate_config(cfg);
     if (rc) return rc;
     const int64_t K = cfg->kernel_d * cfg->kernel_h * cfg->kernel_w;
@@ -828,15 +831,18 @@ extern "C" int sc_conv_plan_build(const sc_conv_config *cfg, const int32_t *d_co
         return fail(SC_ERR_SHAPE, "conv plan needs 0 <= n_q <= n_in <= i32::MAX");
     if (!d_plan) return fail(SC_ERR_NULL, "conv plan buffer is NULL");
     if ((uintptr_t)d_plan % 256 != 0) return fail(SC_ERR_WORKSPACE, "conv plan buffer must be 256-byte aligned");
-    const PlanLayout L = plan_layout(n_q, K);
+    L = plan_layout(n_q, K);
     if (plan_bytes < L.total)
         return fail(SC_ERR_WORKSPACE, "conv plan buffer too small: got " + std::to_string(plan_bytes) + " need " +
                                           std::to_string(L.total));
-    if (n_q > 0 && (!d_coords || !d_map)) return fail(SC_ERR_NULL, "conv plan: coords or map is NULL");
+    if (n_q > 0 && need_coords && !d_coords) return fail(SC_ERR_NULL, "conv plan: coords is NULL");
+    if (n_q > 0 && need_map && !d_map) return fail(SC_ERR_NULL, "conv plan: map is NULL");
     if ((uintptr_t)d_coords % 16 != 0) return fail(SC_ERR_SHAPE, "coords must be 16-byte aligned");
+    if (L.n_tiles > INT32_MAX) return fail(SC_ERR_OVERFLOW, "conv plan tile count overflow");
+    if (L.grid_cap / kPlanGridBlock + (n_q + kPlanGridBlock - 1) / kPlanGridBlock > INT32_MAX)
+        return fail(SC_ERR_OVERFLOW, "conv plan grid overflow");
 
     char *b = static_cast<char *>(d_plan);
-    PlanArgs a;
     a.coords = reinterpret_cast<const int4 *>(d_coords);
     a.map = d_map;
     a.n_q = n_q;
@@ -857,8 +863,12 @@ extern "C" int sc_conv_plan_build(const sc_conv_config *cfg, const int32_t *d_co
     a.brick_cap = L.brick_cap;
     a.n_bsum = L.n_bsum;
     a.grid_cap = L.grid_cap;
+    return SC_OK;
+}
 
-    hipStream_t s = as_stream(stream);
+int launch_plan_order(const PlanArgs &a, const PlanLayout &L, hipStream_t s)
+{
+    const int64_t n_q = a.n_q;
     plan_init_kernel<<<grid_for(L.n_tiles * kPlanTileRows, kThreads, 1024), kThreads, 0, s>>>(a);
     SC_LAUNCH_CHECK("plan_init_kernel launch");
     if (n_q == 0) return SC_OK;
@@ -875,11 +885,9 @@ extern "C" int sc_conv_plan_build(const sc_conv_config *cfg, const int32_t *d_co
     SC_LAUNCH_CHECK("plan_prep_kernel launch");
     plan_place_kernel<<<grid_for(n_q, kThreads, 8192), kThreads, 0, s>>>(a);
     SC_LAUNCH_CHECK("plan_place_kernel launch");
-    if (grid_blocks > INT32_MAX) return fail(SC_ERR_OVERFLOW, "conv plan grid overflow");
     // grid mode uses grid_blocks cell blocks + row_blocks duplicate-row blocks
     const int64_t row_blocks = (n_q + kPlanGridBlock - 1) / kPlanGridBlock;
     const int64_t scan_blocks = grid_blocks + row_blocks > L.n_bsum ? grid_blocks + row_blocks : L.n_bsum;
-    if (scan_blocks > INT32_MAX) return fail(SC_ERR_OVERFLOW, "conv plan grid overflow");
     plan_scan1_kernel<<<(unsigned)scan_blocks, kThreads, 0, s>>>(a);
     SC_LAUNCH_CHECK("plan_scan1_kernel launch");
     plan_scan2_kernel<<<1, kThreads, 0, s>>>(a);
@@ -891,8 +899,52 @@ extern "C" int sc_conv_plan_build(const sc_conv_config *cfg, const int32_t *d_co
     SC_LAUNCH_CHECK("plan_emit_kernel launch");
     plan_fix_kernel<<<grid_for(L.brick_cap, kThreads / 64, 2048), kThreads, 0, s>>>(a);
     SC_LAUNCH_CHECK("plan_fix_kernel launch");
-    if (L.n_tiles > INT32_MAX) return fail(SC_ERR_OVERFLOW, "conv plan tile count overflow");
+    return SC_OK;
+}
+
+int launch_plan_tables(const PlanArgs &a, const PlanLayout &L, hipStream_t s)
+{
+    if (a.n_q == 0) return SC_OK;
     plan_tiles_kernel<<<(unsigned)L.n_tiles, kTileThreads, 0, s>>>(a);
     SC_LAUNCH_CHECK("plan_tiles_kernel launch");
     return SC_OK;
+}
+
+}  // namespace
+
+extern "C" int sc_conv_plan_build(const sc_conv_config *cfg, const int32_t *d_coords, int64_t n_in,
+                                  const int32_t *d_map, int64_t n_q, void *d_plan, size_t plan_bytes,
+                                  sc_stream stream)
+{
+    clear_error();
+    PlanArgs a;
+    PlanLayout L;
+    int rc = plan_args(cfg, d_coords, n_in, d_map, n_q, d_plan, plan_bytes, true, true, a, L);
+    if (rc) return rc;
+    hipStream_t s = as_stream(stream);
+    rc = launch_plan_order(a, L, s);
+    if (rc) return rc;
+    return launch_plan_tables(a, L, s);
+}
+
+extern "C" int sc_conv_plan_order(const sc_conv_config *cfg, const int32_t *d_coords, int64_t n_in, int64_t n_q,
+                                  void *d_plan, size_t plan_bytes, sc_stream stream)
+{
+    clear_error();
+    PlanArgs a;
+    PlanLayout L;
+    int rc = plan_args(cfg, d_coords, n_in, nullptr, n_q, d_plan, plan_bytes, true, false, a, L);
+    if (rc) return rc;
+    return launch_plan_order(a, L, as_stream(stream));
+}
+
+extern "C" int sc_conv_plan_tables(const sc_conv_config *cfg, const int32_t *d_map, int64_t n_in, int64_t n_q,
+                                   void *d_plan, size_t plan_bytes, sc_stream stream)
+{
+    clear_error();
+    PlanArgs a;
+    PlanLayout L;
+    int rc = plan_args(cfg, nullptr, n_in, d_map, n_q, d_plan, plan_bytes, false, true, a, L);
+    if (rc) return rc;
+    return launch_plan_tables(a, L, as_stream(stream));
 }

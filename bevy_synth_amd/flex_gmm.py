@@ -254,6 +254,54 @@ def conv_plan_build_into(cfg: SparseSubmConvConfig, coords: torch.Tensor, neighb
     return ConvPlan(buf, n_in, n_q, K)
 
 
+def conv_plan_order_into(cfg: SparseSubmConvConfig, coords: torch.Tensor, n_q: int,
+                         buf: torch.Tensor) -> None:
+    """First half of the plan build (sc_conv_plan_order): the row order, from
+    the coords alone, so it can run while the map is being built."""
+    check(_capi.load().sc_conv_plan_order(
+        ctypes.byref(cfg.to_c()), _ptr(coords), coords.shape[0], int(n_q), _ptr(buf), buf.numel(),
+        _stream()))
+
+
+def conv_plan_tables_into(cfg: SparseSubmConvConfig, neighbor_rows: torch.Tensor, n_in: int,
+                          buf: torch.Tensor) -> ConvPlan:
+    """Second half (sc_conv_plan_tables): the halo tables, from the map; after
+    both the order and the map build."""
+    n_q, K = neighbor_rows.shape[0], kernel_rows(cfg)
+    check(_capi.load().sc_conv_plan_tables(
+        ctypes.byref(cfg.to_c()), _ptr(neighbor_rows), int(n_in), n_q, _ptr(buf), buf.numel(),
+        _stream()))
+    return ConvPlan(buf, int(n_in), n_q, K)
+
+
+_AUX_STREAMS = {}
+
+
+def _aux_stream(device: torch.device) -> torch.cuda.Stream:
+    """One side stream per device (default priority) for overlapped builds."""
+    key = torch.device(device).index if torch.device(device).index is not None else torch.cuda.current_device()
+    if key not in _AUX_STREAMS:
+        _AUX_STREAMS[key] = torch.cuda.Stream(device=key)
+    return _AUX_STREAMS[key]
+
+
+def map_and_plan_into(cfg: SparseSubmConvConfig, coords: torch.Tensor, neighbor_rows: torch.Tensor,
+                      workspace: torch.Tensor, plan_buf: torch.Tensor) -> ConvPlan:
+    """The neighbour map and its conv plan, with the plan's row order (which
+    reads only the coords) built on a side stream while the map is built on
+    the current one; the halo tables follow on the current stream once both
+    are done.  Same result as neighbor_map_build_into + conv_plan_build_into."""
+    main = torch.cuda.current_stream(coords.device)
+    aux = _aux_stream(coords.device)
+    n_q = neighbor_rows.shape[0]
+    aux.wait_stream(main)
+    with torch.cuda.stream(aux):
+        conv_plan_order_into(cfg, coords, n_q, plan_buf)
+    neighbor_map_build_into(cfg, coords, neighbor_rows, workspace, query_rows=n_q)
+    main.wait_stream(aux)
+    return conv_plan_tables_into(cfg, neighbor_rows, coords.shape[0], plan_buf)
+
+
 def build_conv_plan(cfg: SparseSubmConvConfig, coords: torch.Tensor,
                     neighbor_rows: torch.Tensor) -> ConvPlan:
     """Allocates and builds the conv plan of ``neighbor_rows`` (built from ``coords``)."""

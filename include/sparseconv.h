@@ -214,6 +214,20 @@ int sc_conv_plan_build(const sc_conv_config *cfg, const int32_t *d_coords, int64
                        sc_stream stream);
 
 /*
+ * sc_conv_plan_build in two halves, so that the first can overlap the map
+ * build on another stream: sc_conv_plan_order reads only the coords (the row
+ * order: query rows [0, n_q) of d_coords [n_in][4]); sc_conv_plan_tables then
+ * reads the map (the per-tile halo tables) and must run after both the
+ * order (same plan buffer) and the map build are complete -- stream order or
+ * an event.  Same arguments as sc_conv_plan_build; together they write the
+ * same plan.
+ */
+int sc_conv_plan_order(const sc_conv_config *cfg, const int32_t *d_coords, int64_t n_in, int64_t n_q,
+                       void *d_plan, size_t plan_bytes, sc_stream stream);
+int sc_conv_plan_tables(const sc_conv_config *cfg, const int32_t *d_map, int64_t n_in, int64_t n_q,
+                        void *d_plan, size_t plan_bytes, sc_stream stream);
+
+/*
  * Weights packed for the planned conv: per (group, 128-output-channel tile,
  * offset k, 32-input-channel chunk, 16-channel block) one contiguous
  * fragment in MFMA operand order.  It has no counterpart in the reference's

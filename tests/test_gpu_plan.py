@@ -123,6 +123,33 @@ def test_plan_structure(which):
             assert np.array_equal(h["lmap"][t], h2["lmap"][t])
 
 
+@pytest.mark.parametrize("q", [None, 9000])
+def test_overlapped_map_and_plan_matches_separate_builds(q):
+    """map_and_plan_into (plan order on a side stream during the map build,
+    tables after) == neighbor map build + sc_conv_plan_build on one stream."""
+    coords = synth.config1_coords()
+    cfg = F.SparseSubmConvConfig(32, 32)
+    cd = dev(coords)
+    n_q = len(coords) if q is None else q
+    ref_nbr = F.neighbor_rows_tensor_from_coords_tensor(cfg, cd, query_rows=n_q)
+    ref = F.build_conv_plan(cfg, cd, ref_nbr).to_host()
+    nbr = torch.full((n_q, 27), -7, dtype=torch.int32, device="cuda")
+    ws = F.NeighborMapWorkspace().get(len(coords))
+    buf = torch.empty(F.conv_plan_bytes(n_q, 27), dtype=torch.uint8, device="cuda")
+    for _ in range(3):  # repeated builds into the same buffers
+        plan = F.map_and_plan_into(cfg, cd, nbr, ws, buf)
+        torch.cuda.synchronize()
+        assert torch.equal(nbr, ref_nbr)
+        h = plan.to_host()
+        for key in ("order", "tile_u", "overflow"):
+            assert np.array_equal(h[key], ref[key]), key
+        for t in range(h["n_tiles"]):
+            U = h["tile_u"][t]
+            if U <= F.PLAN_HALO_MAX:
+                assert np.array_equal(h["halo"][t, :U], ref["halo"][t, :U])
+                assert np.array_equal(h["lmap"][t], ref["lmap"][t])
+
+
 @pytest.mark.parametrize("cin,cout,groups,wdt", [(64, 128, 1, "bf16"), (96, 200, 1, "bf16"),
                                                   (64, 64, 2, "bf16"), (128, 64, 1, "i8")])
 def test_weight_pack_layout(cin, cout, groups, wdt):
