@@ -123,10 +123,9 @@ __device__ inline void offset_of(const KernelShape &ks, int k, int o[3])
     const int kh = rem / ks.KW, kw = rem - kh * ks.KW;
     const int d[3] = {ks.sign[0] * (kd - ks.KD / 2), ks.sign[1] * (kh - ks.KH / 2),
                       ks.sign[2] * (kw - ks.KW / 2)};
-    o[0] = o[1] = o[2] = 0;
-    o[ks.order[0]] = d[0];
-    o[ks.order[1]] = d[1];
-    o[ks.order[2]] = d[2];
+    // o[order[j]] = d[j], written as selections (no computed local address)
+    for (int a = 0; a < 3; ++a)
+        o[a] = ks.order[0] == a ? d[0] : (ks.order[1] == a ? d[1] : (ks.order[2] == a ? d[2] : 0));
 }
 
 // ---------------------------------------------------- buffer loads
@@ -146,6 +145,19 @@ __device__ inline uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off)
 {
     const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
     return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ inline uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    return make_uint2(v.x, v.y);
+}
+
+__device__ inline uint32_t bload4(__amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }
 
 // ---------------------------------------------------- activations

@@ -22,8 +22,17 @@
 //
 // When the bbox holds at most 32 cells per row (and the workspace has room),
 // the "table" is a dense bbox-indexed grid of rows instead: the slot of a key
-// is the key itself, so insertion is one atomicMin on a distinct word and a
+// is the key itself, so insertion is one atomicMax of ~row on a distinct word
+// (empty cells are 0, the lowest row of duplicates wins) and a
 // query one load, and the neighbours of nearby voxels share cache lines.
+//
+// When the rows are strictly increasing in (b, x, y, z) (checked by the bbox
+// pass: sorted and unique, the order an argwhere over a grid produces), a
+// row's index is the rank of its cell among the occupied cells. The table is
+// then a rank bitmap: per 32 cells, 32 occupancy bits and the row of the first
+// occupied cell (8 B per 32 cells, 1/16 of the dense grid, small enough to stay
+// in L2), built by one writer per word with no atomics; a query is one 8-byte
+// load and a popcount. Any other row order takes the modes above.
 #include <climits>
 
 #include "sc_common.hpp"
@@ -37,11 +46,32 @@ constexpr uint32_t kStatusNegative = 1u;
 constexpr int kMaxStagedRows = 256;
 constexpr int kMaxStagedOffsets = 512;
 
+// Table budgets, in bbox cells, that the workspace affords: the dense grid
+// (4 B per cell, at most 32 cells per row) and the rank bitmap (8 B per 32 cells).
+struct Limits {
+    uint64_t dense_cells;
+    uint64_t bitmap_cells;
+};
+
+struct Plan {
+    int mode;  // 0: no table (error), 1: 32-bit keys packed with rows, 2: 64-bit keys,
+               // 3: row-only table compared through the coords, 4: dense grid,
+               // 5: rank bitmap (rows strictly increasing in (b, x, y, z))
+    uint64_t total;  // bbox cells (valid for modes 1, 2, 4, 5)
+    int32_t lo[4];
+    int32_t hi[4];
+    uint64_t ext[4];
+};
+
 struct alignas(16) NbrHeader {
     int32_t bmin[4];
     int32_t bmax[4];
     uint32_t status;
-    uint32_t pad[55];
+    uint32_t unsorted;  // nonzero unless the rows are strictly increasing in (b, x, y, z)
+    int32_t mode;       // the table mode chosen (Plan::mode), a diagnostic for callers
+    uint32_t pad0;
+    Plan plan;          // derived once from the fields above, read by every later kernel
+    uint8_t pad[kHeaderBytes - 48 - sizeof(Plan)];
 };
 static_assert(sizeof(NbrHeader) == kHeaderBytes, "header size");
 
@@ -60,13 +90,15 @@ inline uint64_t dense_cells_for(int64_t n)
     return c < (1u << 16) ? (1u << 16) : c;
 }
 
-constexpr size_t kPartialBytes = 1024 * 9 * 4;  // bbox partials (kBboxBlocks x 9 ints)
+constexpr size_t kPartialBytes = 1024 * 10 * 4;  // bbox partials (kBboxBlocks x 10 ints)
+constexpr size_t kOffsetTableBytes = kMaxStagedOffsets * 16;  // per offset {dx, dy, dz, cell delta}
+constexpr size_t kFixedBytes = kHeaderBytes + kPartialBytes + kOffsetTableBytes;
 
 inline size_t workspace_bytes_for(int64_t n)
 {
     const size_t hash_bytes = (size_t)table_capacity(n) * 12u;
     const size_t dense_bytes = (size_t)dense_cells_for(n) * 4u;
-    return kHeaderBytes + kPartialBytes + (hash_bytes > dense_bytes ? hash_bytes : dense_bytes);
+    return kFixedBytes + (hash_bytes > dense_bytes ? hash_bytes : dense_bytes);
 }
 
 // splitmix64 finaliser (Steele, Lea & Flood, OOPSLA 2014).
@@ -77,16 +109,7 @@ __device__ inline uint64_t mix64(uint64_t z)
     return z ^ (z >> 31);
 }
 
-struct Plan {
-    int mode;  // 0: no table (error), 1: 32-bit keys packed with rows, 2: 64-bit keys,
-               // 3: row-only table compared through the coords, 4: dense grid
-    uint64_t total;  // bbox cells (valid for modes 1, 2, 4)
-    int32_t lo[4];
-    int32_t hi[4];
-    uint64_t ext[4];
-};
-
-__device__ inline Plan make_plan(const NbrHeader *h, uint64_t dense_cells)
+__device__ inline Plan make_plan(const NbrHeader *h, Limits lim)
 {
     Plan p;
     p.mode = 0;
@@ -104,7 +127,12 @@ __device__ inline Plan make_plan(const NbrHeader *h, uint64_t dense_cells)
         total *= p.ext[j];
     }
     p.total = total;
-    p.mode = ovf ? 3 : (total <= dense_cells ? 4 : (total <= 0xffffffffull ? 1 : 2));
+    if (ovf)
+        p.mode = 3;
+    else if (h->unsorted == 0 && total <= lim.bitmap_cells)
+        p.mode = 5;
+    else
+        p.mode = total <= lim.dense_cells ? 4 : (total <= 0xffffffffull ? 1 : 2);
     return p;
 }
 
@@ -135,82 +163,127 @@ __global__ void nm_header_init_kernel(NbrHeader *h)
         h->bmax[j] = INT_MIN;
     }
     h->status = 0;
+    h->unsorted = 0;
+    h->mode = 0;
 }
 
-// Fills the table region the plan uses with all-ones (EMPTY keys, EMPTY rows,
-// or -1 grid cells): cap*12 bytes for the hash modes, total*4 for the grid.
-__global__ void nm_table_init_kernel(const NbrHeader *h, uint64_t *words, uint64_t cap,
-                                     uint64_t dense_cells)
+// Rank bitmap lookup: word w of the bitmap holds the occupancy bits of cells
+// 32w..32w+31 (low half) and the row of its first occupied cell (high half).
+// With rows strictly increasing in key order, a cell's row is its rank among
+// the occupied cells: that first row plus the occupied cells below it in the word.
+__device__ inline int32_t rank_lookup(const uint64_t *__restrict__ words, uint64_t q)
 {
-    const Plan p = make_plan(h, dense_cells);
+    const uint64_t w = words[q >> 5];
+    const uint32_t bits = (uint32_t)w, b = (uint32_t)q & 31u;
+    if (!((bits >> b) & 1u)) return SC_INVALID_NEIGHBOR_ROW;
+    return (int32_t)(uint32_t)(w >> 32) + __builtin_popcount(bits & ((1u << b) - 1u));
+}
+
+// Fills the table region the plan uses: all-ones (EMPTY keys, EMPTY rows)
+// over cap*12 bytes for the hash modes; zero (no cell occupied) over the
+// grid's total*4 bytes and the rank bitmap's ceil(total/32) words.
+__global__ void nm_table_init_kernel(const NbrHeader *__restrict__ h, uint64_t *words, uint64_t cap)
+{
+    const Plan p = h->plan;
     if (p.mode == 0) return;
-    const uint64_t n_words = p.mode == 4 ? (p.total + 1) / 2 : cap + cap / 2;
+    uint64_t n_words = cap + cap / 2, fill = kEmpty64;
+    if (p.mode == 4) {
+        n_words = (p.total + 1) / 2;
+        fill = 0;
+    }
+    if (p.mode == 5) {
+        n_words = (p.total + 31) / 32;
+        fill = 0;
+    }
     const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_words; i += stride)
-        words[i] = kEmpty64;
+        words[i] = fill;
 }
 
-// Per-block bbox partials (4 min, 4 max, negative flag), no atomics.
+__device__ inline bool coord_less(const int4 a, const int4 b)
+{
+    if (a.x != b.x) return a.x < b.x;
+    if (a.y != b.y) return a.y < b.y;
+    if (a.z != b.z) return a.z < b.z;
+    return a.w < b.w;
+}
+
+// Per-block bbox partials (4 min, 4 max, negative flag, order flag), no atomics.
 constexpr int kBboxBlocks = 1024;
+constexpr int kPartialInts = 10;
 
 __global__ __launch_bounds__(256) void nm_bbox_partial_kernel(const int4 *__restrict__ coords, int64_t n,
                                                               int32_t *__restrict__ partials)
 {
     int mn[4] = {INT_MAX, INT_MAX, INT_MAX, INT_MAX};
     int mx[4] = {INT_MIN, INT_MIN, INT_MIN, INT_MIN};
-    int neg = 0;
+    int neg = 0, uns = 0;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-        const int4 c = coords[i];
-        const int v[4] = {c.x, c.y, c.z, c.w};
+    // Wave-uniform loop: lane l holds row w0 + l, so lane l - 1 holds its predecessor.
+    for (int64_t w0 = (int64_t)blockIdx.x * blockDim.x + wave * 64; w0 < n; w0 += stride) {
+        const int64_t i = w0 + lane;
+        const bool valid = i < n;
+        const int4 c = valid ? coords[i] : make_int4(0, 0, 0, 0);
+        int4 prev = make_int4(__shfl_up(c.x, 1), __shfl_up(c.y, 1), __shfl_up(c.z, 1), __shfl_up(c.w, 1));
+        if (lane == 0 && valid && i > 0) prev = coords[i - 1];
+        if (valid) {
+            const int v[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            mn[j] = min(mn[j], v[j]);
-            mx[j] = max(mx[j], v[j]);
-            neg |= v[j] < 0;
+            for (int j = 0; j < 4; ++j) {
+                mn[j] = min(mn[j], v[j]);
+                mx[j] = max(mx[j], v[j]);
+                neg |= v[j] < 0;
+            }
+            if (i > 0) uns |= !coord_less(prev, c);
         }
     }
-    __shared__ int s_red[4][9];  // per wave: 4 min, 4 max, neg
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __shared__ int s_red[4][kPartialInts];  // per wave: 4 min, 4 max, neg, unsorted
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         mn[j] = wave_min_i32(mn[j]);
         mx[j] = wave_max_i32(mx[j]);
     }
     neg = wave_max_i32(neg);
+    uns = wave_max_i32(uns);
     if (lane == 0) {
         for (int j = 0; j < 4; ++j) {
             s_red[wave][j] = mn[j];
             s_red[wave][4 + j] = mx[j];
         }
         s_red[wave][8] = neg;
+        s_red[wave][9] = uns;
     }
     __syncthreads();
-    if (threadIdx.x < 9) {
+    if (threadIdx.x < kPartialInts) {
         const int j = threadIdx.x;
         const int nw = blockDim.x >> 6;
         int v = s_red[0][j];
         for (int w = 1; w < nw; ++w) v = j < 4 ? min(v, s_red[w][j]) : max(v, s_red[w][j]);
-        partials[blockIdx.x * 9 + j] = v;
+        partials[blockIdx.x * kPartialInts + j] = v;
     }
 }
 
-// One block: reduces the partials and writes the header (bbox + status).
+// One block: reduces the partials and writes the header (bbox, status, order
+// flag, and the mode every later kernel derives from them).
 __global__ __launch_bounds__(256) void nm_bbox_final_kernel(const int32_t *__restrict__ partials,
-                                                            int nblocks, NbrHeader *h)
+                                                            int nblocks, NbrHeader *h, Limits lim,
+                                                            KernelShape ks, int4 *__restrict__ otab)
 {
     int mn[4] = {INT_MAX, INT_MAX, INT_MAX, INT_MAX};
     int mx[4] = {INT_MIN, INT_MIN, INT_MIN, INT_MIN};
-    int neg = 0;
+    int neg = 0, uns = 0;
     for (int b = threadIdx.x; b < nblocks; b += blockDim.x) {
+        const int32_t *pb = partials + b * kPartialInts;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            mn[j] = min(mn[j], partials[b * 9 + j]);
-            mx[j] = max(mx[j], partials[b * 9 + 4 + j]);
+            mn[j] = min(mn[j], pb[j]);
+            mx[j] = max(mx[j], pb[4 + j]);
         }
-        neg |= partials[b * 9 + 8];
+        neg |= pb[8];
+        uns |= pb[9];
     }
-    __shared__ int s_red[4][9];
+    __shared__ int s_red[4][kPartialInts];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -218,15 +291,17 @@ __global__ __launch_bounds__(256) void nm_bbox_final_kernel(const int32_t *__res
         mx[j] = wave_max_i32(mx[j]);
     }
     neg = wave_max_i32(neg);
+    uns = wave_max_i32(uns);
     if (lane == 0) {
         for (int j = 0; j < 4; ++j) {
             s_red[wave][j] = mn[j];
             s_red[wave][4 + j] = mx[j];
         }
         s_red[wave][8] = neg;
+        s_red[wave][9] = uns;
     }
     __syncthreads();
-    if (threadIdx.x < 9) {
+    if (threadIdx.x < kPartialInts) {
         const int j = threadIdx.x;
         int v = s_red[0][j];
         for (int w = 1; w < (int)(blockDim.x >> 6); ++w) v = j < 4 ? min(v, s_red[w][j]) : max(v, s_red[w][j]);
@@ -234,25 +309,83 @@ __global__ __launch_bounds__(256) void nm_bbox_final_kernel(const int32_t *__res
             h->bmin[j] = v;
         else if (j < 8)
             h->bmax[j - 4] = v;
-        else
+        else if (j == 8)
             h->status = v ? kStatusNegative : 0u;
+        else
+            h->unsorted = (uint32_t)v;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const Plan p = make_plan(h, lim);
+        h->plan = p;
+        h->mode = p.mode;
+    }
+    __syncthreads();
+    // Offset table for the query: {dx, dy, dz} and the 32-bit cell delta of
+    // the offset (wraps; only used for neighbours inside the bbox).
+    const Plan p = h->plan;
+    const uint32_t sy = (uint32_t)p.ext[3], sx = (uint32_t)(p.ext[2] * p.ext[3]);
+    for (int k = threadIdx.x; k < ks.K && k < kMaxStagedOffsets; k += blockDim.x) {
+        int o[3];
+        offset_of(ks, k, o);
+        otab[k] = make_int4(o[0], o[1], o[2], (int)((uint32_t)o[0] * sx + (uint32_t)o[1] * sy + (uint32_t)o[2]));
     }
 }
 
 __global__ __launch_bounds__(256) void nm_insert_kernel(const int4 *__restrict__ coords, int64_t n,
                                                         NbrHeader *h, uint64_t *keys, uint32_t *rows,
-                                                        uint64_t mask, uint64_t dense_cells)
+                                                        uint64_t mask)
 {
-    const Plan p = make_plan(h, dense_cells);
+    const Plan p = h->plan;
     const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (p.mode == 0) return;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    if (p.mode == 5) {
+        // Rank bitmap (words start at zero): a word receives its occupancy bits
+        // and the row of its first occupied cell. The keys strictly increase,
+        // so the rows of a word are consecutive (at most 32). Lane l of a wave
+        // holds row w0 + l: a segmented suffix OR over the lanes of one word
+        // collects their bits, and the word's first lane in this wave ORs them
+        // in (with its row when it is the word's first row). A word split
+        // across two waves gets one OR from each; ORs commute.
+        const int lane = threadIdx.x & 63;
+        for (int64_t w0 = tid - lane; w0 < n; w0 += stride) {
+            const int64_t r = w0 + lane;
+            const bool valid = r < n;
+            uint32_t q = 0, w = 0xffffffffu;  // total <= 2^32 - 1 cells: 32-bit keys
+            if (valid) {
+                const int4 c = coords[r];
+                q = (uint32_t)pack_key(p, c.x, c.y, c.z, c.w);
+                w = q >> 5;
+            }
+            uint32_t wp = __shfl_up(w, 1);
+            if (lane == 0) {
+                wp = 0xfffffffeu;  // no predecessor: differs from every word
+                if (r > 0) {
+                    const int4 cp = coords[r - 1];
+                    wp = (uint32_t)pack_key(p, cp.x, cp.y, cp.z, cp.w) >> 5;
+                }
+            }
+            uint32_t bits = valid ? 1u << (q & 31u) : 0u;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const uint32_t ob = __shfl_down(bits, d), ow = __shfl_down(w, d);
+                if (lane + d < 64 && ow == w) bits |= ob;
+            }
+            const bool head = wp != w;  // the word's first row
+            if (valid && (head || lane == 0))
+                atomicOr((unsigned long long *)&keys[w],
+                         (head ? (unsigned long long)(uint32_t)r << 32 : 0ull) | bits);
+        }
+        return;
+    }
     uint32_t *grid = reinterpret_cast<uint32_t *>(keys);
     for (int64_t r = tid; r < n; r += stride) {
         const int4 c = coords[r];
         if (p.mode == 4) {
-            // cells start at 0xffffffff: the unsigned minimum keeps the lowest row
-            atomicMin(&grid[pack_key(p, c.x, c.y, c.z, c.w)], (uint32_t)r);
+            // cells hold ~row and start at 0 (empty): the unsigned maximum keeps
+            // the lowest row, and an empty cell decodes as ~0 = -1
+            atomicMax(&grid[pack_key(p, c.x, c.y, c.z, c.w)], ~(uint32_t)r);
             continue;
         }
         if (p.mode == 3) {
@@ -294,31 +427,43 @@ __global__ __launch_bounds__(256) void nm_insert_kernel(const int4 *__restrict__
     }
 }
 
-// Dense-grid query: a row's neighbour at offset k is cell base[r] + delta[k]
-// (32-bit mixed-radix strides), valid when the neighbour lies in the bbox.
-// Entries (r, k) are walked incrementally (no division), four loads in
-// flight per lane before their stores.
+// Dense-grid and rank-bitmap query: a row's neighbour at offset k is cell
+// base[r] + delta[k] (32-bit mixed-radix strides), valid when the neighbour
+// lies in the bbox. Entries (r, k) are walked incrementally (no division),
+// four loads in flight per lane before their stores.
+template <bool kRank>
 __device__ inline void query_dense(const int4 *s_coord, const int *s_off, const uint32_t *s_base,
                                    const int *s_delta, int nrows, int K, const Plan &p,
-                                   const uint32_t *__restrict__ grid, int32_t *__restrict__ out)
+                                   const uint64_t *__restrict__ table, int32_t *__restrict__ out)
 {
+    const uint32_t *grid = reinterpret_cast<const uint32_t *>(table);
     const int total = nrows * K;
     const int step_r = (int)blockDim.x / K, step_k = (int)blockDim.x % K;
     int r = (int)threadIdx.x / K, k = (int)threadIdx.x % K;
     for (int e0 = threadIdx.x; e0 < total; e0 += 4 * (int)blockDim.x) {
-        int32_t v[4];
+        // all four loads issue before any result is used
+        uint64_t raw[4];
+        uint32_t bit[4];
         int idx[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int e = e0 + u * (int)blockDim.x;
             idx[u] = e;
-            v[u] = SC_INVALID_NEIGHBOR_ROW;
+            raw[u] = 0;  // decodes to -1 in both tables
+            bit[u] = 0;
             if (e < total) {
                 const int4 c = s_coord[r];
                 const int nx = c.y + s_off[3 * k], ny = c.z + s_off[3 * k + 1], nz = c.w + s_off[3 * k + 2];
                 if (nx >= p.lo[1] && nx <= p.hi[1] && ny >= p.lo[2] && ny <= p.hi[2] && nz >= p.lo[3] &&
-                    nz <= p.hi[3])
-                    v[u] = (int32_t)grid[s_base[r] + (uint32_t)s_delta[k]];
+                    nz <= p.hi[3]) {
+                    const uint32_t q = s_base[r] + (uint32_t)s_delta[k];
+                    if (kRank) {
+                        raw[u] = table[q >> 5];
+                        bit[u] = q & 31u;
+                    } else {
+                        raw[u] = grid[q];
+                    }
+                }
             }
             r += step_r;
             k += step_k;
@@ -328,8 +473,176 @@ __device__ inline void query_dense(const int4 *s_coord, const int *s_off, const 
             }
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-            if (idx[u] < total) out[idx[u]] = v[u];
+        for (int u = 0; u < 4; ++u) {
+            int32_t v = (int32_t)~(uint32_t)raw[u];  // grid cells hold ~row
+            if (kRank) {
+                // empty word or cell: no bit set -> -1
+                const uint32_t bits = (uint32_t)raw[u];
+                v = (bits >> bit[u]) & 1u
+                        ? (int32_t)(uint32_t)(raw[u] >> 32) + __builtin_popcount(bits & ((1u << bit[u]) - 1u))
+                        : SC_INVALID_NEIGHBOR_ROW;
+            }
+            if (idx[u] < total) out[idx[u]] = v;
+        }
+    }
+}
+
+// Dense-grid and rank-bitmap query with one row per lane (rows_per_block ==
+// 256, K <= kCellwiseMaxK): the row's coord and base cell stay in registers,
+// the offset loop is uniform across the wave (offsets and cell deltas come
+// from the table the bbox pass writes, through scalar loads),
+// up to 27 lookups are in flight per lane, and the results pass through LDS
+// ([row][k], conflict-free for odd K) so that the block's rows*K map entries
+// leave as coalesced 16-byte stores.
+constexpr int kCellwiseMaxK = 32;
+constexpr int kCellChunk = 27;
+
+// Dynamic LDS of the query kernel, in ints: the larger of the row-wise
+// results (rows x K) and the entry-wise staging (3 + 1 ints per offset, then
+// 4 + 1 ints per row).
+inline int query_lds_ints(int64_t K, int rows_per_block)
+{
+    const int kst = K <= kMaxStagedOffsets ? (int)K : 0;
+    const int staged = 4 * kst + 5 * kMaxStagedRows;
+    const int rowwise = K <= kCellwiseMaxK ? rows_per_block * (int)K : 0;
+    return staged > rowwise ? staged : rowwise;
+}
+
+// The 3x3x3 kernel with unit axis signs (the decoder's submanifold conv):
+// offset k = (kd*3 + kh)*3 + kw is known at compile time, so its cell delta
+// is a signed sum of three per-launch strides and its bbox test an AND of
+// per-row "one step up / down along kernel axis j stays inside" flags.
+struct Cube3 {
+    uint32_t D[3];  // cell delta of +1 along kernel axis j (wraps)
+    int a[3];       // spatial axis (0 x, 1 y, 2 z) of kernel axis j
+    int s[3];       // its sign
+    int lo[3], hi[3];  // bbox bounds of that spatial axis
+};
+
+// Uniform int through a scalar register.
+__device__ inline int uniform_i32(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Selections by axis pick among register values (never a computed address
+// into a local struct, which would put the struct in scratch memory).
+__device__ inline Cube3 cube3_of(const KernelShape &ks, const Plan &p)
+{
+    Cube3 q;
+    const uint32_t sx = (uint32_t)uniform_i32((int)(uint32_t)(p.ext[2] * p.ext[3]));
+    const uint32_t sy = (uint32_t)uniform_i32((int)(uint32_t)p.ext[3]);
+    const int lx = uniform_i32(p.lo[1]), ly = uniform_i32(p.lo[2]), lz = uniform_i32(p.lo[3]);
+    const int hx = uniform_i32(p.hi[1]), hy = uniform_i32(p.hi[2]), hz = uniform_i32(p.hi[3]);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        const int a = uniform_i32(ks.order[j]);
+        q.a[j] = a;
+        q.s[j] = uniform_i32(ks.sign[j]);
+        const uint32_t st = a == 0 ? sx : (a == 1 ? sy : 1u);
+        q.D[j] = q.s[j] > 0 ? st : 0u - st;
+        q.lo[j] = a == 0 ? lx : (a == 1 ? ly : lz);
+        q.hi[j] = a == 0 ? hx : (a == 1 ? hy : hz);
+    }
+    return q;
+}
+
+template <bool kRank, bool kCube3>
+__device__ inline void query_cells(const int4 *__restrict__ coords, int64_t row0, int nrows, int K,
+                                   const int4 *__restrict__ otab, const Cube3 &cube, const Plan &p,
+                                   const uint64_t *__restrict__ table, uint32_t table_bytes, int *s_out,
+                                   int32_t *__restrict__ out)
+{
+    // Branch-free lookups: a neighbour outside the bbox gets an offset beyond
+    // the table's descriptor and reads 0, which decodes to -1 like an empty
+    // rank word or an empty grid cell.
+    // The descriptor must live in scalar registers (its inputs are uniform).
+    // readfirstlane returns a signed int: each half goes through uint32_t
+    // before widening, or a low half with bit 31 set would sign-extend into
+    // the high half of the address.
+    const uint64_t tp = (uint64_t)(uintptr_t)table;
+    const uint32_t tp_lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)tp);
+    const uint32_t tp_hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(tp >> 32));
+    const uint32_t tbytes = (uint32_t)__builtin_amdgcn_readfirstlane((int)table_bytes);
+    const __amdgpu_buffer_rsrc_t rt =
+        make_rsrc((const void *)(uintptr_t)(((uint64_t)tp_hi << 32) | tp_lo), tbytes);
+    const int rw = (int)threadIdx.x;  // row within the block
+    const bool valid = rw < nrows;
+    int4 c = make_int4(0, 0, 0, 0);
+    uint32_t base = 0;
+    if (valid) {
+        c = coords[row0 + rw];
+        base = (uint32_t)pack_key(p, c.x, c.y, c.z, c.w);
+    }
+    bool up[3] = {false, false, false}, dn[3] = {false, false, false};
+    if (kCube3) {
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int a = cube.a[j];
+            const int ca = a == 0 ? c.y : (a == 1 ? c.z : c.w);
+            up[j] = cube.s[j] > 0 ? ca < cube.hi[j] : ca > cube.lo[j];
+            dn[j] = cube.s[j] > 0 ? ca > cube.lo[j] : ca < cube.hi[j];
+        }
+    }
+    const int KK = kCube3 ? 27 : K;
+    int *so = s_out + rw * KK;
+    for (int k0 = 0; k0 < KK; k0 += kCellChunk) {
+        uint2 raw[kCellChunk];
+        uint32_t q[kCellChunk];
+#pragma unroll
+        for (int u = 0; u < kCellChunk; ++u) {
+            const int k = k0 + u;
+            if (k >= KK) break;
+            bool inside;
+            uint32_t delta = 0;
+            if (kCube3) {
+                const int e[3] = {k / 9 - 1, (k / 3) % 3 - 1, k % 3 - 1};
+                inside = valid;
+#pragma unroll
+                for (int j = 0; j < 3; ++j) {
+                    if (e[j] > 0) inside = inside && up[j];
+                    if (e[j] < 0) inside = inside && dn[j];
+                    delta += e[j] > 0 ? cube.D[j] : (e[j] < 0 ? 0u - cube.D[j] : 0u);
+                }
+            } else {
+                const int4 o = otab[k];  // uniform: scalar loads
+                const int nx = c.y + o.x, ny = c.z + o.y, nz = c.w + o.z;
+                inside = valid && nx >= p.lo[1] && nx <= p.hi[1] && ny >= p.lo[2] && ny <= p.hi[2] &&
+                         nz >= p.lo[3] && nz <= p.hi[3];
+                delta = (uint32_t)o.w;
+            }
+            q[u] = base + delta;
+            const uint32_t off = kRank ? (q[u] >> 5) << 3 : q[u] << 2;
+            if (kRank)
+                raw[u] = bload8(rt, inside ? off : kOobOffset);
+            else
+                raw[u].x = bload4(rt, inside ? off : kOobOffset);
+        }
+#pragma unroll
+        for (int u = 0; u < kCellChunk; ++u) {
+            const int k = k0 + u;
+            if (k >= KK) break;
+            int32_t v;
+            if (kRank) {
+                // rank = first row of the word + occupied cells below b; -1
+                // unless bit b is set (all-ones mask t selects the rank)
+                const uint32_t bits = raw[u].x, b = q[u] & 31u;
+                const int32_t t = __builtin_amdgcn_sbfe((int32_t)bits, b, 1);
+                const int32_t rank = (int32_t)(__builtin_popcount(__builtin_amdgcn_ubfe(bits, 0, b)) + raw[u].y);
+                v = (rank & t) | ~t;
+            } else {
+                v = (int32_t)~raw[u].x;  // grid cells hold ~row (0 = empty)
+            }
+            if (valid) so[k] = v;
+        }
+    }
+    __syncthreads();
+    const int n_ints = nrows * K;
+    if (((uintptr_t)out & 15u) == 0) {
+        const int n4 = n_ints >> 2;
+        int4 *dst4 = reinterpret_cast<int4 *>(out);
+        const int4 *src4 = reinterpret_cast<const int4 *>(s_out);
+        for (int i = threadIdx.x; i < n4; i += blockDim.x) dst4[i] = src4[i];
+        for (int i = (n4 << 2) + threadIdx.x; i < n_ints; i += blockDim.x) out[i] = s_out[i];
+    } else {
+        for (int i = threadIdx.x; i < n_ints; i += blockDim.x) out[i] = s_out[i];
     }
 }
 
@@ -339,34 +652,66 @@ __global__ __launch_bounds__(256) void nm_query_kernel(const int4 *__restrict__ 
                                                        const NbrHeader *__restrict__ h,
                                                        const uint64_t *__restrict__ keys,
                                                        const uint32_t *__restrict__ rows,
-                                                       uint64_t mask, uint64_t dense_cells,
+                                                       uint64_t mask, const int4 *__restrict__ otab,
                                                        int32_t *__restrict__ map)
 {
-    __shared__ int4 s_coord[kMaxStagedRows];
-    __shared__ uint32_t s_base[kMaxStagedRows];
-    __shared__ int s_off[kMaxStagedOffsets * 3];
-    __shared__ int s_delta[kMaxStagedOffsets];
+    // Row-wise path: the [row][k] results. Entry-wise paths: [staged offsets:
+    // 3 ints each][their cell deltas][staged rows: coords, base cells].
+    // Sized by query_lds_ints.
+    extern __shared__ __align__(16) int s_dyn[];
+    const int kst = ks.K <= kMaxStagedOffsets ? ks.K : 0;
+    int *s_off = s_dyn;
+    int *s_delta = s_dyn + 3 * kst;
+    int *s_mem = s_dyn + 4 * kst;
+    int4 *s_coord = reinterpret_cast<int4 *>(s_mem);
+    uint32_t *s_base = reinterpret_cast<uint32_t *>(s_mem + 4 * kMaxStagedRows);
     const int64_t row0 = (int64_t)blockIdx.x * rows_per_block;
     const int nrows = (int)min<int64_t>(rows_per_block, q_rows - row0);
-    const Plan p = make_plan(h, dense_cells);
+    const Plan p = h->plan;
     const bool staged = ks.K <= kMaxStagedOffsets;
+    const bool cellwise = p.mode == 4 || p.mode == 5;
+    // table bytes, addressed through a buffer descriptor on the row-wise path
+    const uint64_t tbytes = p.mode == 5 ? (p.total + 31) / 32 * 8 : p.total * 4;
+    const bool rowwise = cellwise && ks.K <= kCellwiseMaxK && rows_per_block == (int)blockDim.x &&
+                         tbytes <= kOobOffset;
+    int32_t *out = map + row0 * ks.K;
+    if (rowwise) {
+        const bool cube3 = ks.KD == 3 && ks.KH == 3 && ks.KW == 3 && abs(ks.sign[0]) == 1 &&
+                           abs(ks.sign[1]) == 1 && abs(ks.sign[2]) == 1;
+        const Cube3 cube = cube3_of(ks, p);
+        if (p.mode == 5 && cube3)
+            query_cells<true, true>(coords, row0, nrows, ks.K, otab, cube, p, keys, (uint32_t)tbytes, s_dyn,
+                                     out);
+        else if (p.mode == 5)
+            query_cells<true, false>(coords, row0, nrows, ks.K, otab, cube, p, keys, (uint32_t)tbytes, s_dyn,
+                                     out);
+        else if (cube3)
+            query_cells<false, true>(coords, row0, nrows, ks.K, otab, cube, p, keys, (uint32_t)tbytes, s_dyn,
+                                     out);
+        else
+            query_cells<false, false>(coords, row0, nrows, ks.K, otab, cube, p, keys, (uint32_t)tbytes, s_dyn,
+                                     out);
+        return;
+    }
     for (int i = threadIdx.x; i < nrows; i += blockDim.x) {
         const int4 c = coords[row0 + i];
         s_coord[i] = c;
-        if (p.mode == 4) s_base[i] = (uint32_t)pack_key(p, c.x, c.y, c.z, c.w);
+        if (cellwise) s_base[i] = (uint32_t)pack_key(p, c.x, c.y, c.z, c.w);
     }
     if (staged)
         for (int k = threadIdx.x; k < ks.K; k += blockDim.x) {
-            offset_of(ks, k, &s_off[3 * k]);
-            // 32-bit cell delta of the offset (wraps; only used inside the bbox)
-            s_delta[k] = (int)((uint32_t)s_off[3 * k] * (uint32_t)(p.ext[2] * p.ext[3]) +
-                               (uint32_t)s_off[3 * k + 1] * (uint32_t)p.ext[3] + (uint32_t)s_off[3 * k + 2]);
+            const int4 o = otab[k];
+            s_off[3 * k] = o.x;
+            s_off[3 * k + 1] = o.y;
+            s_off[3 * k + 2] = o.z;
+            s_delta[k] = o.w;
         }
     __syncthreads();
-    int32_t *out = map + row0 * ks.K;
-    if (p.mode == 4 && staged) {
-        query_dense(s_coord, s_off, s_base, s_delta, nrows, ks.K, p,
-                    reinterpret_cast<const uint32_t *>(keys), out);
+    if (cellwise && staged) {
+        if (p.mode == 5)
+            query_dense<true>(s_coord, s_off, s_base, s_delta, nrows, ks.K, p, keys, out);
+        else
+            query_dense<false>(s_coord, s_off, s_base, s_delta, nrows, ks.K, p, keys, out);
         return;
     }
     const uint32_t *grid = reinterpret_cast<const uint32_t *>(keys);
@@ -389,8 +734,10 @@ __global__ __launch_bounds__(256) void nm_query_kernel(const int4 *__restrict__ 
         // so is any neighbour outside the bbox of the coord set.
         const bool inside = p.mode != 0 && nx >= p.lo[1] && nx <= p.hi[1] && ny >= p.lo[2] &&
                             ny <= p.hi[2] && nz >= p.lo[3] && nz <= p.hi[3];
-        if (inside && p.mode == 4) {
-            found = (int32_t)grid[pack_key(p, c.x, (int32_t)nx, (int32_t)ny, (int32_t)nz)];
+        if (inside && p.mode == 5) {
+            found = rank_lookup(keys, pack_key(p, c.x, (int32_t)nx, (int32_t)ny, (int32_t)nz));
+        } else if (inside && p.mode == 4) {
+            found = (int32_t)~grid[pack_key(p, c.x, (int32_t)nx, (int32_t)ny, (int32_t)nz)];
         } else if (inside && p.mode == 3) {
             const int4 q = make_int4(c.x, (int32_t)nx, (int32_t)ny, (int32_t)nz);
             uint64_t s = hash_coord(q.x, q.y, q.z, q.w) & mask;
@@ -476,18 +823,23 @@ int sc_neighbor_map_build(const sc_conv_config *cfg, const int32_t *d_coords, in
     if (!mul_ok(query_rows, K, &map_elems)) return fail(SC_ERR_OVERFLOW, "neighbor map size overflow");
 
     hipStream_t s = as_stream(stream);
-    // Workspace: [header 256 B][bbox partials][table or grid].
+    // Workspace: [header 256 B][bbox partials][offset table][hash table, grid or bitmap].
     NbrHeader *h = (NbrHeader *)d_workspace;
     int32_t *partials = (int32_t *)((char *)d_workspace + kHeaderBytes);
     const uint64_t cap = table_capacity(n_rows);
-    uint64_t *keys = (uint64_t *)((char *)d_workspace + kHeaderBytes + kPartialBytes);
+    int4 *otab = (int4 *)((char *)d_workspace + kHeaderBytes + kPartialBytes);
+    uint64_t *keys = (uint64_t *)((char *)d_workspace + kFixedBytes);
     uint32_t *rows = (uint32_t *)(keys + cap);
     // Dense grid when the bbox fits the workspace's grid budget (decided on the
     // device from the bbox; the budget never exceeds 32 cells per row).
-    uint64_t dense_cells = (workspace_bytes - kHeaderBytes - kPartialBytes) / 4u;
+    uint64_t dense_cells = (workspace_bytes - kFixedBytes) / 4u;
     if (dense_cells > dense_cells_for(n_rows)) dense_cells = dense_cells_for(n_rows);
     dense_cells &= ~1ull;  // even: the 8-byte fill of an odd cell count stays inside
     if (dense_cells > 0xffffffffull) dense_cells = 0xfffffffeull;  // 32-bit grid keys
+    // Rank bitmap (sorted, unique rows): 8 B per 32 cells, 32-bit cell keys.
+    uint64_t bitmap_cells = (workspace_bytes - kFixedBytes) / 8u * 32u;
+    if (bitmap_cells > 0xffffffffull) bitmap_cells = 0xffffffffull;
+    const Limits lim{dense_cells, bitmap_cells};
     if (n_rows == 0) {
         nm_header_init_kernel<<<1, 1, 0, s>>>(h);
         SC_LAUNCH_CHECK("nm_header_init_kernel launch");
@@ -497,22 +849,24 @@ int sc_neighbor_map_build(const sc_conv_config *cfg, const int32_t *d_coords, in
     const unsigned bb = grid_for(n_rows, 256, kBboxBlocks);
     nm_bbox_partial_kernel<<<bb, 256, 0, s>>>(c4, n_rows, partials);
     SC_LAUNCH_CHECK("nm_bbox_partial_kernel launch");
-    nm_bbox_final_kernel<<<1, 256, 0, s>>>(partials, (int)bb, h);
+    nm_bbox_final_kernel<<<1, 256, 0, s>>>(partials, (int)bb, h, lim, kernel_shape(cfg), otab);
     SC_LAUNCH_CHECK("nm_bbox_final_kernel launch");
-    nm_table_init_kernel<<<4096, 256, 0, s>>>(h, keys, cap, dense_cells);
+    nm_table_init_kernel<<<4096, 256, 0, s>>>(h, keys, cap);
     SC_LAUNCH_CHECK("nm_table_init_kernel launch");
-    nm_insert_kernel<<<grid_for(n_rows, 256, 65536), 256, 0, s>>>(c4, n_rows, h, keys, rows, cap - 1,
-                                                                  dense_cells);
+    nm_insert_kernel<<<grid_for(n_rows, 256, 65536), 256, 0, s>>>(c4, n_rows, h, keys, rows, cap - 1);
     SC_LAUNCH_CHECK("nm_insert_kernel launch");
     if (query_rows == 0) return SC_OK;
     const KernelShape ks = kernel_shape(cfg);
-    int rpb = (int)(2048 / K);
+    // 256 rows per block (one per lane on the row-wise path) for K <= 32,
+    // else about 2048 (row, offset) entries per block.
+    int rpb = K <= kCellwiseMaxK ? 256 : (int)(2048 / K);
     if (rpb < 1) rpb = 1;
     if (rpb > kMaxStagedRows) rpb = kMaxStagedRows;
     const int64_t blocks = (query_rows + rpb - 1) / rpb;
     if (blocks > INT32_MAX) return fail(SC_ERR_OVERFLOW, "neighbor map grid overflow");
-    nm_query_kernel<<<(unsigned)blocks, 256, 0, s>>>(c4, query_rows, ks, rpb, h, keys, rows, cap - 1,
-                                                     dense_cells, d_map);
+    const size_t lds = (size_t)query_lds_ints(K, rpb) * sizeof(int);
+    nm_query_kernel<<<(unsigned)blocks, 256, lds, s>>>(c4, query_rows, ks, rpb, h, keys, rows, cap - 1,
+                                                       otab, d_map);
     SC_LAUNCH_CHECK("nm_query_kernel launch");
     return SC_OK;
 }

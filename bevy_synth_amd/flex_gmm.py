@@ -150,6 +150,16 @@ def neighbor_map_build_into(cfg: SparseSubmConvConfig, coords: torch.Tensor, out
         workspace.numel(), _stream()))
 
 
+NEIGHBOR_TABLE_MODES = {1: "hash32", 2: "hash64", 3: "hash_coords", 4: "dense_grid", 5: "rank_bitmap"}
+
+
+def neighbor_map_table_mode(workspace: torch.Tensor) -> str:
+    """The table the last build into ``workspace`` chose on the device (the
+    int32 at byte 40 of the workspace header); syncs the current stream."""
+    mode = int(workspace[40:44].view(torch.int32).item())
+    return NEIGHBOR_TABLE_MODES.get(mode, "none")
+
+
 def neighbor_map_check(workspace: torch.Tensor) -> None:
     """Syncs the current stream and raises on device-detected coord errors."""
     check(_capi.load().sc_neighbor_map_check(_ptr(workspace), _stream()))

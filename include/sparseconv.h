@@ -94,7 +94,8 @@ int sc_kernel_offsets(const sc_conv_config *cfg, int32_t *offsets, int64_t capac
 /* --------------------------------------------------------- neighbour map */
 
 /* Bytes of device workspace sc_neighbor_map_build needs for n_rows coords
- * (a hash table of 2..4 slots per row plus a 256-byte header). */
+ * (a 256-byte header, bbox partials, and the larger of a hash table of 2..4
+ * slots per row and a dense grid of 32 cells per row). */
 int sc_neighbor_map_workspace_size(int64_t n_rows, size_t *bytes);
 
 /*
@@ -113,6 +114,10 @@ int sc_neighbor_map_workspace_size(int64_t n_rows, size_t *bytes);
  * above i32::MAX, rejected by the reference at crates/burn_flex_gmm/src/
  * wgpu/neighbor.rs:252-263) is detected on the device: the map is then all
  * -1 and sc_neighbor_map_check reports SC_ERR_COORD.
+ * The table is chosen on the device from the coords' bbox and order; the
+ * int32 at byte 40 of d_workspace records it after the build (a diagnostic):
+ * 1/2 hash table with 32/64-bit keys, 3 hash table over the coords, 4 dense
+ * bbox grid, 5 rank bitmap (rows strictly increasing in (b, x, y, z)).
  */
 int sc_neighbor_map_build(const sc_conv_config *cfg, const int32_t *d_coords, int64_t n_rows,
                           int64_t query_rows, int32_t *d_map, void *d_workspace,

@@ -70,9 +70,9 @@ def test_validate_config_errors(cfg, msg, oracle):
 def test_workspace_sizes():
     n = 1_040_679
     b = F.neighbor_map_workspace_bytes(n)
-    # header 256 B + bbox partials (1024 blocks x 9 i32) +
-    # max(hash table: 2..4 slots x 12 B, dense grid: 32 cells x 4 B) per row
-    fixed = 256 + 1024 * 9 * 4
+    # header 256 B + bbox partials (1024 blocks x 10 i32) + offset table (512 x 16 B)
+    # + max(hash table: 2..4 slots x 12 B, dense grid: 32 cells x 4 B) per row
+    fixed = 256 + 1024 * 10 * 4 + 512 * 16
     assert fixed + 128 * n <= b <= fixed + max(128 * n, 12 * 4 * n)
     assert F.neighbor_map_workspace_bytes(0) > 256
     with pytest.raises(_capi.SparseConvError):

@@ -179,3 +179,94 @@ def test_shuffled_rows_relabel_consistently(oracle):
     shuf = gpu_map(cfg, coords[perm])
     relabeled = np.where(base[perm] >= 0, inv[np.maximum(base[perm], 0)], -1)
     assert np.array_equal(shuf, relabeled)
+
+
+def _map_and_mode(cfg, coords, query_rows=None):
+    c = dev(coords.astype(np.int32))
+    ws = F.NeighborMapWorkspace(c.device).get(len(coords))
+    q = len(coords) if query_rows is None else query_rows
+    out = torch.empty((q, F.kernel_rows(cfg)), dtype=torch.int32, device=c.device)
+    F.neighbor_map_build_into(cfg, c, out, ws, q)
+    F.neighbor_map_check(ws)
+    return out.cpu().numpy(), F.neighbor_map_table_mode(ws)
+
+
+def test_table_modes_by_row_order(oracle):
+    """Sorted unique rows take the rank bitmap; any row order that is not
+    strictly increasing in (b, x, y, z) takes the dense grid or a hash table;
+    every mode gives the oracle's map."""
+    cfg = F.SparseSubmConvConfig(1, 1)
+    oc = ocfg(oracle, cfg)
+    base = synth.config2_coords()
+    assert np.array_equal(np.unique(base, axis=0), base)  # argwhere order: sorted, unique
+    got, mode = _map_and_mode(cfg, base)
+    assert mode == "rank_bitmap"
+    exp = oracle.build_neighbor_rows(oc, base)
+    assert np.array_equal(got, exp)
+    # one swapped pair across a wave and a block boundary of the bbox pass,
+    # inside a wave, and at the very end: all fall back to the dense grid
+    for i in (63, 255, 4000, len(base) - 2):
+        c = base.copy()
+        c[[i, i + 1]] = c[[i + 1, i]]
+        got, mode = _map_and_mode(cfg, c)
+        assert mode == "dense_grid", i
+        assert np.array_equal(got, oracle.build_neighbor_rows(oc, c)), i
+    # a duplicated row (not strictly increasing) keeps the lowest-row rule
+    c = np.insert(base, 1000, base[1000], axis=0)
+    got, mode = _map_and_mode(cfg, c)
+    assert mode == "dense_grid"
+    assert np.array_equal(got, oracle.build_neighbor_rows(oc, c))
+    # query rows map against the full sorted set
+    got, mode = _map_and_mode(cfg, base, query_rows=777)
+    assert mode == "rank_bitmap" and np.array_equal(got, exp[:777])
+
+
+def test_rank_bitmap_sparse_bbox(oracle):
+    """Sorted unique coords over a bbox of more than 32 cells per row (beyond
+    the dense grid's budget) still take the rank bitmap; two batches, words
+    holding many rows and words holding none."""
+    rng = np.random.default_rng(9)
+    n = 30000
+    c = np.zeros((n, 4), np.int32)
+    c[:, 0] = rng.integers(0, 2, n)
+    c[:, 1:] = rng.integers(0, 90, (n, 3))
+    c[:3000, 1:] = c[3000:6000, 1:] + rng.integers(-1, 2, (3000, 3))
+    c[:3000, 0] = c[3000:6000, 0]
+    c[5000:5040] = [0, 7, 7, 0] + np.array([[0, 0, 0, z] for z in range(40)])  # 40 consecutive cells
+    c[:, 1:] = np.maximum(c[:, 1:], 0)
+    c = np.unique(c, axis=0)                                             # sorted, unique
+    cells = float(np.prod([c[:, j].max() - c[:, j].min() + 1 for j in range(4)]))
+    assert cells > 32 * len(c)
+    for kernel in ((3, 3, 3), (5, 5, 5)):
+        cfg = F.SparseSubmConvConfig(1, 1, *kernel)
+        got, mode = _map_and_mode(cfg, c)
+        assert mode == "rank_bitmap"
+        assert np.array_equal(got, oracle.build_neighbor_rows(ocfg(oracle, cfg), c))
+    # the same rows in another order: a hash table, the same map up to relabelling
+    cfg = F.SparseSubmConvConfig(1, 1)
+    perm = rng.permutation(len(c))
+    got, mode = _map_and_mode(cfg, c[perm])
+    assert mode == "hash32"
+    assert np.array_equal(got, oracle.build_neighbor_rows(ocfg(oracle, cfg), c[perm]))
+
+
+def test_config3_shuffled_takes_dense_grid(oracle):
+    """Config 3 at full size in a shuffled row order (dense grid) relabels to
+    the sorted order's map (rank bitmap)."""
+    coords = synth.config3_coords()
+    cfg = F.SparseSubmConvConfig(1, 1)
+    base, mode = _map_and_mode(cfg, coords)
+    assert mode == "rank_bitmap"
+    perm = np.random.default_rng(1).permutation(len(coords))
+    inv = np.empty_like(perm)
+    inv[perm] = np.arange(len(perm))
+    shuf, mode = _map_and_mode(cfg, coords[perm])
+    assert mode == "dense_grid"
+    assert np.array_equal(shuf, np.where(base[perm] >= 0, inv[np.maximum(base[perm], 0)], -1))
+    # one swapped pair across the bbox pass's grid stride (1024 blocks x 256 rows)
+    i = 1024 * 256 - 1
+    sw = np.arange(len(coords))
+    sw[[i, i + 1]] = sw[[i + 1, i]]
+    got, mode = _map_and_mode(cfg, coords[sw])
+    assert mode == "dense_grid"
+    assert np.array_equal(got, np.where(base[sw] >= 0, sw[np.maximum(base[sw], 0)], -1))
