@@ -36,44 +36,13 @@
 #include <climits>
 
 #include "sc_common.hpp"
+#include "sc_neighbor.hpp"
 
 namespace sc {
 namespace {
 
-constexpr size_t kHeaderBytes = 256;
-constexpr uint64_t kEmpty64 = ~0ull;
-constexpr uint32_t kStatusNegative = 1u;
+using namespace nbr;
 constexpr int kMaxStagedRows = 256;
-constexpr int kMaxStagedOffsets = 512;
-
-// Table budgets, in bbox cells, that the workspace affords: the dense grid
-// (4 B per cell, at most 32 cells per row) and the rank bitmap (8 B per 32 cells).
-struct Limits {
-    uint64_t dense_cells;
-    uint64_t bitmap_cells;
-};
-
-struct Plan {
-    int mode;  // 0: no table (error), 1: 32-bit keys packed with rows, 2: 64-bit keys,
-               // 3: row-only table compared through the coords, 4: dense grid,
-               // 5: rank bitmap (rows strictly increasing in (b, x, y, z))
-    uint64_t total;  // bbox cells (valid for modes 1, 2, 4, 5)
-    int32_t lo[4];
-    int32_t hi[4];
-    uint64_t ext[4];
-};
-
-struct alignas(16) NbrHeader {
-    int32_t bmin[4];
-    int32_t bmax[4];
-    uint32_t status;
-    uint32_t unsorted;  // nonzero unless the rows are strictly increasing in (b, x, y, z)
-    int32_t mode;       // the table mode chosen (Plan::mode), a diagnostic for callers
-    uint32_t pad0;
-    Plan plan;          // derived once from the fields above, read by every later kernel
-    uint8_t pad[kHeaderBytes - 48 - sizeof(Plan)];
-};
-static_assert(sizeof(NbrHeader) == kHeaderBytes, "header size");
 
 inline uint64_t table_capacity(int64_t n)
 {
@@ -89,10 +58,6 @@ inline uint64_t dense_cells_for(int64_t n)
     const uint64_t c = (uint64_t)(n > 0 ? n : 0) * 32u;
     return c < (1u << 16) ? (1u << 16) : c;
 }
-
-constexpr size_t kPartialBytes = 1024 * 10 * 4;  // bbox partials (kBboxBlocks x 10 ints)
-constexpr size_t kOffsetTableBytes = kMaxStagedOffsets * 16;  // per offset {dx, dy, dz, cell delta}
-constexpr size_t kFixedBytes = kHeaderBytes + kPartialBytes + kOffsetTableBytes;
 
 inline size_t workspace_bytes_for(int64_t n)
 {
@@ -145,15 +110,6 @@ __device__ inline uint64_t hash_coord(int32_t b, int32_t x, int32_t y, int32_t z
 __device__ inline bool same_coord(const int4 a, const int4 b)
 {
     return a.x == b.x && a.y == b.y && a.z == b.z && a.w == b.w;
-}
-
-__device__ inline uint64_t pack_key(const Plan &p, int32_t b, int32_t x, int32_t y, int32_t z)
-{
-    uint64_t k = (uint64_t)(b - p.lo[0]);
-    k = k * p.ext[1] + (uint64_t)(x - p.lo[1]);
-    k = k * p.ext[2] + (uint64_t)(y - p.lo[2]);
-    k = k * p.ext[3] + (uint64_t)(z - p.lo[3]);
-    return k;
 }
 
 __global__ void nm_header_init_kernel(NbrHeader *h)
@@ -319,6 +275,7 @@ __global__ __launch_bounds__(256) void nm_bbox_final_kernel(const int32_t *__res
         const Plan p = make_plan(h, lim);
         h->plan = p;
         h->mode = p.mode;
+        h->ks = ks;
     }
     __syncthreads();
     // Offset table for the query: {dx, dy, dz} and the 32-bit cell delta of
@@ -508,61 +465,13 @@ inline int query_lds_ints(int64_t K, int rows_per_block)
     return staged > rowwise ? staged : rowwise;
 }
 
-// The 3x3x3 kernel with unit axis signs (the decoder's submanifold conv):
-// offset k = (kd*3 + kh)*3 + kw is known at compile time, so its cell delta
-// is a signed sum of three per-launch strides and its bbox test an AND of
-// per-row "one step up / down along kernel axis j stays inside" flags.
-struct Cube3 {
-    uint32_t D[3];  // cell delta of +1 along kernel axis j (wraps)
-    int a[3];       // spatial axis (0 x, 1 y, 2 z) of kernel axis j
-    int s[3];       // its sign
-    int lo[3], hi[3];  // bbox bounds of that spatial axis
-};
-
-// Uniform int through a scalar register.
-__device__ inline int uniform_i32(int v) { return __builtin_amdgcn_readfirstlane(v); }
-
-// Selections by axis pick among register values (never a computed address
-// into a local struct, which would put the struct in scratch memory).
-__device__ inline Cube3 cube3_of(const KernelShape &ks, const Plan &p)
-{
-    Cube3 q;
-    const uint32_t sx = (uint32_t)uniform_i32((int)(uint32_t)(p.ext[2] * p.ext[3]));
-    const uint32_t sy = (uint32_t)uniform_i32((int)(uint32_t)p.ext[3]);
-    const int lx = uniform_i32(p.lo[1]), ly = uniform_i32(p.lo[2]), lz = uniform_i32(p.lo[3]);
-    const int hx = uniform_i32(p.hi[1]), hy = uniform_i32(p.hi[2]), hz = uniform_i32(p.hi[3]);
-#pragma unroll
-    for (int j = 0; j < 3; ++j) {
-        const int a = uniform_i32(ks.order[j]);
-        q.a[j] = a;
-        q.s[j] = uniform_i32(ks.sign[j]);
-        const uint32_t st = a == 0 ? sx : (a == 1 ? sy : 1u);
-        q.D[j] = q.s[j] > 0 ? st : 0u - st;
-        q.lo[j] = a == 0 ? lx : (a == 1 ? ly : lz);
-        q.hi[j] = a == 0 ? hx : (a == 1 ? hy : hz);
-    }
-    return q;
-}
-
 template <bool kRank, bool kCube3>
 __device__ inline void query_cells(const int4 *__restrict__ coords, int64_t row0, int nrows, int K,
                                    const int4 *__restrict__ otab, const Cube3 &cube, const Plan &p,
                                    const uint64_t *__restrict__ table, uint32_t table_bytes, int *s_out,
                                    int32_t *__restrict__ out)
 {
-    // Branch-free lookups: a neighbour outside the bbox gets an offset beyond
-    // the table's descriptor and reads 0, which decodes to -1 like an empty
-    // rank word or an empty grid cell.
-    // The descriptor must live in scalar registers (its inputs are uniform).
-    // readfirstlane returns a signed int: each half goes through uint32_t
-    // before widening, or a low half with bit 31 set would sign-extend into
-    // the high half of the address.
-    const uint64_t tp = (uint64_t)(uintptr_t)table;
-    const uint32_t tp_lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)tp);
-    const uint32_t tp_hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(tp >> 32));
-    const uint32_t tbytes = (uint32_t)__builtin_amdgcn_readfirstlane((int)table_bytes);
-    const __amdgpu_buffer_rsrc_t rt =
-        make_rsrc((const void *)(uintptr_t)(((uint64_t)tp_hi << 32) | tp_lo), tbytes);
+    const __amdgpu_buffer_rsrc_t rt = cell_table_rsrc(table, table_bytes);
     const int rw = (int)threadIdx.x;  // row within the block
     const bool valid = rw < nrows;
     int4 c = make_int4(0, 0, 0, 0);
@@ -572,15 +481,7 @@ __device__ inline void query_cells(const int4 *__restrict__ coords, int64_t row0
         base = (uint32_t)pack_key(p, c.x, c.y, c.z, c.w);
     }
     bool up[3] = {false, false, false}, dn[3] = {false, false, false};
-    if (kCube3) {
-#pragma unroll
-        for (int j = 0; j < 3; ++j) {
-            const int a = cube.a[j];
-            const int ca = a == 0 ? c.y : (a == 1 ? c.z : c.w);
-            up[j] = cube.s[j] > 0 ? ca < cube.hi[j] : ca > cube.lo[j];
-            dn[j] = cube.s[j] > 0 ? ca > cube.lo[j] : ca < cube.hi[j];
-        }
-    }
+    if (kCube3) cube3_flags(c, cube, up, dn);
     const int KK = kCube3 ? 27 : K;
     int *so = s_out + rw * KK;
     for (int k0 = 0; k0 < KK; k0 += kCellChunk) {
@@ -591,45 +492,17 @@ __device__ inline void query_cells(const int4 *__restrict__ coords, int64_t row0
             const int k = k0 + u;
             if (k >= KK) break;
             bool inside;
-            uint32_t delta = 0;
-            if (kCube3) {
-                const int e[3] = {k / 9 - 1, (k / 3) % 3 - 1, k % 3 - 1};
-                inside = valid;
-#pragma unroll
-                for (int j = 0; j < 3; ++j) {
-                    if (e[j] > 0) inside = inside && up[j];
-                    if (e[j] < 0) inside = inside && dn[j];
-                    delta += e[j] > 0 ? cube.D[j] : (e[j] < 0 ? 0u - cube.D[j] : 0u);
-                }
-            } else {
-                const int4 o = otab[k];  // uniform: scalar loads
-                const int nx = c.y + o.x, ny = c.z + o.y, nz = c.w + o.z;
-                inside = valid && nx >= p.lo[1] && nx <= p.hi[1] && ny >= p.lo[2] && ny <= p.hi[2] &&
-                         nz >= p.lo[3] && nz <= p.hi[3];
-                delta = (uint32_t)o.w;
-            }
-            q[u] = base + delta;
-            const uint32_t off = kRank ? (q[u] >> 5) << 3 : q[u] << 2;
+            q[u] = neighbour_cell<kCube3>(k, c, valid, base, up, dn, cube, p, otab, inside);
             if (kRank)
-                raw[u] = bload8(rt, inside ? off : kOobOffset);
+                raw[u] = bload8(rt, cell_offset<true>(q[u], inside));
             else
-                raw[u].x = bload4(rt, inside ? off : kOobOffset);
+                raw[u].x = bload4(rt, cell_offset<false>(q[u], inside));
         }
 #pragma unroll
         for (int u = 0; u < kCellChunk; ++u) {
             const int k = k0 + u;
             if (k >= KK) break;
-            int32_t v;
-            if (kRank) {
-                // rank = first row of the word + occupied cells below b; -1
-                // unless bit b is set (all-ones mask t selects the rank)
-                const uint32_t bits = raw[u].x, b = q[u] & 31u;
-                const int32_t t = __builtin_amdgcn_sbfe((int32_t)bits, b, 1);
-                const int32_t rank = (int32_t)(__builtin_popcount(__builtin_amdgcn_ubfe(bits, 0, b)) + raw[u].y);
-                v = (rank & t) | ~t;
-            } else {
-                v = (int32_t)~raw[u].x;  // grid cells hold ~row (0 = empty)
-            }
+            const int32_t v = kRank ? decode_rank(raw[u], q[u]) : decode_grid(raw[u].x);
             if (valid) so[k] = v;
         }
     }
@@ -671,13 +544,12 @@ __global__ __launch_bounds__(256) void nm_query_kernel(const int4 *__restrict__ 
     const bool staged = ks.K <= kMaxStagedOffsets;
     const bool cellwise = p.mode == 4 || p.mode == 5;
     // table bytes, addressed through a buffer descriptor on the row-wise path
-    const uint64_t tbytes = p.mode == 5 ? (p.total + 31) / 32 * 8 : p.total * 4;
+    const uint64_t tbytes = cell_table_bytes(p);
     const bool rowwise = cellwise && ks.K <= kCellwiseMaxK && rows_per_block == (int)blockDim.x &&
                          tbytes <= kOobOffset;
     int32_t *out = map + row0 * ks.K;
     if (rowwise) {
-        const bool cube3 = ks.KD == 3 && ks.KH == 3 && ks.KW == 3 && abs(ks.sign[0]) == 1 &&
-                           abs(ks.sign[1]) == 1 && abs(ks.sign[2]) == 1;
+        const bool cube3 = is_cube3(ks);
         const Cube3 cube = cube3_of(ks, p);
         if (p.mode == 5 && cube3)
             query_cells<true, true>(coords, row0, nrows, ks.K, otab, cube, p, keys, (uint32_t)tbytes, s_dyn,

@@ -28,7 +28,11 @@
 // brick's segment sorted by row index so that the order is deterministic.
 //
 // Halo tables:
-//   8. tiles   : one workgroup per tile, one thread per tile row; the
+//   8. tiles   : one workgroup per tile, one thread per tile row, whose
+//                neighbour rows come from its map row or, given the map
+//                build's workspace, from that build's dense grid / rank
+//                bitmap (one L2-resident lookup per offset instead of a
+//                scattered 108-byte map row); the
 //                distinct neighbour rows are numbered in increasing row
 //                order -> halo[] and the u16 local map lmap[k][row], through
 //                an LDS bitmap over the tile's neighbour row range (the usual
@@ -38,6 +42,7 @@
 #include <climits>
 
 #include "sc_common.hpp"
+#include "sc_neighbor.hpp"
 #include "sc_plan.hpp"
 
 namespace sc {
@@ -51,6 +56,9 @@ constexpr int kHashSlots = 1 << kHashBits;  // > 27 * 256 distinct neighbours of
 struct PlanArgs {
     const int4 *coords;
     const int32_t *map;
+    const uint8_t *nbr_ws;  // the map build's workspace (cell-table lookups), or null
+    uint64_t nbr_ws_bytes;
+    KernelShape ks;
     int64_t n_q;
     int64_t n_in;
     int K;
@@ -613,6 +621,50 @@ __device__ inline int tile_scan_excl(int x, int *s_wave, int &total)
 constexpr int kBitmapWords = kHashSlots;  // 8192 words = 262144 row indices
 constexpr int kBitmapBits = kBitmapWords * 32;
 
+// Neighbour rows of query row q (q < 0: padding, all -1) through the map
+// build's cell table: the same rows its map holds, looked up per offset.
+template <bool kRank, bool kCube3>
+__device__ inline void tile_lookups(const PlanArgs &a, const nbr::NbrHeader *nh, int32_t q, int32_t (&v)[32])
+{
+    const nbr::Plan p = nh->plan;
+    const nbr::Cube3 cube = nbr::cube3_of(a.ks, p);
+    const int4 *otab = reinterpret_cast<const int4 *>(a.nbr_ws + nbr::kHeaderBytes + nbr::kPartialBytes);
+    const __amdgpu_buffer_rsrc_t rt =
+        nbr::cell_table_rsrc(a.nbr_ws + nbr::kFixedBytes, (uint32_t)nbr::cell_table_bytes(p));
+    const bool valid = q >= 0;
+    int4 c = make_int4(0, 0, 0, 0);
+    uint32_t base = 0;
+    if (valid) {
+        c = a.coords[q];
+        base = (uint32_t)nbr::pack_key(p, c.x, c.y, c.z, c.w);
+    }
+    bool up[3] = {false, false, false}, dn[3] = {false, false, false};
+    if (kCube3) nbr::cube3_flags(c, cube, up, dn);
+    const int K = kCube3 ? 27 : a.K;
+    uint2 raw[32];
+    uint32_t cell[32];
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+        raw[k] = make_uint2(0u, 0u);
+        cell[k] = 0;
+        if (kCube3 ? k < 27 : k < K) {
+            bool inside;
+            cell[k] = nbr::neighbour_cell<kCube3>(kCube3 ? k : min(k, K - 1), c, valid, base, up, dn, cube, p,
+                                                  otab, inside);
+            if (kRank)
+                raw[k] = bload8(rt, nbr::cell_offset<true>(cell[k], inside));
+            else
+                raw[k].x = bload4(rt, nbr::cell_offset<false>(cell[k], inside));
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+        int32_t x = -1;
+        if (k < K) x = kRank ? nbr::decode_rank(raw[k], cell[k]) : nbr::decode_grid(raw[k].x);
+        v[k] = x < a.n_in ? x : -1;
+    }
+}
+
 __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
 {
     __shared__ uint32_t s_bits[kHashSlots];        // bitmap, or the hash table's keys
@@ -629,13 +681,42 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
     const int64_t n_in = a.n_in;
     const int32_t q = a.order[t * kPlanTileRows + p];
 
-    // The thread's map row (K dwords at dword K*q, rows in brick order, so
-    // scattered across lanes): 16-byte loads from the aligned-down address,
-    // then a shift by the row's dword offset within 16 bytes (s).  Maps of 3
-    // GiB or more take one 4-byte load per entry.
+    // The thread's neighbour rows: from the map build's cell table when the
+    // caller passed its workspace and it holds a dense grid or rank bitmap
+    // built for this kernel shape, else from the thread's map row.
     int32_t v[32];
-    const int64_t map_bytes = a.n_q * (int64_t)K * 4;
-    if (map_bytes + 256 <= (int64_t)kOobOffset) {
+    int table_mode = 0;
+    if (a.nbr_ws) {
+        const nbr::NbrHeader *nh = reinterpret_cast<const nbr::NbrHeader *>(a.nbr_ws);
+        const int mode = nbr::uniform_i32(nh->plan.mode);
+        bool same = true;
+        same = same && nbr::uniform_i32(nh->ks.K) == a.ks.K && nbr::uniform_i32(nh->ks.KD) == a.ks.KD &&
+               nbr::uniform_i32(nh->ks.KH) == a.ks.KH && nbr::uniform_i32(nh->ks.KW) == a.ks.KW;
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+            same = same && nbr::uniform_i32(nh->ks.order[j]) == a.ks.order[j] &&
+                   nbr::uniform_i32(nh->ks.sign[j]) == a.ks.sign[j];
+        const uint64_t tb = nbr::cell_table_bytes(nh->plan);
+        if (same && (mode == 4 || mode == 5) && tb <= kOobOffset && nbr::kFixedBytes + tb <= a.nbr_ws_bytes)
+            table_mode = mode;
+    }
+    if (table_mode != 0) {
+        const nbr::NbrHeader *nh = reinterpret_cast<const nbr::NbrHeader *>(a.nbr_ws);
+        const bool cube3 = nbr::is_cube3(a.ks);
+        if (table_mode == 5 && cube3)
+            tile_lookups<true, true>(a, nh, q, v);
+        else if (table_mode == 5)
+            tile_lookups<true, false>(a, nh, q, v);
+        else if (cube3)
+            tile_lookups<false, true>(a, nh, q, v);
+        else
+            tile_lookups<false, false>(a, nh, q, v);
+    } else if (a.n_q * (int64_t)K * 4 + 256 <= (int64_t)kOobOffset) {
+        // The thread's map row (K dwords at dword K*q, rows in brick order,
+        // so scattered across lanes): 16-byte loads from the aligned-down
+        // address, then a shift by the row's dword offset within 16 bytes
+        // (s).  Maps of 3 GiB or more take one 4-byte load per entry.
+        const int64_t map_bytes = a.n_q * (int64_t)K * 4;
         const __amdgpu_buffer_rsrc_t r = make_rsrc(a.map, (uint32_t)map_bytes);
         const int64_t d0 = q >= 0 ? (int64_t)q * K : 0;
         const int s = (int)(d0 & 3);
@@ -845,6 +926,9 @@ int plan_args(const sc_conv_config *cfg, const int32_t *d_coords, int64_t n_in, 
     char *b = static_cast<char *>(d_plan);
     a.coords = reinterpret_cast<const int4 *>(d_coords);
     a.map = d_map;
+    a.nbr_ws = nullptr;
+    a.nbr_ws_bytes = 0;
+    a.ks = kernel_shape(cfg);
     a.n_q = n_q;
     a.n_in = n_in;
     a.K = (int)K;
@@ -946,5 +1030,23 @@ extern "C" int sc_conv_plan_tables(const sc_conv_config *cfg, const int32_t *d_m
     PlanLayout L;
     int rc = plan_args(cfg, nullptr, n_in, d_map, n_q, d_plan, plan_bytes, false, true, a, L);
     if (rc) return rc;
+    return launch_plan_tables(a, L, as_stream(stream));
+}
+
+extern "C" int sc_conv_plan_tables_ws(const sc_conv_config *cfg, const int32_t *d_coords, const int32_t *d_map,
+                                      int64_t n_in, int64_t n_q, const void *d_map_workspace,
+                                      size_t map_workspace_bytes, void *d_plan, size_t plan_bytes,
+                                      sc_stream stream)
+{
+    clear_error();
+    PlanArgs a;
+    PlanLayout L;
+    int rc = plan_args(cfg, d_coords, n_in, d_map, n_q, d_plan, plan_bytes, true, true, a, L);
+    if (rc) return rc;
+    if (n_q > 0 && !d_map_workspace) return fail(SC_ERR_NULL, "conv plan: map workspace is NULL");
+    if ((uintptr_t)d_map_workspace % 16 != 0)
+        return fail(SC_ERR_WORKSPACE, "neighbor map workspace must be 16-byte aligned");
+    a.nbr_ws = static_cast<const uint8_t *>(d_map_workspace);
+    a.nbr_ws_bytes = map_workspace_bytes;
     return launch_plan_tables(a, L, as_stream(stream));
 }
