@@ -145,7 +145,7 @@ def main():
         F.neighbor_map_build_into(cfg, coords_d, nbr, ws)
 
     def plan_build():
-        F.conv_plan_build_into(cfg, coords_d, nbr, plan_buf, workspace=ws)
+        F.conv_plan_build_into(cfg, coords_d, nbr, plan_buf)
 
     def map_and_plan():
         map_build()

@@ -26,7 +26,6 @@ EXPORTED = (
     "sc_layer_norm", "sc_add", "sc_subdivision_workspace_size", "sc_subdivision_build",
     "sc_gather_rows", "sc_c2s_skip_add", "sc_convert",
     "sc_conv_plan_size", "sc_conv_plan_build", "sc_conv_plan_order", "sc_conv_plan_tables",
-    "sc_conv_plan_tables_ws",
     "sc_subm_conv_forward_planned",
     "sc_conv_weight_pack_size", "sc_conv_weight_pack",
 )
@@ -105,7 +104,6 @@ def load() -> ctypes.CDLL:
     L.sc_conv_plan_build.argtypes = [cfgp, P, i64, P, i64, P, ctypes.c_size_t, P]
     L.sc_conv_plan_order.argtypes = [cfgp, P, i64, i64, P, ctypes.c_size_t, P]
     L.sc_conv_plan_tables.argtypes = [cfgp, P, i64, i64, P, ctypes.c_size_t, P]
-    L.sc_conv_plan_tables_ws.argtypes = [cfgp, P, P, i64, i64, P, ctypes.c_size_t, P, ctypes.c_size_t, P]
     L.sc_subm_conv_forward_planned.argtypes = [cfgp, i32, P, i64, P, i64, i32, P, P, P, P,
                                                ctypes.POINTER(ScConvEpilogue), i32, P, P, P]
     L.sc_conv_weight_pack_size.argtypes = [cfgp, i32, sizep]

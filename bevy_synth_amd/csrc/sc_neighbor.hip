@@ -275,7 +275,6 @@ __global__ __launch_bounds__(256) void nm_bbox_final_kernel(const int32_t *__res
         const Plan p = make_plan(h, lim);
         h->plan = p;
         h->mode = p.mode;
-        h->ks = ks;
     }
     __syncthreads();
     // Offset table for the query: {dx, dy, dz} and the 32-bit cell delta of

@@ -1,7 +1,5 @@
-// Layout of the neighbour-map workspace and the cell-table lookups shared by
-// the map build (sc_neighbor.hip) and the conv plan's halo tables
-// (sc_plan.hip), which can look neighbours up in the map build's table
-// instead of reading the map rows.
+// Layout of the neighbour-map workspace (header, bbox partials, offset table,
+// cell table) and the dense-grid / rank-bitmap lookups of the map build.
 #pragma once
 
 #include "sc_common.hpp"
@@ -39,8 +37,7 @@ struct alignas(16) NbrHeader {
     int32_t mode;       // the table mode chosen (Plan::mode), a diagnostic for callers
     uint32_t pad0;
     Plan plan;          // derived once from the fields above, read by every later kernel
-    KernelShape ks;     // the kernel shape the offset table was built for
-    uint8_t pad[kHeaderBytes - 48 - sizeof(Plan) - sizeof(KernelShape)];
+    uint8_t pad[kHeaderBytes - 48 - sizeof(Plan)];
 };
 static_assert(sizeof(NbrHeader) == kHeaderBytes, "header size");
 

@@ -28,11 +28,7 @@
 // brick's segment sorted by row index so that the order is deterministic.
 //
 // Halo tables:
-//   8. tiles   : one workgroup per tile, one thread per tile row, whose
-//                neighbour rows come from its map row or, given the map
-//                build's workspace, from that build's dense grid / rank
-//                bitmap (one L2-resident lookup per offset instead of a
-//                scattered 108-byte map row); the
+//   8. tiles   : one workgroup per tile, one thread per tile row; the
 //                distinct neighbour rows are numbered in increasing row
 //                order -> halo[] and the u16 local map lmap[k][row], through
 //                an LDS bitmap over the tile's neighbour row range (the usual
@@ -42,7 +38,6 @@
 #include <climits>
 
 #include "sc_common.hpp"
-#include "sc_neighbor.hpp"
 #include "sc_plan.hpp"
 
 namespace sc {
@@ -50,15 +45,15 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kTileThreads = kPlanTileRows;  // plan_tiles_kernel: one thread per tile row
-constexpr int kHashBits = 13;
-constexpr int kHashSlots = 1 << kHashBits;  // > 27 * 256 distinct neighbours of a tile
+// Tile hash table: a tile with more than kPlanHaloMax distinct neighbours
+// overflows to the direct kernel, so insertion stops past that many keys and
+// 2048 slots (load factor < 1/2 for a tile that fits) suffice.
+constexpr int kHashBits = 11;
+constexpr int kHashSlots = 1 << kHashBits;
 
 struct PlanArgs {
     const int4 *coords;
     const int32_t *map;
-    const uint8_t *nbr_ws;  // the map build's workspace (cell-table lookups), or null
-    uint64_t nbr_ws_bytes;
-    KernelShape ks;
     int64_t n_q;
     int64_t n_in;
     int K;
@@ -618,100 +613,31 @@ __device__ inline int tile_scan_excl(int x, int *s_wave, int &total)
 //    usual case for brick-ordered rows): one bit per row index in LDS, then
 //    a per-word prefix of popcounts; rank = prefix + popcount below the bit.
 //  * otherwise: an LDS hash table of the distinct rows, sorted (bitonic).
-constexpr int kBitmapWords = kHashSlots;  // 8192 words = 262144 row indices
+constexpr int kBitmapWords = 4096;  // 131072 row indices
 constexpr int kBitmapBits = kBitmapWords * 32;
-
-// Neighbour rows of query row q (q < 0: padding, all -1) through the map
-// build's cell table: the same rows its map holds, looked up per offset.
-template <bool kRank, bool kCube3>
-__device__ inline void tile_lookups(const PlanArgs &a, const nbr::NbrHeader *nh, int32_t q, int32_t (&v)[32])
-{
-    const nbr::Plan p = nh->plan;
-    const nbr::Cube3 cube = nbr::cube3_of(a.ks, p);
-    const int4 *otab = reinterpret_cast<const int4 *>(a.nbr_ws + nbr::kHeaderBytes + nbr::kPartialBytes);
-    const __amdgpu_buffer_rsrc_t rt =
-        nbr::cell_table_rsrc(a.nbr_ws + nbr::kFixedBytes, (uint32_t)nbr::cell_table_bytes(p));
-    const bool valid = q >= 0;
-    int4 c = make_int4(0, 0, 0, 0);
-    uint32_t base = 0;
-    if (valid) {
-        c = a.coords[q];
-        base = (uint32_t)nbr::pack_key(p, c.x, c.y, c.z, c.w);
-    }
-    bool up[3] = {false, false, false}, dn[3] = {false, false, false};
-    if (kCube3) nbr::cube3_flags(c, cube, up, dn);
-    const int K = kCube3 ? 27 : a.K;
-    uint2 raw[32];
-    uint32_t cell[32];
-#pragma unroll
-    for (int k = 0; k < 32; ++k) {
-        raw[k] = make_uint2(0u, 0u);
-        cell[k] = 0;
-        if (kCube3 ? k < 27 : k < K) {
-            bool inside;
-            cell[k] = nbr::neighbour_cell<kCube3>(kCube3 ? k : min(k, K - 1), c, valid, base, up, dn, cube, p,
-                                                  otab, inside);
-            if (kRank)
-                raw[k] = bload8(rt, nbr::cell_offset<true>(cell[k], inside));
-            else
-                raw[k].x = bload4(rt, nbr::cell_offset<false>(cell[k], inside));
-        }
-    }
-#pragma unroll
-    for (int k = 0; k < 32; ++k) {
-        int32_t x = -1;
-        if (k < K) x = kRank ? nbr::decode_rank(raw[k], cell[k]) : nbr::decode_grid(raw[k].x);
-        v[k] = x < a.n_in ? x : -1;
-    }
-}
 
 __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
 {
-    __shared__ uint32_t s_bits[kHashSlots];        // bitmap, or the hash table's keys
+    // 28 KB in all, so that five workgroups fit a CU
+    __shared__ uint32_t s_bits[kBitmapWords];      // bitmap, or the hash table's keys
     __shared__ __attribute__((aligned(16))) uint16_t s_pre[kBitmapWords];  // word prefix (bitmap path)
+    __shared__ int s_nkeys;                         // keys inserted (hash path)
+    __shared__ int32_t s_halo[kPlanHaloMax];        // the halo rows (bitmap path)
     __shared__ int s_wave[kTileThreads / 64];
     __shared__ int s_mm[2][kTileThreads / 64];
     int32_t *s_key = reinterpret_cast<int32_t *>(s_bits);
-    uint64_t *s_list = reinterpret_cast<uint64_t *>(s_pre);  // kPlanHaloMax entries (8 KB <= 16 KB)
-    static_assert(kPlanHaloMax * 8 <= kBitmapWords * 2, "sort list fits the prefix array");
+    uint64_t *s_list = reinterpret_cast<uint64_t *>(s_pre);  // up to 1024 sorted entries
+    static_assert(kHashSlots <= kBitmapWords, "hash table fits the bitmap array");
+    static_assert(kPlanHaloMax <= 1024 && 1024 * 8 <= kBitmapWords * 2, "sort list fits the prefix array");
     const int64_t t = blockIdx.x;
     const int p = threadIdx.x;
     const int lane = p & 63, wave = p >> 6;
     const int K = a.K;
-    const int64_t n_in = a.n_in;
+    const int32_t n_in = (int32_t)a.n_in;  // <= INT32_MAX
     const int32_t q = a.order[t * kPlanTileRows + p];
 
-    // The thread's neighbour rows: from the map build's cell table when the
-    // caller passed its workspace and it holds a dense grid or rank bitmap
-    // built for this kernel shape, else from the thread's map row.
     int32_t v[32];
-    int table_mode = 0;
-    if (a.nbr_ws) {
-        const nbr::NbrHeader *nh = reinterpret_cast<const nbr::NbrHeader *>(a.nbr_ws);
-        const int mode = nbr::uniform_i32(nh->plan.mode);
-        bool same = true;
-        same = same && nbr::uniform_i32(nh->ks.K) == a.ks.K && nbr::uniform_i32(nh->ks.KD) == a.ks.KD &&
-               nbr::uniform_i32(nh->ks.KH) == a.ks.KH && nbr::uniform_i32(nh->ks.KW) == a.ks.KW;
-#pragma unroll
-        for (int j = 0; j < 3; ++j)
-            same = same && nbr::uniform_i32(nh->ks.order[j]) == a.ks.order[j] &&
-                   nbr::uniform_i32(nh->ks.sign[j]) == a.ks.sign[j];
-        const uint64_t tb = nbr::cell_table_bytes(nh->plan);
-        if (same && (mode == 4 || mode == 5) && tb <= kOobOffset && nbr::kFixedBytes + tb <= a.nbr_ws_bytes)
-            table_mode = mode;
-    }
-    if (table_mode != 0) {
-        const nbr::NbrHeader *nh = reinterpret_cast<const nbr::NbrHeader *>(a.nbr_ws);
-        const bool cube3 = nbr::is_cube3(a.ks);
-        if (table_mode == 5 && cube3)
-            tile_lookups<true, true>(a, nh, q, v);
-        else if (table_mode == 5)
-            tile_lookups<true, false>(a, nh, q, v);
-        else if (cube3)
-            tile_lookups<false, true>(a, nh, q, v);
-        else
-            tile_lookups<false, false>(a, nh, q, v);
-    } else if (a.n_q * (int64_t)K * 4 + 256 <= (int64_t)kOobOffset) {
+    if (a.n_q * (int64_t)K * 4 + 256 <= (int64_t)kOobOffset) {
         // The thread's map row (K dwords at dword K*q, rows in brick order,
         // so scattered across lanes): 16-byte loads from the aligned-down
         // address, then a shift by the row's dword offset within 16 bytes
@@ -778,7 +704,7 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
         __syncthreads();
         // Thread p owns `chunk` consecutive words, chunk odd so that the lanes
         // of a wave (stride chunk words) hit distinct LDS banks; first the
-        // popcounts, then, after the scan, the ranks in word order.
+        // popcounts, then, after the scan, each word's prefix.
         int chunk = (nw + kTileThreads - 1) / kTileThreads;
         chunk |= 1;
         const int w0 = p * chunk, w1 = min(w0 + chunk, nw);
@@ -787,13 +713,8 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
         int U;
         int run = tile_scan_excl(cnt, s_wave, U);
         for (int w = w0; w < w1; ++w) {
-            uint32_t bits = s_bits[w];
             s_pre[w] = (uint16_t)run;
-            while (bits) {
-                if (run < kPlanHaloMax) halo[run] = lo + 32 * w + __builtin_ctz(bits);
-                ++run;
-                bits &= bits - 1u;
-            }
+            run += __builtin_popcount(s_bits[w]);
         }
         if (p == 0) {
             a.tile_u[t] = U;
@@ -801,6 +722,8 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
         }
         if (U > kPlanHaloMax) return;  // handled by the direct-gather kernel
         __syncthreads();
+        // Each neighbour's rank is its local index; its row goes to that
+        // halo slot (neighbours shared by several rows write the same row).
 #pragma unroll
         for (int k = 0; k < 32; ++k) {
             if (k >= K) break;
@@ -808,24 +731,34 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
             if (v[k] >= 0) {
                 const int d = v[k] - lo, w = d >> 5;
                 out = (uint16_t)(s_pre[w] + __builtin_popcount(s_bits[w] & ((1u << (d & 31)) - 1u)));
+                s_halo[out] = v[k];
             }
             lm[k * kPlanTileRows] = out;
         }
+        __syncthreads();
+        for (int i = p; i < U; i += kTileThreads) halo[i] = s_halo[i];  // coalesced
         return;
     }
 
     // ---- wide neighbour range: LDS hash table of the distinct rows (linear
-    // probing; at most 27 * 256 keys in 8192 slots, so every probe ends).  A
-    // slot is read before it is claimed; each neighbour's slot is kept.
+    // probing, every probe loop bounded by the slot count).  A slot is read
+    // before it is claimed; each neighbour's slot is kept.  Once more than
+    // kPlanHaloMax keys are in, the tile overflows whatever follows, and
+    // insertion stops (the count of occupied slots then exceeds kPlanHaloMax).
     for (int i = p; i < kHashSlots; i += kTileThreads) s_key[i] = -1;
+    if (p == 0) s_nkeys = 0;
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < 32; ++k) {
         if (v[k] < 0) continue;
         uint32_t h = slot_hash(v[k]);
         for (int probe = 0; probe < kHashSlots; ++probe) {
+            if (*(volatile int *)&s_nkeys > kPlanHaloMax) break;
             int32_t cur = s_key[h];
-            if (cur == -1) cur = atomicCAS(&s_key[h], -1, v[k]);
+            if (cur == -1) {
+                cur = atomicCAS(&s_key[h], -1, v[k]);
+                if (cur == -1) atomicAdd(&s_nkeys, 1);
+            }
             if (cur == -1 || cur == v[k]) break;
             h = (h + 1) & (kHashSlots - 1);
         }
@@ -926,9 +859,7 @@ int plan_args(const sc_conv_config *cfg, const int32_t *d_coords, int64_t n_in, 
     char *b = static_cast<char *>(d_plan);
     a.coords = reinterpret_cast<const int4 *>(d_coords);
     a.map = d_map;
-    a.nbr_ws = nullptr;
-    a.nbr_ws_bytes = 0;
-    a.ks = kernel_shape(cfg);
+
     a.n_q = n_q;
     a.n_in = n_in;
     a.K = (int)K;
@@ -1030,23 +961,5 @@ extern "C" int sc_conv_plan_tables(const sc_conv_config *cfg, const int32_t *d_m
     PlanLayout L;
     int rc = plan_args(cfg, nullptr, n_in, d_map, n_q, d_plan, plan_bytes, false, true, a, L);
     if (rc) return rc;
-    return launch_plan_tables(a, L, as_stream(stream));
-}
-
-extern "C" int sc_conv_plan_tables_ws(const sc_conv_config *cfg, const int32_t *d_coords, const int32_t *d_map,
-                                      int64_t n_in, int64_t n_q, const void *d_map_workspace,
-                                      size_t map_workspace_bytes, void *d_plan, size_t plan_bytes,
-                                      sc_stream stream)
-{
-    clear_error();
-    PlanArgs a;
-    PlanLayout L;
-    int rc = plan_args(cfg, d_coords, n_in, d_map, n_q, d_plan, plan_bytes, true, true, a, L);
-    if (rc) return rc;
-    if (n_q > 0 && !d_map_workspace) return fail(SC_ERR_NULL, "conv plan: map workspace is NULL");
-    if ((uintptr_t)d_map_workspace % 16 != 0)
-        return fail(SC_ERR_WORKSPACE, "neighbor map workspace must be 16-byte aligned");
-    a.nbr_ws = static_cast<const uint8_t *>(d_map_workspace);
-    a.nbr_ws_bytes = map_workspace_bytes;
     return launch_plan_tables(a, L, as_stream(stream));
 }

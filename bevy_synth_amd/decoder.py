@@ -49,12 +49,8 @@ class Neighborhood:
     def build(cls, cfg: SparseSubmConvConfig, coords: torch.Tensor,
               workspace: Optional[NeighborMapWorkspace] = None, with_plan: bool = True
               ) -> "Neighborhood":
-        ws = workspace or NeighborMapWorkspace(coords.device)
-        nbr = neighbor_rows_tensor_from_coords_tensor(cfg, coords, workspace=ws)
-        plan = None
-        if with_plan and kernel_rows(cfg) <= 32:
-            # the plan's neighbours come from the map build's cell table
-            plan = build_conv_plan(cfg, coords, nbr, workspace=ws.get(coords.shape[0]))
+        nbr = neighbor_rows_tensor_from_coords_tensor(cfg, coords, workspace=workspace)
+        plan = build_conv_plan(cfg, coords, nbr) if with_plan and kernel_rows(cfg) <= 32 else None
         return cls(coords, nbr, plan)
 
 

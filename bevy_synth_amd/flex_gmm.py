@@ -255,14 +255,9 @@ class ConvPlan:
 
 
 def conv_plan_build_into(cfg: SparseSubmConvConfig, coords: torch.Tensor, neighbor_rows: torch.Tensor,
-                         buf: torch.Tensor, workspace: Optional[torch.Tensor] = None) -> ConvPlan:
-    """Stream-ordered plan build into a preallocated 256-byte aligned uint8
-    buffer.  ``workspace``: the map build's workspace (unchanged since), whose
-    cell table then supplies the neighbours instead of the map rows."""
+                         buf: torch.Tensor) -> ConvPlan:
+    """Stream-ordered plan build into a preallocated 256-byte aligned uint8 buffer."""
     n_in, n_q, K = coords.shape[0], neighbor_rows.shape[0], kernel_rows(cfg)
-    if workspace is not None:
-        conv_plan_order_into(cfg, coords, n_q, buf)
-        return conv_plan_tables_into(cfg, neighbor_rows, n_in, buf, coords=coords, workspace=workspace)
     check(_capi.load().sc_conv_plan_build(
         ctypes.byref(cfg.to_c()), _ptr(coords), n_in, _ptr(neighbor_rows), n_q, _ptr(buf),
         buf.numel(), _stream()))
@@ -279,23 +274,13 @@ def conv_plan_order_into(cfg: SparseSubmConvConfig, coords: torch.Tensor, n_q: i
 
 
 def conv_plan_tables_into(cfg: SparseSubmConvConfig, neighbor_rows: torch.Tensor, n_in: int,
-                          buf: torch.Tensor, coords: Optional[torch.Tensor] = None,
-                          workspace: Optional[torch.Tensor] = None) -> ConvPlan:
+                          buf: torch.Tensor) -> ConvPlan:
     """Second half (sc_conv_plan_tables): the halo tables, from the map; after
-    both the order and the map build.  Given the map build's ``coords`` and
-    ``workspace`` (sc_conv_plan_tables_ws), the neighbours come from its cell
-    table instead of the map rows; the plan is the same."""
+    both the order and the map build."""
     n_q, K = neighbor_rows.shape[0], kernel_rows(cfg)
-    if workspace is not None:
-        if coords is None:
-            raise SparseConvError(4, "conv plan tables from the map workspace need the coords")
-        check(_capi.load().sc_conv_plan_tables_ws(
-            ctypes.byref(cfg.to_c()), _ptr(coords), _ptr(neighbor_rows), int(n_in), n_q,
-            _ptr(workspace), workspace.numel(), _ptr(buf), buf.numel(), _stream()))
-    else:
-        check(_capi.load().sc_conv_plan_tables(
-            ctypes.byref(cfg.to_c()), _ptr(neighbor_rows), int(n_in), n_q, _ptr(buf), buf.numel(),
-            _stream()))
+    check(_capi.load().sc_conv_plan_tables(
+        ctypes.byref(cfg.to_c()), _ptr(neighbor_rows), int(n_in), n_q, _ptr(buf), buf.numel(),
+        _stream()))
     return ConvPlan(buf, int(n_in), n_q, K)
 
 
@@ -324,15 +309,12 @@ def map_and_plan_into(cfg: SparseSubmConvConfig, coords: torch.Tensor, neighbor_
         conv_plan_order_into(cfg, coords, n_q, plan_buf)
     neighbor_map_build_into(cfg, coords, neighbor_rows, workspace, query_rows=n_q)
     main.wait_stream(aux)
-    return conv_plan_tables_into(cfg, neighbor_rows, coords.shape[0], plan_buf, coords=coords,
-                                 workspace=workspace)
+    return conv_plan_tables_into(cfg, neighbor_rows, coords.shape[0], plan_buf)
 
 
 def build_conv_plan(cfg: SparseSubmConvConfig, coords: torch.Tensor,
-                    neighbor_rows: torch.Tensor, workspace: Optional[torch.Tensor] = None) -> ConvPlan:
-    """Allocates and builds the conv plan of ``neighbor_rows`` (built from
-    ``coords``; ``workspace``: that map build's workspace, see
-    conv_plan_build_into)."""
+                    neighbor_rows: torch.Tensor) -> ConvPlan:
+    """Allocates and builds the conv plan of ``neighbor_rows`` (built from ``coords``)."""
     _require_cuda("coords", coords)
     _require_cuda("neighbor_rows", neighbor_rows)
     K = kernel_rows(cfg)
@@ -340,7 +322,7 @@ def build_conv_plan(cfg: SparseSubmConvConfig, coords: torch.Tensor,
         raise SparseConvError(2, f"conv plan: neighbor rows must be int32 [N_q, {K}]")
     buf = torch.empty(conv_plan_bytes(neighbor_rows.shape[0], K), dtype=torch.uint8,
                       device=coords.device)
-    return conv_plan_build_into(cfg, coords, neighbor_rows, buf, workspace=workspace)
+    return conv_plan_build_into(cfg, coords, neighbor_rows, buf)
 
 
 def conv_weight_pack_bytes(cfg: SparseSubmConvConfig, w_dtype: torch.dtype) -> int:

@@ -232,20 +232,6 @@ int sc_conv_plan_order(const sc_conv_config *cfg, const int32_t *d_coords, int64
 int sc_conv_plan_tables(const sc_conv_config *cfg, const int32_t *d_map, int64_t n_in, int64_t n_q,
                         void *d_plan, size_t plan_bytes, sc_stream stream);
 
-/*
- * sc_conv_plan_tables taking each tile row's neighbours from the cell table
- * of the sc_neighbor_map_build call that wrote d_map instead of its map row:
- * d_map_workspace is that call's workspace (unchanged since) and d_coords its
- * coords (map_workspace_bytes its size).  For a dense grid or rank bitmap
- * built for the same kernel shape,
- * each (row, offset) is one cached table lookup instead of a scattered
- * K*4-byte map row per tile row; otherwise d_map is read as by
- * sc_conv_plan_tables.  Either way the plan is the same.
- */
-int sc_conv_plan_tables_ws(const sc_conv_config *cfg, const int32_t *d_coords, const int32_t *d_map,
-                           int64_t n_in, int64_t n_q, const void *d_map_workspace,
-                           size_t map_workspace_bytes, void *d_plan, size_t plan_bytes,
-                           sc_stream stream);
 
 /*
  * Weights packed for the planned conv: per (group, 128-output-channel tile,

@@ -123,6 +123,16 @@ def test_plan_structure(which):
             assert np.array_equal(h["lmap"][t], h2["lmap"][t])
 
 
+def assert_same_plan(h, ref):
+    for key in ("order", "tile_u", "overflow"):
+        assert np.array_equal(h[key], ref[key]), key
+    for t in range(h["n_tiles"]):
+        U = h["tile_u"][t]
+        if U <= F.PLAN_HALO_MAX:
+            assert np.array_equal(h["halo"][t, :U], ref["halo"][t, :U]), t
+            assert np.array_equal(h["lmap"][t], ref["lmap"][t]), t
+
+
 @pytest.mark.parametrize("q", [None, 9000])
 def test_overlapped_map_and_plan_matches_separate_builds(q):
     """map_and_plan_into (plan order on a side stream during the map build,
@@ -140,71 +150,7 @@ def test_overlapped_map_and_plan_matches_separate_builds(q):
         plan = F.map_and_plan_into(cfg, cd, nbr, ws, buf)
         torch.cuda.synchronize()
         assert torch.equal(nbr, ref_nbr)
-        h = plan.to_host()
-        for key in ("order", "tile_u", "overflow"):
-            assert np.array_equal(h[key], ref[key]), key
-        for t in range(h["n_tiles"]):
-            U = h["tile_u"][t]
-            if U <= F.PLAN_HALO_MAX:
-                assert np.array_equal(h["halo"][t, :U], ref["halo"][t, :U])
-                assert np.array_equal(h["lmap"][t], ref["lmap"][t])
-
-
-def assert_same_plan(h, ref):
-    for key in ("order", "tile_u", "overflow"):
-        assert np.array_equal(h[key], ref[key]), key
-    for t in range(h["n_tiles"]):
-        U = h["tile_u"][t]
-        if U <= F.PLAN_HALO_MAX:
-            assert np.array_equal(h["halo"][t, :U], ref["halo"][t, :U]), t
-            assert np.array_equal(h["lmap"][t], ref["lmap"][t]), t
-
-
-@pytest.mark.parametrize("case", ["sorted", "shuffled", "kernel331", "axes", "sparse_hash",
-                                  "other_shape", "query_subset"])
-def test_plan_tables_from_map_workspace(case):
-    """sc_conv_plan_tables_ws (neighbours from the map build's dense grid or
-    rank bitmap) gives the plan that reading the map rows gives; a hash-table
-    build, or a workspace built for another kernel shape, reads the map."""
-    rng = np.random.default_rng(5)
-    coords = synth.config1_coords()
-    cfg = F.SparseSubmConvConfig(32, 32)
-    q = None
-    want_mode = "rank_bitmap"
-    if case == "shuffled":
-        coords = coords[rng.permutation(len(coords))]
-        want_mode = "dense_grid"
-    elif case == "kernel331":
-        cfg = F.SparseSubmConvConfig(32, 32, 3, 3, 1)
-    elif case == "axes":
-        cfg = F.SparseSubmConvConfig(32, 32, axis_order=(2, 0, 1), axis_sign=(-1, 1, -1))
-    elif case == "sparse_hash":
-        c = rng.integers(0, 1000, size=(20000, 4)).astype(np.int32)
-        c[:, 0] = rng.integers(0, 2, 20000)
-        c[:3000, 1:] = c[3000:6000, 1:] + rng.integers(-1, 2, (3000, 3))
-        c[:3000, 0] = c[3000:6000, 0]
-        u = np.unique(np.maximum(c, 0), axis=0)
-        coords = u[rng.permutation(len(u))]
-        want_mode = "hash32"
-    elif case == "query_subset":
-        q = 9000
-    cd = dev(coords)
-    n_q = len(coords) if q is None else q
-    ws = F.NeighborMapWorkspace().get(len(coords))
-    nbr = torch.empty((n_q, F.kernel_rows(cfg)), dtype=torch.int32, device="cuda")
-    if case == "other_shape":
-        # the workspace holds the table of a build for another axis order
-        other = F.SparseSubmConvConfig(32, 32, axis_order=(1, 0, 2))
-        F.neighbor_map_build_into(cfg, cd, nbr, ws)
-        ref_nbr = nbr.clone()
-        F.neighbor_map_build_into(other, cd, nbr, ws)
-        nbr = ref_nbr
-    else:
-        F.neighbor_map_build_into(cfg, cd, nbr, ws, query_rows=n_q)
-    assert F.neighbor_map_table_mode(ws) == want_mode
-    ref = F.build_conv_plan(cfg, cd, nbr).to_host()
-    h = check_plan(F.build_conv_plan(cfg, cd, nbr, workspace=ws), nbr.cpu().numpy(), len(coords))
-    assert_same_plan(h, ref)
+        assert_same_plan(plan.to_host(), ref)
 
 
 @pytest.mark.parametrize("cin,cout,groups,wdt", [(64, 128, 1, "bf16"), (96, 200, 1, "bf16"),
