@@ -76,7 +76,7 @@ struct PlanArgs {
 
 constexpr uint32_t kGridEmpty = 0xFFFFFFFFu;
 
-__global__ void plan_init_kernel(PlanArgs a)
+__device__ inline void plan_init(const PlanArgs &a)
 {
     const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -101,6 +101,10 @@ __global__ void plan_init_kernel(PlanArgs a)
     for (int64_t i = a.n_q + tid; i < a.n_tiles * kPlanTileRows; i += stride) a.order[i] = -1;
 }
 
+// Header and padding entries of `order` (only launched without query rows;
+// otherwise plan_bbox_kernel does it).
+__global__ void plan_init_kernel(PlanArgs a) { plan_init(a); }
+
 // Per-block min/max of the query coords -> partials (in the brick-offset
 // array, which the scan overwrites later); plan_bbox_final_kernel reduces them
 // (one atomic-free pass instead of thousands of same-address atomics).
@@ -109,6 +113,7 @@ constexpr int kBboxBlocks = 512;
 __global__ __launch_bounds__(kThreads) void plan_bbox_kernel(PlanArgs a)
 {
     __shared__ int s_mn[4][4], s_mx[4][4];
+    plan_init(a);  // header and order padding (read by no kernel before the next launch)
     int mn[4] = {INT_MAX, INT_MAX, INT_MAX, INT_MAX}, mx[4] = {INT_MIN, INT_MIN, INT_MIN, INT_MIN};
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n_q;
          i += (int64_t)gridDim.x * blockDim.x) {
@@ -248,6 +253,7 @@ struct GridGeom {
     int64_t lo[4];
     int64_t nb[4];
     int64_t cells;
+    int64_t blocks;  // 2048-cell blocks holding cells
 };
 
 __device__ inline GridGeom grid_geom(const PlanHeader *h, int64_t grid_cap)
@@ -255,6 +261,7 @@ __device__ inline GridGeom grid_geom(const PlanHeader *h, int64_t grid_cap)
     GridGeom g;
     g.ok = false;
     g.cells = 0;
+    g.blocks = 0;
     double tot = 512.0;
     for (int j = 0; j < 4; ++j) {
         g.lo[j] = h->bmin[j];
@@ -266,6 +273,7 @@ __device__ inline GridGeom grid_geom(const PlanHeader *h, int64_t grid_cap)
     if (tot > (double)grid_cap) return g;
     g.ok = true;
     g.cells = g.nb[0] * g.nb[1] * g.nb[2] * g.nb[3] * 512;
+    g.blocks = (g.cells + kPlanGridBlock - 1) / kPlanGridBlock;
     return g;
 }
 
@@ -384,6 +392,7 @@ __global__ __launch_bounds__(kThreads) void plan_scan1_kernel(PlanArgs a)
             if (threadIdx.x == 0) a.bsum[rb] = total;
             return;
         }
+        if ((int64_t)blockIdx.x >= gg.blocks) return;  // beyond the cells in use
         const int64_t base = (int64_t)blockIdx.x * kPlanGridBlock + threadIdx.x * 8;
         int cnt = 0;
         if (base < gg.cells) {
@@ -419,7 +428,7 @@ __global__ __launch_bounds__(kThreads) void plan_scan2_kernel(PlanArgs a)
     const bool grid = a.hdr->grid_mode != 0;
     if (!grid && a.hdr->brick_shift < 0) return;
     int32_t *arr = grid ? a.gsum : a.bsum;
-    const int64_t n = grid ? a.grid_cap / kPlanGridBlock : a.n_bsum;
+    const int64_t n = grid ? grid_geom(a.hdr, a.grid_cap).blocks : a.n_bsum;
     int carry = 0;
     for (int64_t base = 0; base < n; base += kThreads * 4) {
         int v[4];
@@ -494,6 +503,7 @@ __global__ __launch_bounds__(kThreads) void plan_emit_kernel(PlanArgs a)
                 if ((flags >> u) & 1u) a.order[pos++] = (int32_t)(r0 + u);
             return;
         }
+        if ((int64_t)blockIdx.x >= gg.blocks) return;  // beyond the cells in use
         const int64_t base = (int64_t)blockIdx.x * kPlanGridBlock + threadIdx.x * 8;
         uint32_t r[8];
         int cnt = 0;
@@ -884,9 +894,11 @@ int plan_args(const sc_conv_config *cfg, const int32_t *d_coords, int64_t n_in, 
 int launch_plan_order(const PlanArgs &a, const PlanLayout &L, hipStream_t s)
 {
     const int64_t n_q = a.n_q;
-    plan_init_kernel<<<grid_for(L.n_tiles * kPlanTileRows, kThreads, 1024), kThreads, 0, s>>>(a);
-    SC_LAUNCH_CHECK("plan_init_kernel launch");
-    if (n_q == 0) return SC_OK;
+    if (n_q == 0) {
+        plan_init_kernel<<<grid_for(L.n_tiles * kPlanTileRows, kThreads, 1024), kThreads, 0, s>>>(a);
+        SC_LAUNCH_CHECK("plan_init_kernel launch");
+        return SC_OK;
+    }
     const unsigned nbb = grid_for(n_q, kThreads, kBboxBlocks);
     plan_bbox_kernel<<<nbb, kThreads, 0, s>>>(a);
     SC_LAUNCH_CHECK("plan_bbox_kernel launch");
