@@ -4,16 +4,20 @@
 // wgpu/neighbor_kernels.rs K1-K8 and their routing in wgpu/neighbor.rs:9-57,
 // 777-936) with one order-independent algorithm:
 //
-//   1. init   : header (bbox accumulators, status) + table slots := EMPTY
-//   2. bbox   : coalesced int4 coord loads, wave64/LDS min-max reduction,
-//               one atomic per block and component; negative coords flagged
+//   1. bbox   : coalesced int4 coord loads, per-block min/max partials
+//               (wave64/LDS reductions, no atomics); negative coords and rows
+//               out of (b, x, y, z) order flagged
+//   2. init   : every block reduces the partials and derives the table
+//               plan; block 0 writes the header and the per-offset table;
+//               all blocks fill the table region
 //   3. insert : key = mixed-radix index of (b,x,y,z) inside the bbox; a
 //               32-bit key packs with the row into one 64-bit slot (single
 //               atomicCAS, atomicMin on the slot keeps the LOWEST row of
 //               duplicates); wider keys use a u64 key array + u32 row array;
 //               a bbox beyond 2^64-1 cells uses a row-only table whose slots
 //               are compared through the coords themselves
-//   4. query  : R rows per block staged in LDS, one (row, k) entry per lane,
+//   4. query  : one row per lane for the dense tables (below), else R rows
+//               per block staged in LDS, one (row, k) entry per lane;
 //               coalesced map writes; neighbours outside the bbox (including
 //               negative ones) are rejected before probing
 //
@@ -135,27 +139,6 @@ __device__ inline int32_t rank_lookup(const uint64_t *__restrict__ words, uint64
     return (int32_t)(uint32_t)(w >> 32) + __builtin_popcount(bits & ((1u << b) - 1u));
 }
 
-// Fills the table region the plan uses: all-ones (EMPTY keys, EMPTY rows)
-// over cap*12 bytes for the hash modes; zero (no cell occupied) over the
-// grid's total*4 bytes and the rank bitmap's ceil(total/32) words.
-__global__ void nm_table_init_kernel(const NbrHeader *__restrict__ h, uint64_t *words, uint64_t cap)
-{
-    const Plan p = h->plan;
-    if (p.mode == 0) return;
-    uint64_t n_words = cap + cap / 2, fill = kEmpty64;
-    if (p.mode == 4) {
-        n_words = (p.total + 1) / 2;
-        fill = 0;
-    }
-    if (p.mode == 5) {
-        n_words = (p.total + 31) / 32;
-        fill = 0;
-    }
-    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_words; i += stride)
-        words[i] = fill;
-}
-
 __device__ inline bool coord_less(const int4 a, const int4 b)
 {
     if (a.x != b.x) return a.x < b.x;
@@ -164,11 +147,14 @@ __device__ inline bool coord_less(const int4 a, const int4 b)
     return a.w < b.w;
 }
 
-// Per-block bbox partials (4 min, 4 max, negative flag, order flag), no atomics.
-constexpr int kBboxBlocks = 1024;
+// Per-block bbox partials (4 min, 4 max, negative flag, order flag), no atomics;
+// at most 256 blocks of 1024 threads, so that every block of the next launch
+// can reduce the partials.
+constexpr int kBboxBlocks = 256;
+constexpr int kBboxThreads = 1024;
 constexpr int kPartialInts = 10;
 
-__global__ __launch_bounds__(256) void nm_bbox_partial_kernel(const int4 *__restrict__ coords, int64_t n,
+__global__ __launch_bounds__(kBboxThreads) void nm_bbox_partial_kernel(const int4 *__restrict__ coords, int64_t n,
                                                               int32_t *__restrict__ partials)
 {
     int mn[4] = {INT_MAX, INT_MAX, INT_MAX, INT_MAX};
@@ -176,25 +162,35 @@ __global__ __launch_bounds__(256) void nm_bbox_partial_kernel(const int4 *__rest
     int neg = 0, uns = 0;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    // Wave-uniform loop: lane l holds row w0 + l, so lane l - 1 holds its predecessor.
-    for (int64_t w0 = (int64_t)blockIdx.x * blockDim.x + wave * 64; w0 < n; w0 += stride) {
-        const int64_t i = w0 + lane;
-        const bool valid = i < n;
-        const int4 c = valid ? coords[i] : make_int4(0, 0, 0, 0);
-        int4 prev = make_int4(__shfl_up(c.x, 1), __shfl_up(c.y, 1), __shfl_up(c.z, 1), __shfl_up(c.w, 1));
-        if (lane == 0 && valid && i > 0) prev = coords[i - 1];
-        if (valid) {
-            const int v[4] = {c.x, c.y, c.z, c.w};
+    // Wave-uniform loop, four rows per lane in flight: in each of them lane
+    // l holds row w0 + u * stride + l, so lane l - 1 holds its predecessor.
+    for (int64_t w0 = (int64_t)blockIdx.x * blockDim.x + wave * 64; w0 < n; w0 += 4 * stride) {
+        int4 c[4], pl[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                mn[j] = min(mn[j], v[j]);
-                mx[j] = max(mx[j], v[j]);
-                neg |= v[j] < 0;
+        for (int u = 0; u < 4; ++u) {
+            const int64_t i = w0 + u * stride + lane;
+            c[u] = i < n ? coords[i] : make_int4(0, 0, 0, 0);
+            pl[u] = lane == 0 && i < n && i > 0 ? coords[i - 1] : make_int4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t i = w0 + u * stride + lane;
+            const int4 cu = c[u];
+            int4 prev = make_int4(__shfl_up(cu.x, 1), __shfl_up(cu.y, 1), __shfl_up(cu.z, 1), __shfl_up(cu.w, 1));
+            if (lane == 0) prev = pl[u];
+            if (i < n) {
+                const int v[4] = {cu.x, cu.y, cu.z, cu.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    mn[j] = min(mn[j], v[j]);
+                    mx[j] = max(mx[j], v[j]);
+                    neg |= v[j] < 0;
+                }
+                if (i > 0) uns |= !coord_less(prev, cu);
             }
-            if (i > 0) uns |= !coord_less(prev, c);
         }
     }
-    __shared__ int s_red[4][kPartialInts];  // per wave: 4 min, 4 max, neg, unsorted
+    __shared__ int s_red[kBboxThreads / 64][kPartialInts];  // per wave: 4 min, 4 max, neg, unsorted
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         mn[j] = wave_min_i32(mn[j]);
@@ -220,12 +216,20 @@ __global__ __launch_bounds__(256) void nm_bbox_partial_kernel(const int4 *__rest
     }
 }
 
-// One block: reduces the partials and writes the header (bbox, status, order
-// flag, and the mode every later kernel derives from them).
-__global__ __launch_bounds__(256) void nm_bbox_final_kernel(const int32_t *__restrict__ partials,
-                                                            int nblocks, NbrHeader *h, Limits lim,
-                                                            KernelShape ks, int4 *__restrict__ otab)
+// Every block reduces the partials (at most kBboxBlocks x 10 ints, a few KB
+// from L2) and derives the table plan from them, then fills its share of the
+// table region: all-ones (EMPTY keys, EMPTY rows) over cap*12 bytes for the
+// hash modes; zero (no cell occupied) over the grid's total*4 bytes and the
+// rank bitmap's ceil(total/32) words.  Block 0 also writes the header (bbox,
+// status, order flag, plan) and the offset table {dx, dy, dz, cell delta}
+// that the insert and query kernels read.
+__global__ __launch_bounds__(256) void nm_plan_init_kernel(const int32_t *__restrict__ partials, int nblocks,
+                                                           NbrHeader *__restrict__ h, Limits lim, KernelShape ks,
+                                                           int4 *__restrict__ otab, uint64_t *__restrict__ words,
+                                                           uint64_t cap)
 {
+    __shared__ int s_red[4][kPartialInts];
+    __shared__ NbrHeader s_h;
     int mn[4] = {INT_MAX, INT_MAX, INT_MAX, INT_MAX};
     int mx[4] = {INT_MIN, INT_MIN, INT_MIN, INT_MIN};
     int neg = 0, uns = 0;
@@ -239,7 +243,6 @@ __global__ __launch_bounds__(256) void nm_bbox_final_kernel(const int32_t *__res
         neg |= pb[8];
         uns |= pb[9];
     }
-    __shared__ int s_red[4][kPartialInts];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -262,30 +265,47 @@ __global__ __launch_bounds__(256) void nm_bbox_final_kernel(const int32_t *__res
         int v = s_red[0][j];
         for (int w = 1; w < (int)(blockDim.x >> 6); ++w) v = j < 4 ? min(v, s_red[w][j]) : max(v, s_red[w][j]);
         if (j < 4)
-            h->bmin[j] = v;
+            s_h.bmin[j] = v;
         else if (j < 8)
-            h->bmax[j - 4] = v;
+            s_h.bmax[j - 4] = v;
         else if (j == 8)
-            h->status = v ? kStatusNegative : 0u;
+            s_h.status = v ? kStatusNegative : 0u;
         else
-            h->unsorted = (uint32_t)v;
+            s_h.unsorted = (uint32_t)v;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        const Plan p = make_plan(h, lim);
-        h->plan = p;
-        h->mode = p.mode;
+        const Plan p = make_plan(&s_h, lim);
+        s_h.plan = p;
+        s_h.mode = p.mode;
+        s_h.pad0 = 0;
     }
     __syncthreads();
-    // Offset table for the query: {dx, dy, dz} and the 32-bit cell delta of
-    // the offset (wraps; only used for neighbours inside the bbox).
-    const Plan p = h->plan;
-    const uint32_t sy = (uint32_t)p.ext[3], sx = (uint32_t)(p.ext[2] * p.ext[3]);
-    for (int k = threadIdx.x; k < ks.K && k < kMaxStagedOffsets; k += blockDim.x) {
-        int o[3];
-        offset_of(ks, k, o);
-        otab[k] = make_int4(o[0], o[1], o[2], (int)((uint32_t)o[0] * sx + (uint32_t)o[1] * sy + (uint32_t)o[2]));
+    const Plan p = s_h.plan;
+    if (blockIdx.x == 0) {
+        static_assert(sizeof(NbrHeader) % 16 == 0, "header copies in 16-byte pieces");
+        if (threadIdx.x < sizeof(NbrHeader) / 16)
+            reinterpret_cast<uint4 *>(h)[threadIdx.x] = reinterpret_cast<const uint4 *>(&s_h)[threadIdx.x];
+        // 32-bit cell delta of each offset (wraps; only used for neighbours inside the bbox)
+        const uint32_t sy = (uint32_t)p.ext[3], sx = (uint32_t)(p.ext[2] * p.ext[3]);
+        for (int k = threadIdx.x; k < ks.K && k < kMaxStagedOffsets; k += blockDim.x) {
+            int o[3];
+            offset_of(ks, k, o);
+            otab[k] = make_int4(o[0], o[1], o[2], (int)((uint32_t)o[0] * sx + (uint32_t)o[1] * sy + (uint32_t)o[2]));
+        }
     }
+    if (p.mode == 0) return;
+    uint64_t n_words = cap + cap / 2, fill = kEmpty64;
+    if (p.mode == 4) {
+        n_words = (p.total + 1) / 2;
+        fill = 0;
+    }
+    if (p.mode == 5) {
+        n_words = (p.total + 31) / 32;
+        fill = 0;
+    }
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_words; i += stride) words[i] = fill;
 }
 
 __global__ __launch_bounds__(256) void nm_insert_kernel(const int4 *__restrict__ coords, int64_t n,
@@ -717,13 +737,11 @@ int sc_neighbor_map_build(const sc_conv_config *cfg, const int32_t *d_coords, in
         return SC_OK;
     }
     const int4 *c4 = (const int4 *)d_coords;
-    const unsigned bb = grid_for(n_rows, 256, kBboxBlocks);
-    nm_bbox_partial_kernel<<<bb, 256, 0, s>>>(c4, n_rows, partials);
+    const unsigned bb = grid_for(n_rows, kBboxThreads, kBboxBlocks);
+    nm_bbox_partial_kernel<<<bb, kBboxThreads, 0, s>>>(c4, n_rows, partials);
     SC_LAUNCH_CHECK("nm_bbox_partial_kernel launch");
-    nm_bbox_final_kernel<<<1, 256, 0, s>>>(partials, (int)bb, h, lim, kernel_shape(cfg), otab);
-    SC_LAUNCH_CHECK("nm_bbox_final_kernel launch");
-    nm_table_init_kernel<<<4096, 256, 0, s>>>(h, keys, cap);
-    SC_LAUNCH_CHECK("nm_table_init_kernel launch");
+    nm_plan_init_kernel<<<512, 256, 0, s>>>(partials, (int)bb, h, lim, kernel_shape(cfg), otab, keys, cap);
+    SC_LAUNCH_CHECK("nm_plan_init_kernel launch");
     nm_insert_kernel<<<grid_for(n_rows, 256, 65536), 256, 0, s>>>(c4, n_rows, h, keys, rows, cap - 1);
     SC_LAUNCH_CHECK("nm_insert_kernel launch");
     if (query_rows == 0) return SC_OK;
