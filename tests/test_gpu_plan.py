@@ -80,7 +80,8 @@ def check_plan(plan, nbr, n_in):
     return h
 
 
-@pytest.mark.parametrize("which", ["config1", "random_batches", "clusters", "query_subset", "duplicates"])
+@pytest.mark.parametrize("which", ["config1", "random_batches", "clusters", "query_subset", "duplicates",
+                                   "wide_bbox"])
 def test_plan_structure(which):
     rng = np.random.default_rng(11)
     cfg = F.SparseSubmConvConfig(32, 32)
@@ -102,6 +103,14 @@ def test_plan_structure(which):
         base = synth.config1_coords()
         coords = np.concatenate([base, base[rng.integers(0, len(base), 3000)]])
         coords = coords[rng.permutation(len(coords))]
+    elif which == "wide_bbox":
+        # a bounding box far beyond the occupancy grid's budget (16 cells per
+        # row): the counting-sort order, with duplicated coords in two batches
+        c = rng.integers(0, 1000, size=(20000, 4)).astype(np.int32)
+        c[:, 0] = rng.integers(0, 2, 20000)
+        c[:4000] = c[4000:8000] + np.array([0, 1, 0, 0], np.int32)       # neighbours in x
+        c[-300:] = c[:300]                                               # duplicates
+        coords = c[rng.permutation(len(c))]
     else:
         coords = synth.config1_coords()
         q = 9000
@@ -109,8 +118,11 @@ def test_plan_structure(which):
     nbr = F.neighbor_rows_tensor_from_coords_tensor(cfg, cd, query_rows=q)
     plan = F.build_conv_plan(cfg, cd, nbr)
     h = check_plan(plan, nbr.cpu().numpy(), len(coords))
+    assert h["grid_mode"] == (0 if which == "wide_bbox" else 1)
     if which == "clusters":
         assert h["n_overflow"] == h["n_tiles"]
+    if which in ("duplicates", "config1"):
+        assert h["n_unique"] == len(np.unique(coords, axis=0))
     # deterministic: a second build gives the same tables (entries past a
     # tile's halo count, and the tables of overflowing tiles, are not written)
     h2 = F.build_conv_plan(cfg, cd, nbr).to_host()
