@@ -313,6 +313,39 @@ __global__ void c2s_skip_add_kernel(T *h, int64_t n, int64_t out_ch, const Tp *_
     }
 }
 
+// bf16 output rows, out_ch a multiple of 8, 16-byte aligned: one thread per
+// 8-channel vector of h (one 16-byte load and store), 32-bit index math; the
+// parent values of the vector's channels are read individually (consecutive
+// channels share a parent channel `rep` at a time, so they hit one line).
+template <typename Tp>
+__global__ void c2s_skip_add_vec_kernel(uint16_t *h, int n, int vpr, const Tp *__restrict__ parent,
+                                        int64_t parent_rows, int64_t parent_ch, const int32_t *__restrict__ idx,
+                                        int rep)
+{
+    const int S = (int)(parent_ch / 8);
+    const int64_t total = (int64_t)n * vpr;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
+        const int a = (int)(e / vpr), v = (int)(e - (int64_t)a * vpr);
+        const int64_t li = idx[a];
+        if (li < 0 || li >= parent_rows * 8) continue;  // out-of-range index: no skip term
+        const Tp *pr = parent + (li >> 3) * parent_ch + (li & 7) * S;
+        uint4 *hp = reinterpret_cast<uint4 *>(h + (int64_t)e * 8);
+        uint4 x = *hp;
+        uint32_t w[4] = {x.x, x.y, x.z, x.w};
+        const int j0 = 8 * v;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float s0 = load_as_f32<Tp>(pr, (j0 + 2 * u) / rep);
+            const float s1 = load_as_f32<Tp>(pr, (j0 + 2 * u + 1) / rep);
+            const float lo = bf16_to_f32((uint16_t)(w[u] & 0xFFFFu)) + s0;
+            const float hi = bf16_to_f32((uint16_t)(w[u] >> 16)) + s1;
+            w[u] = (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+        }
+        *hp = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
 template <typename Tin, typename Tout>
 int launch_layer_norm(const void *in, int64_t rows, int64_t ch, const float *w,
                              const float *b, float eps, int silu, void *out, hipStream_t s)
@@ -544,6 +577,20 @@ int sc_c2s_skip_add(int dtype, void *d_h, int64_t n, int64_t out_channels, int p
     if (!d_h || !d_parent || !d_idx) return fail(SC_ERR_NULL, "c2s_skip_add: NULL pointer");
     const int64_t rep = out_channels / S;
     hipStream_t s = as_stream(stream);
+    if (dtype == SC_DTYPE_BF16 && out_channels % 8 == 0 && (uintptr_t)d_h % 16 == 0 && n <= INT32_MAX &&
+        out_channels / 8 <= INT32_MAX && (parent_dtype == SC_DTYPE_BF16 || parent_dtype == SC_DTYPE_F32)) {
+        const int vpr = (int)(out_channels / 8);
+        const unsigned gv = grid_for(n * vpr, 256, 65536);
+        if (parent_dtype == SC_DTYPE_BF16)
+            c2s_skip_add_vec_kernel<uint16_t><<<gv, 256, 0, s>>>((uint16_t *)d_h, (int)n, vpr,
+                                                                 (const uint16_t *)d_parent, parent_rows,
+                                                                 parent_channels, d_idx, (int)rep);
+        else
+            c2s_skip_add_vec_kernel<float><<<gv, 256, 0, s>>>((uint16_t *)d_h, (int)n, vpr, (const float *)d_parent,
+                                                              parent_rows, parent_channels, d_idx, (int)rep);
+        SC_LAUNCH_CHECK("c2s_skip_add_vec_kernel launch");
+        return SC_OK;
+    }
     const unsigned g = grid_for(n * out_channels, 256, 65536);
 #define SKIP_LAUNCH(T, TP)                                                                    \
     c2s_skip_add_kernel<T, TP><<<g, 256, 0, s>>>((T *)d_h, n, out_channels, (const TP *)d_parent, \

@@ -116,6 +116,28 @@ def test_gather_rows_and_skip_add(oracle):
     assert np.array_equal(hd.cpu().numpy(), h + oracle.repeat_interleave(cf, cout // (cin // 8)))
 
 
+@pytest.mark.parametrize("cin,cout,pdt", [(64, 32, torch.bfloat16), (64, 32, torch.float32),
+                                          (128, 64, torch.bfloat16), (64, 8, torch.bfloat16),
+                                          (32, 12, torch.bfloat16)])
+def test_skip_add_bf16(oracle, cin, cout, pdt):
+    """bf16 child rows: the 8-channel vector kernel (cout a multiple of 8) or
+    the element kernel (cout = 12); the sum is rounded to bf16 once."""
+    rng = np.random.default_rng(6)
+    P = 700
+    parents = np.zeros((P, 4), np.int32)
+    parents[:, 1:] = rng.integers(0, 100, (P, 3))
+    r = oracle.bf16_round
+    feats = r(rng.standard_normal((P, cin)).astype(np.float32))
+    mask = (rng.random((P, 8)) < 0.5).astype(np.uint8)
+    _, li, _ = F.subdivision_build(dev(parents), mask=dev(mask))
+    _, cf = oracle.channel2spatial(parents.astype(np.uint32), feats, cin, mask)
+    h = r(rng.standard_normal((len(cf), cout)).astype(np.float32))
+    hd = dev(h).to(torch.bfloat16)
+    F.c2s_skip_add(hd, dev(feats).to(pdt), li)
+    want = r(h + oracle.repeat_interleave(cf, cout // (cin // 8)))
+    assert np.array_equal(hd.float().cpu().numpy(), want)
+
+
 def _c2s_inputs(rng, P_grid=(8, 7, 6), cin=64, cout=32):
     g = np.stack(np.meshgrid(*[np.arange(s) for s in P_grid], indexing="ij"), -1).reshape(-1, 3)
     keep = rng.random(len(g)) < 0.6
