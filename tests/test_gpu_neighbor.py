@@ -270,3 +270,23 @@ def test_config3_shuffled_takes_dense_grid(oracle):
     got, mode = _map_and_mode(cfg, coords[sw])
     assert mode == "dense_grid"
     assert np.array_equal(got, np.where(base[sw] >= 0, sw[np.maximum(base[sw], 0)], -1))
+
+
+@pytest.mark.parametrize("kernel", [(3, 3, 3), (3, 3, 1), (1, 1, 1), (2, 2, 2), (5, 5, 5), (1, 3, 5)])
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_rank_bitmap_small_dense_bboxes(oracle, kernel, seed):
+    """Sorted unique coords in small bboxes (rows at every face and corner of
+    the bbox, 32-cell words crossed by neighbour runs, a partial last word,
+    a batch holding one voxel): the rank bitmap against the oracle."""
+    rng = np.random.default_rng(100 + seed)
+    ext = rng.integers(1, 12, 3)
+    cells = np.stack(np.meshgrid(*[np.arange(e) for e in ext], indexing="ij"), -1).reshape(-1, 3)
+    keep = rng.random(len(cells)) < rng.uniform(0.2, 0.9)
+    c = np.zeros((int(keep.sum()) + 1, 4), np.int32)
+    c[:-1, 1:] = cells[keep] + rng.integers(0, 5, 3)
+    c[-1] = [1, 3, 2, 1]                                       # second batch, one voxel
+    c = np.unique(c, axis=0)
+    cfg = F.SparseSubmConvConfig(1, 1, *kernel)
+    got, mode = _map_and_mode(cfg, c)
+    assert mode == "rank_bitmap"
+    assert np.array_equal(got, oracle.build_neighbor_rows(ocfg(oracle, cfg), c))
