@@ -727,8 +727,12 @@ int sc_neighbor_map_build(const sc_conv_config *cfg, const int32_t *d_coords, in
     if (dense_cells > dense_cells_for(n_rows)) dense_cells = dense_cells_for(n_rows);
     dense_cells &= ~1ull;  // even: the 8-byte fill of an odd cell count stays inside
     if (dense_cells > 0xffffffffull) dense_cells = 0xfffffffeull;  // 32-bit grid keys
-    // Rank bitmap (sorted, unique rows): 8 B per 32 cells, 32-bit cell keys.
+    // Rank bitmap (sorted, unique rows): 8 B per 32 cells, 32-bit cell keys,
+    // at most 512 cells per row (what the default workspace holds; a larger
+    // workspace does not make a sparser bbox take the bitmap).
     uint64_t bitmap_cells = (workspace_bytes - kFixedBytes) / 8u * 32u;
+    const uint64_t bitmap_cap = 16u * dense_cells_for(n_rows);
+    if (bitmap_cells > bitmap_cap) bitmap_cells = bitmap_cap;
     if (bitmap_cells > 0xffffffffull) bitmap_cells = 0xffffffffull;
     const Limits lim{dense_cells, bitmap_cells};
     if (n_rows == 0) {
