@@ -197,4 +197,13 @@ __device__ inline int wave_max_i32(int v)
     return v;
 }
 
+__device__ inline int tile_for_block(int b, int G)
+{
+    // Dispatch assigns workgroup b to XCD b % 8; give each XCD a contiguous
+    // range of row tiles so that neighbouring tiles share its L2.
+    const int x = b & 7, pos = b >> 3;
+    const int q = G >> 3, r = G & 7;
+    return x * q + min(x, r) + pos;
+}
+
 }  // namespace sc

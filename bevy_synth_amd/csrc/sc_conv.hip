@@ -175,15 +175,6 @@ struct Out4<uint16_t> {
     }
 };
 
-__device__ inline int tile_for_block(int b, int G)
-{
-    // Dispatch assigns workgroup b to XCD b % 8; give each XCD a contiguous
-    // range of row tiles so that neighbouring tiles share its L2.
-    const int x = b & 7, pos = b >> 3;
-    const int q = G >> 3, r = G & 7;
-    return x * q + min(x, r) + pos;
-}
-
 // ------------------------------------------------------------- MFMA tile
 
 // Per-tile list of kernel offsets (K <= 32) used by at least one row of the

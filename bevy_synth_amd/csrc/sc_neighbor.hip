@@ -531,7 +531,14 @@ __device__ inline void query_cells(const int4 *__restrict__ coords, int64_t row0
         const int n4 = n_ints >> 2;
         int4 *dst4 = reinterpret_cast<int4 *>(out);
         const int4 *src4 = reinterpret_cast<const int4 *>(s_out);
-        for (int i = threadIdx.x; i < n4; i += blockDim.x) dst4[i] = src4[i];
+        // Streaming stores: the map is not read back by this kernel, and
+        // keeping it out of L2 leaves the cell table resident there.
+        typedef int i32x4 __attribute__((ext_vector_type(4)));
+        for (int i = threadIdx.x; i < n4; i += blockDim.x) {
+            const int4 v = src4[i];
+            const i32x4 t = {v.x, v.y, v.z, v.w};
+            __builtin_nontemporal_store(t, reinterpret_cast<i32x4 *>(dst4) + i);
+        }
         for (int i = (n4 << 2) + threadIdx.x; i < n_ints; i += blockDim.x) out[i] = s_out[i];
     } else {
         for (int i = threadIdx.x; i < n_ints; i += blockDim.x) out[i] = s_out[i];
@@ -557,7 +564,9 @@ __global__ __launch_bounds__(256) void nm_query_kernel(const int4 *__restrict__ 
     int *s_mem = s_dyn + 4 * kst;
     int4 *s_coord = reinterpret_cast<int4 *>(s_mem);
     uint32_t *s_base = reinterpret_cast<uint32_t *>(s_mem + 4 * kMaxStagedRows);
-    const int64_t row0 = (int64_t)blockIdx.x * rows_per_block;
+    // Each XCD takes a contiguous range of row blocks, so its L2 holds the
+    // part of the cell table those rows' neighbours fall in.
+    const int64_t row0 = (int64_t)tile_for_block((int)blockIdx.x, (int)gridDim.x) * rows_per_block;
     const int nrows = (int)min<int64_t>(rows_per_block, q_rows - row0);
     const Plan p = h->plan;
     const bool staged = ks.K <= kMaxStagedOffsets;
