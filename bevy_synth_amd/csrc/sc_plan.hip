@@ -639,7 +639,8 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
     uint64_t *s_list = reinterpret_cast<uint64_t *>(s_pre);  // up to 1024 sorted entries
     static_assert(kHashSlots <= kBitmapWords, "hash table fits the bitmap array");
     static_assert(kPlanHaloMax <= 1024 && 1024 * 8 <= kBitmapWords * 2, "sort list fits the prefix array");
-    const int64_t t = blockIdx.x;
+    // XCD-contiguous tiles: neighbouring tiles read neighbouring map rows.
+    const int64_t t = tile_for_block((int)blockIdx.x, (int)gridDim.x);
     const int p = threadIdx.x;
     const int lane = p & 63, wave = p >> 6;
     const int K = a.K;
@@ -743,10 +744,10 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
                 out = (uint16_t)(s_pre[w] + __builtin_popcount(s_bits[w] & ((1u << (d & 31)) - 1u)));
                 s_halo[out] = v[k];
             }
-            lm[k * kPlanTileRows] = out;
+            __builtin_nontemporal_store(out, &lm[k * kPlanTileRows]);  // streaming: keeps map rows in L2
         }
         __syncthreads();
-        for (int i = p; i < U; i += kTileThreads) halo[i] = s_halo[i];  // coalesced
+        for (int i = p; i < U; i += kTileThreads) __builtin_nontemporal_store(s_halo[i], &halo[i]);  // coalesced
         return;
     }
 
