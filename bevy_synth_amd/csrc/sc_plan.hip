@@ -420,8 +420,30 @@ __global__ __launch_bounds__(kThreads) void plan_scan1_kernel(PlanArgs a)
     if (threadIdx.x == 0) a.bsum[blockIdx.x] = total;
 }
 
-// Exclusive scan of the block totals (gsum or bsum; one block, carried over
-// 1024-entry chunks).  Grid mode: the total (distinct coords) -> n_unique.
+// In-place exclusive scan of arr[0, n) by one block in a single pass: thread
+// p sums a contiguous segment of ceil(n / 256) entries (rounded up to 4), one
+// block-wide scan of the sums, then each thread writes its segment's
+// prefixes.  Returns the total.
+__device__ inline int block_scan_array(int32_t *arr, int64_t n, int *s_wave)
+{
+    const int64_t seg = ((n + kThreads - 1) / kThreads + 3) & ~(int64_t)3;
+    const int64_t b0 = min((int64_t)threadIdx.x * seg, n), b1 = min(b0 + seg, n);
+    int sum = 0;
+#pragma unroll 8
+    for (int64_t i = b0; i < b1; ++i) sum += arr[i];
+    int total;
+    int run = block_scan_excl(sum, s_wave, total);
+#pragma unroll 8
+    for (int64_t i = b0; i < b1; ++i) {
+        const int v = arr[i];
+        arr[i] = run;
+        run += v;
+    }
+    return total;
+}
+
+// Exclusive scan of the block totals (gsum or bsum, one block).  Grid mode:
+// the total (distinct coords) -> n_unique.
 __global__ __launch_bounds__(kThreads) void plan_scan2_kernel(PlanArgs a)
 {
     __shared__ int s_wave[kThreads / 64];
@@ -429,50 +451,9 @@ __global__ __launch_bounds__(kThreads) void plan_scan2_kernel(PlanArgs a)
     if (!grid && a.hdr->brick_shift < 0) return;
     int32_t *arr = grid ? a.gsum : a.bsum;
     const int64_t n = grid ? grid_geom(a.hdr, a.grid_cap).blocks : a.n_bsum;
-    int carry = 0;
-    for (int64_t base = 0; base < n; base += kThreads * 4) {
-        int v[4];
-        int sum = 0;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int64_t i = base + threadIdx.x * 4 + u;
-            v[u] = i < n ? arr[i] : 0;
-            sum += v[u];
-        }
-        int total;
-        int ex = block_scan_excl(sum, s_wave, total);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int64_t i = base + threadIdx.x * 4 + u;
-            if (i < n) arr[i] = carry + ex;
-            ex += v[u];
-        }
-        carry += total;
-    }
-    if (grid && threadIdx.x == 0) a.hdr->n_unique = carry;
-    if (grid && a.hdr->n_extras > 0) {
-        const int64_t nr = row_blocks(a);
-        carry = 0;
-        for (int64_t base = 0; base < nr; base += kThreads * 4) {
-            int v[4];
-            int sum = 0;
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int64_t i = base + threadIdx.x * 4 + u;
-                v[u] = i < nr ? a.bsum[i] : 0;
-                sum += v[u];
-            }
-            int total;
-            int ex = block_scan_excl(sum, s_wave, total);
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int64_t i = base + threadIdx.x * 4 + u;
-                if (i < nr) a.bsum[i] = carry + ex;
-                ex += v[u];
-            }
-            carry += total;
-        }
-    }
+    const int total = block_scan_array(arr, n, s_wave);
+    if (grid && threadIdx.x == 0) a.hdr->n_unique = total;
+    if (grid && a.hdr->n_extras > 0) block_scan_array(a.bsum, row_blocks(a), s_wave);
 }
 
 __device__ inline int64_t brick_start(const PlanArgs &a, uint32_t br)
@@ -925,7 +906,7 @@ int launch_plan_order(const PlanArgs &a, const PlanLayout &L, hipStream_t s)
                                                                           : emit_blocks,
                        kThreads, 0, s>>>(a);
     SC_LAUNCH_CHECK("plan_emit_kernel launch");
-    plan_fix_kernel<<<grid_for(L.brick_cap, kThreads / 64, 2048), kThreads, 0, s>>>(a);
+    plan_fix_kernel<<<grid_for(L.brick_cap, kThreads / 64, 512), kThreads, 0, s>>>(a);
     SC_LAUNCH_CHECK("plan_fix_kernel launch");
     return SC_OK;
 }
