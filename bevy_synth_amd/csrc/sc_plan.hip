@@ -14,11 +14,13 @@
 //   3. prep    : grid mode when the bounding box, cut into 8^3 bricks, has
 //                at most grid_cap cells: the occupancy grid := EMPTY
 //   4. place   : each row atomicMin's its row index into its cell (cells in
-//                brick-major order, lexicographic inside a brick); the row
-//                displaced from a cell (a duplicated coord) goes to a list
-//   5. scan1/2 : occupied cells per 2048-cell block, then one block scans
-//                the block totals
+//                brick-major order, lexicographic inside a brick) and flags
+//                the cell's 2048-cell block; the row displaced from a cell
+//                (a duplicated coord) goes to a list
+//   5. scan1/2 : occupied cells per flagged 2048-cell block (unflagged
+//                blocks count 0 unread), then one block scans the totals
 //   6. emit    : the occupied cells' rows compacted in cell order -> order
+//                (blocks without occupied cells unread)
 //   7. fix     : rows of duplicated coords appended after the distinct ones
 // The order is a pure function of the coords (no sort, no atomics whose
 // interleaving shows): bricks in (batch, x, y, z) order, lexicographic inside
@@ -298,6 +300,8 @@ __global__ __launch_bounds__(kThreads) void plan_prep_kernel(PlanArgs a)
             a.hdr->n_bricks = (uint64_t)(gg.cells / 512);
         }
         for (int64_t i = tid; i < gg.cells; i += stride) a.grid[i] = kGridEmpty;
+        // per 2048-cell block: touched flag (set by place, read by scan1)
+        for (int64_t i = tid; i < gg.blocks; i += stride) a.gsum[i] = 0;
         return;
     }
     const BrickGrid g = brick_grid(a.hdr, a.brick_cap);
@@ -316,8 +320,10 @@ __global__ __launch_bounds__(kThreads) void plan_place_kernel(PlanArgs a)
         const GridGeom gg = grid_geom(a.hdr, a.grid_cap);
         for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n_q;
              i += (int64_t)gridDim.x * blockDim.x) {
-            const uint32_t old = atomicMin(&a.grid[grid_cell(gg, a.coords[i])], (uint32_t)i);
+            const int64_t cell = grid_cell(gg, a.coords[i]);
+            const uint32_t old = atomicMin(&a.grid[cell], (uint32_t)i);
             if (old != kGridEmpty) atomicAdd(&a.hdr->n_extras, 1);
+            a.gsum[cell / kPlanGridBlock] = 1;  // the block holds a cell: scan1 and emit read it
         }
         return;
     }
@@ -375,7 +381,8 @@ __device__ inline int extras_in(const PlanArgs &a, const GridGeom &gg, int64_t r
     return __builtin_popcount(f);
 }
 
-// Grid mode: occupied cells per 2048-cell block -> gsum, and with duplicated
+// Grid mode: occupied cells per 2048-cell block -> gsum (in place of the
+// block's flag; an unflagged block holds no cell and is not read), and with duplicated
 // coords the extra rows per 2048-row block -> bsum; fallback: exclusive
 // scan of the brick counts within 1024-entry blocks, block totals -> bsum.
 __global__ __launch_bounds__(kThreads) void plan_scan1_kernel(PlanArgs a)
@@ -393,6 +400,7 @@ __global__ __launch_bounds__(kThreads) void plan_scan1_kernel(PlanArgs a)
             return;
         }
         if ((int64_t)blockIdx.x >= gg.blocks) return;  // beyond the cells in use
+        if (a.gsum[blockIdx.x] == 0) return;           // no cell placed: the count stays 0
         const int64_t base = (int64_t)blockIdx.x * kPlanGridBlock + threadIdx.x * 8;
         int cnt = 0;
         if (base < gg.cells) {
@@ -485,6 +493,9 @@ __global__ __launch_bounds__(kThreads) void plan_emit_kernel(PlanArgs a)
             return;
         }
         if ((int64_t)blockIdx.x >= gg.blocks) return;  // beyond the cells in use
+        const int64_t next = (int64_t)blockIdx.x + 1 < gg.blocks ? (int64_t)a.gsum[blockIdx.x + 1]
+                                                                  : (int64_t)a.hdr->n_unique;
+        if (next == (int64_t)a.gsum[blockIdx.x]) return;  // no occupied cell in the block
         const int64_t base = (int64_t)blockIdx.x * kPlanGridBlock + threadIdx.x * 8;
         uint32_t r[8];
         int cnt = 0;
