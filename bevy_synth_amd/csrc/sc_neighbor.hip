@@ -533,12 +533,7 @@ __device__ inline void query_cells(const int4 *__restrict__ coords, int64_t row0
         const int4 *src4 = reinterpret_cast<const int4 *>(s_out);
         // Streaming stores: the map is not read back by this kernel, and
         // keeping it out of L2 leaves the cell table resident there.
-        typedef int i32x4 __attribute__((ext_vector_type(4)));
-        for (int i = threadIdx.x; i < n4; i += blockDim.x) {
-            const int4 v = src4[i];
-            const i32x4 t = {v.x, v.y, v.z, v.w};
-            __builtin_nontemporal_store(t, reinterpret_cast<i32x4 *>(dst4) + i);
-        }
+        for (int i = threadIdx.x; i < n4; i += blockDim.x) dst4[i] = src4[i];
         for (int i = (n4 << 2) + threadIdx.x; i < n_ints; i += blockDim.x) out[i] = s_out[i];
     } else {
         for (int i = threadIdx.x; i < n_ints; i += blockDim.x) out[i] = s_out[i];

@@ -736,10 +736,10 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
                 out = (uint16_t)(s_pre[w] + __builtin_popcount(s_bits[w] & ((1u << (d & 31)) - 1u)));
                 s_halo[out] = v[k];
             }
-            __builtin_nontemporal_store(out, &lm[k * kPlanTileRows]);  // streaming: keeps map rows in L2
+            lm[k * kPlanTileRows] = out;
         }
         __syncthreads();
-        for (int i = p; i < U; i += kTileThreads) __builtin_nontemporal_store(s_halo[i], &halo[i]);  // coalesced
+        for (int i = p; i < U; i += kTileThreads) halo[i] = s_halo[i];  // coalesced
         return;
     }
 
