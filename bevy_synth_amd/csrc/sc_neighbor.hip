@@ -531,8 +531,8 @@ __device__ inline void query_cells(const int4 *__restrict__ coords, int64_t row0
         const int n4 = n_ints >> 2;
         int4 *dst4 = reinterpret_cast<int4 *>(out);
         const int4 *src4 = reinterpret_cast<const int4 *>(s_out);
-        // Streaming stores: the map is not read back by this kernel, and
-        // keeping it out of L2 leaves the cell table resident there.
+        // Ordinary stores: the conv plan reads the map next, and finds part of
+        // it still in L2 (nontemporal stores speed this kernel up and slow that one down).
         for (int i = threadIdx.x; i < n4; i += blockDim.x) dst4[i] = src4[i];
         for (int i = (n4 << 2) + threadIdx.x; i < n_ints; i += blockDim.x) out[i] = s_out[i];
     } else {
