@@ -9,8 +9,8 @@
 //
 // Row order (tiles of 256 consecutive entries of `order`):
 //   1. init    : header, padding entries of `order` := -1
-//   2. bbox    : min/max of the query coords (per-block partials, then one
-//                block reduces them; no atomics)
+//   2. bbox    : min/max of the query coords (per-block partials, which
+//                every prep block reduces; no atomics)
 //   3. prep    : grid mode when the bounding box, cut into 8^3 bricks, has
 //                at most grid_cap cells: the occupancy grid := EMPTY
 //   4. place   : each row atomicMin's its row index into its cell (cells in
@@ -108,8 +108,8 @@ __device__ inline void plan_init(const PlanArgs &a)
 __global__ void plan_init_kernel(PlanArgs a) { plan_init(a); }
 
 // Per-block min/max of the query coords -> partials (in the brick-offset
-// array, which the scan overwrites later); plan_bbox_final_kernel reduces them
-// (one atomic-free pass instead of thousands of same-address atomics).
+// array, which the scan overwrites later); every block of plan_prep_kernel
+// reduces them (atomic-free, and no launch of its own).
 constexpr int kBboxBlocks = 512;
 
 __global__ __launch_bounds__(kThreads) void plan_bbox_kernel(PlanArgs a)
@@ -147,36 +147,6 @@ __global__ __launch_bounds__(kThreads) void plan_bbox_kernel(PlanArgs a)
         }
         a.offsets[blockIdx.x * 8 + j] = lo;
         a.offsets[blockIdx.x * 8 + 4 + j] = hi;
-    }
-}
-
-__global__ __launch_bounds__(kThreads) void plan_bbox_final_kernel(PlanArgs a, int nblocks)
-{
-    __shared__ int s_v[8][kThreads / 64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    int v[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = j < 4 ? INT_MAX : INT_MIN;
-    for (int b = threadIdx.x; b < nblocks; b += blockDim.x)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            v[j] = min(v[j], a.offsets[b * 8 + j]);
-            v[4 + j] = max(v[4 + j], a.offsets[b * 8 + 4 + j]);
-        }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        v[j] = j < 4 ? wave_min_i32(v[j]) : wave_max_i32(v[j]);
-        if (lane == 0) s_v[j][wave] = v[j];
-    }
-    __syncthreads();
-    if (threadIdx.x < 8) {
-        const int j = threadIdx.x;
-        int r = s_v[j][0];
-        for (int w = 1; w < (int)blockDim.x / 64; ++w) r = j < 4 ? min(r, s_v[j][w]) : max(r, s_v[j][w]);
-        if (j < 4)
-            a.hdr->bmin[j] = r;
-        else
-            a.hdr->bmax[j - 4] = r;
     }
 }
 
@@ -287,24 +257,63 @@ __device__ inline int64_t grid_cell(const GridGeom &g, int4 c)
     return brick * 512 + ((x & 7) * 64 + (y & 7) * 8 + (z & 7));
 }
 
-// Chooses the ordering mode; grid mode: grid := EMPTY; fallback: brick counts := 0.
-__global__ __launch_bounds__(kThreads) void plan_prep_kernel(PlanArgs a)
+// Every block reduces the bbox partials of plan_bbox_kernel (nbb blocks x 8
+// ints, from L2; block 0 writes the bbox to the header) and chooses the
+// ordering mode; grid mode: grid := EMPTY, block flags := 0; fallback: brick
+// counts := 0.
+__global__ __launch_bounds__(kThreads) void plan_prep_kernel(PlanArgs a, int nbb)
 {
+    __shared__ PlanHeader s_h;  // only bmin / bmax are set
+    __shared__ int s_v[8][kThreads / 64];
+    {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        int v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = j < 4 ? INT_MAX : INT_MIN;
+        for (int b = threadIdx.x; b < nbb; b += blockDim.x)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v[j] = min(v[j], a.offsets[b * 8 + j]);
+                v[4 + j] = max(v[4 + j], a.offsets[b * 8 + 4 + j]);
+            }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            v[j] = j < 4 ? wave_min_i32(v[j]) : wave_max_i32(v[j]);
+            if (lane == 0) s_v[j][wave] = v[j];
+        }
+        __syncthreads();
+        if (threadIdx.x < 8) {
+            const int j = threadIdx.x;
+            int r = s_v[j][0];
+            for (int w = 1; w < (int)blockDim.x / 64; ++w) r = j < 4 ? min(r, s_v[j][w]) : max(r, s_v[j][w]);
+            if (j < 4) {
+                s_h.bmin[j] = r;
+                if (blockIdx.x == 0) a.hdr->bmin[j] = r;
+            } else {
+                s_h.bmax[j - 4] = r;
+                if (blockIdx.x == 0) a.hdr->bmax[j - 4] = r;
+            }
+        }
+        __syncthreads();
+    }
     const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    const GridGeom gg = grid_geom(a.hdr, a.grid_cap);
+    const GridGeom gg = grid_geom(&s_h, a.grid_cap);
     if (gg.ok) {
         if (tid == 0) {
             a.hdr->grid_mode = 1;
             a.hdr->brick_shift = 3;
             a.hdr->n_bricks = (uint64_t)(gg.cells / 512);
         }
-        for (int64_t i = tid; i < gg.cells; i += stride) a.grid[i] = kGridEmpty;
+        // cells: a multiple of 512; the grid is 256-byte aligned
+        uint4 *g4 = reinterpret_cast<uint4 *>(a.grid);
+        const uint4 empty4 = make_uint4(kGridEmpty, kGridEmpty, kGridEmpty, kGridEmpty);
+        for (int64_t i = tid; i < gg.cells / 4; i += stride) g4[i] = empty4;
         // per 2048-cell block: touched flag (set by place, read by scan1)
         for (int64_t i = tid; i < gg.blocks; i += stride) a.gsum[i] = 0;
         return;
     }
-    const BrickGrid g = brick_grid(a.hdr, a.brick_cap);
+    const BrickGrid g = brick_grid(&s_h, a.brick_cap);
     if (tid == 0) {
         a.hdr->brick_shift = g.shift;
         a.hdr->n_bricks = g.total;
@@ -895,13 +904,11 @@ int launch_plan_order(const PlanArgs &a, const PlanLayout &L, hipStream_t s)
     const unsigned nbb = grid_for(n_q, kThreads, kBboxBlocks);
     plan_bbox_kernel<<<nbb, kThreads, 0, s>>>(a);
     SC_LAUNCH_CHECK("plan_bbox_kernel launch");
-    plan_bbox_final_kernel<<<1, kThreads, 0, s>>>(a, (int)nbb);
-    SC_LAUNCH_CHECK("plan_bbox_final_kernel launch");
     // The ordering mode (occupancy grid or counting sort) is chosen on the
     // device from the bounding box; every launch below covers both.
     const int64_t grid_blocks = L.grid_cap / kPlanGridBlock;
-    plan_prep_kernel<<<grid_for(L.grid_cap > L.brick_cap ? L.grid_cap : L.brick_cap, kThreads, 8192), kThreads, 0,
-                       s>>>(a);
+    plan_prep_kernel<<<grid_for(L.grid_cap > L.brick_cap ? L.grid_cap : L.brick_cap, kThreads, 1024), kThreads, 0,
+                       s>>>(a, (int)nbb);
     SC_LAUNCH_CHECK("plan_prep_kernel launch");
     plan_place_kernel<<<grid_for(n_q, kThreads, 8192), kThreads, 0, s>>>(a);
     SC_LAUNCH_CHECK("plan_place_kernel launch");
