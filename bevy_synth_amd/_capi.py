@@ -28,6 +28,7 @@ EXPORTED = (
     "sc_conv_plan_size", "sc_conv_plan_build", "sc_conv_plan_order", "sc_conv_plan_tables",
     "sc_subm_conv_forward_planned",
     "sc_conv_weight_pack_size", "sc_conv_weight_pack",
+    "sc_subdivision_build_static",
 )
 
 
@@ -112,6 +113,7 @@ def load() -> ctypes.CDLL:
     L.sc_add.argtypes = [i32, P, P, i64, P, P]
     L.sc_subdivision_workspace_size.argtypes = [i64, sizep]
     L.sc_subdivision_build.argtypes = [P, P, P, P, i64, P, P, P, P, P, ctypes.c_size_t, P]
+    L.sc_subdivision_build_static.argtypes = [P, P, P, P, i64, P, P, P, P, P]
     L.sc_gather_rows.argtypes = [i32, P, i64, i64, i64, P, i64, P, P]
     L.sc_c2s_skip_add.argtypes = [i32, P, i64, i64, i32, P, i64, i64, P, P]
     L.sc_convert.argtypes = [i32, P, i32, P, i64, P]

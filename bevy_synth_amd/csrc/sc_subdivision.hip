@@ -13,6 +13,8 @@
 //           child-ascending output, identical to argwhere's row-major order.
 #include "sc_common.hpp"
 
+#include <mutex>
+
 namespace sc {
 namespace {
 
@@ -143,6 +145,102 @@ __global__ void write_zero_count(int64_t *count) { *count = 0; }
 
 inline int64_t n_blocks(int64_t P) { return (P + kParentsPerBlock - 1) / kParentsPerBlock; }
 
+// Bytes of block counts + offsets for P parents.
+inline size_t workspace_bytes_for(int64_t P) { return (size_t)(2 * n_blocks(P) + 2) * sizeof(int64_t); }
+
+// Argument checks shared by both entry points (the workspace is checked by
+// the caller).
+int check_args(const float *d_logits, const uint8_t *d_mask, const float *thresholds,
+               const int32_t *d_parent_coords, int64_t parent_rows, int32_t *d_child_coords,
+               int32_t *d_linear_idx, int32_t *d_pairs, int64_t *d_count)
+{
+    if (parent_rows < 0 || parent_rows > INT32_MAX / 8)
+        return fail(SC_ERR_SHAPE, "subdivision parent rows out of range");
+    if (!d_count) return fail(SC_ERR_NULL, "subdivision count pointer is NULL");
+    if (parent_rows == 0) return SC_OK;
+    if ((d_logits == nullptr) == (d_mask == nullptr))
+        return fail(SC_ERR_NULL, "subdivision needs exactly one of logits or mask");
+    if (d_logits && !thresholds) return fail(SC_ERR_NULL, "subdivision thresholds are NULL");
+    if (!d_parent_coords || !d_child_coords || !d_linear_idx)
+        return fail(SC_ERR_NULL, "subdivision: NULL pointer");
+    const uintptr_t al = (uintptr_t)d_parent_coords | (uintptr_t)d_child_coords |
+                         (uintptr_t)(d_logits ? (const void *)d_logits : (const void *)d_mask);
+    if (al % 16 != 0 || (d_pairs && (uintptr_t)d_pairs % 8 != 0))
+        return fail(SC_ERR_SHAPE, "subdivision buffers must be 16-byte aligned");
+    return SC_OK;
+}
+
+// The three launches over a workspace of workspace_bytes_for(parent_rows)
+// bytes (the caller's, or the library's static scratch).  count writes every
+// block total and scan every offset, so nothing in the workspace needs to
+// start at zero.
+int launch_subdivision(const float *d_logits, const uint8_t *d_mask, const float *thresholds,
+                       const int32_t *d_parent_coords, int64_t parent_rows, int32_t *d_child_coords,
+                       int32_t *d_linear_idx, int32_t *d_pairs, int64_t *d_count, int64_t *ws, hipStream_t s)
+{
+    if (parent_rows == 0) {
+        write_zero_count<<<1, 1, 0, s>>>(d_count);
+        SC_LAUNCH_CHECK("write_zero_count launch");
+        return SC_OK;
+    }
+    Thresholds th;
+    for (int c = 0; c < 8; ++c) th.t[c] = thresholds ? thresholds[c] : 0.f;
+    const int64_t nb = n_blocks(parent_rows);
+    int64_t *counts = ws;
+    int64_t *offsets = counts + nb;
+    subdiv_count_kernel<<<(unsigned)nb, kThreads, 0, s>>>(d_logits, d_mask, th, parent_rows, counts);
+    SC_LAUNCH_CHECK("subdiv_count_kernel launch");
+    subdiv_scan_kernel<<<1, 1024, 0, s>>>(counts, nb, offsets, d_count);
+    SC_LAUNCH_CHECK("subdiv_scan_kernel launch");
+    subdiv_emit_kernel<<<(unsigned)nb, kThreads, 0, s>>>(d_logits, d_mask, th, parent_rows,
+                                                         (const int4 *)d_parent_coords, offsets,
+                                                         (int4 *)d_child_coords, d_linear_idx,
+                                                         (int2 *)d_pairs);
+    SC_LAUNCH_CHECK("subdiv_emit_kernel launch");
+    return SC_OK;
+}
+
+// ------------------------------------------------------ static scratch
+// The workspace of sc_subdivision_build_static: block counts and offsets for
+// up to kStaticMaxParents parents (1 MiB + 16 B), one copy per GPU, held
+// until the process ends.  In host code `scratch` names a host-side stand-in,
+// never the device array: every host use goes through the per-device
+// address from hipGetSymbolAddress (static_scratch_for).
+constexpr int64_t kStaticMaxParents = (int64_t)1 << 26;
+constexpr int64_t kStaticMaxBlocks = kStaticMaxParents / kParentsPerBlock;
+static __device__ __align__(256) int64_t scratch[2 * kStaticMaxBlocks + 2];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+int64_t *g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the device that stream s belongs to (the
+// current device for the NULL stream), looked up once per device with that
+// device current.
+int static_scratch_for(hipStream_t s, int64_t **out)
+{
+    int dev = 0;
+    if (s)
+        SC_HIP_CHECK(hipStreamGetDevice(s, &dev), "hipStreamGetDevice");
+    else
+        SC_HIP_CHECK(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return fail(SC_ERR_UNSUPPORTED, "device ordinal out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        int cur = 0;
+        SC_HIP_CHECK(hipGetDevice(&cur), "hipGetDevice");
+        if (cur != dev) SC_HIP_CHECK(hipSetDevice(dev), "hipSetDevice");
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur != dev) SC_HIP_CHECK(hipSetDevice(cur), "hipSetDevice");
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        if (!p || (uintptr_t)p % 256 != 0) return fail(SC_ERR_HIP, "static subdivision scratch is misaligned");
+        g_scratch_ptr[dev] = static_cast<int64_t *>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return SC_OK;
+}
+
 }  // namespace
 }  // namespace sc
 
@@ -156,7 +254,7 @@ int sc_subdivision_workspace_size(int64_t parent_rows, size_t *bytes)
     if (!bytes) return fail(SC_ERR_NULL, "bytes out-pointer is NULL");
     if (parent_rows < 0 || parent_rows > INT32_MAX / 8)
         return fail(SC_ERR_SHAPE, "subdivision parent rows out of range");
-    *bytes = (size_t)(2 * n_blocks(parent_rows) + 2) * sizeof(int64_t);
+    *bytes = workspace_bytes_for(parent_rows);
     return SC_OK;
 }
 
@@ -167,41 +265,40 @@ int sc_subdivision_build(const float *d_logits, const uint8_t *d_mask, const flo
                          sc_stream stream)
 {
     clear_error();
-    if (parent_rows < 0 || parent_rows > INT32_MAX / 8)
-        return fail(SC_ERR_SHAPE, "subdivision parent rows out of range");
-    if (!d_count) return fail(SC_ERR_NULL, "subdivision count pointer is NULL");
-    hipStream_t s = as_stream(stream);
-    if (parent_rows == 0) {
-        write_zero_count<<<1, 1, 0, s>>>(d_count);
-        SC_LAUNCH_CHECK("write_zero_count launch");
-        return SC_OK;
+    int rc = check_args(d_logits, d_mask, thresholds, d_parent_coords, parent_rows, d_child_coords, d_linear_idx,
+                        d_pairs, d_count);
+    if (rc) return rc;
+    if (parent_rows > 0) {
+        if (!d_workspace) return fail(SC_ERR_NULL, "subdivision: NULL pointer");
+        if ((uintptr_t)d_workspace % 8 != 0) return fail(SC_ERR_SHAPE, "subdivision buffers must be 16-byte aligned");
+        if (workspace_bytes < workspace_bytes_for(parent_rows))
+            return fail(SC_ERR_WORKSPACE, "subdivision workspace too small");
     }
-    if ((d_logits == nullptr) == (d_mask == nullptr))
-        return fail(SC_ERR_NULL, "subdivision needs exactly one of logits or mask");
-    if (d_logits && !thresholds) return fail(SC_ERR_NULL, "subdivision thresholds are NULL");
-    if (!d_parent_coords || !d_child_coords || !d_linear_idx || !d_workspace)
-        return fail(SC_ERR_NULL, "subdivision: NULL pointer");
-    const uintptr_t al = (uintptr_t)d_parent_coords | (uintptr_t)d_child_coords |
-                         (uintptr_t)(d_logits ? (const void *)d_logits : (const void *)d_mask);
-    if (al % 16 != 0 || (uintptr_t)d_workspace % 8 != 0 || (d_pairs && (uintptr_t)d_pairs % 8 != 0))
-        return fail(SC_ERR_SHAPE, "subdivision buffers must be 16-byte aligned");
-    const int64_t nb = n_blocks(parent_rows);
-    const size_t need = (size_t)(2 * nb + 2) * sizeof(int64_t);
-    if (workspace_bytes < need) return fail(SC_ERR_WORKSPACE, "subdivision workspace too small");
-    Thresholds th;
-    for (int c = 0; c < 8; ++c) th.t[c] = thresholds ? thresholds[c] : 0.f;
-    int64_t *counts = (int64_t *)d_workspace;
-    int64_t *offsets = counts + nb;
-    subdiv_count_kernel<<<(unsigned)nb, kThreads, 0, s>>>(d_logits, d_mask, th, parent_rows, counts);
-    SC_LAUNCH_CHECK("subdiv_count_kernel launch");
-    subdiv_scan_kernel<<<1, 1024, 0, s>>>(counts, nb, offsets, d_count);
-    SC_LAUNCH_CHECK("subdiv_scan_kernel launch");
-    subdiv_emit_kernel<<<(unsigned)nb, kThreads, 0, s>>>(d_logits, d_mask, th, parent_rows,
-                                                         (const int4 *)d_parent_coords, offsets,
-                                                         (int4 *)d_child_coords, d_linear_idx,
-                                                         (int2 *)d_pairs);
-    SC_LAUNCH_CHECK("subdiv_emit_kernel launch");
-    return SC_OK;
+    return launch_subdivision(d_logits, d_mask, thresholds, d_parent_coords, parent_rows, d_child_coords,
+                              d_linear_idx, d_pairs, d_count, static_cast<int64_t *>(d_workspace), as_stream(stream));
+}
+
+int sc_subdivision_build_static(const float *d_logits, const uint8_t *d_mask, const float *thresholds,
+                                const int32_t *d_parent_coords, int64_t parent_rows,
+                                int32_t *d_child_coords, int32_t *d_linear_idx, int32_t *d_pairs,
+                                int64_t *d_count, sc_stream stream)
+{
+    clear_error();
+    int rc = check_args(d_logits, d_mask, thresholds, d_parent_coords, parent_rows, d_child_coords, d_linear_idx,
+                        d_pairs, d_count);
+    if (rc) return rc;
+    if (parent_rows > kStaticMaxParents)
+        return fail(SC_ERR_WORKSPACE, "sc_subdivision_build_static takes at most " +
+                                          std::to_string(kStaticMaxParents) + " parent rows, got " +
+                                          std::to_string(parent_rows) + " (use sc_subdivision_build)");
+    hipStream_t s = as_stream(stream);
+    int64_t *ws = nullptr;
+    if (parent_rows > 0) {
+        rc = static_scratch_for(s, &ws);
+        if (rc) return rc;
+    }
+    return launch_subdivision(d_logits, d_mask, thresholds, d_parent_coords, parent_rows, d_child_coords,
+                              d_linear_idx, d_pairs, d_count, ws, s);
 }
 
 }  // extern "C"

@@ -311,6 +311,26 @@ int sc_subdivision_build(const float *d_logits, const uint8_t *d_mask, const flo
                          sc_stream stream);
 
 /*
+ * sc_subdivision_build without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops that
+ * forbid hipMalloc).  It has no counterpart in the reference.  Same
+ * arguments and results as sc_subdivision_build; its scratch (block counts
+ * and offsets, 1 MiB + 16 B) is a static device array inside the library,
+ * one copy per GPU, held until the process ends.  parent_rows is limited to
+ * 2^26 (67,108,864; larger counts fail with SC_ERR_WORKSPACE and
+ * launch nothing).  It calls no allocator.  Every call on one GPU shares that
+ * array: calls that overlap on one GPU (different streams, or threads without
+ * stream ordering between them) race and must not be issued; calls ordered
+ * on one stream are fine.  The first call on a device looks up the array's
+ * address there (hipGetSymbolAddress), which is not capturable: make one
+ * call on each device before capturing.
+ */
+int sc_subdivision_build_static(const float *d_logits, const uint8_t *d_mask, const float *thresholds,
+                                const int32_t *d_parent_coords, int64_t parent_rows,
+                                int32_t *d_child_coords, int32_t *d_linear_idx, int32_t *d_pairs,
+                                int64_t *d_count, sc_stream stream);
+
+/*
  * Row gather from a [src_rows*split][width] view of src ([src_rows][split*width]):
  *   out[a, :] = view[idx[a], :]      for a < n_out
  * This is conv1's child selection (reshape [P, 8*Cout] -> [8P, Cout], then
