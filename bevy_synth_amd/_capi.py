@@ -28,7 +28,7 @@ EXPORTED = (
     "sc_conv_plan_size", "sc_conv_plan_build", "sc_conv_plan_order", "sc_conv_plan_tables",
     "sc_subm_conv_forward_planned",
     "sc_conv_weight_pack_size", "sc_conv_weight_pack",
-    "sc_subdivision_build_static",
+    "sc_subdivision_build_static", "sc_conv_plan_check", "sc_conv_epilogue_workspace_size",
 )
 
 
@@ -59,6 +59,8 @@ class ScConvEpilogue(ctypes.Structure):
         ("ln_bias", ctypes.c_void_p),
         ("ln_eps", ctypes.c_float),
         ("silu", ctypes.c_int),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
     ]
 
 
@@ -107,6 +109,8 @@ def load() -> ctypes.CDLL:
     L.sc_conv_plan_tables.argtypes = [cfgp, P, i64, i64, P, ctypes.c_size_t, P]
     L.sc_subm_conv_forward_planned.argtypes = [cfgp, i32, P, i64, P, i64, i32, P, P, P, P,
                                                ctypes.POINTER(ScConvEpilogue), i32, P, P, P]
+    L.sc_conv_plan_check.argtypes = [P, P]
+    L.sc_conv_epilogue_workspace_size.argtypes = [cfgp, i32, i64, i32, ctypes.POINTER(ScConvEpilogue), sizep]
     L.sc_conv_weight_pack_size.argtypes = [cfgp, i32, sizep]
     L.sc_conv_weight_pack.argtypes = [cfgp, i32, P, P, P]
     L.sc_layer_norm.argtypes = [i32, P, i64, i64, P, P, ctypes.c_float, i32, i32, P, P]

@@ -98,11 +98,14 @@ __global__ void add_kernel(const T *__restrict__ a, const T *__restrict__ b, T *
 // layer_norm_row_stats_kernel (crates/burn_flex_gmm/src/wgpu/ops.rs:162-187)
 // and layer_norm_affine_silu_kernel (:418-446); the wave reduction sums in a
 // fixed tree order.
+// A non-NULL `res` ([rows][channels] in the output dtype) is added after
+// SiLU, before the single rounding to the output dtype (the conv block's
+// + residual, when the conv could not fuse the row's LayerNorm).
 template <typename Tin, typename Tout, int VPL>
 __global__ __launch_bounds__(256) void layer_norm_kernel(const Tin *in, int64_t rows, int channels,
                                                          const float *__restrict__ w,
                                                          const float *__restrict__ b, float eps,
-                                                         int apply_silu, Tout *out)
+                                                         int apply_silu, const Tout *res, Tout *out)
 {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
@@ -136,6 +139,7 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const Tin *in, int64_t 
             if (w) t *= w[j];
             if (b) t += b[j];
             if (apply_silu) t = silu_f32(t);
+            if (res) t += load_as_f32<Tout>(res + row * channels, j);
             store_from_f32<Tout>(y, j, t);
         }
     }
@@ -179,7 +183,7 @@ template <typename Tin, typename Tout, int LPR, int NV>
 __global__ __launch_bounds__(256) void layer_norm_vec_kernel(const Tin *in, int64_t rows, int channels,
                                                              const float *__restrict__ w,
                                                              const float *__restrict__ b, float eps,
-                                                             int apply_silu, Tout *out)
+                                                             int apply_silu, const Tout *res, Tout *out)
 {
     constexpr int VEC = Vec16<Tin>::N;
     constexpr int RPW = 64 / LPR;  // rows per wave
@@ -221,6 +225,7 @@ __global__ __launch_bounds__(256) void layer_norm_vec_kernel(const Tin *in, int6
             if (w) z *= w[c0 + e];
             if (b) z += b[c0 + e];
             if (apply_silu) z = silu_f32(z);
+            if (res) z += load_as_f32<Tout>(res + row * channels, c0 + e);
             t[e] = z;
         }
         if constexpr (sizeof(Tout) == 2) {
@@ -252,7 +257,8 @@ __global__ __launch_bounds__(256) void layer_norm_wide_kernel(const Tin *in, int
                                                               int channels,
                                                               const float *__restrict__ w,
                                                               const float *__restrict__ b,
-                                                              float eps, int apply_silu, Tout *out)
+                                                              float eps, int apply_silu, const Tout *res,
+                                                              Tout *out)
 {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
@@ -274,6 +280,7 @@ __global__ __launch_bounds__(256) void layer_norm_wide_kernel(const Tin *in, int
         if (w) t *= w[j];
         if (b) t += b[j];
         if (apply_silu) t = silu_f32(t);
+        if (res) t += load_as_f32<Tout>(res + row * channels, j);
         store_from_f32<Tout>(y, j, t);
     }
 }
@@ -348,11 +355,12 @@ __global__ void c2s_skip_add_vec_kernel(uint16_t *h, int n, int vpr, const Tp *_
 
 template <typename Tin, typename Tout>
 int launch_layer_norm(const void *in, int64_t rows, int64_t ch, const float *w,
-                             const float *b, float eps, int silu, void *out, hipStream_t s)
+                             const float *b, float eps, int silu, const void *res_, void *out, hipStream_t s)
 {
     const unsigned g = grid_for(rows, 4, INT32_MAX);
     const Tin *x = (const Tin *)in;
     Tout *y = (Tout *)out;
+    const Tout *res = (const Tout *)res_;
     const int C = (int)ch;
     constexpr int VEC = Vec16<Tin>::N;
     const bool aligned = ((uintptr_t)in % 16 == 0) && ((uintptr_t)out % 16 == 0);
@@ -363,7 +371,7 @@ int launch_layer_norm(const void *in, int64_t rows, int64_t ch, const float *w,
         const int nv = V / lpr;
         const int64_t rows_per_block = 4 * (64 / lpr);
         const unsigned gv = grid_for(rows, (int)rows_per_block, INT32_MAX);
-#define LN_VEC(L, N) layer_norm_vec_kernel<Tin, Tout, L, N><<<gv, 256, 0, s>>>(x, rows, C, w, b, eps, silu, y)
+#define LN_VEC(L, N) layer_norm_vec_kernel<Tin, Tout, L, N><<<gv, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y)
         bool launched = true;
         if (lpr == 8 && nv == 1) LN_VEC(8, 1);
         else if (lpr == 16 && nv == 1) LN_VEC(16, 1);
@@ -381,19 +389,39 @@ int launch_layer_norm(const void *in, int64_t rows, int64_t ch, const float *w,
     }
     const int vpl = (C + 63) / 64;
     if (vpl <= 1)
-        layer_norm_kernel<Tin, Tout, 1><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, y);
+        layer_norm_kernel<Tin, Tout, 1><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y);
     else if (vpl <= 2)
-        layer_norm_kernel<Tin, Tout, 2><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, y);
+        layer_norm_kernel<Tin, Tout, 2><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y);
     else if (vpl <= 4)
-        layer_norm_kernel<Tin, Tout, 4><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, y);
+        layer_norm_kernel<Tin, Tout, 4><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y);
     else if (vpl <= 8)
-        layer_norm_kernel<Tin, Tout, 8><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, y);
+        layer_norm_kernel<Tin, Tout, 8><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y);
     else if (vpl <= 16)
-        layer_norm_kernel<Tin, Tout, 16><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, y);
+        layer_norm_kernel<Tin, Tout, 16><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y);
     else
-        layer_norm_wide_kernel<Tin, Tout><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, y);
+        layer_norm_wide_kernel<Tin, Tout><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y);
     SC_LAUNCH_CHECK("layer_norm_kernel launch");
     return SC_OK;
+}
+
+int layer_norm_rows(int in_dtype, const void *d_in, int64_t rows, int64_t channels, const float *d_w,
+                    const float *d_b, float eps, int apply_silu, int out_dtype, const void *d_res, void *d_out,
+                    hipStream_t s)
+{
+    if (rows < 0 || channels <= 0 || channels > INT32_MAX)
+        return fail(SC_ERR_SHAPE, "layer_norm: invalid rows/channels");
+    if (rows == 0) return SC_OK;
+    if (!d_in || !d_out) return fail(SC_ERR_NULL, "layer_norm: NULL pointer");
+    if (in_dtype == SC_DTYPE_F32 && out_dtype == SC_DTYPE_F32)
+        return launch_layer_norm<float, float>(d_in, rows, channels, d_w, d_b, eps, apply_silu, d_res, d_out, s);
+    if (in_dtype == SC_DTYPE_F32 && out_dtype == SC_DTYPE_BF16)
+        return launch_layer_norm<float, uint16_t>(d_in, rows, channels, d_w, d_b, eps, apply_silu, d_res, d_out, s);
+    if (in_dtype == SC_DTYPE_BF16 && out_dtype == SC_DTYPE_F32)
+        return launch_layer_norm<uint16_t, float>(d_in, rows, channels, d_w, d_b, eps, apply_silu, d_res, d_out, s);
+    if (in_dtype == SC_DTYPE_BF16 && out_dtype == SC_DTYPE_BF16)
+        return launch_layer_norm<uint16_t, uint16_t>(d_in, rows, channels, d_w, d_b, eps, apply_silu, d_res, d_out,
+                                                     s);
+    return fail(SC_ERR_DTYPE, "layer_norm: dtypes must be f32 or bf16");
 }
 
 }  // namespace sc
@@ -514,20 +542,8 @@ int sc_layer_norm(int in_dtype, const void *d_in, int64_t rows, int64_t channels
                   sc_stream stream)
 {
     clear_error();
-    if (rows < 0 || channels <= 0 || channels > INT32_MAX)
-        return fail(SC_ERR_SHAPE, "layer_norm: invalid rows/channels");
-    if (rows == 0) return SC_OK;
-    if (!d_in || !d_out) return fail(SC_ERR_NULL, "layer_norm: NULL pointer");
-    hipStream_t s = as_stream(stream);
-    if (in_dtype == SC_DTYPE_F32 && out_dtype == SC_DTYPE_F32)
-        return launch_layer_norm<float, float>(d_in, rows, channels, d_w, d_b, eps, apply_silu, d_out, s);
-    if (in_dtype == SC_DTYPE_F32 && out_dtype == SC_DTYPE_BF16)
-        return launch_layer_norm<float, uint16_t>(d_in, rows, channels, d_w, d_b, eps, apply_silu, d_out, s);
-    if (in_dtype == SC_DTYPE_BF16 && out_dtype == SC_DTYPE_F32)
-        return launch_layer_norm<uint16_t, float>(d_in, rows, channels, d_w, d_b, eps, apply_silu, d_out, s);
-    if (in_dtype == SC_DTYPE_BF16 && out_dtype == SC_DTYPE_BF16)
-        return launch_layer_norm<uint16_t, uint16_t>(d_in, rows, channels, d_w, d_b, eps, apply_silu, d_out, s);
-    return fail(SC_ERR_DTYPE, "layer_norm: dtypes must be f32 or bf16");
+    return layer_norm_rows(in_dtype, d_in, rows, channels, d_w, d_b, eps, apply_silu, out_dtype, nullptr, d_out,
+                           as_stream(stream));
 }
 
 int sc_gather_rows(int dtype, const void *d_src, int64_t src_rows, int64_t split, int64_t width,

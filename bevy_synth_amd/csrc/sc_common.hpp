@@ -34,6 +34,11 @@ int hip_fail(hipError_t err, const char *what);
 int validate_config(const sc_conv_config *cfg);
 // In-place x / (1 + exp(-x)) over n values (f32 or bf16); stream-ordered.
 int silu_inplace(int dtype, void *d, int64_t n, hipStream_t s);
+// Row LayerNorm (+ SiLU) (+ a residual in the output dtype, added before the
+// one rounding to the output dtype); d_res may be NULL.  Stream-ordered.
+int layer_norm_rows(int in_dtype, const void *d_in, int64_t rows, int64_t channels, const float *d_w,
+                    const float *d_b, float eps, int apply_silu, int out_dtype, const void *d_res, void *d_out,
+                    hipStream_t s);
 
 inline bool mul_ok(int64_t a, int64_t b, int64_t *out)
 {

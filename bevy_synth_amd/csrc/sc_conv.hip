@@ -70,9 +70,46 @@ struct ConvArgs {
     // Optional tile list: workgroup b takes tile tile_list[b] if b < *tile_count.
     const int32_t *tile_list;
     const int32_t *tile_count;
-    // Weights packed by sc_conv_weight_pack (the halo-staged kernel's layout).
+    // Weights packed by sc_conv_weight_pack (the halo-staged kernel's layout),
+    // starting with their PackHeader.
     const void *wpack;
+    // Header of the plan whose order / tile list the direct kernel follows
+    // (checked against the call's shape before anything else is read).
+    const PlanHeader *plan_hdr;
 };
+
+// Header of a packed weight buffer (its first 256 bytes): the shape the
+// weights were packed for.  The planned conv compares it with the call's
+// config before it reads a fragment.
+constexpr uint32_t kPackMagic = 0x31574353u;  // "SCW1"
+constexpr size_t kPackHeaderBytes = 256;
+struct alignas(16) PackHeader {
+    uint32_t magic;
+    int32_t groups;
+    int32_t cout_g;
+    int32_t cin_g;
+    int32_t K;
+    int32_t src_dtype;  // SC_DTYPE_BF16 or SC_DTYPE_I8
+    int32_t n_ot;       // 128-channel output tiles per group
+    int32_t pad0;
+    int64_t bytes;      // whole buffer, header included
+    uint32_t pad[54];
+};
+static_assert(sizeof(PackHeader) == kPackHeaderBytes, "pack header size");
+
+// A plan built for this call's map shape (n_q, n_in, K)?
+__device__ inline bool plan_matches(const PlanHeader *h, const ConvArgs &a)
+{
+    return h->n_q == a.n_q && h->n_in == a.n_in && h->K == a.K;
+}
+
+// Records a mismatch in the plan's status (first workgroup only; the caller
+// reads it with sc_conv_plan_check).
+__device__ inline void flag_plan_status(const PlanHeader *h, uint32_t bits)
+{
+    if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x == 0)
+        atomicOr(const_cast<uint32_t *>(&h->status), bits);
+}
 
 // ------------------------------------------------------------ loaders
 
@@ -593,10 +630,15 @@ __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
 
     int tile;
     if (args.tile_list) {
-        // plan tile tile_list[b / kSubTiles], part b % kSubTiles
+        // Plan tile tile_list[b / kSubTiles], part b % kSubTiles.  The plan's
+        // header is checked first (the halo kernel flags a mismatch), and a
+        // listed tile must lie inside the order.
+        if (!plan_matches(args.plan_hdr, args)) return;
         const int b = (int)blockIdx.x / kSubTiles;
         if (b >= *args.tile_count) return;
-        tile = args.tile_list[b] * kSubTiles + (int)blockIdx.x % kSubTiles;
+        const int lt = args.tile_list[b];
+        if (lt < 0 || (int64_t)lt * kPlanTileRows >= args.n_q) return;
+        tile = lt * kSubTiles + (int)blockIdx.x % kSubTiles;
     } else {
         tile = tile_for_block(blockIdx.x, gridDim.x);
     }
@@ -974,6 +1016,19 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
     const int row0 = kNT == 128 ? 128 * rh : 64 * wave;    // first tile row of the wave
     const int K = args.K;
 
+    // The plan must be the one built for this map shape and the packed
+    // weights the ones packed for this config: otherwise nothing past the two
+    // headers is read, nothing is written, and the plan's status records it.
+    {
+        const PackHeader *wh = static_cast<const PackHeader *>(args.wpack);
+        const bool plan_ok = plan_matches(plan.hdr, args);
+        const bool w_ok = wh->magic == kPackMagic && wh->groups == (int)gridDim.z && wh->cout_g == args.cout_g &&
+                          wh->cin_g == args.cin_g && wh->K == K;
+        if (!plan_ok || !w_ok) {
+            flag_plan_status(plan.hdr, (plan_ok ? 0u : kPlanStatusMapMismatch) | (w_ok ? 0u : kPlanStatusWeightMismatch));
+            return;
+        }
+    }
     const int tile = tile_for_block(blockIdx.x, gridDim.x);
     const int U = plan.tile_u[tile];
     if (U > kPlanHaloMax) return;  // listed in plan.overflow; the direct kernel takes it
@@ -1026,7 +1081,8 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
         constexpr uint32_t kFrag = 64u * kWLane;
         const uint32_t w_tile_bytes = (uint32_t)K * (uint32_t)nkc * 8u * kFrag;
         const __amdgpu_buffer_rsrc_t w_rsrc =
-            make_rsrc(args.wpack, (uint32_t)((int64_t)args.cin / args.cin_g * n_ot) * w_tile_bytes);
+            make_rsrc(static_cast<const char *>(args.wpack) + kPackHeaderBytes,
+                      (uint32_t)((int64_t)args.cin / args.cin_g * n_ot) * w_tile_bytes);
         const uint32_t w_lane = (uint32_t)(g * n_ot + (o0 >> 7)) * w_tile_bytes +
                                 (uint32_t)((o0 & 127) / 16 + 4 * ch) * kFrag + (uint32_t)(lane * kWLane);
         const int n_halo_instr = (U + 15) >> 4;
@@ -1244,7 +1300,10 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
     constexpr int kRG = sizeof(TO) == 2 ? 4 : 2;
     int32_t qrow[kI];
 #pragma unroll
-    for (int i = 0; i < kI; ++i) qrow[i] = plan.order[(int64_t)tile * kPlanTileRows + row0 + 16 * i + l16];
+    for (int i = 0; i < kI; ++i) {
+        const int32_t q = plan.order[(int64_t)tile * kPlanTileRows + row0 + 16 * i + l16];
+        qrow[i] = q < args.n_q ? q : -1;  // -1 pads the order; nothing past n_q is written
+    }
 #pragma unroll
     for (int ih = 0; ih < kI; ih += kRG) {
         typename Out4<TO>::V rv[kRG][4];
@@ -1306,11 +1365,24 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
 // pack_flex_weight (crates/burn_flex_gmm/src/lib.rs:377-426): a one-time
 // per-layer reorder so that the conv's weight reads are contiguous.
 template <typename TS>
-__global__ void pack_weights_kernel(const TS *__restrict__ w, uint16_t *__restrict__ dst, int groups, int cout_g,
-                                    int cin_g, int K)
+__global__ void pack_weights_kernel(const TS *__restrict__ w, unsigned char *__restrict__ buf, int groups,
+                                    int cout_g, int cin_g, int K, int src_dtype, int64_t bytes)
 {
     const int nkc = cin_g / 32, n_ot = (cout_g + kBN - 1) / kBN;
     const int64_t pieces = (int64_t)groups * n_ot * K * nkc * 8 * 64;
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        PackHeader *h = reinterpret_cast<PackHeader *>(buf);
+        h->magic = kPackMagic;
+        h->groups = groups;
+        h->cout_g = cout_g;
+        h->cin_g = cin_g;
+        h->K = K;
+        h->src_dtype = src_dtype;
+        h->n_ot = n_ot;
+        h->pad0 = 0;
+        h->bytes = bytes;
+    }
+    uint16_t *dst = reinterpret_cast<uint16_t *>(buf + kPackHeaderBytes);
     for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < pieces;
          p += (int64_t)gridDim.x * blockDim.x) {
         const int lane = (int)(p & 63);
@@ -1375,6 +1447,7 @@ __global__ __launch_bounds__(256) void conv_scalar_kernel(ConvArgs args)
         }
         if constexpr (sizeof(TW) == 1) acc *= args.w_scale ? args.w_scale[o] : 1.f;
         float v = acc + (args.bias ? args.bias[o] : 0.f);
+        if (args.silu) v = silu_f32(v);
         if (res) v += load_as_f32<TO>(res, e);
         store_from_f32<TO>(out, e, v);
     }
@@ -1412,6 +1485,7 @@ int launch_conv(const ConvArgs &a, int groups, bool mfma, const void *plan, hipS
                 const PlanView pv = plan_view(plan, L);
                 dim3 hgrid((unsigned)L.n_tiles, (unsigned)ntile, (unsigned)groups);
                 ConvArgs h = a;
+                h.plan_hdr = pv.hdr;
                 if (sizeof(TW) != 1) h.w_scale = nullptr;
                 if (a.cout_g <= 64) {  // 64-channel tiles: no half-empty MFMA tile
                     hgrid.y = (unsigned)((a.cout_g + 63) / 64);
@@ -1426,6 +1500,7 @@ int launch_conv(const ConvArgs &a, int groups, bool mfma, const void *plan, hipS
                 }
                 SC_LAUNCH_CHECK("conv_halo_kernel launch");
                 ConvArgs b = a;
+                b.plan_hdr = pv.hdr;
                 b.perm = pv.order;
                 b.tile_list = pv.overflow;
                 b.tile_count = &pv.hdr->n_overflow;
@@ -1466,6 +1541,15 @@ static int launch_conv_typed(const ConvArgs &a, bool act_f32, int w_dtype, int o
     }
     if (out_dtype == SC_DTYPE_F32) return launch_conv<uint16_t, int8_t, float>(a, groups, mfma, plan, s);
     return launch_conv<uint16_t, int8_t, uint16_t>(a, groups, mfma, plan, s);
+}
+
+// Shapes the MFMA tiles take (pointer alignment and tensor sizes aside):
+// Cin per group a multiple of the 64-byte reduction chunk, at most 32 offsets.
+static bool mfma_shape_ok(const sc_conv_config *cfg, int act_dtype)
+{
+    const int bk = kChunkBytes / (int)dtype_size(act_dtype);
+    const int64_t K = cfg->kernel_d * cfg->kernel_h * cfg->kernel_w;
+    return bk > 0 && cfg->in_channels_per_group % bk == 0 && K <= kMaxTableK;
 }
 
 static int conv_forward_impl(const sc_conv_config *cfg, int act_dtype, const void *d_input,
@@ -1518,8 +1602,6 @@ static int conv_forward_impl(const sc_conv_config *cfg, int act_dtype, const voi
     a.cin_g = (int)cfg->in_channels_per_group;
     a.cout_g = (int)cfg->out_channels_per_group;
     a.K = (int)K;
-    a.vec_out = (a.cout_g % 4 == 0) && (a.cout % 4 == 0) && ((uintptr_t)d_out % 16 == 0) &&
-                ((uintptr_t)d_residual % 16 == 0);
     a.ln = 0;
     a.ln_w = a.ln_b = nullptr;
     a.ln_eps = 0.f;
@@ -1528,34 +1610,53 @@ static int conv_forward_impl(const sc_conv_config *cfg, int act_dtype, const voi
     a.tile_list = nullptr;
     a.tile_count = nullptr;
     a.wpack = d_wpack;
+    a.plan_hdr = nullptr;
 
     const size_t asz = dtype_size(act_dtype);
-    const int bk = kChunkBytes / (int)asz;
     const uintptr_t align = (uintptr_t)d_input | (uintptr_t)d_weight | (uintptr_t)d_map;
-    // The MFMA kernel addresses input and weights through buffer descriptors
-    // with 32-bit byte offsets (absent rows use offsets >= 3 GiB): both
-    // tensors must stay below 2 GiB.
     const int64_t in_bytes = n_in * cfg->in_channels * (int64_t)asz;
     const int64_t w_bytes = cfg->out_channels * K * cfg->in_channels_per_group * (int64_t)dtype_size(w_dtype);
-    const bool mfma = (a.cin_g % bk == 0) && K <= kMaxTableK && (align % 16 == 0) &&
-                      in_bytes < (int64_t)1 << 31 && w_bytes < (int64_t)1 << 31;
+    const bool mfma = mfma_shape_ok(cfg, act_dtype) && (align % 16 == 0) && in_bytes < (int64_t)1 << 31 &&
+                      w_bytes < (int64_t)1 << 31;
     const int groups = (int)cfg->groups;
     hipStream_t s = as_stream(stream);
     const bool want_ln = epi && epi->layer_norm, want_silu = epi && epi->silu;
-    // In-kernel epilogue when one workgroup holds whole rows; otherwise the
-    // conv writes its output and LayerNorm/SiLU and the residual run after it.
-    const bool fuse = mfma && groups == 1 && a.cout_g <= kBN;
-    if (want_ln || want_silu) {
-        if (fuse) {
-            a.ln = want_ln;
-            a.ln_w = epi->ln_weight;
-            a.ln_b = epi->ln_bias;
-            a.ln_eps = epi->ln_eps;
-            a.silu = want_silu;
-        } else {
-            a.residual = nullptr;
+    // LayerNorm needs every channel of a row in one workgroup: it is fused
+    // into the MFMA tile's epilogue when groups == 1 and Cout <= 128.  SiLU
+    // without LayerNorm and the residual are per element and fuse into every
+    // conv kernel.  Otherwise the conv stores its f32 accumulators (into
+    // d_out for an f32 output, else into the caller's workspace) and one row
+    // kernel applies LayerNorm -> SiLU -> + residual and rounds once.
+    const bool row_fuse = mfma && groups == 1 && a.cout_g <= kBN;
+    const bool split_ln = want_ln && !row_fuse;
+    void *conv_out = d_out;
+    int conv_out_dtype = out_dtype;
+    if (!split_ln) {
+        a.ln = want_ln;
+        a.ln_w = want_ln ? epi->ln_weight : nullptr;
+        a.ln_b = want_ln ? epi->ln_bias : nullptr;
+        a.ln_eps = want_ln ? epi->ln_eps : 0.f;
+        a.silu = want_silu;
+    } else {
+        a.residual = nullptr;
+        if (out_dtype != SC_DTYPE_F32) {
+            int64_t need;
+            if (!mul_ok(n_q, cfg->out_channels, &need) || !mul_ok(need, 4, &need))
+                return fail(SC_ERR_OVERFLOW, "sparse conv size overflow");
+            if (!epi->workspace || epi->workspace_bytes < (size_t)need)
+                return fail(SC_ERR_WORKSPACE,
+                            "sparse conv: LayerNorm over " + std::to_string(cfg->out_channels) +
+                                " channels cannot run in the conv tile; a bf16 output then needs an f32 "
+                                "workspace of " + std::to_string(need) + " bytes (sc_conv_epilogue_workspace_size)");
+            if ((uintptr_t)epi->workspace % 16 != 0)
+                return fail(SC_ERR_WORKSPACE, "sparse conv epilogue workspace must be 16-byte aligned");
+            conv_out = epi->workspace;
+            conv_out_dtype = SC_DTYPE_F32;
         }
     }
+    a.out = conv_out;
+    a.vec_out = (a.cout_g % 4 == 0) && (a.cout % 4 == 0) && ((uintptr_t)conv_out % 16 == 0) &&
+                ((uintptr_t)a.residual % 16 == 0);
     // The halo-staged path (bf16 activations, up to 27 offsets) reads the
     // plan; other shapes ignore it.
     if (d_plan && (uintptr_t)d_plan % 256 != 0)
@@ -1563,15 +1664,10 @@ static int conv_forward_impl(const sc_conv_config *cfg, int act_dtype, const voi
     if (d_wpack && (uintptr_t)d_wpack % 16 != 0)
         return fail(SC_ERR_SHAPE, "packed weights must be 16-byte aligned");
     const void *plan = (d_plan && act_bf16 && mfma && K <= kHaloK) ? d_plan : nullptr;
-    int rc2 = launch_conv_typed(a, act_f32, w_dtype, out_dtype, groups, mfma, plan, s);
-    if (rc2 != SC_OK || fuse || !(want_ln || want_silu)) return rc2;
-    if (want_ln)
-        rc2 = sc_layer_norm(out_dtype, d_out, n_q, cfg->out_channels, epi->ln_weight, epi->ln_bias,
-                            epi->ln_eps, want_silu, out_dtype, d_out, stream);
-    else
-        rc2 = silu_inplace(out_dtype, d_out, n_q * cfg->out_channels, s);
-    if (rc2 != SC_OK || !d_residual) return rc2;
-    return sc_add(out_dtype, d_out, d_residual, n_q * cfg->out_channels, d_out, stream);
+    int rc2 = launch_conv_typed(a, act_f32, w_dtype, conv_out_dtype, groups, mfma, plan, s);
+    if (rc2 != SC_OK || !split_ln) return rc2;
+    return layer_norm_rows(SC_DTYPE_F32, conv_out, n_q, cfg->out_channels, epi->ln_weight, epi->ln_bias,
+                           epi->ln_eps, want_silu, out_dtype, d_residual, d_out, s);
 }
 
 
@@ -1623,7 +1719,7 @@ static int weight_pack_bytes(const sc_conv_config *cfg, int w_dtype, size_t *byt
     const long double b = (long double)cfg->groups * n_ot * kBN * K * cfg->in_channels_per_group * 2.0L;
     if (b >= (long double)((int64_t)1 << 31))
         return fail(SC_ERR_OVERFLOW, "packed weights must stay below 2 GiB");
-    *bytes = (size_t)b;
+    *bytes = (size_t)b + kPackHeaderBytes;
     return SC_OK;
 }
 
@@ -1641,20 +1737,61 @@ extern "C" int sc_conv_weight_pack(const sc_conv_config *cfg, int w_dtype, const
     size_t bytes = 0;
     int rc = weight_pack_bytes(cfg, w_dtype, &bytes);
     if (rc) return rc;
-    if (bytes == 0) return SC_OK;
-    if (!d_weight || !d_packed) return fail(SC_ERR_NULL, "weight packing: NULL pointer");
+    if (!d_packed) return fail(SC_ERR_NULL, "weight packing: NULL pointer");
+    if (bytes > kPackHeaderBytes && !d_weight) return fail(SC_ERR_NULL, "weight packing: NULL pointer");
     if ((uintptr_t)d_packed % 16 != 0) return fail(SC_ERR_SHAPE, "packed weights must be 16-byte aligned");
     const int groups = (int)cfg->groups, cout_g = (int)cfg->out_channels_per_group,
               cin_g = (int)cfg->in_channels_per_group;
     const int K = (int)(cfg->kernel_d * cfg->kernel_h * cfg->kernel_w);
-    const int64_t pieces = (int64_t)(bytes / 16);  // 8 bf16 per lane and fragment
+    const int64_t pieces = (int64_t)((bytes - kPackHeaderBytes) / 16);  // 8 bf16 per lane and fragment
     hipStream_t s = as_stream(stream);
+    unsigned char *buf = static_cast<unsigned char *>(d_packed);
     if (w_dtype == SC_DTYPE_BF16)
         pack_weights_kernel<uint16_t><<<grid_for(pieces, 256, 16384), 256, 0, s>>>(
-            static_cast<const uint16_t *>(d_weight), static_cast<uint16_t *>(d_packed), groups, cout_g, cin_g, K);
+            static_cast<const uint16_t *>(d_weight), buf, groups, cout_g, cin_g, K, w_dtype, (int64_t)bytes);
     else
         pack_weights_kernel<int8_t><<<grid_for(pieces, 256, 16384), 256, 0, s>>>(
-            static_cast<const int8_t *>(d_weight), static_cast<uint16_t *>(d_packed), groups, cout_g, cin_g, K);
+            static_cast<const int8_t *>(d_weight), buf, groups, cout_g, cin_g, K, w_dtype, (int64_t)bytes);
     SC_LAUNCH_CHECK("pack_weights_kernel launch");
+    return SC_OK;
+}
+
+extern "C" int sc_conv_plan_check(const void *d_plan, sc_stream stream)
+{
+    clear_error();
+    if (!d_plan) return fail(SC_ERR_NULL, "conv plan buffer is NULL");
+    hipStream_t s = as_stream(stream);
+    uint32_t status = 0;
+    SC_HIP_CHECK(hipMemcpyAsync(&status, &static_cast<const PlanHeader *>(d_plan)->status, sizeof(status),
+                                hipMemcpyDeviceToHost, s),
+                 "conv plan status readback");
+    SC_HIP_CHECK(hipStreamSynchronize(s), "conv plan status sync");
+    if (status & kPlanStatusMapMismatch)
+        return fail(SC_ERR_SHAPE, "sparse conv: the conv plan was built for another map (n_q, n_in or K differ); "
+                                  "the conv wrote nothing");
+    if (status & kPlanStatusWeightMismatch)
+        return fail(SC_ERR_SHAPE, "sparse conv: the packed weights were packed for another config; "
+                                  "the conv wrote nothing");
+    return SC_OK;
+}
+
+extern "C" int sc_conv_epilogue_workspace_size(const sc_conv_config *cfg, int act_dtype, int64_t n_q,
+                                               int out_dtype, const sc_conv_epilogue *epi, size_t *bytes)
+{
+    clear_error();
+    if (!bytes) return fail(SC_ERR_NULL, "bytes out-pointer is NULL");
+    int rc = validate_config(cfg);
+    if (rc) return rc;
+    if (n_q < 0) return fail(SC_ERR_SHAPE, "negative row count");
+    if (act_dtype != SC_DTYPE_F32 && act_dtype != SC_DTYPE_BF16)
+        return fail(SC_ERR_DTYPE, "sparse conv input dtype must be f32 or bf16");
+    *bytes = 0;
+    const bool row_fuse = mfma_shape_ok(cfg, act_dtype) && cfg->groups == 1 && cfg->out_channels_per_group <= kBN;
+    if (epi && epi->layer_norm && out_dtype != SC_DTYPE_F32 && !row_fuse) {
+        int64_t need;
+        if (!mul_ok(n_q, cfg->out_channels, &need) || !mul_ok(need, 4, &need))
+            return fail(SC_ERR_OVERFLOW, "sparse conv size overflow");
+        *bytes = (size_t)need;
+    }
     return SC_OK;
 }

@@ -37,6 +37,12 @@ constexpr int kPlanScanBlock = 1024;  // entries per block of the brick-count sc
 constexpr int kPlanGridBlock = 2048;  // grid cells per compaction block
 constexpr int kPlanGridPerRow = 16;   // grid budget: cells per query row
 
+// PlanHeader::status bits.  The build clears them; the planned conv sets
+// them (and writes nothing) when the plan or the packed weights it is given
+// were built for another shape; sc_conv_plan_check reads them back.
+constexpr uint32_t kPlanStatusMapMismatch = 1u;     // plan's n_q / n_in / K differ from the call's
+constexpr uint32_t kPlanStatusWeightMismatch = 2u;  // packed weights packed for another config
+
 struct alignas(16) PlanHeader {
     int64_t n_q;
     int64_t n_in;

@@ -264,6 +264,12 @@ def conv_plan_build_into(cfg: SparseSubmConvConfig, coords: torch.Tensor, neighb
     return ConvPlan(buf, n_in, n_q, K)
 
 
+def conv_plan_check(plan: "ConvPlan") -> None:
+    """Syncs the current stream and raises if a planned conv found ``plan`` or
+    its packed weights built for another shape (the conv then wrote nothing)."""
+    check(_capi.load().sc_conv_plan_check(_ptr(plan.buf), _stream()))
+
+
 def conv_plan_order_into(cfg: SparseSubmConvConfig, coords: torch.Tensor, n_q: int,
                          buf: torch.Tensor) -> None:
     """First half of the plan build (sc_conv_plan_order): the row order, from
@@ -357,7 +363,8 @@ def sparse_subm_conv_forward(cfg: SparseSubmConvConfig, input: torch.Tensor,
                              layer_norm: bool = False, ln_weight: Optional[torch.Tensor] = None,
                              ln_bias: Optional[torch.Tensor] = None, ln_eps: float = 1e-6,
                              silu: bool = False, plan: Optional[ConvPlan] = None,
-                             packed_weight: Optional[torch.Tensor] = None) -> torch.Tensor:
+                             packed_weight: Optional[torch.Tensor] = None,
+                             workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """sparse_subm_conv_forward_wgpu (crates/burn_flex_gmm/src/wgpu/sparse_conv.rs:310-367).
 
     input [N_in, Cin] f32|bf16; neighbor_rows [N_q, K] int32 (N_q <= N_in);
@@ -369,6 +376,10 @@ def sparse_subm_conv_forward(cfg: SparseSubmConvConfig, input: torch.Tensor,
     With ``plan`` (a ConvPlan of this map) and ``packed_weight``
     (pack_conv_weight of ``weight``) bf16 convs take the halo-staged kernel
     (same result up to the fixed f32 summation order).
+    A LayerNorm that cannot run inside the conv tile (groups > 1 or Cout >
+    128) is applied to the f32 conv output by a row kernel; with a bf16
+    output that needs an f32 staging buffer (``workspace``, uint8, grown here
+    when missing or too small).
     Returns [N_q, Cout] in out_dtype (default: the input dtype)."""
     _require_cuda("input", input)
     _require_cuda("neighbor_rows", neighbor_rows)
@@ -421,6 +432,14 @@ def sparse_subm_conv_forward(cfg: SparseSubmConvConfig, input: torch.Tensor,
         epi.ln_bias = None if ln_bias is None else ln_bias.data_ptr()
         epi.ln_eps = float(ln_eps)
         epi.silu = int(silu)
+        need = ctypes.c_size_t()
+        check(_capi.load().sc_conv_epilogue_workspace_size(ctypes.byref(c), _dt(input), n_q, _dt(out),
+                                                           ctypes.byref(epi), ctypes.byref(need)))
+        if need.value:
+            if workspace is None or workspace.numel() < need.value:
+                workspace = torch.empty(need.value, dtype=torch.uint8, device=input.device)
+            epi.workspace = workspace.data_ptr()
+            epi.workspace_bytes = workspace.numel()
         if plan is not None:
             check(_capi.load().sc_subm_conv_forward_planned(
                 ctypes.byref(c), _dt(input), _ptr(input), input.shape[0], _ptr(neighbor_rows), n_q,

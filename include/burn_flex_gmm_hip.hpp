@@ -354,6 +354,17 @@ inline Result<DeviceTensor> sparse_subm_conv_forward_hip(const SparseSubmConvCon
     epi.ln_bias = opt.ln_bias ? (const float *)opt.ln_bias->data() : nullptr;
     epi.ln_eps = opt.ln_eps;
     epi.silu = opt.silu ? 1 : 0;
+    // f32 staging for a LayerNorm the conv tile cannot hold (bf16 output, Cout > 128 or groups > 1)
+    size_t ws_bytes = 0;
+    int wrc = sc_conv_epilogue_workspace_size(&c, to_sc_dtype(input.dtype()), (int64_t)n_q, to_sc_dtype(od), &epi,
+                                              &ws_bytes);
+    if (wrc != SC_OK) return R::err(detail::status_message(wrc));
+    Result<DeviceTensor> ws = DeviceTensor::empty({ws_bytes}, DType::U8);
+    if (ws_bytes) {
+        if (ws.is_err()) return R::err(ws.error());
+        epi.workspace = ws.value().data();
+        epi.workspace_bytes = ws_bytes;
+    }
     const float *scale = opt.w_scale ? (const float *)opt.w_scale->data() : nullptr;
     const int rc =
         opt.plan ? sc_subm_conv_forward_planned(
@@ -367,6 +378,10 @@ inline Result<DeviceTensor> sparse_subm_conv_forward_hip(const SparseSubmConvCon
                                               (const float *)bias.data(), &epi, to_sc_dtype(od),
                                               out.value().data(), stream);
     if (rc != SC_OK) return R::err(detail::status_message(rc));
+    if (ws_bytes) {  // the staging buffer is freed on return: let the conv finish with it first
+        const hipError_t e = hipStreamSynchronize(stream);
+        if (e != hipSuccess) return R::err(std::string("hipStreamSynchronize failed: ") + hipGetErrorString(e));
+    }
     return out;
 }
 

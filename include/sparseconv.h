@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define SC_ABI_VERSION 1
+#define SC_ABI_VERSION 2
 #define SC_INVALID_NEIGHBOR_ROW (-1) /* crates/burn_flex_gmm/src/lib.rs:3 */
 
 /* Mirror of SparseSubmConvConfig, crates/burn_flex_gmm/src/lib.rs:5-17. */
@@ -170,20 +170,38 @@ typedef struct sc_conv_epilogue {
     const float *ln_bias;    /* [Cout] or NULL */
     float ln_eps;
     int silu;                /* 0 / 1 */
+    /* f32 staging for a LayerNorm the conv tile cannot hold (below), 16-byte
+     * aligned, or NULL; sc_conv_epilogue_workspace_size gives the size. */
+    void *workspace;
+    size_t workspace_bytes;
 } sc_conv_epilogue;
 
 /* sc_subm_conv_forward with a fused epilogue (same arguments, epi replaces
- * d_residual; epi may be NULL).  The epilogue runs inside the conv kernel, on
- * the f32 accumulators, when one workgroup holds whole rows (groups == 1,
- * Cout <= 128, the MFMA tile); otherwise the conv stores its output in
- * out_dtype and LayerNorm/SiLU and the residual run as separate
- * stream-ordered kernels (for a bf16 output that is one more bf16 rounding,
- * before the LayerNorm). */
+ * d_residual; epi may be NULL).  Every value is rounded to out_dtype once,
+ * at the end.  SiLU without LayerNorm and the residual run inside the conv
+ * kernel, on the f32 accumulators, for every shape; so does LayerNorm when
+ * one workgroup holds whole rows (groups == 1, Cout <= 128, the MFMA tile:
+ * Cin_g a multiple of 32 (bf16) / 16 (f32), K <= 32, 16-byte aligned
+ * pointers).  Otherwise the conv stores its f32 accumulators -- into d_out
+ * for an f32 output, else into epi->workspace (n_q * Cout * 4 bytes; without
+ * it the call fails with SC_ERR_WORKSPACE) -- and one stream-ordered row
+ * kernel applies LayerNorm -> SiLU -> + residual to them (the reference
+ * normalises its f32 conv output the same way, sparse_decoder_wgpu_ops.rs
+ * :1642-1711). */
 int sc_subm_conv_forward_fused(const sc_conv_config *cfg, int act_dtype, const void *d_input,
                                int64_t n_in, const int32_t *d_map, int64_t n_q, int w_dtype,
                                const void *d_weight, const float *d_w_scale, const float *d_bias,
                                const sc_conv_epilogue *epi, int out_dtype, void *d_out,
                                sc_stream stream);
+
+/* Bytes of epi->workspace a fused or planned conv with this epilogue needs:
+ * n_q * Cout * 4 when epi asks for LayerNorm with a bf16 output and the
+ * shape keeps the row out of one conv tile (groups > 1, Cout > 128, Cin_g
+ * not a multiple of 32, K > 32), else 0.  (Misaligned pointers or tensors of
+ * 2 GiB and more also keep the row out of the tile; the conv then reports
+ * the size it needs.)  Host only. */
+int sc_conv_epilogue_workspace_size(const sc_conv_config *cfg, int act_dtype, int64_t n_q, int out_dtype,
+                                    const sc_conv_epilogue *epi, size_t *bytes);
 
 /* ----------------------------------------------------------- conv plan */
 
@@ -244,8 +262,9 @@ int sc_conv_plan_tables(const sc_conv_config *cfg, const int32_t *d_map, int64_t
  * widened exactly, |q| <= 127, and their [Cout] f32 scales, passed to the
  * conv as usual, are applied in its epilogue).  Cin per group must be a
  * multiple of 32.  d_weight is the reference layout [Cout][KD][KH][KW]
- * [Cin_g]; d_packed is 16-byte aligned, sc_conv_weight_pack_size bytes
- * (2 bytes per weight of each 128-channel output tile).
+ * [Cin_g]; d_packed is 16-byte aligned, sc_conv_weight_pack_size bytes: a
+ * 256-byte header recording the config the weights were packed for (groups,
+ * Cout_g, Cin_g, K), then 2 bytes per weight of each 128-channel output tile.
  */
 int sc_conv_weight_pack_size(const sc_conv_config *cfg, int w_dtype, size_t *bytes);
 int sc_conv_weight_pack(const sc_conv_config *cfg, int w_dtype, const void *d_weight, void *d_packed,
@@ -260,6 +279,11 @@ int sc_conv_weight_pack(const sc_conv_config *cfg, int w_dtype, const void *d_we
  * sc_subm_conv_forward_fused up to f32 summation order: the halo kernel sums
  * each row's (32-channel chunk, offset) products chunk-major instead of
  * offset-major, in a fixed order, so results are bit-identical run to run.
+ * The kernels compare the plan's header (n_q, n_in, K) and the packed
+ * weights' header (groups, Cout_g, Cin_g, K) with this call before they
+ * read anything else from either buffer: on a mismatch d_out is left
+ * untouched and the plan's status records it (sc_conv_plan_check).  A plan
+ * from another map of the same n_q / n_in / K is not detected.
  */
 int sc_subm_conv_forward_planned(const sc_conv_config *cfg, int act_dtype, const void *d_input,
                                  int64_t n_in, const int32_t *d_map, int64_t n_q, int w_dtype,
@@ -267,6 +291,14 @@ int sc_subm_conv_forward_planned(const sc_conv_config *cfg, int act_dtype, const
                                  const float *d_w_scale, const float *d_bias,
                                  const sc_conv_epilogue *epi, int out_dtype, void *d_out,
                                  const void *d_plan, sc_stream stream);
+
+/* Syncs `stream` and reports whether a planned conv on d_plan found the plan
+ * or the packed weights built for another shape (SC_ERR_SHAPE; the conv then
+ * wrote nothing).  The status is cleared when the plan is rebuilt (the
+ * reference checks shapes before every launch, crates/burn_flex_gmm/src/
+ * wgpu/sparse_conv.rs:369-473; here the plan lives on the device, so the
+ * check runs there). */
+int sc_conv_plan_check(const void *d_plan, sc_stream stream);
 
 /* ------------------------------------------------------------ block ops */
 

@@ -27,7 +27,7 @@ def test_library_exports_every_header_symbol():
     for s in syms:
         assert hasattr(L, s), f"libsparseconv.so does not export {s}"
     assert sorted(_capi.EXPORTED) == syms
-    assert L.sc_abi_version() == 1
+    assert L.sc_abi_version() == 2
 
 
 def test_status_strings():
@@ -124,7 +124,33 @@ def test_plan_size_matches_layout():
 
 def test_weight_pack_size():
     cfg = F.SparseSubmConvConfig(128, 200)
-    assert F.conv_weight_pack_bytes(cfg, torch.bfloat16) == 2 * 128 * 27 * 128 * 2
-    assert F.conv_weight_pack_bytes(cfg, torch.int8) == 2 * 128 * 27 * 128 * 2  # widened to bf16
+    # 256-byte header (the config the weights were packed for) + 2 output tiles of bf16 fragments
+    assert F.conv_weight_pack_bytes(cfg, torch.bfloat16) == 256 + 2 * 128 * 27 * 128 * 2
+    assert F.conv_weight_pack_bytes(cfg, torch.int8) == 256 + 2 * 128 * 27 * 128 * 2  # widened to bf16
     with pytest.raises(_capi.SparseConvError):
         F.conv_weight_pack_bytes(F.SparseSubmConvConfig(48, 64), torch.bfloat16)
+
+
+def test_epilogue_workspace_size():
+    """sc_conv_epilogue_workspace_size: an f32 staging buffer only for a
+    LayerNorm the conv tile cannot hold with a bf16 output."""
+    import ctypes
+    L = _capi.load()
+
+    def need(cin, cout, groups=1, ln=True, out_dtype=1, act=1, n=1000):
+        epi = _capi.ScConvEpilogue()
+        epi.layer_norm = int(ln)
+        out = ctypes.c_size_t(123)
+        c = F.SparseSubmConvConfig(cin, cout, groups=groups).to_c()
+        assert L.sc_conv_epilogue_workspace_size(ctypes.byref(c), act, n, out_dtype, ctypes.byref(epi),
+                                                 ctypes.byref(out)) == 0
+        return out.value
+    assert need(128, 128) == 0
+    assert need(64, 96) == 0
+    assert need(128, 256) == 1000 * 256 * 4
+    assert need(256, 512) == 1000 * 512 * 4
+    assert need(128, 256, groups=2) == 1000 * 256 * 4
+    assert need(128, 256, out_dtype=0) == 0       # f32 output holds the staging itself
+    assert need(128, 256, ln=False) == 0          # SiLU / residual fuse for every shape
+    assert need(48, 64) == 1000 * 64 * 4          # Cin_g not a multiple of 32: no MFMA tile
+    assert need(48, 64, act=0) == 0               # ... but f32 tiles take multiples of 16
