@@ -404,6 +404,81 @@ int launch_layer_norm(const void *in, int64_t rows, int64_t ch, const float *w,
     return SC_OK;
 }
 
+// Skinny linear out[r, o] = b[o] + sum_i x[r, i] w[o, i] for Cout <= 8 (the
+// C2S to_subdiv head; linear_skinny_kernel, crates/burn_flex_gmm/src/wgpu/
+// ops.rs:135-160, which the decoder uses for out_channels <= 8,
+// sparse_decoder_wgpu_ops.rs:109-127).  Lane (group g, output o) of a wave
+// holds w[o, c0 .. c0+64) in registers per 64-channel chunk and accumulates
+// kRows rows of group g (8 groups x kRows = 64 rows per wave pass); the 8
+// lanes of a group read the same row slice.  f32 accumulation, chunks and
+// channels in increasing order, bias added last.
+constexpr int kSkinnyRows = 8;
+
+template <typename Tin>
+__global__ __launch_bounds__(256) void linear_skinny_kernel(const Tin *__restrict__ x, int64_t rows, int cin,
+                                                            const float *__restrict__ w,
+                                                            const float *__restrict__ b, int cout,
+                                                            float *__restrict__ out)
+{
+    const int lane = threadIdx.x & 63;
+    const int o = lane & 7, g = lane >> 3;
+    const bool live_o = o < cout;
+    const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+    const bool vec = cin % 64 == 0;
+    for (int64_t base = wave * 64; base < rows; base += nwaves * 64) {
+        float acc[kSkinnyRows];
+#pragma unroll
+        for (int r = 0; r < kSkinnyRows; ++r) acc[r] = 0.f;
+        for (int c0 = 0; c0 < cin; c0 += 64) {
+            float wr[64];
+            const float *wo = w + (int64_t)(live_o ? o : 0) * cin + c0;
+#pragma unroll
+            for (int i = 0; i < 64; ++i) wr[i] = (live_o && c0 + i < cin) ? wo[i] : 0.f;
+#pragma unroll
+            for (int r = 0; r < kSkinnyRows; ++r) {
+                const int64_t row = base + g * kSkinnyRows + r;
+                if (row >= rows) continue;
+                const Tin *xr = x + row * cin + c0;
+                float a = acc[r];
+                if (vec) {
+                    constexpr int VEC = 16 / (int)sizeof(Tin);
+#pragma unroll
+                    for (int v = 0; v < 64 / VEC; ++v) {
+                        const uint4 u = reinterpret_cast<const uint4 *>(xr)[v];
+                        float f[VEC];
+                        if constexpr (sizeof(Tin) == 4) {
+                            f[0] = __builtin_bit_cast(float, u.x);
+                            f[1] = __builtin_bit_cast(float, u.y);
+                            f[2] = __builtin_bit_cast(float, u.z);
+                            f[3] = __builtin_bit_cast(float, u.w);
+                        } else {
+                            const uint32_t q[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                            for (int k = 0; k < 4; ++k) {
+                                f[2 * k] = bf16_to_f32((uint16_t)(q[k] & 0xffffu));
+                                f[2 * k + 1] = bf16_to_f32((uint16_t)(q[k] >> 16));
+                            }
+                        }
+#pragma unroll
+                        for (int e = 0; e < VEC; ++e) a += f[e] * wr[v * VEC + e];
+                    }
+                } else {
+                    for (int i = 0; i < 64 && c0 + i < cin; ++i) a += load_as_f32<Tin>(xr, i) * wr[i];
+                }
+                acc[r] = a;
+            }
+        }
+        if (!live_o) continue;
+        const float bo = b ? b[o] : 0.f;
+#pragma unroll
+        for (int r = 0; r < kSkinnyRows; ++r) {
+            const int64_t row = base + g * kSkinnyRows + r;
+            if (row < rows) out[row * cout + o] = acc[r] + bo;
+        }
+    }
+}
+
 int layer_norm_rows(int in_dtype, const void *d_in, int64_t rows, int64_t channels, const float *d_w,
                     const float *d_b, float eps, int apply_silu, int out_dtype, const void *d_res, void *d_out,
                     hipStream_t s)
@@ -544,6 +619,31 @@ int sc_layer_norm(int in_dtype, const void *d_in, int64_t rows, int64_t channels
     clear_error();
     return layer_norm_rows(in_dtype, d_in, rows, channels, d_w, d_b, eps, apply_silu, out_dtype, nullptr, d_out,
                            as_stream(stream));
+}
+
+int sc_linear_skinny(int in_dtype, const void *d_x, int64_t rows, int64_t in_channels, const float *d_w,
+                     const float *d_b, int64_t out_channels, float *d_out, sc_stream stream)
+{
+    clear_error();
+    if (rows < 0 || in_channels <= 0 || in_channels > INT32_MAX)
+        return fail(SC_ERR_SHAPE, "skinny linear: invalid rows/in_channels");
+    if (out_channels < 1 || out_channels > 8)
+        return fail(SC_ERR_UNSUPPORTED, "skinny linear takes 1..8 output channels");
+    if (rows == 0) return SC_OK;
+    if (!d_x || !d_w || !d_out) return fail(SC_ERR_NULL, "skinny linear: NULL pointer");
+    if ((uintptr_t)d_x % 16 != 0) return fail(SC_ERR_SHAPE, "skinny linear input must be 16-byte aligned");
+    hipStream_t s = as_stream(stream);
+    const unsigned g = grid_for(rows, 4 * 64, 8192);  // 4 waves x 64 rows per block and pass
+    if (in_dtype == SC_DTYPE_F32)
+        linear_skinny_kernel<float><<<g, 256, 0, s>>>((const float *)d_x, rows, (int)in_channels, d_w, d_b,
+                                                     (int)out_channels, d_out);
+    else if (in_dtype == SC_DTYPE_BF16)
+        linear_skinny_kernel<uint16_t><<<g, 256, 0, s>>>((const uint16_t *)d_x, rows, (int)in_channels, d_w, d_b,
+                                                        (int)out_channels, d_out);
+    else
+        return fail(SC_ERR_DTYPE, "skinny linear input must be f32 or bf16");
+    SC_LAUNCH_CHECK("linear_skinny_kernel launch");
+    return SC_OK;
 }
 
 int sc_gather_rows(int dtype, const void *d_src, int64_t src_rows, int64_t split, int64_t width,

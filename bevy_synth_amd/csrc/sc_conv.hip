@@ -76,6 +76,25 @@ struct ConvArgs {
     // Header of the plan whose order / tile list the direct kernel follows
     // (checked against the call's shape before anything else is read).
     const PlanHeader *plan_hdr;
+    // LayerNorm over consecutive groups of ln_group channels: the row's
+    // Cout, or one child's scatter_ch (64 or 128) in the C2S scatter.
+    int ln_group;
+    // C2S forms of the decoder's upsample block (NULL otherwise).  Child
+    // scatter (conv1): query row r's channels [c*scatter_ch, (c+1)*scatter_ch)
+    // go to output row scatter_rows[8r + c] (a child row; -1 or >= scatter_n:
+    // dropped), pitch scatter_ch.
+    const int32_t *scatter_rows;
+    int64_t scatter_n;
+    int scatter_ch;
+    // Channel-repeated parent skip (conv2): value (r, o) += parent[li >> 3]
+    // [(li & 7) * skip_S + o / skip_R], li = skip_idx[r], parent in the
+    // output dtype.
+    const void *skip_parent;
+    const int32_t *skip_idx;
+    int64_t skip_parent_rows;
+    int64_t skip_parent_ch;
+    int skip_S;
+    int skip_R;
 };
 
 // Header of a packed weight buffer (its first 256 bytes): the shape the
@@ -211,6 +230,49 @@ struct Out4<uint16_t> {
         v[3] = bf16_to_f32((uint16_t)(u.y >> 16));
     }
 };
+
+// Epilogue store of channels [col, col + nv) (nv <= 4, col within the
+// output row) of query row qrow, whose values after bias / LayerNorm / SiLU
+// are v: adds the C2S skip or the residual, and writes to the child row the
+// scatter names (or to row qrow).  The C2S forms go through here; the plain
+// forms keep their own (prefetching) stores.
+template <typename TO>
+__device__ inline void store_general(const ConvArgs &a, int64_t qrow, int64_t col, int nv, const float *v, bool vec)
+{
+    TO *out = static_cast<TO *>(a.out);
+    int64_t base;
+    if (a.scatter_rows) {
+        const int64_t c = col / a.scatter_ch;
+        const int32_t r = a.scatter_rows[qrow * 8 + c];
+        if (r < 0 || r >= a.scatter_n) return;
+        base = (int64_t)r * a.scatter_ch + (col - c * a.scatter_ch);
+    } else {
+        base = qrow * a.cout + col;
+    }
+    float t[4] = {v[0], nv > 1 ? v[1] : 0.f, nv > 2 ? v[2] : 0.f, nv > 3 ? v[3] : 0.f};
+    if (a.skip_idx) {
+        const int32_t li = a.skip_idx[qrow];
+        if (li >= 0 && li < a.skip_parent_rows * 8) {
+            const TO *pp = static_cast<const TO *>(a.skip_parent) + (int64_t)(li >> 3) * a.skip_parent_ch +
+                           (int64_t)(li & 7) * a.skip_S;
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc)
+                if (cc < nv) t[cc] += load_as_f32<TO>(pp, (col + cc) / a.skip_R);
+        }
+    } else if (a.residual) {
+        const TO *res = static_cast<const TO *>(a.residual);
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc)
+            if (cc < nv) t[cc] += load_as_f32<TO>(res, qrow * a.cout + col + cc);
+    }
+    if (vec && nv == 4) {
+        *reinterpret_cast<typename Out4<TO>::V *>(out + base) = Out4<TO>::pack(t);
+    } else {
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc)
+            if (cc < nv) store_from_f32<TO>(out, base + cc, t[cc]);
+    }
+}
 
 // ------------------------------------------------------------- MFMA tile
 
@@ -501,6 +563,20 @@ __global__ __launch_bounds__(kThreads, 2) void conv_mfma_kernel(ConvArgs args)
                     const float t = acc[i][j][e];
                     acc[i][j][e] = silu_f32(t);
                 }
+        }
+        if (args.scatter_rows || args.skip_idx) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int e4 = 0; e4 < 4; ++e4) {
+                    const int oc = o0 + j * 32 + 8 * e4 + 4 * half;
+                    if (oc >= args.cout_g) continue;
+                    float v[4];
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) v[c] = acc[i][j][4 * e4 + c];
+                    store_general<TO>(args, row0 + r, out_col0 + oc, min(4, args.cout_g - oc), v, vec_ok);
+                }
+            continue;
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -881,7 +957,46 @@ __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
                 const float scale = (kI8 && args.w_scale && ok) ? args.w_scale[out_col0 + o] : 1.f;
                 acc[i][j][e] = ok ? (kI8 ? acc[i][j][e] * scale + bias : acc[i][j][e] + bias) : 0.f;
             }
-        if (args.ln) {
+        if (args.ln && args.ln_group == 64 && args.cout_g > 64) {
+            // LayerNorm per 64-channel half of the 128-channel tile (one C2S
+            // child each): channel blocks j < 4 and j >= 4.
+            float sum[2] = {0.f, 0.f}, qv[2] = {0.f, 0.f}, mean[2], inv_std[2];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) sum[j >> 2] += acc[i][j][e];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                sum[h] += __shfl_xor(sum[h], 16, 64);
+                sum[h] += __shfl_xor(sum[h], 32, 64);
+                mean[h] = sum[h] * (1.0f / 64.0f);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int o = o0 + j * 16 + 4 * q4 + e;
+                    const float d = acc[i][j][e] - mean[j >> 2];
+                    qv[j >> 2] += o < args.cout_g ? d * d : 0.f;
+                }
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                qv[h] += __shfl_xor(qv[h], 16, 64);
+                qv[h] += __shfl_xor(qv[h], 32, 64);
+                inv_std[h] = rsqrt_f32(qv[h] * (1.0f / 64.0f) + args.ln_eps);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int o = o0 + j * 16 + 4 * q4 + e;
+                    const bool ok = o < args.cout_g;
+                    float t = (acc[i][j][e] - mean[j >> 2]) * inv_std[j >> 2];
+                    if (args.ln_w && ok) t *= args.ln_w[o % 64];
+                    if (args.ln_b && ok) t += args.ln_b[o % 64];
+                    acc[i][j][e] = t;
+                }
+        } else if (args.ln) {
             float sum = 0.f;
 #pragma unroll
             for (int j = 0; j < 8; ++j)
@@ -889,7 +1004,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
                 for (int e = 0; e < 4; ++e) sum += acc[i][j][e];
             sum += __shfl_xor(sum, 16, 64);
             sum += __shfl_xor(sum, 32, 64);
-            const float inv_c = 1.0f / (float)args.cout_g;
+            const float inv_c = 1.0f / (float)args.ln_group;
             const float mean = sum * inv_c;
             float qv = 0.f;
 #pragma unroll
@@ -910,8 +1025,8 @@ __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
                     const int o = o0 + j * 16 + 4 * q4 + e;
                     const bool ok = o < args.cout_g;
                     float t = (acc[i][j][e] - mean) * inv_std;
-                    if (args.ln_w && ok) t *= args.ln_w[o];
-                    if (args.ln_b && ok) t += args.ln_b[o];
+                    if (args.ln_w && ok) t *= args.ln_w[o % args.ln_group];
+                    if (args.ln_b && ok) t += args.ln_b[o % args.ln_group];
                     acc[i][j][e] = t;
                 }
         }
@@ -923,6 +1038,16 @@ __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
                     const float t = acc[i][j][e];
                     acc[i][j][e] = silu_f32(t);
                 }
+        }
+        if (args.scatter_rows || args.skip_idx) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int oc = o0 + j * 16 + 4 * q4;
+                if (oc >= args.cout_g) continue;
+                float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+                store_general<TO>(args, qrow, out_col0 + oc, min(4, args.cout_g - oc), v, vec_ok);
+            }
+            continue;
         }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -1247,7 +1372,10 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
                 }
             }
         };
-        const float inv_c = 1.0f / (float)args.cout_g;
+        // LayerNorm groups of 64 channels in a 128-channel tile (one C2S child
+        // per wave half): each wave's statistics are its group's, no exchange.
+        const bool half_groups = kNT == 128 && args.ln_group == 64;
+        const float inv_c = 1.0f / (float)args.ln_group;
         float mean[kI], inv_std[kI], part[kI];
 #pragma unroll
         for (int i = 0; i < kI; ++i) {
@@ -1260,7 +1388,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
             sum += __shfl_xor(sum, 32, 64);
             part[i] = sum;
         }
-        row_total(part);
+        if (!half_groups) row_total(part);
 #pragma unroll
         for (int i = 0; i < kI; ++i) mean[i] = part[i] * inv_c;
 #pragma unroll
@@ -1278,7 +1406,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
             qv += __shfl_xor(qv, 32, 64);
             part[i] = qv;
         }
-        row_total(part);
+        if (!half_groups) row_total(part);
 #pragma unroll
         for (int i = 0; i < kI; ++i) inv_std[i] = rsqrt_f32(part[i] * inv_c + args.ln_eps);
 #pragma unroll
@@ -1287,8 +1415,9 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
             for (int e = 0; e < 4; ++e) {
                 const int o = oc0 + j * 16 + 4 * q4 + e;
                 const bool ok = o < args.cout_g;
-                const float lw = (args.ln_w && ok) ? args.ln_w[o] : 1.f;
-                const float lb = (args.ln_b && ok) ? args.ln_b[o] : 0.f;
+                const int og = o % args.ln_group;  // channel within the LayerNorm group
+                const float lw = (args.ln_w && ok) ? args.ln_w[og] : 1.f;
+                const float lb = (args.ln_b && ok) ? args.ln_b[og] : 0.f;
 #pragma unroll
                 for (int i = 0; i < kI; ++i) acc[i][j][e] = (acc[i][j][e] - mean[i]) * inv_std[i] * lw + lb;
                 __builtin_amdgcn_sched_barrier(0);
@@ -1303,6 +1432,24 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
     for (int i = 0; i < kI; ++i) {
         const int32_t q = plan.order[(int64_t)tile * kPlanTileRows + row0 + 16 * i + l16];
         qrow[i] = q < args.n_q ? q : -1;  // -1 pads the order; nothing past n_q is written
+    }
+    if (args.scatter_rows || args.skip_idx) {
+#pragma unroll
+        for (int i = 0; i < kI; ++i) {
+            if (qrow[i] < 0) continue;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int oc = oc0 + j * 16 + 4 * q4;
+                if (oc >= args.cout_g) continue;
+                float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+                if (args.silu) {
+#pragma unroll
+                    for (int cc = 0; cc < 4; ++cc) v[cc] = silu_f32(v[cc]);
+                }
+                store_general<TO>(args, qrow[i], out_col0 + oc, min(4, args.cout_g - oc), v, vec_ok);
+            }
+        }
+        return;
     }
 #pragma unroll
     for (int ih = 0; ih < kI; ih += kRG) {
@@ -1448,6 +1595,11 @@ __global__ __launch_bounds__(256) void conv_scalar_kernel(ConvArgs args)
         if constexpr (sizeof(TW) == 1) acc *= args.w_scale ? args.w_scale[o] : 1.f;
         float v = acc + (args.bias ? args.bias[o] : 0.f);
         if (args.silu) v = silu_f32(v);
+        if (args.scatter_rows || args.skip_idx) {
+            const float v4[4] = {v, 0.f, 0.f, 0.f};
+            store_general<TO>(args, r, o, 1, v4, false);
+            continue;
+        }
         if (res) v += load_as_f32<TO>(res, e);
         store_from_f32<TO>(out, e, v);
     }
@@ -1552,6 +1704,55 @@ static bool mfma_shape_ok(const sc_conv_config *cfg, int act_dtype)
     return bk > 0 && cfg->in_channels_per_group % bk == 0 && K <= kMaxTableK;
 }
 
+// The C2S epilogue forms of an epilogue (child scatter of conv1, parent skip
+// of conv2), checked against the config.
+struct C2SForms {
+    bool scatter = false, skip = false;
+    int64_t scatter_ch = 0, scatter_n = 0;
+    int64_t skip_S = 0, skip_R = 0;
+};
+
+static int c2s_forms(const sc_conv_config *cfg, const sc_conv_epilogue *epi, C2SForms &f)
+{
+    f = C2SForms{};
+    if (!epi) return SC_OK;
+    f.scatter = epi->child_rows != nullptr;
+    f.skip = epi->skip_index != nullptr;
+    if (!f.scatter && !f.skip) return SC_OK;
+    if (f.scatter && f.skip) return fail(SC_ERR_UNSUPPORTED, "sparse conv: child scatter and parent skip are exclusive");
+    if (epi->residual) return fail(SC_ERR_UNSUPPORTED, "sparse conv: the C2S forms take no residual");
+    if (cfg->groups != 1) return fail(SC_ERR_UNSUPPORTED, "sparse conv: the C2S forms need groups == 1");
+    if (f.scatter) {
+        if (cfg->out_channels % 32 != 0)
+            return fail(SC_ERR_SHAPE, "sparse conv child scatter: Cout must be 8 children x a multiple of 4 channels");
+        if (epi->n_child_rows < 0) return fail(SC_ERR_SHAPE, "sparse conv child scatter: negative child row count");
+        f.scatter_ch = cfg->out_channels / 8;
+        f.scatter_n = epi->n_child_rows;
+    } else {
+        const int64_t pc = epi->skip_parent_channels;
+        if (!epi->skip_parent) return fail(SC_ERR_NULL, "sparse conv parent skip: parent features are NULL");
+        if (epi->skip_parent_rows < 0 || pc <= 0 || pc % 8 != 0 || cfg->out_channels % (pc / 8) != 0)
+            return fail(SC_ERR_SHAPE, "decoder invalid skip channel ratio (in=" + std::to_string(pc) +
+                                          ", out=" + std::to_string(cfg->out_channels) + ")");
+        if (epi->skip_parent_rows > INT32_MAX / 8)
+            return fail(SC_ERR_SHAPE, "sparse conv parent skip: too many parent rows");
+        f.skip_S = pc / 8;
+        f.skip_R = cfg->out_channels / f.skip_S;
+    }
+    return SC_OK;
+}
+
+// Whether LayerNorm runs in the conv tile's epilogue: the whole row (or, in
+// the child scatter, one child's 64 or 128 channels inside a 128-channel
+// tile of the bf16 kernels) in one workgroup.
+static bool ln_in_tile(const sc_conv_config *cfg, int act_dtype, const C2SForms &f)
+{
+    if (!mfma_shape_ok(cfg, act_dtype) || cfg->groups != 1) return false;
+    if (f.scatter)
+        return act_dtype == SC_DTYPE_BF16 && (f.scatter_ch == 64 || f.scatter_ch == 128);
+    return cfg->out_channels_per_group <= kBN;
+}
+
 static int conv_forward_impl(const sc_conv_config *cfg, int act_dtype, const void *d_input,
                              int64_t n_in, const int32_t *d_map, int64_t n_q, int w_dtype,
                              const void *d_weight, const float *d_w_scale, const float *d_bias,
@@ -1584,6 +1785,9 @@ static int conv_forward_impl(const sc_conv_config *cfg, int act_dtype, const voi
         return fail(SC_ERR_OVERFLOW, "sparse conv size overflow");
     if (cfg->in_channels_per_group > INT32_MAX || cfg->out_channels_per_group > INT32_MAX)
         return fail(SC_ERR_OVERFLOW, "sparse conv channel count overflow");
+    C2SForms c2s;
+    rc = c2s_forms(cfg, epi, c2s);
+    if (rc) return rc;
     if (n_q == 0) return SC_OK;
     if (!d_input || !d_map || !d_weight || !d_out) return fail(SC_ERR_NULL, "sparse conv: NULL pointer");
 
@@ -1611,6 +1815,17 @@ static int conv_forward_impl(const sc_conv_config *cfg, int act_dtype, const voi
     a.tile_count = nullptr;
     a.wpack = d_wpack;
     a.plan_hdr = nullptr;
+    a.ln_group = (int)cfg->out_channels_per_group;
+    a.scatter_rows = c2s.scatter ? epi->child_rows : nullptr;
+    a.scatter_n = c2s.scatter_n;
+    a.scatter_ch = (int)c2s.scatter_ch;
+    a.skip_parent = c2s.skip ? epi->skip_parent : nullptr;
+    a.skip_idx = c2s.skip ? epi->skip_index : nullptr;
+    a.skip_parent_rows = c2s.skip ? epi->skip_parent_rows : 0;
+    a.skip_parent_ch = c2s.skip ? epi->skip_parent_channels : 0;
+    a.skip_S = (int)c2s.skip_S;
+    a.skip_R = (int)c2s.skip_R;
+    if (c2s.scatter) a.ln_group = a.scatter_ch;
 
     const size_t asz = dtype_size(act_dtype);
     const uintptr_t align = (uintptr_t)d_input | (uintptr_t)d_weight | (uintptr_t)d_map;
@@ -1627,8 +1842,13 @@ static int conv_forward_impl(const sc_conv_config *cfg, int act_dtype, const voi
     // conv kernel.  Otherwise the conv stores its f32 accumulators (into
     // d_out for an f32 output, else into the caller's workspace) and one row
     // kernel applies LayerNorm -> SiLU -> + residual and rounds once.
-    const bool row_fuse = mfma && groups == 1 && a.cout_g <= kBN;
+    const bool row_fuse = mfma && ln_in_tile(cfg, act_dtype, c2s);
     const bool split_ln = want_ln && !row_fuse;
+    if (split_ln && c2s.skip)
+        return fail(SC_ERR_UNSUPPORTED, "sparse conv: LayerNorm before the parent skip needs the row in one tile");
+    // rows and channels the row kernel normalises (the children in a scatter)
+    const int64_t ln_rows = c2s.scatter ? c2s.scatter_n : n_q;
+    const int64_t ln_ch = c2s.scatter ? c2s.scatter_ch : cfg->out_channels;
     void *conv_out = d_out;
     int conv_out_dtype = out_dtype;
     if (!split_ln) {
@@ -1641,11 +1861,11 @@ static int conv_forward_impl(const sc_conv_config *cfg, int act_dtype, const voi
         a.residual = nullptr;
         if (out_dtype != SC_DTYPE_F32) {
             int64_t need;
-            if (!mul_ok(n_q, cfg->out_channels, &need) || !mul_ok(need, 4, &need))
+            if (!mul_ok(ln_rows, ln_ch, &need) || !mul_ok(need, 4, &need))
                 return fail(SC_ERR_OVERFLOW, "sparse conv size overflow");
             if (!epi->workspace || epi->workspace_bytes < (size_t)need)
                 return fail(SC_ERR_WORKSPACE,
-                            "sparse conv: LayerNorm over " + std::to_string(cfg->out_channels) +
+                            "sparse conv: LayerNorm over " + std::to_string(ln_ch) +
                                 " channels cannot run in the conv tile; a bf16 output then needs an f32 "
                                 "workspace of " + std::to_string(need) + " bytes (sc_conv_epilogue_workspace_size)");
             if ((uintptr_t)epi->workspace % 16 != 0)
@@ -1656,7 +1876,7 @@ static int conv_forward_impl(const sc_conv_config *cfg, int act_dtype, const voi
     }
     a.out = conv_out;
     a.vec_out = (a.cout_g % 4 == 0) && (a.cout % 4 == 0) && ((uintptr_t)conv_out % 16 == 0) &&
-                ((uintptr_t)a.residual % 16 == 0);
+                ((uintptr_t)a.residual % 16 == 0) && (a.scatter_ch % 4 == 0);
     // The halo-staged path (bf16 activations, up to 27 offsets) reads the
     // plan; other shapes ignore it.
     if (d_plan && (uintptr_t)d_plan % 256 != 0)
@@ -1666,8 +1886,8 @@ static int conv_forward_impl(const sc_conv_config *cfg, int act_dtype, const voi
     const void *plan = (d_plan && act_bf16 && mfma && K <= kHaloK) ? d_plan : nullptr;
     int rc2 = launch_conv_typed(a, act_f32, w_dtype, conv_out_dtype, groups, mfma, plan, s);
     if (rc2 != SC_OK || !split_ln) return rc2;
-    return layer_norm_rows(SC_DTYPE_F32, conv_out, n_q, cfg->out_channels, epi->ln_weight, epi->ln_bias,
-                           epi->ln_eps, want_silu, out_dtype, d_residual, d_out, s);
+    return layer_norm_rows(SC_DTYPE_F32, conv_out, ln_rows, ln_ch, epi->ln_weight, epi->ln_bias, epi->ln_eps,
+                           want_silu, out_dtype, d_residual, d_out, s);
 }
 
 
@@ -1786,10 +2006,13 @@ extern "C" int sc_conv_epilogue_workspace_size(const sc_conv_config *cfg, int ac
     if (act_dtype != SC_DTYPE_F32 && act_dtype != SC_DTYPE_BF16)
         return fail(SC_ERR_DTYPE, "sparse conv input dtype must be f32 or bf16");
     *bytes = 0;
-    const bool row_fuse = mfma_shape_ok(cfg, act_dtype) && cfg->groups == 1 && cfg->out_channels_per_group <= kBN;
-    if (epi && epi->layer_norm && out_dtype != SC_DTYPE_F32 && !row_fuse) {
+    C2SForms c2s;
+    rc = c2s_forms(cfg, epi, c2s);
+    if (rc) return rc;
+    if (epi && epi->layer_norm && out_dtype != SC_DTYPE_F32 && !ln_in_tile(cfg, act_dtype, c2s)) {
         int64_t need;
-        if (!mul_ok(n_q, cfg->out_channels, &need) || !mul_ok(need, 4, &need))
+        if (!mul_ok(c2s.scatter ? c2s.scatter_n : n_q, c2s.scatter ? c2s.scatter_ch : cfg->out_channels, &need) ||
+            !mul_ok(need, 4, &need))
             return fail(SC_ERR_OVERFLOW, "sparse conv size overflow");
         *bytes = (size_t)need;
     }

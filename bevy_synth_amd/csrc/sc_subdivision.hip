@@ -112,7 +112,7 @@ __global__ __launch_bounds__(kThreads) void subdiv_emit_kernel(const float *logi
                                                                const int4 *__restrict__ parent_coords,
                                                                const int64_t *block_offsets,
                                                                int4 *child_coords, int32_t *linear_idx,
-                                                               int2 *pairs)
+                                                               int2 *pairs, int32_t *child_rows)
 {
     __shared__ int s_wave[kThreads / 64];
     const int64_t p0 = (int64_t)blockIdx.x * kParentsPerBlock + (int64_t)threadIdx.x * kParentsPerThread;
@@ -127,6 +127,16 @@ __global__ __launch_bounds__(kThreads) void subdiv_emit_kernel(const float *logi
     int64_t out = block_offsets[blockIdx.x] + block_exclusive_scan(cnt, s_wave, total);
 #pragma unroll
     for (int i = 0; i < kParentsPerThread; ++i) {
+        if (child_rows && p0 + i < P) {
+            // the inverse of linear_idx: child row of (parent, c), -1 if inactive
+            int32_t cr[8];
+            int32_t o = (int32_t)out;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) cr[c] = (m[i] >> c) & 1u ? o++ : -1;
+            int4 *dst = reinterpret_cast<int4 *>(child_rows + (p0 + i) * 8);
+            dst[0] = make_int4(cr[0], cr[1], cr[2], cr[3]);
+            dst[1] = make_int4(cr[4], cr[5], cr[6], cr[7]);
+        }
         if (!m[i]) continue;
         const int64_t p = p0 + i;
         const int4 pc = parent_coords[p];
@@ -176,7 +186,8 @@ int check_args(const float *d_logits, const uint8_t *d_mask, const float *thresh
 // start at zero.
 int launch_subdivision(const float *d_logits, const uint8_t *d_mask, const float *thresholds,
                        const int32_t *d_parent_coords, int64_t parent_rows, int32_t *d_child_coords,
-                       int32_t *d_linear_idx, int32_t *d_pairs, int64_t *d_count, int64_t *ws, hipStream_t s)
+                       int32_t *d_linear_idx, int32_t *d_pairs, int32_t *d_child_rows, int64_t *d_count,
+                       int64_t *ws, hipStream_t s)
 {
     if (parent_rows == 0) {
         write_zero_count<<<1, 1, 0, s>>>(d_count);
@@ -195,7 +206,7 @@ int launch_subdivision(const float *d_logits, const uint8_t *d_mask, const float
     subdiv_emit_kernel<<<(unsigned)nb, kThreads, 0, s>>>(d_logits, d_mask, th, parent_rows,
                                                          (const int4 *)d_parent_coords, offsets,
                                                          (int4 *)d_child_coords, d_linear_idx,
-                                                         (int2 *)d_pairs);
+                                                         (int2 *)d_pairs, d_child_rows);
     SC_LAUNCH_CHECK("subdiv_emit_kernel launch");
     return SC_OK;
 }
@@ -275,7 +286,30 @@ int sc_subdivision_build(const float *d_logits, const uint8_t *d_mask, const flo
             return fail(SC_ERR_WORKSPACE, "subdivision workspace too small");
     }
     return launch_subdivision(d_logits, d_mask, thresholds, d_parent_coords, parent_rows, d_child_coords,
-                              d_linear_idx, d_pairs, d_count, static_cast<int64_t *>(d_workspace), as_stream(stream));
+                              d_linear_idx, d_pairs, nullptr, d_count, static_cast<int64_t *>(d_workspace),
+                              as_stream(stream));
+}
+
+int sc_subdivision_build_indexed(const float *d_logits, const uint8_t *d_mask, const float *thresholds,
+                                 const int32_t *d_parent_coords, int64_t parent_rows,
+                                 int32_t *d_child_coords, int32_t *d_linear_idx, int32_t *d_pairs,
+                                 int32_t *d_child_rows, int64_t *d_count, void *d_workspace,
+                                 size_t workspace_bytes, sc_stream stream)
+{
+    clear_error();
+    int rc = check_args(d_logits, d_mask, thresholds, d_parent_coords, parent_rows, d_child_coords, d_linear_idx,
+                        d_pairs, d_count);
+    if (rc) return rc;
+    if (parent_rows > 0) {
+        if (!d_workspace || !d_child_rows) return fail(SC_ERR_NULL, "subdivision: NULL pointer");
+        if ((uintptr_t)d_workspace % 8 != 0 || (uintptr_t)d_child_rows % 16 != 0)
+            return fail(SC_ERR_SHAPE, "subdivision buffers must be 16-byte aligned");
+        if (workspace_bytes < workspace_bytes_for(parent_rows))
+            return fail(SC_ERR_WORKSPACE, "subdivision workspace too small");
+    }
+    return launch_subdivision(d_logits, d_mask, thresholds, d_parent_coords, parent_rows, d_child_coords,
+                              d_linear_idx, d_pairs, d_child_rows, d_count, static_cast<int64_t *>(d_workspace),
+                              as_stream(stream));
 }
 
 int sc_subdivision_build_static(const float *d_logits, const uint8_t *d_mask, const float *thresholds,
@@ -298,7 +332,7 @@ int sc_subdivision_build_static(const float *d_logits, const uint8_t *d_mask, co
         if (rc) return rc;
     }
     return launch_subdivision(d_logits, d_mask, thresholds, d_parent_coords, parent_rows, d_child_coords,
-                              d_linear_idx, d_pairs, d_count, ws, s);
+                              d_linear_idx, d_pairs, nullptr, d_count, ws, s);
 }
 
 }  // extern "C"

@@ -26,9 +26,9 @@ from typing import List, Optional, Sequence, Tuple, Union
 import torch
 
 from .flex_gmm import (ConvPlan, NeighborMapWorkspace, SparseSubmConvConfig, build_conv_plan,
-                       c2s_skip_add, gather_rows, kernel_rows, layer_norm,
+                       c2s_skip_add, gather_rows, kernel_rows, layer_norm, linear_skinny,
                        neighbor_rows_tensor_from_coords_tensor, pack_conv_weight,
-                       sparse_subm_conv_forward, subdivision_build)
+                       sparse_subm_conv_forward, subdivision_build, subdivision_build_indexed)
 
 LAYER_NORM32_EPS = 1e-6  # sparse_decoder.rs:43
 
@@ -77,7 +77,9 @@ class ConvLayer:
 
     def __call__(self, x: torch.Tensor, nbr: Union[torch.Tensor, Neighborhood], out_dtype=None,
                  residual: Optional[torch.Tensor] = None, layer_norm: bool = False,
-                 silu: bool = False, ln_eps: float = LAYER_NORM32_EPS) -> torch.Tensor:
+                 silu: bool = False, ln_eps: float = LAYER_NORM32_EPS, **c2s) -> torch.Tensor:
+        """``c2s``: the C2S epilogue forms of sparse_subm_conv_forward
+        (child_rows / n_child_rows, skip_parent / skip_index)."""
         plan, packed = None, None
         if isinstance(nbr, Neighborhood):
             if nbr.plan is not None and x.dtype == torch.bfloat16:
@@ -87,7 +89,7 @@ class ConvLayer:
         return sparse_subm_conv_forward(self.cfg, x, nbr, self.weight, self.bias, self.w_scale,
                                         residual=residual, out_dtype=out_dtype,
                                         layer_norm=layer_norm, ln_eps=ln_eps, silu=silu,
-                                        plan=plan, packed_weight=packed)
+                                        plan=plan, packed_weight=packed, **c2s)
 
 
 @dataclass
@@ -111,6 +113,15 @@ class C2SUpsampleBlock:
     conv1: ConvLayer   # Cin -> 8*Cout on parent coords
     conv2: ConvLayer   # Cout -> Cout on child coords
     eps: float = LAYER_NORM32_EPS
+    # to_subdiv head (Linear Cin -> 8, f32): the subdivision logits when no
+    # mask or logits are given (sparse_decoder_runtime_impl.rs:859-866)
+    to_subdiv_weight: Optional[torch.Tensor] = None
+    to_subdiv_bias: Optional[torch.Tensor] = None
+    # fused: conv1 writes only the active children's slices and normalises
+    # them in its epilogue; conv2 adds the parent skip in its epilogue.
+    # Unfused: the reference's composition (conv1 [P, 8*Cout] -> select ->
+    # LayerNorm -> conv2 -> skip add), kept as the comparison path.
+    fused: bool = True
 
     def __call__(self, parent_coords: torch.Tensor, parent_feats: torch.Tensor,
                  logits: Optional[torch.Tensor] = None, mask: Optional[torch.Tensor] = None,
@@ -134,33 +145,54 @@ class C2SUpsampleBlock:
         """The block on a parent Neighborhood; returns the children's
         Neighborhood (map + plan, for the next stage's convs) and features."""
         dt = parent_feats.dtype
-        child_coords, linear_idx, _ = subdivision_build(parent_nb.coords, logits=logits, mask=mask,
-                                                        thresholds=thresholds, with_pairs=False)
+        if logits is None and mask is None:
+            if self.to_subdiv_weight is None:
+                raise ValueError("C2S upsample needs a mask, logits or a to_subdiv head")
+            logits = self.subdivision_logits(parent_feats)
         h = layer_norm(parent_feats, self.norm1_weight, self.norm1_bias, eps=self.eps, silu=True)
-        h1 = self.conv1(h, parent_nb, out_dtype=dt)
-        h_up = gather_rows(h1, 8, linear_idx)
-        h_up = layer_norm(h_up, eps=self.eps, silu=True, out=h_up)
+        if self.fused:
+            child_coords, linear_idx, child_rows = subdivision_build_indexed(
+                parent_nb.coords, logits=logits, mask=mask, thresholds=thresholds)
+            h_up = self.conv1(h, parent_nb, out_dtype=dt, layer_norm=True, silu=True, ln_eps=self.eps,
+                              child_rows=child_rows, n_child_rows=child_coords.shape[0])
+        else:
+            child_coords, linear_idx, _ = subdivision_build(parent_nb.coords, logits=logits, mask=mask,
+                                                            thresholds=thresholds, with_pairs=False)
+            h1 = self.conv1(h, parent_nb, out_dtype=dt)
+            h_up = gather_rows(h1, 8, linear_idx)
+            h_up = layer_norm(h_up, eps=self.eps, silu=True, out=h_up)
         child_nb = Neighborhood.build(self.conv2.cfg, child_coords, workspace,
                                       with_plan=parent_nb.plan is not None)
-        out = self.conv2(h_up, child_nb, out_dtype=dt)
-        c2s_skip_add(out, parent_feats, linear_idx)
+        if self.fused:
+            out = self.conv2(h_up, child_nb, out_dtype=dt, skip_parent=parent_feats, skip_index=linear_idx)
+        else:
+            out = self.conv2(h_up, child_nb, out_dtype=dt)
+            c2s_skip_add(out, parent_feats, linear_idx)
         return child_nb, out
+
+    def subdivision_logits(self, parent_feats: torch.Tensor) -> torch.Tensor:
+        """to_subdiv: [P, 8] f32 logits of the parent features (the skinny
+        linear, linear_skinny_forward_wgpu, crates/burn_flex_gmm/src/wgpu/
+        ops.rs:1390-1410)."""
+        return linear_skinny(parent_feats, self.to_subdiv_weight, self.to_subdiv_bias)
 
 
 def transposed_upsample(parent_coords: torch.Tensor, parent_feats: torch.Tensor,
                         conv1x1: ConvLayer, mask: torch.Tensor
                         ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """2x2x2 stride-2 transposed sparse conv as C2S: a 1x1x1 conv Cin -> 8*Cout
-    on the parents, then child selection.  Returns (child coords, child feats,
+    on the parents whose epilogue writes each active child's Cout slice to the
+    child's row (no [P, 8*Cout] tensor).  Returns (child coords, child feats,
     linear_idx)."""
     K = conv1x1.cfg.kernel_d * conv1x1.cfg.kernel_h * conv1x1.cfg.kernel_w
     if K != 1:
         raise ValueError("transposed_upsample needs a 1x1x1 conv")
-    child_coords, linear_idx, _ = subdivision_build(parent_coords, mask=mask, with_pairs=False)
+    child_coords, linear_idx, child_rows = subdivision_build_indexed(parent_coords, mask=mask)
     P = parent_coords.shape[0]
     ident = torch.arange(P, dtype=torch.int32, device=parent_coords.device).reshape(P, 1)
-    h1 = conv1x1(parent_feats, ident, out_dtype=parent_feats.dtype)
-    return child_coords, gather_rows(h1, 8, linear_idx), linear_idx
+    h_up = conv1x1(parent_feats, ident, out_dtype=parent_feats.dtype, child_rows=child_rows,
+                   n_child_rows=child_coords.shape[0])
+    return child_coords, h_up, linear_idx
 
 
 @dataclass

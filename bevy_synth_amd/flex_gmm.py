@@ -364,7 +364,10 @@ def sparse_subm_conv_forward(cfg: SparseSubmConvConfig, input: torch.Tensor,
                              ln_bias: Optional[torch.Tensor] = None, ln_eps: float = 1e-6,
                              silu: bool = False, plan: Optional[ConvPlan] = None,
                              packed_weight: Optional[torch.Tensor] = None,
-                             workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                             workspace: Optional[torch.Tensor] = None,
+                             child_rows: Optional[torch.Tensor] = None, n_child_rows: Optional[int] = None,
+                             skip_parent: Optional[torch.Tensor] = None,
+                             skip_index: Optional[torch.Tensor] = None) -> torch.Tensor:
     """sparse_subm_conv_forward_wgpu (crates/burn_flex_gmm/src/wgpu/sparse_conv.rs:310-367).
 
     input [N_in, Cin] f32|bf16; neighbor_rows [N_q, K] int32 (N_q <= N_in);
@@ -380,6 +383,13 @@ def sparse_subm_conv_forward(cfg: SparseSubmConvConfig, input: torch.Tensor,
     128) is applied to the f32 conv output by a row kernel; with a bf16
     output that needs an f32 staging buffer (``workspace``, uint8, grown here
     when missing or too small).
+    C2S forms (sparse_decoder_runtime_impl.rs:2240-2255, 1054-1133):
+    ``child_rows`` [N_q, 8] int32 (subdivision_build_indexed) makes this conv1
+    of the upsample block -- query row r's channels [c*C, (c+1)*C), C =
+    Cout/8, are child c's features and land in row child_rows[r, c] of an
+    [n_child_rows, C] output (LayerNorm then per child); ``skip_parent`` [P,
+    Cp] with ``skip_index`` [N_q] (the children's linear_idx) adds the
+    channel-repeated parent skip (conv2).
     Returns [N_q, Cout] in out_dtype (default: the input dtype)."""
     _require_cuda("input", input)
     _require_cuda("neighbor_rows", neighbor_rows)
@@ -406,11 +416,24 @@ def sparse_subm_conv_forward(cfg: SparseSubmConvConfig, input: torch.Tensor,
             raise SparseConvError(2, "w_scale must be f32 [Cout]")
     n_q = neighbor_rows.shape[0]
     od = input.dtype if out_dtype is None else out_dtype
+    out_shape = (n_q, cfg.out_channels)
+    if child_rows is not None:
+        _require_cuda("child_rows", child_rows)
+        if child_rows.dtype != torch.int32 or child_rows.shape != (n_q, 8):
+            raise SparseConvError(2, "child_rows must be int32 [N_q, 8]")
+        if n_child_rows is None or cfg.out_channels % 8:
+            raise SparseConvError(2, "child scatter needs n_child_rows and Cout = 8 * C")
+        out_shape = (int(n_child_rows), cfg.out_channels // 8)
+    if skip_index is not None:
+        _require_cuda("skip_index", skip_index)
+        _require_cuda("skip_parent", skip_parent)
+        if skip_index.dtype != torch.int32 or skip_index.shape != (n_q,) or skip_parent.dtype != od:
+            raise SparseConvError(2, "skip_index must be int32 [N_q] and skip_parent in the output dtype")
     if out is None:
-        out = torch.empty((n_q, cfg.out_channels), dtype=od, device=input.device)
+        out = torch.empty(out_shape, dtype=od, device=input.device)
     else:
         _require_cuda("out", out)
-        if out.shape != (n_q, cfg.out_channels) or out.dtype != od:
+        if tuple(out.shape) != out_shape or out.dtype != od:
             raise SparseConvError(2, "out has the wrong shape or dtype")
     if residual is not None:
         _require_cuda("residual", residual)
@@ -424,8 +447,16 @@ def sparse_subm_conv_forward(cfg: SparseSubmConvConfig, input: torch.Tensor,
     if plan is not None and (plan.n_q != n_q or plan.n_in != input.shape[0] or plan.K != K):
         raise SparseConvError(2, f"conv plan was built for n_in={plan.n_in} n_q={plan.n_q} K={plan.K}, "
                                  f"got n_in={input.shape[0]} n_q={n_q} K={K}")
-    if layer_norm or silu or plan is not None:
+    if layer_norm or silu or plan is not None or child_rows is not None or skip_index is not None:
         epi = _capi.ScConvEpilogue()
+        if child_rows is not None:
+            epi.child_rows = child_rows.data_ptr()
+            epi.n_child_rows = int(n_child_rows)
+        if skip_index is not None:
+            epi.skip_parent = skip_parent.data_ptr()
+            epi.skip_index = skip_index.data_ptr()
+            epi.skip_parent_rows = skip_parent.shape[0]
+            epi.skip_parent_channels = skip_parent.shape[1]
         epi.residual = None if residual is None else residual.data_ptr()
         epi.layer_norm = int(layer_norm)
         epi.ln_weight = None if ln_weight is None else ln_weight.data_ptr()
@@ -533,6 +564,61 @@ def subdivision_build(parent_coords: torch.Tensor, logits: Optional[torch.Tensor
         _ptr(pairs), _ptr(count), _ptr(ws), ws.numel(), _stream()))
     a = int(count.item())
     return child[:a], lin[:a], (pairs[:a] if pairs is not None else None)
+
+
+def subdivision_build_indexed(parent_coords: torch.Tensor, logits: Optional[torch.Tensor] = None,
+                              mask: Optional[torch.Tensor] = None,
+                              thresholds: Optional[Sequence[float]] = None
+                              ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """subdivision_build plus the inverse of linear_idx (sc_subdivision_build_indexed):
+    returns (child_coords [A,4], linear_idx [A], child_rows [P,8] int32 with
+    child_rows[p, c] = the row of child (p, c) or -1).  Syncs once to read A."""
+    _require_cuda("parent_coords", parent_coords)
+    P = parent_coords.shape[0]
+    dev = parent_coords.device
+    if (logits is None) == (mask is None):
+        raise SparseConvError(8, "subdivision needs exactly one of logits or mask")
+    if logits is not None:
+        if logits.shape != (P, 8) or logits.dtype != torch.float32:
+            raise SparseConvError(2, "decoder subdivision logits tensor must be f32 [P, 8]")
+        th = (ctypes.c_float * 8)(*([0.0] * 8 if thresholds is None else list(thresholds)))
+    else:
+        if mask.shape != (P, 8) or mask.dtype not in (torch.uint8, torch.bool):
+            raise SparseConvError(2, "subdivision mask must be u8/bool [P, 8]")
+        mask = mask.to(torch.uint8).contiguous()
+        th = None
+    cap = max(8 * P, 1)
+    child = torch.empty((cap, 4), dtype=torch.int32, device=dev)
+    lin = torch.empty((cap,), dtype=torch.int32, device=dev)
+    rows = torch.empty((max(P, 1), 8), dtype=torch.int32, device=dev)
+    count = torch.empty((1,), dtype=torch.int64, device=dev)
+    wsb = ctypes.c_size_t()
+    check(_capi.load().sc_subdivision_workspace_size(P, ctypes.byref(wsb)))
+    ws = torch.empty(max(wsb.value, 16), dtype=torch.uint8, device=dev)
+    check(_capi.load().sc_subdivision_build_indexed(
+        _ptr(logits), _ptr(mask), th, _ptr(parent_coords), P, _ptr(child), _ptr(lin), None, _ptr(rows),
+        _ptr(count), _ptr(ws), ws.numel(), _stream()))
+    a = int(count.item())
+    return child[:a], lin[:a], rows[:P]
+
+
+def linear_skinny(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """linear_skinny_forward_wgpu (crates/burn_flex_gmm/src/wgpu/ops.rs:1390-1410):
+    x [rows, Cin] f32|bf16, weight [Cout <= 8, Cin] f32, bias [Cout] f32 ->
+    [rows, Cout] f32 (the C2S to_subdiv logits)."""
+    _require_cuda("x", x)
+    _require_cuda("weight", weight)
+    rows, cin = x.shape
+    cout = weight.shape[0]
+    if weight.dtype != torch.float32 or weight.shape != (cout, cin):
+        raise SparseConvError(2, f"skinny linear input/weight mismatch: input_in_channels={cin} "
+                                 f"weight {tuple(weight.shape)}")
+    if bias is not None and (bias.dtype != torch.float32 or bias.numel() != cout):
+        raise SparseConvError(2, f"skinny linear bias mismatch: out_channels={cout} bias_len={bias.numel()}")
+    out = torch.empty((rows, cout), dtype=torch.float32, device=x.device)
+    check(_capi.load().sc_linear_skinny(_dt(x), _ptr(x), rows, cin, _ptr(weight), _ptr(bias), cout, _ptr(out),
+                                        _stream()))
+    return out
 
 
 def gather_rows(src: torch.Tensor, split: int, idx: torch.Tensor) -> torch.Tensor:

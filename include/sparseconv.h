@@ -174,6 +174,25 @@ typedef struct sc_conv_epilogue {
      * aligned, or NULL; sc_conv_epilogue_workspace_size gives the size. */
     void *workspace;
     size_t workspace_bytes;
+    /* C2S forms of the decoder's upsample block (all NULL / 0 otherwise;
+     * groups == 1, no residual; the two are exclusive):
+     *  - child scatter, conv1 on the parents (Cout = 8 * C, C a multiple of
+     *    4): parent row r's channels [c*C, (c+1)*C) are child c's features
+     *    and go to row child_rows[8r + c] of d_out ([n_child_rows][C]); -1
+     *    (inactive child) drops them.  LayerNorm then runs over each child's
+     *    C channels.  This is conv1 + reshape [P, 8C] -> [8P, C] + select
+     *    (sparse_decoder_runtime_impl.rs:2240-2255) without the [P, 8C]
+     *    tensor; child_rows comes from sc_subdivision_build_indexed.
+     *  - parent skip, conv2 on the children: with S = skip_parent_channels/8
+     *    and R = Cout/S, y[a, o] += parent[li / 8][(li % 8)*S + o / R],
+     *    li = skip_index[a] (the children's linear_idx), parent in out_dtype
+     *    (sparse_decoder_runtime_impl.rs:1054-1076,1123-1133). */
+    const int32_t *child_rows;
+    int64_t n_child_rows;
+    const void *skip_parent;
+    const int32_t *skip_index;
+    int64_t skip_parent_rows;
+    int64_t skip_parent_channels;
 } sc_conv_epilogue;
 
 /* sc_subm_conv_forward with a fused epilogue (same arguments, epi replaces
@@ -314,6 +333,15 @@ int sc_layer_norm(int in_dtype, const void *d_in, int64_t rows, int64_t channels
                   const float *d_w, const float *d_b, float eps, int apply_silu, int out_dtype,
                   void *d_out, sc_stream stream);
 
+/* Skinny linear for the C2S to_subdiv head: out[r, o] = b[o] + sum_i x[r, i]
+ * w[o, i] (linear_skinny_forward_wgpu, crates/burn_flex_gmm/src/wgpu/
+ * ops.rs:1390-1410; kernel :135-160).  x [rows][in_channels] f32 or bf16
+ * (16-byte aligned), w [out_channels][in_channels] f32, b [out_channels] f32
+ * or NULL, out [rows][out_channels] f32; out_channels 1..8.  f32
+ * accumulation in a fixed order. */
+int sc_linear_skinny(int in_dtype, const void *d_x, int64_t rows, int64_t in_channels, const float *d_w,
+                     const float *d_b, int64_t out_channels, float *d_out, sc_stream stream);
+
 /* out = a + b elementwise over n values (add_inplace, sparse_decoder_wgpu_ops.rs
  * :1747-1757).  All three share `dtype`; d_out may alias d_a. */
 int sc_add(int dtype, const void *d_a, const void *d_b, int64_t n, void *d_out, sc_stream stream);
@@ -341,6 +369,19 @@ int sc_subdivision_build(const float *d_logits, const uint8_t *d_mask, const flo
                          int32_t *d_child_coords, int32_t *d_linear_idx, int32_t *d_pairs,
                          int64_t *d_count, void *d_workspace, size_t workspace_bytes,
                          sc_stream stream);
+
+/*
+ * sc_subdivision_build that also writes the inverse of linear_idx:
+ * d_child_rows [P][8] int32 (16-byte aligned) holds, for child c of parent p,
+ * its row a in the outputs above (linear_idx[a] == 8p + c), or -1 when the
+ * child is inactive.  That is the table the conv1 child scatter
+ * (sc_conv_epilogue.child_rows) reads.
+ */
+int sc_subdivision_build_indexed(const float *d_logits, const uint8_t *d_mask, const float *thresholds,
+                                 const int32_t *d_parent_coords, int64_t parent_rows,
+                                 int32_t *d_child_coords, int32_t *d_linear_idx, int32_t *d_pairs,
+                                 int32_t *d_child_rows, int64_t *d_count, void *d_workspace,
+                                 size_t workspace_bytes, sc_stream stream);
 
 /*
  * sc_subdivision_build without a workspace argument, for callers that cannot

@@ -239,6 +239,32 @@ def conv_ref_f64(cfg: OracleConfig, weight, bias, inp, nbr,
     return out
 
 
+def conv_gemm_f64(cfg: OracleConfig, weight, bias, inp, nbr,
+                  w_scale: Optional[np.ndarray] = None, chunk: int = 1024) -> np.ndarray:
+    """conv_ref_f64's definition (bias + scale * sum over valid neighbours) as an
+    fp64 im2col GEMM in numpy, for the sampled checks at full size (pinned
+    equal to conv_ref_f64 in tests/test_oracle.py).  Map entries outside
+    [0, rows of inp) are absent."""
+    K = cfg.kernel_rows
+    g = cfg.groups
+    cin_g, cout_g = cfg.in_channels // g, cfg.out_channels // g
+    x = np.asarray(inp, dtype=np.float64).reshape(-1, cfg.in_channels)
+    n = x.shape[0]
+    xz = np.vstack([x, np.zeros((1, cfg.in_channels))])
+    m = np.asarray(nbr, dtype=np.int64).reshape(-1, K)
+    m = np.where((m >= 0) & (m < n), m, n)
+    w = np.asarray(weight, dtype=np.float64).reshape(cfg.out_channels, K * cin_g)
+    out = np.zeros((m.shape[0], cfg.out_channels), dtype=np.float64)
+    for r0 in range(0, m.shape[0], chunk):
+        rows = xz[m[r0:r0 + chunk]]                      # [R, K, Cin]
+        for gi in range(g):
+            cols = rows[:, :, gi * cin_g:(gi + 1) * cin_g].reshape(rows.shape[0], K * cin_g)
+            out[r0:r0 + chunk, gi * cout_g:(gi + 1) * cout_g] = cols @ w[gi * cout_g:(gi + 1) * cout_g].T
+    if w_scale is not None:
+        out *= np.asarray(w_scale, dtype=np.float64).reshape(1, -1)
+    return out + np.asarray(bias, dtype=np.float64).reshape(1, -1)
+
+
 def bf16_round(x) -> np.ndarray:
     """bf16_round_to_f32, crates/burn_flex_gmm/src/wgpu.rs:57-67."""
     a = np.ascontiguousarray(x, dtype=np.float32)

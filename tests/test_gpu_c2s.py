@@ -1,0 +1,171 @@
+"""GPU parity of the fused C2S upsample pieces: the indexed subdivision (the
+inverse of linear_idx), the to_subdiv skinny linear, conv1's child scatter
+with the per-child LayerNorm -> SiLU in its epilogue, conv2's parent skip in
+its epilogue, and the whole fused block against the oracle at the config-4
+parent set (113,857 parents at 512 channels -> 256-channel children).
+
+References: the fp64 conv definition (oracle.conv_gemm_f64, pinned to
+conv_ref_f64), the oracle's LayerNorm / SiLU / repeat-interleave skip, and
+numpy's argwhere order.  bf16 tolerance 1e-2 (tests/tolerance.py)."""
+import numpy as np
+import pytest
+import torch
+
+from bevy_synth_amd import decoder as D
+from bevy_synth_amd import flex_gmm as F
+from bevy_synth_amd import synth
+from tests.c2s_check import check_up_fused
+from tests.sampling import sample_rows
+from tests.tolerance import TOL_BF16, TOL_F32, assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def bf16_dev(x_f32):
+    return dev(synth.bf16_bits(x_f32).view(np.int16)).view(torch.bfloat16)
+
+
+def rbf(x):
+    return synth.bf16_to_f32(synth.bf16_bits(np.asarray(x, np.float32)))
+
+
+def host(t):
+    return t.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("P", [1, 1023, 1025, 70001])
+def test_subdivision_indexed_child_rows(P):
+    rng = np.random.default_rng(P)
+    parents = np.zeros((P, 4), np.int32)
+    parents[:, 1:] = rng.integers(0, 300, (P, 3))
+    mask = (rng.random((P, 8)) < 0.4).astype(np.uint8)
+    cc, li, rows = F.subdivision_build_indexed(dev(parents), mask=dev(mask))
+    cc0, li0, _ = F.subdivision_build(dev(parents), mask=dev(mask))
+    assert torch.equal(cc, cc0) and torch.equal(li, li0)
+    pairs = np.argwhere(mask)
+    exp = np.full((P, 8), -1, np.int32)
+    exp[pairs[:, 0], pairs[:, 1]] = np.arange(len(pairs), dtype=np.int32)
+    assert np.array_equal(rows.cpu().numpy(), exp)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("cin,cout", [(512, 8), (64, 3), (100, 8)])
+def test_linear_skinny(dtype, cin, cout):
+    rng = np.random.default_rng(cin * cout)
+    rows = 70001
+    x = synth.normal_f32(rng, (rows, cin))
+    if dtype == torch.bfloat16:
+        x = rbf(x)
+    w = synth.normal_f32(rng, (cout, cin), 1 / np.sqrt(cin))
+    b = synth.normal_f32(rng, cout)
+    xd = bf16_dev(x) if dtype == torch.bfloat16 else dev(x)
+    got = F.linear_skinny(xd, dev(w), dev(b)).cpu().numpy()
+    exp = x.astype(np.float64) @ w.T.astype(np.float64) + b
+    assert_close(got, exp, TOL_F32, "skinny linear")
+
+
+def _parents_and_mask(n=6000, frac=0.45, seed=3):
+    coords = synth.config1_coords()[:n]
+    rng = np.random.default_rng(seed)
+    mask = (rng.random((len(coords), 8)) < frac).astype(np.uint8)
+    return coords, mask
+
+
+@pytest.mark.parametrize("cchild,ln", [(16, True), (64, True), (128, True), (256, True), (64, False)])
+@pytest.mark.parametrize("planned", [False, True])
+def test_conv1_child_scatter(oracle, cchild, ln, planned):
+    """conv1 (Cin -> 8*C) on the parents writes child c of parent p to row
+    child_rows[p, c], normalised over its C channels: in the tile epilogue
+    (C = 64: one wave half; C = 128: the tile) or on f32 staging (C = 16, 256)."""
+    coords, mask = _parents_and_mask()
+    rng = np.random.default_rng(cchild)
+    cin, cout = 64, 8 * cchild
+    x = rbf(synth.normal_f32(rng, (len(coords), cin)))
+    w = rbf(synth.conv_weight(rng, cout, 27, cin, 1 / np.sqrt(27 * cin)))
+    b = synth.normal_f32(rng, cout, 0.5)
+    cfg = F.SparseSubmConvConfig(cin, cout)
+    cd = dev(coords)
+    cc, li, rows = F.subdivision_build_indexed(cd, mask=dev(mask))
+    A = cc.shape[0]
+    nbr = F.neighbor_rows_tensor_from_coords_tensor(cfg, cd)
+    wd = bf16_dev(w)
+    kw = {}
+    if planned:
+        kw = dict(plan=F.build_conv_plan(cfg, cd, nbr), packed_weight=F.pack_conv_weight(cfg, wd))
+    got = F.sparse_subm_conv_forward(cfg, bf16_dev(x), nbr, wd, dev(b), layer_norm=ln, silu=ln,
+                                     child_rows=rows, n_child_rows=A, **kw)
+    assert tuple(got.shape) == (A, cchild)
+    conv = oracle.conv_gemm_f64(oracle.OracleConfig(cin, cout), w, b, x, nbr.cpu().numpy())
+    lin = li.cpu().numpy()
+    sl = conv.reshape(len(coords), 8, cchild)[lin // 8, lin % 8].astype(np.float32)
+    exp = oracle.silu(oracle.layer_norm(sl, None, None, 1e-6)) if ln else sl
+    assert_close(host(got), exp, TOL_BF16, f"child scatter C={cchild}")
+
+
+@pytest.mark.parametrize("cp,cout", [(512, 256), (128, 64), (64, 128)])
+def test_conv2_parent_skip(oracle, cp, cout):
+    """conv2 on the children + the channel-repeated parent skip in its epilogue
+    (S = Cp/8 parent channels per child, each repeated Cout/S times)."""
+    coords, mask = _parents_and_mask(3000, 0.5, seed=cp)
+    rng = np.random.default_rng(cp + cout)
+    cd = dev(coords)
+    cc, li, _ = F.subdivision_build(cd, mask=dev(mask), with_pairs=False)
+    A = cc.shape[0]
+    cfg = F.SparseSubmConvConfig(cout, cout)
+    nbr = F.neighbor_rows_tensor_from_coords_tensor(cfg, cc)
+    h = rbf(synth.normal_f32(rng, (A, cout)))
+    w = rbf(synth.conv_weight(rng, cout, 27, cout, 1 / np.sqrt(27 * cout)))
+    b = synth.normal_f32(rng, cout, 0.1)
+    parent = rbf(synth.normal_f32(rng, (len(coords), cp)))
+    wd = bf16_dev(w)
+    plan = F.build_conv_plan(cfg, cc, nbr)
+    got = F.sparse_subm_conv_forward(cfg, bf16_dev(h), nbr, wd, dev(b), skip_parent=bf16_dev(parent),
+                                     skip_index=li, plan=plan, packed_weight=F.pack_conv_weight(cfg, wd))
+    lin = li.cpu().numpy()
+    S = cp // 8
+    skip = parent.reshape(len(coords), 8, S)[lin // 8, lin % 8]
+    exp = oracle.conv_gemm_f64(oracle.OracleConfig(cout, cout), w, b, h, nbr.cpu().numpy()) + \
+        oracle.repeat_interleave(skip, cout // S)
+    assert_close(host(got), exp, TOL_BF16, "conv + parent skip")
+
+
+def test_c2s_block_fused_config4_parents(oracle):
+    """The fused block on config 4's parent set (the config-2 shell + cube,
+    113,857 parents at 512 channels, near-surface children at 256 channels):
+    to_subdiv logits, indexed subdivision, conv1 scatter with per-child LN
+    (256 channels: f32 staging), conv2 + parent skip; 2,000 sampled children
+    (first / last / overflow tiles included) against the oracle chain, the
+    child coords against numpy, and the unfused composition within 2^-5."""
+    g = synth.ShellCubeGeometry()
+    parents = g.coords()
+    rng = np.random.default_rng(404)
+    cin, cout = 512, 256
+    P = len(parents)
+    x = bf16_dev(synth.normal_f32(rng, (P, cin)))
+
+    def layer(ci, co):
+        w = rbf(synth.conv_weight(rng, co, 27, ci, 1 / np.sqrt(27 * ci)))
+        return D.ConvLayer(F.SparseSubmConvConfig(ci, co), bf16_dev(w), dev(synth.normal_f32(rng, co, 0.1)))
+    up = D.C2SUpsampleBlock(cin, cout, dev((1 + 0.1 * rng.standard_normal(cin)).astype(np.float32)),
+                            dev((0.1 * rng.standard_normal(cin)).astype(np.float32)),
+                            layer(cin, 8 * cout), layer(cout, cout),
+                            to_subdiv_weight=dev(synth.normal_f32(rng, (8, cin), 1 / np.sqrt(cin))),
+                            to_subdiv_bias=dev(np.full(8, 0.3, np.float32)))
+    pnb = D.Neighborhood.build(up.conv1.cfg, dev(parents))
+    logits = up.subdivision_logits(x)
+    cnb, y = up.forward(pnb, x, logits=logits)
+    lg = logits.cpu().numpy()
+    mask = lg > 0
+    pairs = np.argwhere(mask)
+    assert 0 < len(pairs) < 8 * P
+    assert np.array_equal(cnb.coords.cpu().numpy(), synth.child_expand(parents, mask.astype(np.uint8)))
+    rows = sample_rows(len(pairs), rng, 2000, plan=cnb.plan)
+    check_up_fused(oracle, up, pnb, x, y, cnb, pairs, rows)
+    up.fused = False
+    _, y_ref = up.forward(pnb, x, logits=logits)
+    d = (y.float() - y_ref.float()).abs().max().item()
+    assert d <= 2 ** -5 * max(1.0, y_ref.float().abs().max().item()), d

@@ -16,6 +16,8 @@ import torch
 from bevy_synth_amd import decoder as D
 from bevy_synth_amd import flex_gmm as F
 from bevy_synth_amd import synth
+from tests.c2s_check import check_up_fused
+from tests.sampling import sample_rows
 from tests.tolerance import TOL_BF16, assert_close
 
 pytestmark = pytest.mark.gpu
@@ -39,7 +41,7 @@ def conv_rows(oracle, cfg, w, b, x, nbr_rows, w_scale=None):
     local[nbr_rows >= 0] = pos
     xin = x(need) if len(need) else np.zeros((0, cfg.in_channels), np.float32)
     oc = oracle.OracleConfig(cfg.in_channels, cfg.out_channels)
-    return oracle.conv_ref_f64(oc, w, b, xin, local, w_scale)
+    return oracle.conv_gemm_f64(oc, w, b, xin, local, w_scale)
 
 
 def qw(layer):
@@ -64,35 +66,10 @@ def check_block(oracle, blk, nb, x_dev, y_dev, rows):
     assert_close(host_f32(y_dev[dev(rows.astype(np.int64))]), y, TOL_BF16, "residual block")
 
 
-def check_up(oracle, up, nb_p, x_dev, y_dev, nb_c, mask, rows):
-    """C2SUpsampleBlock at sampled children: SiLU(LN(x; norm1)) -> conv1 ->
-    child slice -> SiLU(LN) -> conv2 -> + channel-repeated parent skip."""
-    r = oracle.bf16_round
-    cin, cout = up.in_channels, up.out_channels
-    pairs = np.argwhere(mask.cpu().numpy())
-    li = pairs[:, 0] * 8 + pairs[:, 1]                 # the device's child order
-    nc = nb_c.nbr[dev(rows.astype(np.int64))].cpu().numpy()
-    rc = np.unique(nc[nc >= 0])                       # children whose h_up conv2 reads
-    par = np.unique(li[rc] // 8)                       # their parents (conv1 rows)
-    npar = nb_p.nbr[dev(par.astype(np.int64))].cpu().numpy()
-    rp = np.unique(npar[npar >= 0])
-    n1w, n1b = up.norm1_weight.cpu().numpy(), up.norm1_bias.cpu().numpy()
-    h0 = r(oracle.silu(oracle.layer_norm(host_f32(x_dev[dev(rp.astype(np.int64))]), n1w, n1b, 1e-6)))
-    q1, s1 = qw(up.conv1)
-    h1 = r(conv_rows(oracle, up.conv1.cfg, q1, up.conv1.bias.cpu().numpy(),
-                     lambda idx: h0[np.searchsorted(rp, idx)], npar, s1).astype(np.float32))
-    sl = h1[np.searchsorted(par, li[rc] // 8)].reshape(len(rc), 8, cout)[np.arange(len(rc)), li[rc] % 8]
-    hup = r(oracle.silu(oracle.layer_norm(sl, None, None, 1e-6)))
-    q2, s2 = qw(up.conv2)
-    y = conv_rows(oracle, up.conv2.cfg, q2, up.conv2.bias.cpu().numpy(),
-                  lambda idx: hup[np.searchsorted(rc, idx)], nc, s2)
-    pf = host_f32(x_dev[dev((li[rows] // 8).astype(np.int64))]).reshape(len(rows), 8, cin // 8)
-    skip = pf[np.arange(len(rows)), li[rows] % 8]      # [rows, cin/8]
-    y = y + np.repeat(skip, cout // (cin // 8), axis=1)
-    assert_close(host_f32(y_dev[dev(rows.astype(np.int64))]), y, TOL_BF16, "c2s upsample block")
-
-
-def test_config5_int8_decoder_stack(oracle):
+@pytest.fixture(scope="module")
+def config5_run():
+    """Config 5's stack run once: (stack, masks, final Neighborhood, output,
+    trace of every residual block and upsample)."""
     coords, masks = synth.config5_stack_inputs()
     rng = np.random.default_rng(55)
     stack = D.int8_stack([512, 256, 128, 64], 2, seed=5)
@@ -100,21 +77,35 @@ def test_config5_int8_decoder_stack(oracle):
     trace = []
     nb, y = stack(dev(coords), x, [dev(m) for m in masks], trace=trace)
     torch.cuda.synchronize()
+    return coords, stack, masks, nb, y, trace
+
+
+def test_config5_int8_decoder_stack(config5_run):
+    coords, stack, masks, nb, y, trace = config5_run
     # coords of every stage: the argwhere-order expansion, exactly
     want = coords
     for m in masks:
         want = synth.child_expand(want, m)
     assert np.array_equal(nb.coords.cpu().numpy(), want)
     assert y.shape == (len(want), 64) and bool(torch.isfinite(y.float()).all())
-    assert all(e[2].plan is not None for e in trace), "every resolution got a conv plan"
-    for e in trace:
-        s, kind = e[0], e[1]
-        n_out = e[4].shape[0]
-        rows = np.unique(rng.integers(0, n_out, 6))
-        if kind == "block":
-            check_block(oracle, e[5], e[2], e[3], e[4], rows)
-        else:
-            check_up(oracle, stack.stages[s].up, e[2], e[3], e[4], e[5], dev(masks[s]), rows)
+    assert len(trace) == 9 and all(e[2].plan is not None for e in trace), "every resolution got a conv plan"
+
+
+@pytest.mark.parametrize("idx", range(9))
+def test_config5_layer_parity(oracle, config5_run, idx):
+    """Each residual block and fused upsample of the config-5 stack at 2,000
+    sampled output rows (first, last and overflow tiles included) against the
+    oracle chain fed the device's own block input."""
+    coords, stack, masks, nb, y, trace = config5_run
+    s, kind, nb_in, x_in, y_out, extra = trace[idx]
+    rng = np.random.default_rng(500 + idx)
+    if kind == "block":
+        rows = sample_rows(y_out.shape[0], rng, 2000, plan=nb_in.plan)
+        check_block(oracle, extra, nb_in, x_in, y_out, rows)
+    else:
+        pairs = np.argwhere(masks[s])
+        rows = sample_rows(y_out.shape[0], rng, 2000, plan=extra.plan)
+        check_up_fused(oracle, stack.stages[s].up, nb_in, x_in, y_out, extra, pairs, rows)
 
 
 def test_config4_transposed_upsample_and_conv(oracle):
@@ -142,13 +133,16 @@ def test_config4_transposed_upsample_and_conv(oracle):
     y = D.ConvLayer(ccfg, bf(w2), dev(b2))(feats, nb)
     torch.cuda.synchronize()
     n = len(cc)
-    rows = np.unique(rng.integers(0, n, 12))
+    rows = sample_rows(n, rng, 2000, plan=nb.plan)
     lin = li.cpu().numpy()
     # the transposed conv at sampled children (a 1x1x1 conv of the parent)
     got_t = host_f32(feats[dev(rows.astype(np.int64))])
     par, c = lin[rows] // 8, lin[rows] % 8
-    exp_t = np.einsum("ri,rci->rc", x[par].astype(np.float64),
-                      wt[:, 0, :].reshape(8, cout, cin)[c].astype(np.float64))
+    wc = wt[:, 0, :].reshape(8, cout, cin).astype(np.float64)
+    exp_t = np.zeros((len(rows), cout))
+    for ci in range(8):
+        sel = c == ci
+        exp_t[sel] = x[par[sel]].astype(np.float64) @ wc[ci].T
     assert_close(got_t, exp_t, TOL_BF16, "config 4 transposed conv")
     # the 3x3x3 conv at sampled children, on the device's bf16 children
     nbr_rows = nb.nbr[dev(rows.astype(np.int64))].cpu().numpy()
@@ -172,7 +166,7 @@ def test_config2_conv_planned(oracle):
     y = layer(bf(x), nb)
     y_direct = layer(bf(x), nb.nbr)       # unplanned direct-gather kernel
     torch.cuda.synchronize()
-    rows = np.unique(rng.integers(0, len(coords), 24))
+    rows = sample_rows(len(coords), rng, 2000, plan=nb.plan)
     nbr_rows = nb.nbr[dev(rows.astype(np.int64))].cpu().numpy()
     exp = conv_rows(oracle, cfg, w, b, lambda idx: x[idx], nbr_rows)
     assert_close(host_f32(y[dev(rows.astype(np.int64))]), exp, TOL_BF16, "config 2 planned conv")

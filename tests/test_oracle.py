@@ -229,6 +229,34 @@ def test_dense_grid_equals_numpy_correlation(oracle):
                    exp.reshape(-1, cout)) < 1e-12
 
 
+@pytest.mark.parametrize("groups,int8", [(1, False), (2, False), (1, True)])
+def test_conv_gemm_f64_equals_conv_ref_f64(oracle, groups, int8):
+    """The numpy im2col form used for the large sampled GPU checks is the same
+    definition as conv_ref_f64 (itself pinned by the correlation above): random
+    coords, absent neighbours, grouped channels, int8 weights with
+    per-channel scales; entries past the input count as absent."""
+    rng = np.random.default_rng(17 + groups + int8)
+    coords = _random_coords(rng, 400, 12)
+    cin, cout = 8 * groups, 6 * groups
+    cfg = oracle.OracleConfig(cin, cout, groups=groups)
+    x = rng.standard_normal((400, cin)).astype(np.float32)
+    if int8:
+        w = rng.integers(-127, 128, (cout, 27, cin // groups)).astype(np.float32)
+        sc = rng.uniform(0.5, 1.5, cout).astype(np.float32) / 127
+    else:
+        w = rng.standard_normal((cout, 27, cin // groups)).astype(np.float32)
+        sc = None
+    b = rng.standard_normal(cout).astype(np.float32)
+    nbr = oracle.build_neighbor_rows(cfg, coords)
+    nbr[::7, 3] = -1           # absent neighbours mid-row
+    exp = oracle.conv_ref_f64(cfg, w, b, x, nbr, sc)
+    got = oracle.conv_gemm_f64(cfg, w, b, x, nbr, sc, chunk=64)
+    nbr[::5, 4] = 400          # past the input: absent in the GEMM form (the device's rule)
+    nbr2 = np.where(nbr >= 400, -1, nbr)
+    assert np.array_equal(oracle.conv_gemm_f64(cfg, w, b, x, nbr, sc), oracle.conv_gemm_f64(cfg, w, b, x, nbr2, sc))
+    assert np.max(np.abs(got - exp)) <= 1e-12 * max(1.0, float(np.max(np.abs(exp))))
+
+
 def test_k1_conv_is_dense_gemm_and_isolated_rows_get_bias(oracle):
     rng = np.random.default_rng(9)
     n, cin, cout = 50, 16, 24
