@@ -101,6 +101,74 @@ def cpu_baseline(coords, x_f32, w1, w2, sample_rows):
     }
 
 
+class Config3Step:
+    """The timed step of config 3 and its buffers: neighbour map + conv plan
+    + conv3x3x3 -> LayerNorm -> SiLU (fused) -> conv3x3x3 -> + x (fused), bf16
+    with f32 accumulation, weights packed once.  tests/test_gpu_bench_step.py
+    runs this same object and checks its output against the oracle."""
+
+    def __init__(self, dev, seed: int = 2026):
+        import numpy as np
+        import torch
+
+        from bevy_synth_amd import flex_gmm as F
+        from bevy_synth_amd import synth
+
+        self.coords = coords = synth.config3_coords()
+        self.n = n = len(coords)
+        self.C = C = 128
+        rng = np.random.default_rng(seed)
+        self.x_f32 = synth.bf16_to_f32(synth.bf16_bits(synth.normal_f32(rng, (n, C))))
+        std = 1.0 / np.sqrt(27 * C)
+        self.w1 = synth.bf16_to_f32(synth.bf16_bits(synth.conv_weight(rng, C, 27, C, std)))
+        self.w2 = synth.bf16_to_f32(synth.bf16_bits(synth.conv_weight(rng, C, 27, C, std)))
+
+        def to_bf16(a):
+            return torch.from_numpy(synth.bf16_bits(a).view(np.int16)).to(dev).view(torch.bfloat16)
+
+        self.coords_d = torch.from_numpy(coords).to(dev)
+        self.x = to_bf16(self.x_f32)
+        self.w1_d, self.w2_d = to_bf16(self.w1), to_bf16(self.w2)
+        self.bias = torch.zeros(C, dtype=torch.float32, device=dev)
+        self.cfg = cfg = F.SparseSubmConvConfig(C, C)
+        self.nbr = torch.empty((n, 27), dtype=torch.int32, device=dev)
+        self.ws = F.NeighborMapWorkspace(dev).get(n)
+        self.plan_buf = torch.empty(F.conv_plan_bytes(n, 27), dtype=torch.uint8, device=dev)
+        self.h = torch.empty((n, C), dtype=torch.bfloat16, device=dev)
+        self.out = torch.empty((n, C), dtype=torch.bfloat16, device=dev)
+        self.w1_p, self.w2_p = F.pack_conv_weight(cfg, self.w1_d), F.pack_conv_weight(cfg, self.w2_d)
+        self.plan = F.ConvPlan(self.plan_buf, n, n, 27)
+        self.F = F
+
+    def map_build(self):
+        self.F.neighbor_map_build_into(self.cfg, self.coords_d, self.nbr, self.ws)
+
+    def plan_build(self):
+        self.F.conv_plan_build_into(self.cfg, self.coords_d, self.nbr, self.plan_buf)
+
+    def map_and_plan(self):
+        self.map_build()
+        self.plan_build()
+
+    def conv1(self):  # conv -> LayerNorm -> SiLU, fused in the conv epilogue
+        self.F.sparse_subm_conv_forward(self.cfg, self.x, self.nbr, self.w1_d, self.bias, out=self.h,
+                                        layer_norm=True, ln_eps=1e-6, silu=True, plan=self.plan,
+                                        packed_weight=self.w1_p)
+
+    def ln_silu(self):  # the unfused LayerNorm + SiLU kernel, timed for reference only
+        self.F.layer_norm(self.h, eps=1e-6, silu=True, out=self.h)
+
+    def conv2(self):  # conv -> + x, fused
+        self.F.sparse_subm_conv_forward(self.cfg, self.h, self.nbr, self.w2_d, self.bias, residual=self.x,
+                                        out=self.out, plan=self.plan, packed_weight=self.w2_p)
+
+    def step(self):
+        self.map_build()
+        self.plan_build()
+        self.conv1()
+        self.conv2()
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -116,57 +184,11 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    coords = synth.config3_coords()
-    n = len(coords)
-    C = 128
-    rng = np.random.default_rng(2026)
-    x_f32 = synth.bf16_to_f32(synth.bf16_bits(synth.normal_f32(rng, (n, C))))
-    std = 1.0 / np.sqrt(27 * C)
-    w1 = synth.bf16_to_f32(synth.bf16_bits(synth.conv_weight(rng, C, 27, C, std)))
-    w2 = synth.bf16_to_f32(synth.bf16_bits(synth.conv_weight(rng, C, 27, C, std)))
-
-    def to_bf16(a):
-        return torch.from_numpy(synth.bf16_bits(a).view(np.int16)).to(dev).view(torch.bfloat16)
-
-    coords_d = torch.from_numpy(coords).to(dev)
-    x = to_bf16(x_f32)
-    w1_d, w2_d = to_bf16(w1), to_bf16(w2)
-    bias = torch.zeros(C, dtype=torch.float32, device=dev)
-    cfg = F.SparseSubmConvConfig(C, C)
-    nbr = torch.empty((n, 27), dtype=torch.int32, device=dev)
-    ws = F.NeighborMapWorkspace(dev).get(n)
-    plan_buf = torch.empty(F.conv_plan_bytes(n, 27), dtype=torch.uint8, device=dev)
-    h = torch.empty((n, C), dtype=torch.bfloat16, device=dev)
-    out = torch.empty((n, C), dtype=torch.bfloat16, device=dev)
-    w1_p, w2_p = F.pack_conv_weight(cfg, w1_d), F.pack_conv_weight(cfg, w2_d)
-    plan = F.ConvPlan(plan_buf, n, n, 27)
-
-    def map_build():
-        F.neighbor_map_build_into(cfg, coords_d, nbr, ws)
-
-    def plan_build():
-        F.conv_plan_build_into(cfg, coords_d, nbr, plan_buf)
-
-    def map_and_plan():
-        map_build()
-        plan_build()
-
-    def conv1():  # conv -> LayerNorm -> SiLU, fused in the conv epilogue
-        F.sparse_subm_conv_forward(cfg, x, nbr, w1_d, bias, out=h, layer_norm=True, ln_eps=1e-6,
-                                   silu=True, plan=plan, packed_weight=w1_p)
-
-    def ln_silu():  # the unfused LayerNorm + SiLU kernel, timed for reference only
-        F.layer_norm(h, eps=1e-6, silu=True, out=h)
-
-    def conv2():  # conv -> + x, fused
-        F.sparse_subm_conv_forward(cfg, h, nbr, w2_d, bias, residual=x, out=out, plan=plan,
-                                   packed_weight=w2_p)
-
-    def step():
-        map_build()
-        plan_build()
-        conv1()
-        conv2()
+    st = Config3Step(dev)
+    n, C, coords, x_f32, w1, w2 = st.n, st.C, st.coords, st.x_f32, st.w1, st.w2
+    nbr, ws, h, out = st.nbr, st.ws, st.h, st.out
+    map_build, plan_build, map_and_plan = st.map_build, st.plan_build, st.map_and_plan
+    conv1, conv2, ln_silu, step = st.conv1, st.conv2, st.ln_silu, st.step
 
     # One untimed step, then everything that needs the host (the map status
     # check, the pair count, the calibration copy), so that the W warmup

@@ -26,6 +26,7 @@ def sample_rows(n, rng, k=2000, plan=None, extra=()):
         must.append(tile_rows(plan, tiles).astype(np.int64))
     must = np.unique(np.concatenate(must))
     must = must[(must >= 0) & (must < n)]
-    left = max(0, k - len(must))
-    rand = rng.choice(n, size=min(left, n), replace=False) if left else np.zeros(0, np.int64)
+    pool = np.setdiff1d(np.arange(n, dtype=np.int64), must, assume_unique=True)
+    left = min(max(0, k - len(must)), len(pool))
+    rand = rng.choice(pool, size=left, replace=False) if left else np.zeros(0, np.int64)
     return np.unique(np.concatenate([must, rand]))
