@@ -16,6 +16,7 @@ SC_OK = 0
 SC_DTYPE_F32 = 0
 SC_DTYPE_BF16 = 1
 SC_DTYPE_I8 = 2
+SC_DTYPE_F16 = 3
 
 # Every symbol include/sparseconv.h declares (checked by tests/test_abi.py).
 EXPORTED = (

@@ -79,8 +79,10 @@ int silu_inplace(int dtype, void *d, int64_t n, hipStream_t s)
         silu_kernel<float><<<g, 256, 0, s>>>((float *)d, n);
     else if (dtype == SC_DTYPE_BF16)
         silu_kernel<uint16_t><<<g, 256, 0, s>>>((uint16_t *)d, n);
+    else if (dtype == SC_DTYPE_F16)
+        silu_kernel<_Float16><<<g, 256, 0, s>>>((_Float16 *)d, n);
     else
-        return fail(SC_ERR_DTYPE, "silu: dtype must be f32 or bf16");
+        return fail(SC_ERR_DTYPE, "silu: dtype must be f32, bf16 or f16");
     SC_LAUNCH_CHECK("silu_kernel launch");
     return SC_OK;
 }
@@ -165,8 +167,8 @@ __device__ inline void unpack16(const uint4 &u, float *f)
         const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            f[2 * i] = bf16_to_f32((uint16_t)(w[i] & 0xffffu));
-            f[2 * i + 1] = bf16_to_f32((uint16_t)(w[i] >> 16));
+            f[2 * i] = half_lo<Tin>(w[i]);
+            f[2 * i + 1] = half_hi<Tin>(w[i]);
         }
     }
 }
@@ -231,15 +233,15 @@ __global__ __launch_bounds__(256) void layer_norm_vec_kernel(const Tin *in, int6
         if constexpr (sizeof(Tout) == 2) {
             if constexpr (VEC == 8) {
                 uint4 o;
-                o.x = (uint32_t)f32_to_bf16(t[0]) | ((uint32_t)f32_to_bf16(t[1]) << 16);
-                o.y = (uint32_t)f32_to_bf16(t[2]) | ((uint32_t)f32_to_bf16(t[3]) << 16);
-                o.z = (uint32_t)f32_to_bf16(t[4]) | ((uint32_t)f32_to_bf16(t[5]) << 16);
-                o.w = (uint32_t)f32_to_bf16(t[6]) | ((uint32_t)f32_to_bf16(t[7]) << 16);
+                o.x = pack_half2<Tout>(t[0], t[1]);
+                o.y = pack_half2<Tout>(t[2], t[3]);
+                o.z = pack_half2<Tout>(t[4], t[5]);
+                o.w = pack_half2<Tout>(t[6], t[7]);
                 *reinterpret_cast<uint4 *>(y + c0) = o;
             } else {
                 uint2 o;
-                o.x = (uint32_t)f32_to_bf16(t[0]) | ((uint32_t)f32_to_bf16(t[1]) << 16);
-                o.y = (uint32_t)f32_to_bf16(t[2]) | ((uint32_t)f32_to_bf16(t[3]) << 16);
+                o.x = pack_half2<Tout>(t[0], t[1]);
+                o.y = pack_half2<Tout>(t[2], t[3]);
                 *reinterpret_cast<uint2 *>(y + c0) = o;
             }
         } else {
@@ -456,8 +458,8 @@ __global__ __launch_bounds__(256) void linear_skinny_kernel(const Tin *__restric
                             const uint32_t q[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
                             for (int k = 0; k < 4; ++k) {
-                                f[2 * k] = bf16_to_f32((uint16_t)(q[k] & 0xffffu));
-                                f[2 * k + 1] = bf16_to_f32((uint16_t)(q[k] >> 16));
+                                f[2 * k] = half_lo<Tin>(q[k]);
+                                f[2 * k + 1] = half_hi<Tin>(q[k]);
                             }
                         }
 #pragma unroll
@@ -487,16 +489,18 @@ int layer_norm_rows(int in_dtype, const void *d_in, int64_t rows, int64_t channe
         return fail(SC_ERR_SHAPE, "layer_norm: invalid rows/channels");
     if (rows == 0) return SC_OK;
     if (!d_in || !d_out) return fail(SC_ERR_NULL, "layer_norm: NULL pointer");
-    if (in_dtype == SC_DTYPE_F32 && out_dtype == SC_DTYPE_F32)
-        return launch_layer_norm<float, float>(d_in, rows, channels, d_w, d_b, eps, apply_silu, d_res, d_out, s);
-    if (in_dtype == SC_DTYPE_F32 && out_dtype == SC_DTYPE_BF16)
-        return launch_layer_norm<float, uint16_t>(d_in, rows, channels, d_w, d_b, eps, apply_silu, d_res, d_out, s);
-    if (in_dtype == SC_DTYPE_BF16 && out_dtype == SC_DTYPE_F32)
-        return launch_layer_norm<uint16_t, float>(d_in, rows, channels, d_w, d_b, eps, apply_silu, d_res, d_out, s);
-    if (in_dtype == SC_DTYPE_BF16 && out_dtype == SC_DTYPE_BF16)
-        return launch_layer_norm<uint16_t, uint16_t>(d_in, rows, channels, d_w, d_b, eps, apply_silu, d_res, d_out,
-                                                     s);
-    return fail(SC_ERR_DTYPE, "layer_norm: dtypes must be f32 or bf16");
+#define LN_CASE(DI, TI, DO, TO)                                                                          \
+    if (in_dtype == DI && out_dtype == DO)                                                              \
+        return launch_layer_norm<TI, TO>(d_in, rows, channels, d_w, d_b, eps, apply_silu, d_res, d_out, s);
+    LN_CASE(SC_DTYPE_F32, float, SC_DTYPE_F32, float)
+    LN_CASE(SC_DTYPE_F32, float, SC_DTYPE_BF16, uint16_t)
+    LN_CASE(SC_DTYPE_F32, float, SC_DTYPE_F16, _Float16)
+    LN_CASE(SC_DTYPE_BF16, uint16_t, SC_DTYPE_F32, float)
+    LN_CASE(SC_DTYPE_BF16, uint16_t, SC_DTYPE_BF16, uint16_t)
+    LN_CASE(SC_DTYPE_F16, _Float16, SC_DTYPE_F32, float)
+    LN_CASE(SC_DTYPE_F16, _Float16, SC_DTYPE_F16, _Float16)
+#undef LN_CASE
+    return fail(SC_ERR_DTYPE, "layer_norm: unsupported dtype pair (f32 / bf16 / f16)");
 }
 
 }  // namespace sc
@@ -582,7 +586,12 @@ int sc_convert(int in_dtype, const void *d_in, int out_dtype, void *d_out, int64
         convert_kernel<float, uint16_t><<<g, 256, 0, s>>>((const float *)d_in, (uint16_t *)d_out, n);
     else if (in_dtype == SC_DTYPE_BF16 && out_dtype == SC_DTYPE_F32)
         convert_kernel<uint16_t, float><<<g, 256, 0, s>>>((const uint16_t *)d_in, (float *)d_out, n);
-    else if (in_dtype == out_dtype && (in_dtype == SC_DTYPE_F32 || in_dtype == SC_DTYPE_BF16)) {
+    else if (in_dtype == SC_DTYPE_F32 && out_dtype == SC_DTYPE_F16)
+        convert_kernel<float, _Float16><<<g, 256, 0, s>>>((const float *)d_in, (_Float16 *)d_out, n);
+    else if (in_dtype == SC_DTYPE_F16 && out_dtype == SC_DTYPE_F32)
+        convert_kernel<_Float16, float><<<g, 256, 0, s>>>((const _Float16 *)d_in, (float *)d_out, n);
+    else if (in_dtype == out_dtype &&
+             (in_dtype == SC_DTYPE_F32 || in_dtype == SC_DTYPE_BF16 || in_dtype == SC_DTYPE_F16)) {
         SC_HIP_CHECK(hipMemcpyAsync(d_out, d_in, (size_t)n * dtype_size(in_dtype),
                                     hipMemcpyDeviceToDevice, s),
                      "convert copy");
@@ -606,8 +615,10 @@ int sc_add(int dtype, const void *d_a, const void *d_b, int64_t n, void *d_out, 
     else if (dtype == SC_DTYPE_BF16)
         add_kernel<uint16_t><<<g, 256, 0, s>>>((const uint16_t *)d_a, (const uint16_t *)d_b,
                                                (uint16_t *)d_out, n);
+    else if (dtype == SC_DTYPE_F16)
+        add_kernel<_Float16><<<g, 256, 0, s>>>((const _Float16 *)d_a, (const _Float16 *)d_b, (_Float16 *)d_out, n);
     else
-        return fail(SC_ERR_DTYPE, "add: dtype must be f32 or bf16");
+        return fail(SC_ERR_DTYPE, "add: dtype must be f32, bf16 or f16");
     SC_LAUNCH_CHECK("add_kernel launch");
     return SC_OK;
 }
@@ -640,8 +651,11 @@ int sc_linear_skinny(int in_dtype, const void *d_x, int64_t rows, int64_t in_cha
     else if (in_dtype == SC_DTYPE_BF16)
         linear_skinny_kernel<uint16_t><<<g, 256, 0, s>>>((const uint16_t *)d_x, rows, (int)in_channels, d_w, d_b,
                                                         (int)out_channels, d_out);
+    else if (in_dtype == SC_DTYPE_F16)
+        linear_skinny_kernel<_Float16><<<g, 256, 0, s>>>((const _Float16 *)d_x, rows, (int)in_channels, d_w, d_b,
+                                                        (int)out_channels, d_out);
     else
-        return fail(SC_ERR_DTYPE, "skinny linear input must be f32 or bf16");
+        return fail(SC_ERR_DTYPE, "skinny linear input must be f32, bf16 or f16");
     SC_LAUNCH_CHECK("linear_skinny_kernel launch");
     return SC_OK;
 }
@@ -719,8 +733,10 @@ int sc_c2s_skip_add(int dtype, void *d_h, int64_t n, int64_t out_channels, int p
         SKIP_LAUNCH(uint16_t, float);
     else if (dtype == SC_DTYPE_BF16 && parent_dtype == SC_DTYPE_BF16)
         SKIP_LAUNCH(uint16_t, uint16_t);
+    else if (dtype == SC_DTYPE_F16 && parent_dtype == SC_DTYPE_F16)
+        SKIP_LAUNCH(_Float16, _Float16);
     else
-        return fail(SC_ERR_DTYPE, "c2s_skip_add: dtypes must be f32 or bf16");
+        return fail(SC_ERR_DTYPE, "c2s_skip_add: dtypes must be f32 or bf16 (or f16 with f16)");
 #undef SKIP_LAUNCH
     SC_LAUNCH_CHECK("c2s_skip_add_kernel launch");
     return SC_OK;

@@ -54,6 +54,7 @@ inline size_t dtype_size(int dt)
     case SC_DTYPE_F32: return 4;
     case SC_DTYPE_BF16: return 2;
     case SC_DTYPE_I8: return 1;
+    case SC_DTYPE_F16: return 2;
     default: return 0;
     }
 }
@@ -83,18 +84,50 @@ __host__ __device__ inline float bf16_to_f32(uint16_t h)
     return __builtin_bit_cast(float, static_cast<uint32_t>(h) << 16);
 }
 
+// ------------------------------------------------------------ f16 bits
+// IEEE binary16 storage is _Float16 (bf16 storage is uint16_t).  f32 -> f16
+// is v_cvt_f16_f32 in the default round-to-nearest-even mode, subnormals
+// kept: the rounding of half::f16::from_f32 / burn's F16 cast that the
+// reference's f16 fences apply (sparse_decoder_wgpu_ops.rs:1082-1088,
+// 1722-1726).
+typedef _Float16 f16_t;
+
+__device__ inline uint16_t f32_to_f16_bits(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+__device__ inline float f16_bits_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
 template <typename T> __device__ inline float load_as_f32(const T *p, int64_t i);
 template <> __device__ inline float load_as_f32<float>(const float *p, int64_t i) { return p[i]; }
 template <> __device__ inline float load_as_f32<uint16_t>(const uint16_t *p, int64_t i)
 {
     return bf16_to_f32(p[i]);
 }
+template <> __device__ inline float load_as_f32<_Float16>(const _Float16 *p, int64_t i) { return (float)p[i]; }
 
 template <typename T> __device__ inline void store_from_f32(T *p, int64_t i, float v);
 template <> __device__ inline void store_from_f32<float>(float *p, int64_t i, float v) { p[i] = v; }
 template <> __device__ inline void store_from_f32<uint16_t>(uint16_t *p, int64_t i, float v)
 {
     p[i] = f32_to_bf16(v);
+}
+template <> __device__ inline void store_from_f32<_Float16>(_Float16 *p, int64_t i, float v) { p[i] = (_Float16)v; }
+
+// Two 16-bit values (bf16 or f16 by T) of a 32-bit word -> f32, and back.
+template <typename T> __device__ inline float half_lo(uint32_t w)
+{
+    if constexpr (sizeof(T) == 2 && !__is_same(T, uint16_t)) return f16_bits_to_f32((uint16_t)(w & 0xffffu));
+    else return bf16_to_f32((uint16_t)(w & 0xffffu));
+}
+template <typename T> __device__ inline float half_hi(uint32_t w)
+{
+    if constexpr (sizeof(T) == 2 && !__is_same(T, uint16_t)) return f16_bits_to_f32((uint16_t)(w >> 16));
+    else return bf16_to_f32((uint16_t)(w >> 16));
+}
+template <typename T> __device__ inline uint32_t pack_half2(float lo, float hi)
+{
+    if constexpr (__is_same(T, uint16_t))
+        return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+    else
+        return (uint32_t)f32_to_f16_bits(lo) | ((uint32_t)f32_to_f16_bits(hi) << 16);
 }
 
 // ---------------------------------------------------- kernel offsets

@@ -70,7 +70,7 @@ class ConvLayer:
 
     def packed_weight(self) -> Optional[torch.Tensor]:
         cin_g = self.cfg.to_c().in_channels_per_group
-        if (self.packed is None and self.weight.dtype in (torch.bfloat16, torch.int8)
+        if (self.packed is None and self.weight.dtype in (torch.bfloat16, torch.float16, torch.int8)
                 and cin_g % 32 == 0):
             self.packed = pack_conv_weight(self.cfg, self.weight)
         return self.packed
@@ -82,7 +82,7 @@ class ConvLayer:
         (child_rows / n_child_rows, skip_parent / skip_index)."""
         plan, packed = None, None
         if isinstance(nbr, Neighborhood):
-            if nbr.plan is not None and x.dtype == torch.bfloat16:
+            if nbr.plan is not None and x.dtype in (torch.bfloat16, torch.float16):
                 packed = self.packed_weight()
                 plan = nbr.plan if packed is not None else None
             nbr = nbr.nbr

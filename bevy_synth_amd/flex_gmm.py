@@ -40,6 +40,7 @@ _DTYPES = {
     torch.float32: _capi.SC_DTYPE_F32,
     torch.bfloat16: _capi.SC_DTYPE_BF16,
     torch.int8: _capi.SC_DTYPE_I8,
+    torch.float16: _capi.SC_DTYPE_F16,
 }
 
 
@@ -333,9 +334,10 @@ def build_conv_plan(cfg: SparseSubmConvConfig, coords: torch.Tensor,
 
 def conv_weight_pack_bytes(cfg: SparseSubmConvConfig, w_dtype: torch.dtype) -> int:
     out = ctypes.c_size_t()
-    dt = {torch.bfloat16: _capi.SC_DTYPE_BF16, torch.int8: _capi.SC_DTYPE_I8}.get(w_dtype)
+    dt = {torch.bfloat16: _capi.SC_DTYPE_BF16, torch.int8: _capi.SC_DTYPE_I8,
+          torch.float16: _capi.SC_DTYPE_F16}.get(w_dtype)
     if dt is None:
-        raise SparseConvError(3, "weight packing takes bf16 or int8 weights")
+        raise SparseConvError(3, "weight packing takes bf16, f16 or int8 weights")
     check(_capi.load().sc_conv_weight_pack_size(ctypes.byref(cfg.to_c()), dt, ctypes.byref(out)))
     return out.value
 

@@ -69,7 +69,8 @@ typedef enum sc_status {
 typedef enum sc_dtype {
     SC_DTYPE_F32 = 0,
     SC_DTYPE_BF16 = 1,
-    SC_DTYPE_I8 = 2
+    SC_DTYPE_I8 = 2,
+    SC_DTYPE_F16 = 3  /* IEEE binary16: the decoder's compute_fp16 mode */
 } sc_dtype;
 
 /* hipStream_t, passed through untyped so that the header needs no HIP. */

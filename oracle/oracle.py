@@ -108,6 +108,7 @@ def lib():
         L.orc_conv_legacy.argtypes = [cfgp, P, P, P, i64, P, P]
         L.orc_conv_ref_f64.argtypes = [cfgp, P, P, P, P, i64, P, i64, P]
         L.orc_bf16_round.argtypes = [P, P, i64]
+        L.orc_f16_round.argtypes = [P, P, i64]
         L.orc_layer_norm.argtypes = [P, i64, i64, P, P, ctypes.c_float]
         L.orc_silu.argtypes = [P, i64]
         L.orc_subdivision_active.argtypes = [P, i64, P, P]
@@ -270,6 +271,15 @@ def bf16_round(x) -> np.ndarray:
     a = np.ascontiguousarray(x, dtype=np.float32)
     out = np.empty_like(a)
     lib().orc_bf16_round(_p(a), _p(out), a.size)
+    return out
+
+
+def f16_round(x) -> np.ndarray:
+    """quantize_f16_inplace / quantize_f16_tensor_wgpu (burn_trellis
+    sparse_decoder_wgpu_ops.rs:1722-1726, 1082-1088): f32 -> f16 (RNE) -> f32."""
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(a)
+    lib().orc_f16_round(_p(a), _p(out), a.size)
     return out
 
 

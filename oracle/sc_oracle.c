@@ -462,6 +462,62 @@ void orc_bf16_round(const float *in, float *out, int64_t n)
     }
 }
 
+/* f32 -> IEEE binary16 -> f32 with round-to-nearest-even, subnormals kept,
+ * overflow to +-inf: quantize_f16_inplace (sparse_decoder_wgpu_ops.rs
+ * :1722-1726, half::f16::from_f32(v).to_f32()) and the F32 -> F16 -> F32
+ * casts of quantize_f16_tensor_wgpu (:1082-1088). */
+static uint16_t f32_to_f16_bits(float f)
+{
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t e = (x >> 23) & 0xffu, m = x & 0x7fffffu;
+    if (e == 0xffu) return (uint16_t)(sign | 0x7c00u | (m ? 0x200u | (m >> 13) : 0u));
+    const int32_t E = (int32_t)e - 127 + 15; /* f16 biased exponent */
+    if (E >= 31) return (uint16_t)(sign | 0x7c00u);
+    if (E <= 0) {                            /* f16 subnormal (or zero) */
+        if (E < -10) return (uint16_t)sign;  /* below half the smallest subnormal */
+        const uint32_t M = m | 0x800000u;
+        const int shift = 14 - E;            /* value = M * 2^(E-14) units of 2^-24 */
+        uint32_t h = M >> shift;
+        const uint32_t rem = M & ((1u << shift) - 1u), half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (h & 1u))) ++h; /* may carry into the smallest normal */
+        return (uint16_t)(sign | h);
+    }
+    uint32_t h = ((uint32_t)E << 10) | (m >> 13);
+    const uint32_t rem = m & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h; /* a carry may reach the inf pattern */
+    return (uint16_t)(sign | h);
+}
+
+static float f16_bits_to_f32(uint16_t h)
+{
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+    uint32_t x;
+    if (e == 0x1fu) {
+        x = sign | 0x7f800000u | (m << 13);
+    } else if (e == 0) {
+        if (m == 0) {
+            x = sign;
+        } else { /* subnormal: m * 2^-24, exact in f32 */
+            float v = (float)m * 5.9604644775390625e-08f;
+            memcpy(&x, &v, 4);
+            x |= sign;
+        }
+    } else {
+        x = sign | ((e + 112u) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &x, 4);
+    return f;
+}
+
+void orc_f16_round(const float *in, float *out, int64_t n)
+{
+    for (int64_t i = 0; i < n; ++i) out[i] = f16_bits_to_f32(f32_to_f16_bits(in[i]));
+}
+
 /*
  * layer_norm_inplace, sparse_decoder_wgpu_ops.rs:1642-1711 (burn_trellis
  * runtime_model): two-pass f32 mean and biased variance per row,

@@ -385,3 +385,23 @@ def test_c2s_block_matches_numpy_composition(oracle):
     skip = feats.reshape(P * 8, cin // 8)[li]
     exp = (h2.reshape(len(li), cin // 8, -1) + skip[:, :, None]).reshape(len(li), cout)
     assert rel_err(out, exp) < 1e-4
+
+
+def test_f16_round_matches_numpy_float16(oracle):
+    """f16_round (quantize_f16_inplace: f32 -> binary16 RNE -> f32) bit for bit
+    against numpy's float16 cast: normals at every scale, subnormals, the
+    overflow boundary (65504 / 65520), exact ties between f16 neighbours
+    (round to even), signed zeros and infinities."""
+    rng = np.random.default_rng(0)
+    parts = [rng.standard_normal(50000).astype(np.float32) * np.float32(s)
+             for s in (1e-7, 1e-5, 1e-3, 1.0, 100.0, 3e4, 7e4)]
+    edge = np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, 65536.0, -65520.0, np.inf, -np.inf,
+                     2.0 ** -24, 2.0 ** -25, 2.0 ** -25 * 1.0001, 2.0 ** -14, 2.0 ** -14 * (1 - 2.0 ** -11)],
+                    np.float32)
+    h = rng.integers(0x0001, 0x7bff, 20000).astype(np.uint16).view(np.float16).astype(np.float32)
+    ties = (h.view(np.uint32) + (1 << 12)).view(np.float32)      # exactly half an f16 ulp above (normals)
+    x = np.concatenate(parts + [edge, ties, -ties])
+    with np.errstate(over="ignore"):
+        exp = x.astype(np.float16).astype(np.float32)
+    got = oracle.f16_round(x)
+    assert np.array_equal(got.view(np.uint32), exp.view(np.uint32))
