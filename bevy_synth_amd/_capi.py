@@ -30,7 +30,7 @@ EXPORTED = (
     "sc_subm_conv_forward_planned",
     "sc_conv_weight_pack_size", "sc_conv_weight_pack",
     "sc_subdivision_build_static", "sc_conv_plan_check", "sc_conv_epilogue_workspace_size",
-    "sc_subdivision_build_indexed", "sc_linear_skinny",
+    "sc_subdivision_build_indexed", "sc_linear_skinny", "sc_linear_forward",
 )
 
 
@@ -126,6 +126,8 @@ def load() -> ctypes.CDLL:
     L.sc_subdivision_workspace_size.argtypes = [i64, sizep]
     L.sc_subdivision_build.argtypes = [P, P, P, P, i64, P, P, P, P, P, ctypes.c_size_t, P]
     L.sc_subdivision_build_indexed.argtypes = [P, P, P, P, i64, P, P, P, P, P, P, ctypes.c_size_t, P]
+    L.sc_linear_forward.argtypes = [i32, P, i64, i64, i64, i32, P, P, P, ctypes.POINTER(ScConvEpilogue), i32,
+                                    P, P]
     L.sc_linear_skinny.argtypes = [i32, P, i64, i64, P, P, i64, P, P]
     L.sc_subdivision_build_static.argtypes = [P, P, P, P, i64, P, P, P, P, P]
     L.sc_gather_rows.argtypes = [i32, P, i64, i64, i64, P, i64, P, P]

@@ -102,11 +102,13 @@ static bool ln_in_tile(const sc_conv_config *cfg, int act_dtype, const C2SForms 
     return cfg->out_channels_per_group <= kBN;
 }
 
+// dense: the linear layer (a 1x1x1 kernel without a map: query row r reads
+// input row r).
 static int conv_forward_impl(const sc_conv_config *cfg, int act_dtype, const void *d_input,
                              int64_t n_in, const int32_t *d_map, int64_t n_q, int w_dtype,
                              const void *d_weight, const float *d_w_scale, const float *d_bias,
                              const sc_conv_epilogue *epi, int out_dtype, void *d_out,
-                             const void *d_plan, const void *d_wpack, sc_stream stream)
+                             const void *d_plan, const void *d_wpack, sc_stream stream, bool dense = false)
 {
     clear_error();
     const void *d_residual = epi ? epi->residual : nullptr;
@@ -143,7 +145,7 @@ static int conv_forward_impl(const sc_conv_config *cfg, int act_dtype, const voi
     rc = c2s_forms(cfg, epi, c2s);
     if (rc) return rc;
     if (n_q == 0) return SC_OK;
-    if (!d_input || !d_map || !d_weight || !d_out) return fail(SC_ERR_NULL, "sparse conv: NULL pointer");
+    if (!d_input || (!d_map && !dense) || !d_weight || !d_out) return fail(SC_ERR_NULL, "sparse conv: NULL pointer");
 
     ConvArgs a;
     a.input = d_input;
@@ -266,6 +268,29 @@ extern "C" int sc_subm_conv_forward_fused(const sc_conv_config *cfg, int act_dty
 {
     return conv_forward_impl(cfg, act_dtype, d_input, n_in, d_map, n_q, w_dtype, d_weight, d_w_scale,
                              d_bias, epi, out_dtype, d_out, nullptr, nullptr, stream);
+}
+
+extern "C" int sc_linear_forward(int act_dtype, const void *d_input, int64_t rows, int64_t in_channels,
+                                 int64_t out_channels, int w_dtype, const void *d_weight, const float *d_w_scale,
+                                 const float *d_bias, const sc_conv_epilogue *epi, int out_dtype, void *d_out,
+                                 sc_stream stream)
+{
+    clear_error();
+    if (epi && (epi->child_rows || epi->skip_index))
+        return fail(SC_ERR_UNSUPPORTED, "linear: the C2S epilogue forms belong to the sparse conv");
+    sc_conv_config c{};
+    c.in_channels = in_channels;
+    c.out_channels = out_channels;
+    c.kernel_d = c.kernel_h = c.kernel_w = 1;
+    c.in_channels_per_group = in_channels;
+    c.out_channels_per_group = out_channels;
+    c.groups = 1;
+    c.axis_order[0] = 0;
+    c.axis_order[1] = 1;
+    c.axis_order[2] = 2;
+    c.axis_sign[0] = c.axis_sign[1] = c.axis_sign[2] = 1;
+    return conv_forward_impl(&c, act_dtype, d_input, rows, nullptr, rows, w_dtype, d_weight, d_w_scale, d_bias,
+                             epi, out_dtype, d_out, nullptr, nullptr, stream, true);
 }
 
 extern "C" int sc_subm_conv_forward_planned(const sc_conv_config *cfg, int act_dtype,

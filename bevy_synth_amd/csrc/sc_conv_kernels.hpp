@@ -23,7 +23,7 @@ constexpr int kSubTiles = kPlanTileRows / kTileRows;  // direct tiles per plan t
 
 struct ConvArgs {
     const void *input;
-    const int32_t *map;
+    const int32_t *map;  // [n_q][K]; NULL only for the dense linear (K = 1, query row r reads row r)
     const void *weight;
     const float *w_scale;
     const float *bias;
@@ -409,12 +409,21 @@ __global__ __launch_bounds__(kThreads, 2) void conv_mfma_kernel(ConvArgs args)
     const int64_t in_col0 = (int64_t)g * args.cin_g;
     const int64_t out_col0 = (int64_t)g * args.cout_g;
     const int nrows = (int)min<int64_t>(kRows, args.n_q - row0);
-    const int32_t *map_tile = args.map + row0 * K;
+    const int32_t *map_tile = args.map ? args.map + row0 * K : nullptr;
     const int64_t n_in = args.n_in;
     const uint32_t row_bytes = (uint32_t)(args.cin * (int64_t)sizeof(TA));
 
-    const int nk = build_offset_list(map_tile, nrows, K, n_in, s_kmask, s_klist, &s_nk);
-    fill_row_offsets(map_tile, nrows, K, n_in, row_bytes, s_klist, nk, s_aoff);
+    int nk;
+    if (args.map) {
+        nk = build_offset_list(map_tile, nrows, K, n_in, s_kmask, s_klist, &s_nk);
+        fill_row_offsets(map_tile, nrows, K, n_in, row_bytes, s_klist, nk, s_aoff);
+    } else {
+        // no map: the dense linear (K = 1), query row r reads input row r
+        nk = 1;
+        if (tid == 0) s_klist[0] = 0;
+        s_aoff[0][tid] = tid < nrows && row0 + tid < n_in ? (uint32_t)(row0 + tid) * row_bytes : kOobOffset;
+        __syncthreads();
+    }
 
     const int nkc = args.cin_g / kBK;  // chunks per offset
     const int S = nk * nkc;
@@ -519,21 +528,24 @@ __global__ __launch_bounds__(kThreads, 2) void conv_mfma_kernel(ConvArgs args)
     TO *__restrict__ out = static_cast<TO *>(args.out);
     const TO *__restrict__ res = static_cast<const TO *>(args.residual);
     const bool vec_ok = args.vec_out != 0;
+    // bias / int8 scale per channel, applied to both row blocks at once
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int o = o0 + j * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
+            const bool ok = o < args.cout_g;
+            const float bias = (args.bias && ok) ? args.bias[out_col0 + o] : 0.f;
+            const float scale = (kI8 && args.w_scale && ok) ? args.w_scale[out_col0 + o] : 1.f;
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                acc[i][j][e] = ok ? (kI8 ? acc[i][j][e] * scale + bias : acc[i][j][e] + bias) : 0.f;
+        }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int r = wave * 64 + i * 32 + (lane & 31);
         if (r >= nrows) continue;  // lanes l and l^32 share r: both skip together
         const int64_t rowbase = (row0 + r) * args.cout + out_col0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int o = o0 + j * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
-                const bool ok = o < args.cout_g;
-                const float bias = (args.bias && ok) ? args.bias[out_col0 + o] : 0.f;
-                const float scale = (kI8 && args.w_scale && ok) ? args.w_scale[out_col0 + o] : 1.f;
-                acc[i][j][e] = ok ? (kI8 ? acc[i][j][e] * scale + bias : acc[i][j][e] + bias) : 0.f;
-            }
         if (args.ln) {
             // Two-pass f32 statistics over the row's Cout channels (the
             // reference's layer_norm_row_stats, wgpu/ops.rs:162-187).
@@ -752,10 +764,11 @@ __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
             rv = pq >= 0 && pq < args.n_q;
         }
         s_qrow[tid] = rv ? (int32_t)qrow : -1;
-        const int32_t *mrow = args.map + (rv ? qrow : 0) * K;
+        // no map: the dense linear (K = 1), query row q reads input row q
+        const int32_t *mrow = args.map ? args.map + (rv ? qrow : 0) * K : nullptr;
         int32_t v[kMaxTableK];
 #pragma unroll
-        for (int k = 0; k < kMaxTableK; ++k) v[k] = (rv && k < K) ? mrow[k] : -1;
+        for (int k = 0; k < kMaxTableK; ++k) v[k] = (rv && k < K) ? (mrow ? mrow[k] : (int32_t)qrow) : -1;
 #pragma unroll
         for (int k = 0; k < kMaxTableK; ++k) {
             const bool ok = v[k] >= 0 && v[k] < n_in;
@@ -952,25 +965,33 @@ __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
     TO *__restrict__ out = static_cast<TO *>(args.out);
     const TO *__restrict__ res = static_cast<const TO *>(args.residual);
     const bool vec_ok = args.vec_out != 0;
+    const bool c2s = args.scatter_rows || args.skip_idx;
+    // LayerNorm groups: the row (ln_group = Cout_g <= 128, or a 128-channel
+    // C2S child = the tile) or the two 64-channel halves of the tile (C2S
+    // children of 64 channels).  Partial sums are kept per half either way.
+    const bool halves = args.ln_group == 64 && args.cout_g > 64;
+    const float inv_c = 1.0f / (float)args.ln_group;
+    // bias / int8 scale per channel, applied to the 4 row blocks at once (each
+    // value is then dead: no 32 + 32 registers held through the epilogue)
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int o = o0 + j * 16 + 4 * q4 + e;
+            const bool ok = o < args.cout_g;
+            const float bias = (args.bias && ok) ? args.bias[out_col0 + o] : 0.f;
+            const float scale = (kI8 && args.w_scale && ok) ? args.w_scale[out_col0 + o] : 1.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                acc[i][j][e] = ok ? (kI8 ? acc[i][j][e] * scale + bias : acc[i][j][e] + bias) : 0.f;
+        }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int32_t qrow = s_qrow[wave * 64 + i * 16 + l16];
         if (qrow < 0) continue;
         const int64_t rowbase = (int64_t)qrow * args.cout + out_col0;
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int o = o0 + j * 16 + 4 * q4 + e;
-                const bool ok = o < args.cout_g;
-                const float bias = (args.bias && ok) ? args.bias[out_col0 + o] : 0.f;
-                const float scale = (kI8 && args.w_scale && ok) ? args.w_scale[out_col0 + o] : 1.f;
-                acc[i][j][e] = ok ? (kI8 ? acc[i][j][e] * scale + bias : acc[i][j][e] + bias) : 0.f;
-            }
-        if (args.ln && args.ln_group == 64 && args.cout_g > 64) {
-            // LayerNorm per 64-channel half of the 128-channel tile (one C2S
-            // child each): channel blocks j < 4 and j >= 4.
-            float sum[2] = {0.f, 0.f}, qv[2] = {0.f, 0.f}, mean[2], inv_std[2];
+        if (args.ln) {
+            float sum[2] = {0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < 8; ++j)
 #pragma unroll
@@ -979,8 +1000,10 @@ __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
             for (int h = 0; h < 2; ++h) {
                 sum[h] += __shfl_xor(sum[h], 16, 64);
                 sum[h] += __shfl_xor(sum[h], 32, 64);
-                mean[h] = sum[h] * (1.0f / 64.0f);
             }
+            if (!halves) sum[0] = sum[1] = sum[0] + sum[1];
+            const float mean[2] = {sum[0] * inv_c, sum[1] * inv_c};
+            float qv[2] = {0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < 8; ++j)
 #pragma unroll
@@ -993,50 +1016,22 @@ __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
             for (int h = 0; h < 2; ++h) {
                 qv[h] += __shfl_xor(qv[h], 16, 64);
                 qv[h] += __shfl_xor(qv[h], 32, 64);
-                inv_std[h] = rsqrt_f32(qv[h] * (1.0f / 64.0f) + args.ln_eps);
             }
+            if (!halves) qv[0] = qv[1] = qv[0] + qv[1];
+            const float inv_std[2] = {rsqrt_f32(qv[0] * inv_c + args.ln_eps), rsqrt_f32(qv[1] * inv_c + args.ln_eps)};
+            // channel within the LayerNorm group: o itself for a whole row,
+            // o - o0 (+ 64 for the upper half) inside a C2S child
+            const int gbase = args.ln_group == args.cout_g ? 0 : o0;
 #pragma unroll
             for (int j = 0; j < 8; ++j)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int o = o0 + j * 16 + 4 * q4 + e;
                     const bool ok = o < args.cout_g;
+                    const int og = halves ? (o - o0) & 63 : o - gbase;
                     float t = (acc[i][j][e] - mean[j >> 2]) * inv_std[j >> 2];
-                    if (args.ln_w && ok) t *= args.ln_w[o % 64];
-                    if (args.ln_b && ok) t += args.ln_b[o % 64];
-                    acc[i][j][e] = t;
-                }
-        } else if (args.ln) {
-            float sum = 0.f;
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) sum += acc[i][j][e];
-            sum += __shfl_xor(sum, 16, 64);
-            sum += __shfl_xor(sum, 32, 64);
-            const float inv_c = 1.0f / (float)args.ln_group;
-            const float mean = sum * inv_c;
-            float qv = 0.f;
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int o = o0 + j * 16 + 4 * q4 + e;
-                    const float d = acc[i][j][e] - mean;
-                    qv += o < args.cout_g ? d * d : 0.f;
-                }
-            qv += __shfl_xor(qv, 16, 64);
-            qv += __shfl_xor(qv, 32, 64);
-            const float inv_std = rsqrt_f32(qv * inv_c + args.ln_eps);
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int o = o0 + j * 16 + 4 * q4 + e;
-                    const bool ok = o < args.cout_g;
-                    float t = (acc[i][j][e] - mean) * inv_std;
-                    if (args.ln_w && ok) t *= args.ln_w[o % args.ln_group];
-                    if (args.ln_b && ok) t += args.ln_b[o % args.ln_group];
+                    if (args.ln_w && ok) t *= args.ln_w[og];
+                    if (args.ln_b && ok) t += args.ln_b[og];
                     acc[i][j][e] = t;
                 }
         }
@@ -1049,20 +1044,14 @@ __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
                     acc[i][j][e] = silu_f32(t);
                 }
         }
-        if (args.scatter_rows || args.skip_idx) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int oc = o0 + j * 16 + 4 * q4;
-                if (oc >= args.cout_g) continue;
-                float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
-                store_general<TO>(args, qrow, out_col0 + oc, min(4, args.cout_g - oc), v, vec_ok);
-            }
-            continue;
-        }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int oc = o0 + j * 16 + 4 * q4;
             float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+            if (c2s) {
+                if (oc < args.cout_g) store_general<TO>(args, qrow, out_col0 + oc, min(4, args.cout_g - oc), v, vec_ok);
+                continue;
+            }
             if (vec_ok && oc + 3 < args.cout_g) {
                 typename Out4<TO>::V *dst = reinterpret_cast<typename Out4<TO>::V *>(out + rowbase + oc);
                 if (res) {
@@ -1588,7 +1577,7 @@ __global__ __launch_bounds__(256) void conv_scalar_kernel(ConvArgs args)
         const int64_t g = o / args.cout_g;
         float acc = 0.f;
         for (int k = 0; k < args.K; ++k) {
-            const int32_t nb = args.map[r * args.K + k];
+            const int32_t nb = args.map ? args.map[r * args.K + k] : (int32_t)r;  // no map: dense linear
             if (nb < 0 || nb >= args.n_in) continue;
             const TA *a = input + (int64_t)nb * args.cin + g * args.cin_g;
             const TW *w = weight + (o * args.K + k) * args.cin_g;

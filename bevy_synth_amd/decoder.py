@@ -26,7 +26,7 @@ from typing import List, Optional, Sequence, Tuple, Union
 import torch
 
 from .flex_gmm import (ConvPlan, NeighborMapWorkspace, SparseSubmConvConfig, build_conv_plan,
-                       c2s_skip_add, gather_rows, kernel_rows, layer_norm, linear_skinny,
+                       c2s_skip_add, gather_rows, kernel_rows, layer_norm, linear_forward, linear_skinny,
                        neighbor_rows_tensor_from_coords_tensor, pack_conv_weight,
                        sparse_subm_conv_forward, subdivision_build, subdivision_build_indexed)
 
@@ -77,9 +77,10 @@ class ConvLayer:
 
     def __call__(self, x: torch.Tensor, nbr: Union[torch.Tensor, Neighborhood], out_dtype=None,
                  residual: Optional[torch.Tensor] = None, layer_norm: bool = False,
-                 silu: bool = False, ln_eps: float = LAYER_NORM32_EPS, **c2s) -> torch.Tensor:
-        """``c2s``: the C2S epilogue forms of sparse_subm_conv_forward
-        (child_rows / n_child_rows, skip_parent / skip_index)."""
+                 silu: bool = False, ln_eps: float = LAYER_NORM32_EPS, **epi) -> torch.Tensor:
+        """``epi``: further epilogue arguments of sparse_subm_conv_forward
+        (ln_weight / ln_bias, the C2S forms child_rows / n_child_rows and
+        skip_parent / skip_index)."""
         plan, packed = None, None
         if isinstance(nbr, Neighborhood):
             if nbr.plan is not None and x.dtype in (torch.bfloat16, torch.float16):
@@ -89,7 +90,7 @@ class ConvLayer:
         return sparse_subm_conv_forward(self.cfg, x, nbr, self.weight, self.bias, self.w_scale,
                                         residual=residual, out_dtype=out_dtype,
                                         layer_norm=layer_norm, ln_eps=ln_eps, silu=silu,
-                                        plan=plan, packed_weight=packed, **c2s)
+                                        plan=plan, packed_weight=packed, **epi)
 
 
 @dataclass
@@ -102,6 +103,47 @@ class ResidualBlock:
         # conv1 carries LayerNorm + SiLU in its epilogue; conv2 adds the residual.
         h = self.conv1(x, nbr, out_dtype=x.dtype, layer_norm=True, silu=True, ln_eps=self.eps)
         return self.conv2(h, nbr, out_dtype=x.dtype, residual=x)
+
+
+@dataclass
+class LinearLayer:
+    """A dense layer, weight [Cout, Cin] (the reference's LinearLayer layout,
+    sparse_decoder.rs; bf16 / f16 / f32, or int8 with w_scale), bias [Cout] f32."""
+
+    weight: torch.Tensor
+    bias: Optional[torch.Tensor] = None
+    w_scale: Optional[torch.Tensor] = None
+
+    def __call__(self, x: torch.Tensor, out_dtype=None, silu: bool = False,
+                 residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+        return linear_forward(x, self.weight, self.bias, self.w_scale, residual=residual, out_dtype=out_dtype,
+                              silu=silu)
+
+
+@dataclass
+class ConvNeXtBlock:
+    """TRELLIS2's sparse ConvNeXt block (convnext_blocks_forward_wgpu_tensor,
+    sparse_decoder_wgpu_ops.rs:1091-1161; MLP :356-489):
+        h = LN(conv3x3x3(x); norm affine) -> mlp_0 -> SiLU -> mlp_2 -> + x.
+    The LayerNorm runs in the conv's epilogue (on f32 staging above 128
+    channels), SiLU in mlp_0's and the residual in mlp_2's; each stored tensor
+    is rounded once to the activation dtype."""
+
+    conv: ConvLayer
+    norm_weight: torch.Tensor
+    norm_bias: torch.Tensor
+    mlp_0: LinearLayer
+    mlp_2: LinearLayer
+    eps: float = LAYER_NORM32_EPS
+
+    def __call__(self, x: torch.Tensor, nbr: Union[torch.Tensor, "Neighborhood"]) -> torch.Tensor:
+        h = self.conv(x, nbr, out_dtype=x.dtype, layer_norm=True, ln_eps=self.eps, ln_weight=self.norm_weight,
+                      ln_bias=self.norm_bias)
+        return self.forward_tail(h, x)
+
+    def forward_tail(self, h: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+        hid = self.mlp_0(h, out_dtype=x.dtype, silu=True)
+        return self.mlp_2(hid, out_dtype=x.dtype, residual=x)
 
 
 @dataclass

@@ -491,6 +491,55 @@ def sparse_subm_conv_forward(cfg: SparseSubmConvConfig, input: torch.Tensor,
     return out
 
 
+def linear_forward(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                   w_scale: Optional[torch.Tensor] = None, residual: Optional[torch.Tensor] = None,
+                   out_dtype: Optional[torch.dtype] = None, silu: bool = False, layer_norm: bool = False,
+                   ln_weight: Optional[torch.Tensor] = None, ln_bias: Optional[torch.Tensor] = None,
+                   ln_eps: float = 1e-6, out: Optional[torch.Tensor] = None,
+                   workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """linear_forward_wgpu (burn_trellis sparse_decoder_wgpu_ops.rs:79-160) through
+    sc_linear_forward: x [rows, Cin] @ weight[Cout, Cin]^T + bias, with the conv
+    epilogue (LayerNorm over the row, SiLU, + residual) fused.  Same dtype rules
+    as sparse_subm_conv_forward."""
+    _require_cuda("x", x)
+    _require_cuda("weight", weight)
+    rows, cin = x.shape
+    if weight.dim() != 2 or weight.shape[1] != cin:
+        raise SparseConvError(2, f"linear: invalid input channels {cin}, weight {tuple(weight.shape)}")
+    cout = weight.shape[0]
+    for name, t in (("bias", bias), ("w_scale", w_scale), ("ln_weight", ln_weight), ("ln_bias", ln_bias)):
+        if t is not None:
+            _require_cuda(name, t)
+            if t.dtype != torch.float32 or t.numel() != cout:
+                raise SparseConvError(2, f"linear: {name} must be f32 [{cout}]")
+    od = x.dtype if out_dtype is None else out_dtype
+    if out is None:
+        out = torch.empty((rows, cout), dtype=od, device=x.device)
+    if residual is not None:
+        _require_cuda("residual", residual)
+        if residual.shape != (rows, cout) or residual.dtype != od:
+            raise SparseConvError(2, "linear: residual must be [rows, Cout] in the output dtype")
+    epi = _capi.ScConvEpilogue()
+    epi.residual = None if residual is None else residual.data_ptr()
+    epi.layer_norm = int(layer_norm)
+    epi.ln_weight = None if ln_weight is None else ln_weight.data_ptr()
+    epi.ln_bias = None if ln_bias is None else ln_bias.data_ptr()
+    epi.ln_eps = float(ln_eps)
+    epi.silu = int(silu)
+    need = ctypes.c_size_t()
+    c = SparseSubmConvConfig(cin, cout, 1, 1, 1).to_c()
+    check(_capi.load().sc_conv_epilogue_workspace_size(ctypes.byref(c), _dt(x), rows, _dt(out), ctypes.byref(epi),
+                                                       ctypes.byref(need)))
+    if need.value:
+        if workspace is None or workspace.numel() < need.value:
+            workspace = torch.empty(need.value, dtype=torch.uint8, device=x.device)
+        epi.workspace = workspace.data_ptr()
+        epi.workspace_bytes = workspace.numel()
+    check(_capi.load().sc_linear_forward(_dt(x), _ptr(x), rows, cin, cout, _dt(weight), _ptr(weight), _ptr(w_scale),
+                                         _ptr(bias), ctypes.byref(epi), _dt(out), _ptr(out), _stream()))
+    return out
+
+
 def layer_norm(x: torch.Tensor, weight: Optional[torch.Tensor] = None,
                bias: Optional[torch.Tensor] = None, eps: float = 1e-6, silu: bool = False,
                out_dtype: Optional[torch.dtype] = None,

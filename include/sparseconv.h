@@ -223,6 +223,23 @@ int sc_subm_conv_forward_fused(const sc_conv_config *cfg, int act_dtype, const v
 int sc_conv_epilogue_workspace_size(const sc_conv_config *cfg, int act_dtype, int64_t n_q, int out_dtype,
                                     const sc_conv_epilogue *epi, size_t *bytes);
 
+/*
+ * Dense linear layer out = x W^T + b with the conv's epilogue (SiLU,
+ * residual, LayerNorm over the row): linear_forward_wgpu
+ * (sparse_decoder_wgpu_ops.rs:79-160) as used by the ConvNeXt block's MLP
+ * (convnext_block_mlp_forward_wgpu, :356-489: mlp_0 -> SiLU -> mlp_2 + x).
+ * x [rows][in_channels], W [out_channels][in_channels] (the reference's
+ * LinearLayer layout), b [out_channels] f32 or NULL; dtypes as for
+ * sc_subm_conv_forward_fused (bf16 / f16 / f32 activations; int8 weights
+ * with d_w_scale).  It is that conv with a 1x1x1 kernel and no map (row r
+ * reads row r), on the same MFMA tiles.  epi may be NULL; the C2S forms are
+ * refused.
+ */
+int sc_linear_forward(int act_dtype, const void *d_input, int64_t rows, int64_t in_channels,
+                      int64_t out_channels, int w_dtype, const void *d_weight, const float *d_w_scale,
+                      const float *d_bias, const sc_conv_epilogue *epi, int out_dtype, void *d_out,
+                      sc_stream stream);
+
 /* ----------------------------------------------------------- conv plan */
 
 /*
