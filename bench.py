@@ -42,6 +42,8 @@ def parse():
                     help="query rows of the CPU baseline sample (0 = skip)")
     ap.add_argument("--only", choices=["map", "plan", "mapplan", "conv", "ln"], default=None,
                     help="run just this part of the step --steps times (for rocprofv3) and exit")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the config 2 / 4 / 5 component timings")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 1 GiB device-to-device copy (the known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -63,16 +65,30 @@ def events_ms(fn, iters, warmup=0):
     return s.elapsed_time(e) / iters
 
 
-def cpu_baseline(coords, x_f32, w1, w2, sample_rows):
-    """The reference CPU path (burn_flex_gmm flex: build_neighbor_rows with a
-    HashMap, im2col gather + single-thread sgemm) restated in C (oracle/), on
-    the same step: map build over all N coords + two convs, LN+SiLU and the
-    residual add over `sample_rows` query rows.  voxels/s = 1 / (t_map/N +
-    t_rest/sample)."""
+def host_cpu():
+    """(CPU model, cores this process may run on, threads for the all-cores
+    baseline: those cores, capped by OMP_NUM_THREADS when set)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    cores = len(os.sched_getaffinity(0))
+    threads = cores
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = max(1, min(cores, int(os.environ["OMP_NUM_THREADS"])))
+    return model, cores, threads
+
+
+def _config3_cpu_step(O, coords, x_f32, w1, w2, sample_rows, threads):
+    """Seconds for the map over all coords and for the block over the first
+    `sample_rows` query rows, with the flex conv on `threads` threads."""
     import numpy as np
-    from oracle import oracle as O
-    O.build()
-    n = len(coords)
+    O.set_num_threads(threads)
     cfg = O.OracleConfig(128, 128)
     b = np.zeros(128, np.float32)
     t0 = time.perf_counter()
@@ -89,16 +105,140 @@ def cpu_baseline(coords, x_f32, w1, w2, sample_rows):
     y = O.conv_flex_precomputed(cfg, w2, b, h_full, nbr[rows]) + x_f32[rows]
     t_rest = time.perf_counter() - t0
     assert y.shape == (sample_rows, 128)
-    per_voxel = t_map / n + t_rest / sample_rows
+    O.set_num_threads(1)
+    return t_map, t_rest
+
+
+def cpu_baseline(coords, x_f32, w1, w2, sample_rows):
+    """The reference CPU path (burn_flex_gmm flex: build_neighbor_rows with a
+    HashMap, im2col gather + sgemm) restated in C (oracle/), timed on this
+    host: the config-3 step -- map over all N coords, conv1 / LN / SiLU /
+    conv2 / + x over `sample_rows` query rows, voxels/s = 1 / (t_map / N +
+    t_rest / sample) -- on 1 thread (the reference's matrixmultiply is
+    single-threaded: the headline baseline) and on all the host's cores
+    (OpenMP over row blocks); and config 1 (64^3 sphere shell, 14,648
+    voxels, C = 64, f32: map + conv over every row) on both."""
+    import numpy as np
+    from bevy_synth_amd import synth
+    from oracle import oracle as O
+    O.build()
+    model, cores, threads = host_cpu()
+    n = len(coords)
+    t_map1, t_rest1 = _config3_cpu_step(O, coords, x_f32, w1, w2, sample_rows, 1)
+    t_mapn, t_restn = _config3_cpu_step(O, coords, x_f32, w1, w2, sample_rows, threads)
+    # config 1, every row
+    c1 = synth.config1_coords()
+    rng = np.random.default_rng(1)
+    x1 = rng.standard_normal((len(c1), 64)).astype(np.float32)
+    wc1 = (rng.standard_normal((64, 27, 64)) / np.sqrt(27 * 64)).astype(np.float32)
+    cfg1 = O.OracleConfig(64, 64)
+    cfg1_res = {}
+    for t in (1, threads):
+        O.set_num_threads(t)
+        t0 = time.perf_counter()
+        nb1 = O.build_neighbor_rows(cfg1, c1, lowest_row_on_duplicate=False)
+        y1 = O.conv_flex_precomputed(cfg1, wc1, np.zeros(64, np.float32), x1, nb1)
+        dt = time.perf_counter() - t0
+        assert y1.shape == (len(c1), 64)
+        pairs = int((nb1 >= 0).sum())
+        cfg1_res[t] = {"voxels_per_s": len(c1) / dt, "seconds": dt, "useful_gflops": 2.0 * pairs * 64 * 64 / dt / 1e9,
+                       "cores": t}
+    O.set_num_threads(1)
     return {
-        "value": 1.0 / per_voxel,
+        "value": 1.0 / (t_map1 / n + t_rest1 / sample_rows),
         "unit": "voxels/s",
         "cores": 1,
         "kind": "port",
-        "sample": (f"config 3 step: map build over all {n} coords ({t_map:.2f} s) + conv/LN/SiLU/"
-                   f"conv/add over the first {sample_rows} query rows ({t_rest:.2f} s), f32, "
+        "sample": (f"config 3 step: map build over all {n} coords ({t_map1:.2f} s) + conv/LN/SiLU/"
+                   f"conv/add over the first {sample_rows} query rows ({t_rest1:.2f} s), f32, 1 thread, "
                    f"oracle/sc_oracle.c restating crates/burn_flex_gmm/src/lib.rs:69-109,242-375"),
+        "host": {"cpu_model": model, "cores_available": cores},
+        "all_cores": {"value": 1.0 / (t_mapn / n + t_restn / sample_rows), "unit": "voxels/s", "cores": threads,
+                      "sample": f"same step; flex conv on {threads} OpenMP threads over row blocks "
+                                f"(map {t_mapn:.2f} s, block {t_restn:.2f} s)"},
+        "config1": {"voxels": len(c1), "one_thread": cfg1_res[1], "all_cores": cfg1_res[threads],
+                    "sample": "config 1 (64^3 sphere shell r=24, C=64, f32): map + flex conv over every row"},
     }
+
+
+def config_components(dev, steps: int = 5):
+    """The other BASELINE configs on this GPU, for the record (parity cases,
+    not the headline): config 2's planned 3x3x3 conv (C = 256, bf16), config
+    4's 2x2x2 transposed upsample (a 1x1x1 conv with the child scatter) then
+    the children's map + plan + 3x3x3 conv (C = 256), and config 5's int8
+    decoder stack (3 stages of 2 residual blocks + fused C2S upsample,
+    512 -> 64 channels).  ms per call, after one untimed call."""
+    import numpy as np
+    import torch
+
+    from bevy_synth_amd import decoder as D
+    from bevy_synth_amd import flex_gmm as F
+    from bevy_synth_amd import synth
+
+    def bf(a):
+        return torch.from_numpy(synth.bf16_bits(a).view(np.int16)).to(dev).view(torch.bfloat16)
+
+    def wall_ms(fn, n):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / n
+
+    out = {}
+    rng = np.random.default_rng(7)
+    # config 2
+    c2 = synth.config2_coords()
+    C = 256
+    cfg = F.SparseSubmConvConfig(C, C)
+    nb = D.Neighborhood.build(cfg, torch.from_numpy(c2).to(dev))
+    layer = D.ConvLayer(cfg, bf(synth.conv_weight(rng, C, 27, C, 1 / np.sqrt(27 * C))),
+                        torch.zeros(C, dtype=torch.float32, device=dev))
+    x2 = bf(synth.normal_f32(rng, (len(c2), C)))
+    P2 = int((nb.nbr >= 0).sum().item())
+    ms = events_ms(lambda: layer(x2, nb), steps, 2)
+    out["config2"] = {"voxels": len(c2), "pairs": P2, "conv_ms": ms,
+                      "conv_useful_tflops": 2.0 * P2 * C * C / (ms * 1e-3) / 1e12,
+                      "map_plus_plan_ms": wall_ms(lambda: D.Neighborhood.build(cfg, nb.coords), steps)}
+    # config 4
+    g = synth.ShellCubeGeometry()
+    parents = g.coords()
+    mask = torch.from_numpy(synth.subdivision_mask_near_surface(parents, g)).to(dev)
+    pc = torch.from_numpy(parents).to(dev)
+    cin, cout = 512, 256
+    tl = D.ConvLayer(F.SparseSubmConvConfig(cin, 8 * cout, 1, 1, 1),
+                     bf(synth.normal_f32(rng, (8 * cout, 1, cin), 1 / np.sqrt(8 * cin))),
+                     torch.zeros(8 * cout, dtype=torch.float32, device=dev))
+    xp = bf(synth.normal_f32(rng, (len(parents), cin)))
+    ccfg = F.SparseSubmConvConfig(cout, cout)
+    cl = D.ConvLayer(ccfg, bf(synth.conv_weight(rng, cout, 27, cout, 1 / np.sqrt(27 * cout))),
+                     torch.zeros(cout, dtype=torch.float32, device=dev))
+    cc, feats, _ = D.transposed_upsample(pc, xp, tl, mask)
+    cnb = D.Neighborhood.build(ccfg, cc)
+    P4 = int((cnb.nbr >= 0).sum().item())
+    t_up = wall_ms(lambda: D.transposed_upsample(pc, xp, tl, mask), steps)
+    t_conv = events_ms(lambda: cl(feats, cnb), steps, 2)
+    out["config4"] = {"parents": len(parents), "children": int(cc.shape[0]), "child_pairs": P4,
+                      "transposed_upsample_ms": t_up,
+                      "child_map_plus_plan_ms": wall_ms(lambda: D.Neighborhood.build(ccfg, cc), steps),
+                      "conv_ms": t_conv, "conv_useful_tflops": 2.0 * P4 * cout * cout / (t_conv * 1e-3) / 1e12}
+    # config 5
+    coords5, masks = synth.config5_stack_inputs()
+    stack = D.int8_stack([512, 256, 128, 64], 2, seed=5, device=dev)
+    x5 = bf(synth.normal_f32(rng, (len(coords5), 512)))
+    c5 = torch.from_numpy(coords5).to(dev)
+    m5 = [torch.from_numpy(m).to(dev) for m in masks]
+    res = {}
+
+    def run5():
+        res["nb"], res["y"] = stack(c5, x5, m5)
+    t5 = wall_ms(run5, max(2, steps // 2))
+    out["config5"] = {"start_voxels": len(coords5), "end_voxels": int(res["y"].shape[0]), "stack_ms": t5,
+                      "note": "18 convs (int8 weights, bf16 activations), 4 maps + plans, fused C2S upsamples; "
+                              "includes the host syncs of the child counts"}
+    return out
 
 
 class Config3Step:
@@ -249,12 +389,19 @@ def main():
     conv_tflops = flops / (ms_conv * 1e-3) / 1e12
     map_bytes = n * 16 + n * 27 * 4
     map_gbps = map_bytes / (ms_map * 1e-3) / 1e9
-    traffic = None
+    traffic, traffic_source = None, None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get("conv_halo_kernel/config3", None)
+            tj = json.load(f)
+            traffic = tj.get("conv_halo_kernel/config3", None)
+            traffic_source = tj.get("source", None)
 
+    configs = None
+    if not args.no_configs:
+        print("[bench] configs 2 / 4 / 5 ...", file=sys.stderr, flush=True)
+        configs = config_components(dev)
+        print(f"[bench] configs: {json.dumps(configs)}", file=sys.stderr, flush=True)
     cpu = None
     if args.cpu_sample > 0:
         print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
@@ -279,7 +426,8 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "kernel": "conv_halo_kernel<bf16,bf16>",
                      "achieved": conv_tflops, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": conv_tflops / PEAK_BF16_TFLOPS, "traffic": traffic},
+                     "frac": conv_tflops / PEAK_BF16_TFLOPS, "traffic": traffic,
+                     "traffic_source": f"profile-time figure, not measured in this run: {traffic_source}"},
         "components": {
             "map_and_plan_ms": ms_map_plan, "map_build_ms": ms_map, "plan_build_ms": ms_plan,
             "conv_ms": ms_conv,
@@ -290,6 +438,7 @@ def main():
             "conv_issued_tflops_dense27": 2.0 * n * 27 * C * C / (ms_conv * 1e-3) / 1e12,
         },
         "cpu_baseline": cpu,
+        "configs": configs,
     }
     print(json.dumps(line), flush=True)
 

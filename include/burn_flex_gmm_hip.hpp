@@ -111,7 +111,7 @@ inline Result<size_t> kernel_rows(const SparseSubmConvConfig &config)
     return Result<size_t>::ok((size_t)k);
 }
 
-enum class DType { F32, BF16, I8, I32, U8 };
+enum class DType { F32, BF16, I8, I32, U8, F16 };
 
 inline size_t dtype_bytes(DType d)
 {
@@ -121,6 +121,7 @@ inline size_t dtype_bytes(DType d)
     case DType::I8: return 1;
     case DType::I32: return 4;
     case DType::U8: return 1;
+    case DType::F16: return 2;
     }
     return 0;
 }
@@ -131,6 +132,7 @@ inline int to_sc_dtype(DType d)
     case DType::F32: return SC_DTYPE_F32;
     case DType::BF16: return SC_DTYPE_BF16;
     case DType::I8: return SC_DTYPE_I8;
+    case DType::F16: return SC_DTYPE_F16;
     default: return -1;
     }
 }

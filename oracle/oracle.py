@@ -109,6 +109,7 @@ def lib():
         L.orc_conv_ref_f64.argtypes = [cfgp, P, P, P, P, i64, P, i64, P]
         L.orc_bf16_round.argtypes = [P, P, i64]
         L.orc_f16_round.argtypes = [P, P, i64]
+        L.orc_set_num_threads.argtypes = [ctypes.c_int]
         L.orc_layer_norm.argtypes = [P, i64, i64, P, P, ctypes.c_float]
         L.orc_silu.argtypes = [P, i64]
         L.orc_subdivision_active.argtypes = [P, i64, P, P]
@@ -190,6 +191,13 @@ def pack_flex_weight(cfg: OracleConfig, weight: np.ndarray) -> np.ndarray:
                    * cc.out_channels_per_group, dtype=np.float32)
     _check(lib().orc_pack_flex_weight(ctypes.byref(cc), _p(w), _p(out)), "pack")
     return out
+
+
+def set_num_threads(n: int) -> None:
+    """Threads of conv_flex_precomputed's gather and sgemm (1 = the reference's
+    single-threaded matrixmultiply; more = the all-cores CPU baseline).
+    Results do not depend on it."""
+    lib().orc_set_num_threads(int(n))
 
 
 def conv_flex_precomputed(cfg: OracleConfig, weight, bias, inp, nbr,

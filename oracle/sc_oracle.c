@@ -283,16 +283,28 @@ int orc_pack_flex_weight(const orc_cfg *c, const float *w, float *packed)
     return ORC_OK;
 }
 
-/* C[m,n] += A[m,k] @ B[k,n], row-major, single thread.  Stands in for the
+/* Threads of the flex conv's gather and sgemm (1: the reference's
+ * single-threaded matrixmultiply; more: the all-cores CPU baseline, OpenMP
+ * over 64-row blocks).  Each row is computed by one thread in the same
+ * operation order, so results do not depend on the thread count. */
+static int g_orc_threads = 1;
+
+void orc_set_num_threads(int n) { g_orc_threads = n > 0 ? n : 1; }
+
+/* C[m,n] += A[m,k] @ B[k,n], row-major.  Stands in for the
  * matrixmultiply::sgemm call at crates/burn_flex_gmm/src/lib.rs:354-371
  * (alpha=1, beta=1: the product is formed, then added to C). */
 static void orc_sgemm_acc(int64_t m, int64_t k, int64_t n, const float *A, int64_t lda,
                           const float *B, int64_t ldb, float *C, int64_t ldc)
 {
     const int64_t MB = 64, KB = 256;
-    float *acc = (float *)malloc(sizeof(float) * (size_t)(MB * n));
-    for (int64_t i0 = 0; i0 < m; i0 += MB) {
+    const int64_t nblk = (m + MB - 1) / MB;
+#pragma omp parallel for num_threads(g_orc_threads) schedule(static) if (g_orc_threads > 1)
+    for (int64_t bi = 0; bi < nblk; ++bi) {
+        const int64_t i0 = bi * MB;
         int64_t i1 = i0 + MB < m ? i0 + MB : m;
+        float *acc = (float *)malloc(sizeof(float) * (size_t)(MB * n));
+        if (!acc) continue; /* cannot happen at the sizes used; leaves C unchanged */
         memset(acc, 0, sizeof(float) * (size_t)((i1 - i0) * n));
         for (int64_t p0 = 0; p0 < k; p0 += KB) {
             int64_t p1 = p0 + KB < k ? p0 + KB : k;
@@ -308,8 +320,8 @@ static void orc_sgemm_acc(int64_t m, int64_t k, int64_t n, const float *A, int64
         }
         for (int64_t i = i0; i < i1; ++i)
             for (int64_t j = 0; j < n; ++j) C[i * ldc + j] += acc[(i - i0) * n + j];
+        free(acc);
     }
-    free(acc);
 }
 
 /*
@@ -346,17 +358,20 @@ int orc_conv_flex_precomputed(const orc_cfg *c, const float *w, const float *bia
     int rc = ORC_OK;
     for (int64_t g = 0; g < c->groups && rc == ORC_OK; ++g) {
         memset(g_buf, 0, sizeof(float) * (size_t)(n_q * kin));
-        for (int64_t r = 0; r < n_q && rc == ORC_OK; ++r)
+        int bad = 0;
+#pragma omp parallel for num_threads(g_orc_threads) schedule(static) reduction(| : bad) if (g_orc_threads > 1)
+        for (int64_t r = 0; r < n_q; ++r)
             for (int64_t k = 0; k < K; ++k) {
                 int32_t s = nbr[r * K + k];
                 if (s == ORC_INVALID_NEIGHBOR) continue;
                 if (s < 0 || s >= n_in) {
-                    rc = ORC_ERR_INDEX;
-                    break;
+                    bad = 1;
+                    continue;
                 }
                 memcpy(&g_buf[r * kin + k * cin], &input[(int64_t)s * C_in + g * cin],
                        sizeof(float) * (size_t)cin);
             }
+        if (bad) rc = ORC_ERR_INDEX;
         if (rc == ORC_OK)
             orc_sgemm_acc(n_q, kin, n, g_buf, kin, &packed[g * kin * n], n, &out[g * n], C_out);
     }

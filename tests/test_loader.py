@@ -1,0 +1,153 @@
+"""The safetensors loader of the decoder's layers (include/sparse_decoder_loading.hpp,
+after sparse_decoder_loading.rs:1-310), driven by tests/cpp/test_loader.cpp on
+a file this test writes: f32 / f16 / bf16 payloads, conv weights
+[Cout, KD, KH, KW, Cin_g], grouped channels, a linear layer, and the
+reference's refusals (rank, dtype, channel mismatches, missing tensors).
+
+The host part (decoding, f16 rounding, error messages) runs without a GPU;
+the device part checks the uploaded weights bit for bit (bf16 with the
+reference's round-to-nearest-even, f16 as stored) and the packed copy
+against the planned conv's fragment layout."""
+import json
+import os
+import struct
+import subprocess
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+BIN = os.path.join(ROOT, "tests", "cpp", "test_loader")
+
+
+def _bf16_bits(a):
+    """Truncated bf16 bits (the payload a bf16 safetensors file holds)."""
+    return (np.asarray(a, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def write_safetensors(path, tensors):
+    """tensors: name -> (dtype string, shape, raw bytes)."""
+    header, blobs, off = {"__metadata__": {"format": "pt", "note": 'a "quoted" value'}}, [], 0
+    for name, (dt, shape, raw) in tensors.items():
+        header[name] = {"dtype": dt, "shape": list(shape), "data_offsets": [off, off + len(raw)]}
+        blobs.append(raw)
+        off += len(raw)
+    h = json.dumps(header).encode()
+    h += b" " * (-len(h) % 8)
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(h)))
+        f.write(h)
+        for b in blobs:
+            f.write(b)
+
+
+def make_file(path):
+    rng = np.random.default_rng(7)
+    w32 = rng.standard_normal((64, 3, 3, 3, 32)).astype(np.float32) * 0.2
+    w16 = (rng.standard_normal((64, 3, 3, 3, 32)) * 0.2).astype(np.float16)
+    wbf = _bf16_bits(rng.standard_normal((64, 3, 3, 3, 32)) * 0.2)
+    wg = rng.standard_normal((64, 3, 3, 3, 32)).astype(np.float32)     # Cin_g 32, expected_in 64 -> 2 groups
+    lin = _bf16_bits(rng.standard_normal((16, 32)))
+    edge = np.array([0.0, -0.0, 65504, 6.1e-5, 5.96e-8, 1.0 / 3, np.inf], np.float16)
+    T = {
+        "conv_f32.weight": ("F32", w32.shape, w32.tobytes()),
+        "conv_f32.bias": ("F32", (64,), rng.standard_normal(64).astype(np.float32).tobytes()),
+        "conv_f16.weight": ("F16", w16.shape, w16.tobytes()),
+        "conv_f16.bias": ("F16", (64,), rng.standard_normal(64).astype(np.float16).tobytes()),
+        "conv_bf16.weight": ("BF16", wbf.shape, wbf.tobytes()),
+        "conv_bf16.bias": ("BF16", (64,), _bf16_bits(rng.standard_normal(64)).tobytes()),
+        "grouped.weight": ("F32", wg.shape, wg.tobytes()),
+        "grouped.bias": ("F32", (64,), np.zeros(64, np.float32).tobytes()),
+        "bad_rank.weight": ("F32", (64, 32), np.zeros((64, 32), np.float32).tobytes()),
+        "bad_rank.bias": ("F32", (64,), np.zeros(64, np.float32).tobytes()),
+        "bias_len.weight": ("F32", (8, 1, 1, 1, 32), np.zeros((8, 32), np.float32).tobytes()),
+        "bias_len.bias": ("F32", (9,), np.zeros(9, np.float32).tobytes()),
+        "bad_dtype.weight": ("I32", (4,), np.arange(4, dtype=np.int32).tobytes()),
+        "lin.weight": ("BF16", (16, 32), lin.tobytes()),
+        "lin.bias": ("F32", (16,), rng.standard_normal(16).astype(np.float32).tobytes()),
+        "edge_f16": ("F16", edge.shape, edge.tobytes()),
+    }
+    write_safetensors(path, T)
+    return {"w32": w32, "w16": w16, "wbf": wbf, "wg": wg, "lin": lin, "edge": edge, "T": T}
+
+
+def _run(mode, tmp_path):
+    if not os.path.exists(BIN):
+        pytest.skip("tests/cpp/test_loader is built by __graft_entry__.build()")
+    f = tmp_path / "layers.safetensors"
+    ref = make_file(str(f))
+    r = subprocess.run([BIN, mode, str(f), str(tmp_path)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    errs = dict(line.split(": ", 1) for line in (tmp_path / "errors.txt").read_text().splitlines())
+    return ref, errs
+
+
+def _f32(tmp_path, name):
+    return np.fromfile(str(tmp_path / name), dtype=np.float32)
+
+
+def test_loader_host_decode(tmp_path, oracle):
+    ref, errs = _run("host", tmp_path)
+    assert np.array_equal(_f32(tmp_path, "conv_f32.weight.f32"), ref["w32"].ravel())
+    assert np.array_equal(_f32(tmp_path, "conv_f16.weight.f32"), ref["w16"].astype(np.float32).ravel())
+    bf = (ref["wbf"].astype(np.uint32) << 16).view(np.float32)
+    assert np.array_equal(_f32(tmp_path, "conv_bf16.weight.f32"), bf.ravel())
+    got_edge = _f32(tmp_path, "edge_f16.f32")
+    assert np.array_equal(got_edge.view(np.uint32), ref["edge"].astype(np.float32).view(np.uint32))
+    # round_vec_to_f16 (the compute_fp16 copies) == the oracle's f16 rounding == numpy's
+    r16 = _f32(tmp_path, "round_f16.f32")
+    assert np.array_equal(r16.view(np.uint32), oracle.f16_round(ref["w32"]).ravel().view(np.uint32))
+    assert errs["bad_dtype.weight"] == "tensor 'bad_dtype.weight' has unsupported dtype I32; expected f32/f16/bf16"
+    assert errs["missing.weight"] == "missing tensor 'missing.weight' in safetensors"
+    assert errs["vector_len"] == "tensor 'conv_f32.bias' expected len=63, got len=64"
+
+
+def _pack_reference(w_bits, groups, cout_g, cin_g, K):
+    """The planned conv's fragment layout (sc_conv_weight_pack): per (group,
+    128-channel tile, offset, 32-channel chunk, 16-channel block) 64 lanes x 8
+    values, lane (l16, q4) = w[16 jj + l16, k, 32 c + 8 q4 ..], zeros past Cout_g."""
+    n_ot, nkc = (cout_g + 127) // 128, cin_g // 32
+    w = w_bits.reshape(groups * cout_g, K, cin_g)
+    out = np.zeros((groups, n_ot, K, nkc, 8, 64, 8), np.uint16)
+    for g in range(groups):
+        for ot in range(n_ot):
+            for jj in range(8):
+                for lane in range(64):
+                    o = ot * 128 + 16 * jj + (lane & 15)
+                    if o >= cout_g:
+                        continue
+                    for c in range(nkc):
+                        i0 = 32 * c + 8 * (lane >> 4)
+                        out[g, ot, :, c, jj, lane, :] = w[g * cout_g + o, :, i0:i0 + 8]
+    return out.ravel()
+
+
+@pytest.mark.gpu
+def test_loader_device_layers(tmp_path, oracle):
+    ref, errs = _run("device", tmp_path)
+    cfg = {l.split()[0]: list(map(int, l.split()[1:])) for l in (tmp_path / "config.txt").read_text().splitlines()}
+    # (Cin, Cout, KD, KH, KW, Cin_g, Cout_g, groups, packed)
+    assert cfg["0_conv_f32"] == [32, 64, 3, 3, 3, 32, 64, 1, 1]
+    assert cfg["3_conv_f32"] == [32, 64, 3, 3, 3, 32, 64, 1, 0]          # f32 compute: no packing
+    assert cfg["4_grouped"] == [64, 64, 3, 3, 3, 32, 32, 2, 1]
+    bits = lambda name: np.fromfile(str(tmp_path / name), dtype=np.uint16)
+    # bf16 compute from f32: the reference's round-to-nearest-even
+    w0 = (oracle.bf16_round(ref["w32"]).view(np.uint32) >> 16).astype(np.uint16).ravel()
+    assert np.array_equal(bits("0_conv_f32.weight.bin"), w0)
+    assert np.array_equal(bits("0_conv_f32.packed.bin")[128:], _pack_reference(w0, 1, 64, 32, 27))
+    # f16 compute from an f16 file: the stored bits
+    w1 = ref["w16"].view(np.uint16).ravel()
+    assert np.array_equal(bits("1_conv_f16.weight.bin"), w1)
+    assert np.array_equal(bits("1_conv_f16.packed.bin")[128:], _pack_reference(w1, 1, 64, 32, 27))
+    assert np.array_equal(bits("2_conv_bf16.weight.bin"), ref["wbf"].ravel())
+    assert np.array_equal(np.fromfile(str(tmp_path / "3_conv_f32.weight.bin"), np.float32), ref["w32"].ravel())
+    wg = (oracle.bf16_round(ref["wg"]).view(np.uint32) >> 16).astype(np.uint16).ravel()
+    assert np.array_equal(bits("4_grouped.packed.bin")[128:], _pack_reference(wg, 2, 32, 32, 27))
+    lin_f32 = (ref["lin"].astype(np.uint32) << 16).view(np.float32)       # the file's bf16 values
+    assert np.array_equal(bits("lin.weight.bin"), lin_f32.astype(np.float16).view(np.uint16).ravel())
+    # the reference's refusals, same messages
+    assert errs["5_bad_rank"] == "tensor 'bad_rank.weight' expected rank=5, got rank=2"
+    assert errs["6_conv_f32"] == "tensor 'conv_f32.weight' expected_in=48 is incompatible with in_per_group=32"
+    assert errs["7_conv_f32"] == "tensor 'conv_f32.weight' expected out_channels=65, got 64"
+    assert errs["8_bias_len"] == "tensor 'bias_len.bias' expected shape=[8]"
+    assert errs["lin_bad"] == "tensor 'lin.weight' expected in_channels=31, got 32"
