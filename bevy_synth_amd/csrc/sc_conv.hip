@@ -181,6 +181,14 @@ static int conv_forward_impl(const sc_conv_config *cfg, int act_dtype, const voi
     a.skip_parent_ch = c2s.skip ? epi->skip_parent_channels : 0;
     a.skip_S = (int)c2s.skip_S;
     a.skip_R = (int)c2s.skip_R;
+    auto log2_or_neg = [](int64_t v) {
+        if (v <= 0 || (v & (v - 1)) != 0) return -1;
+        int sh = 0;
+        while (((int64_t)1 << sh) < v) ++sh;
+        return sh;
+    };
+    a.scatter_shift = log2_or_neg(c2s.scatter_ch);
+    a.skip_shift = log2_or_neg(c2s.skip_R);
     if (c2s.scatter) a.ln_group = a.scatter_ch;
 
     const size_t asz = dtype_size(act_dtype);

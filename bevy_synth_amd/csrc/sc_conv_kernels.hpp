@@ -75,6 +75,8 @@ struct ConvArgs {
     int64_t skip_parent_ch;
     int skip_S;
     int skip_R;
+    int scatter_shift;  // log2(scatter_ch), or -1 when not a power of two
+    int skip_shift;     // log2(skip_R), or -1 when not a power of two
 };
 
 // Header of a packed weight buffer (its first 256 bytes): the shape the
@@ -244,39 +246,60 @@ __device__ inline f32x4 mfma_16x16x32(const uint4 &a, const uint4 &b, const f32x
                                                        c, 0, 0, 0);
 }
 
-// Epilogue store of channels [col, col + nv) (nv <= 4, col within the
-// output row) of query row qrow, whose values after bias / LayerNorm / SiLU
-// are v: adds the C2S skip or the residual, and writes to the child row the
-// scatter names (or to row qrow).  The C2S forms go through here; the plain
-// forms keep their own (prefetching) stores.
+// C2S epilogue stores (child scatter of conv1, parent skip of conv2).  Per
+// output row, c2s_row reads the row's linear index once and keeps the parent
+// slice it adds; c2s_store4 then writes channels [col, col + nv) (nv <= 4,
+// col a multiple of 4 within the output row whenever nv == 4) with 32-bit
+// index arithmetic and shifts for the power-of-two child widths and repeat
+// factors of the decoder.
+struct C2SRow {
+    const void *skip_row;  // parent slice added to this row, or NULL
+};
+
 template <typename TO>
-__device__ inline void store_general(const ConvArgs &a, int64_t qrow, int64_t col, int nv, const float *v, bool vec)
+__device__ inline C2SRow c2s_row(const ConvArgs &a, int64_t qrow)
+{
+    C2SRow c{nullptr};
+    if (a.skip_idx) {
+        const int32_t li = a.skip_idx[qrow];
+        if (li >= 0 && (int64_t)li < a.skip_parent_rows * 8)
+            c.skip_row = static_cast<const TO *>(a.skip_parent) + (int64_t)(li >> 3) * a.skip_parent_ch +
+                         (int64_t)(li & 7) * a.skip_S;
+    }
+    return c;
+}
+
+// kSharedSkip: the one-load form of repeat factors >= 4 (left out of the
+// LayerNorm kernels, whose register budget it exceeds; the decoder's parent
+// skip follows a conv without LayerNorm).
+template <typename TO, bool kSharedSkip = true>
+__device__ inline void c2s_store4(const ConvArgs &a, const C2SRow &c, int64_t qrow, int col, int nv, const float *v,
+                                  bool vec)
 {
     TO *out = static_cast<TO *>(a.out);
     int64_t base;
     if (a.scatter_rows) {
-        const int64_t c = col / a.scatter_ch;
-        const int32_t r = a.scatter_rows[qrow * 8 + c];
+        const int ch = a.scatter_shift >= 0 ? col >> a.scatter_shift : col / a.scatter_ch;
+        const int32_t r = a.scatter_rows[qrow * 8 + ch];
         if (r < 0 || r >= a.scatter_n) return;
-        base = (int64_t)r * a.scatter_ch + (col - c * a.scatter_ch);
+        base = (int64_t)r * a.scatter_ch + (col - ch * a.scatter_ch);
     } else {
         base = qrow * a.cout + col;
     }
     float t[4] = {v[0], nv > 1 ? v[1] : 0.f, nv > 2 ? v[2] : 0.f, nv > 3 ? v[3] : 0.f};
-    if (a.skip_idx) {
-        const int32_t li = a.skip_idx[qrow];
-        if (li >= 0 && li < a.skip_parent_rows * 8) {
-            const TO *pp = static_cast<const TO *>(a.skip_parent) + (int64_t)(li >> 3) * a.skip_parent_ch +
-                           (int64_t)(li & 7) * a.skip_S;
+    if (c.skip_row) {
+        const TO *pp = static_cast<const TO *>(c.skip_row);
+        if (kSharedSkip && nv == 4 && a.skip_shift >= 2) {
+            // repeat factor >= 4: the 4 channels (col % 4 == 0) add one parent value
+            const float sv = load_as_f32<TO>(pp, col >> a.skip_shift);
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) t[cc] += sv;
+        } else {
 #pragma unroll
             for (int cc = 0; cc < 4; ++cc)
-                if (cc < nv) t[cc] += load_as_f32<TO>(pp, (col + cc) / a.skip_R);
+                if (cc < nv)
+                    t[cc] += load_as_f32<TO>(pp, a.skip_shift >= 0 ? (col + cc) >> a.skip_shift : (col + cc) / a.skip_R);
         }
-    } else if (a.residual) {
-        const TO *res = static_cast<const TO *>(a.residual);
-#pragma unroll
-        for (int cc = 0; cc < 4; ++cc)
-            if (cc < nv) t[cc] += load_as_f32<TO>(res, qrow * a.cout + col + cc);
     }
     if (vec && nv == 4) {
         *reinterpret_cast<typename Out4<TO>::V *>(out + base) = Out4<TO>::pack(t);
@@ -599,7 +622,8 @@ __global__ __launch_bounds__(kThreads, 2) void conv_mfma_kernel(ConvArgs args)
                     float v[4];
 #pragma unroll
                     for (int c = 0; c < 4; ++c) v[c] = acc[i][j][4 * e4 + c];
-                    store_general<TO>(args, row0 + r, out_col0 + oc, min(4, args.cout_g - oc), v, vec_ok);
+                    c2s_store4<TO>(args, c2s_row<TO>(args, row0 + r), row0 + r, (int)(out_col0 + oc),
+                                   min(4, args.cout_g - oc), v, vec_ok);
                 }
             continue;
         }
@@ -1044,12 +1068,14 @@ __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
                     acc[i][j][e] = silu_f32(t);
                 }
         }
+        const C2SRow crow = c2s ? c2s_row<TO>(args, qrow) : C2SRow{nullptr};
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int oc = o0 + j * 16 + 4 * q4;
             float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
             if (c2s) {
-                if (oc < args.cout_g) store_general<TO>(args, qrow, out_col0 + oc, min(4, args.cout_g - oc), v, vec_ok);
+                if (oc < args.cout_g)
+                    c2s_store4<TO>(args, crow, qrow, (int)(out_col0 + oc), min(4, args.cout_g - oc), v, vec_ok);
                 continue;
             }
             if (vec_ok && oc + 3 < args.cout_g) {
@@ -1437,6 +1463,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
 #pragma unroll
         for (int i = 0; i < kI; ++i) {
             if (qrow[i] < 0) continue;
+            const C2SRow crow = c2s_row<TO>(args, qrow[i]);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int oc = oc0 + j * 16 + 4 * q4;
@@ -1446,8 +1473,11 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
 #pragma unroll
                     for (int cc = 0; cc < 4; ++cc) v[cc] = silu_f32(v[cc]);
                 }
-                store_general<TO>(args, qrow[i], out_col0 + oc, min(4, args.cout_g - oc), v, vec_ok);
+                c2s_store4<TO, !kLN>(args, crow, qrow[i], (int)(out_col0 + oc), min(4, args.cout_g - oc), v, vec_ok);
             }
+            // one row block at a time: loads hoisted across blocks would
+            // hold their registers beside the whole accumulator
+            __builtin_amdgcn_sched_barrier(0);
         }
         return;
     }
@@ -1597,7 +1627,7 @@ __global__ __launch_bounds__(256) void conv_scalar_kernel(ConvArgs args)
         if (args.silu) v = silu_f32(v);
         if (args.scatter_rows || args.skip_idx) {
             const float v4[4] = {v, 0.f, 0.f, 0.f};
-            store_general<TO>(args, r, o, 1, v4, false);
+            c2s_store4<TO>(args, c2s_row<TO>(args, r), r, (int)o, 1, v4, false);
             continue;
         }
         if (res) v += load_as_f32<TO>(res, e);
