@@ -167,7 +167,8 @@ def config_components(dev, steps: int = 5):
     4's 2x2x2 transposed upsample (a 1x1x1 conv with the child scatter) then
     the children's map + plan + 3x3x3 conv (C = 256), and config 5's int8
     decoder stack (3 stages of 2 residual blocks + fused C2S upsample,
-    512 -> 64 channels).  ms per call, after one untimed call."""
+    512 -> 64 channels), and the neighbour map in its dense-grid and hash
+    table modes.  ms per call, after one untimed call."""
     import numpy as np
     import torch
 
@@ -238,6 +239,29 @@ def config_components(dev, steps: int = 5):
     out["config5"] = {"start_voxels": len(coords5), "end_voxels": int(res["y"].shape[0]), "stack_ms": t5,
                       "note": "18 convs (int8 weights, bf16 activations), 4 maps + plans, fused C2S upsamples; "
                               "includes the host syncs of the child counts"}
+    del stack, res, x5
+
+    # The neighbour map in its other table modes: config 3's coords shuffled
+    # (unsorted rows: the dense grid) and config 5's last C2S child set
+    # (parent-major order over a sparse 512^3 box: the hash table).
+    def map_mode(coords_np, what):
+        cd = torch.from_numpy(np.ascontiguousarray(coords_np)).to(dev)
+        n = len(coords_np)
+        mcfg = F.SparseSubmConvConfig(64, 64)
+        nbr = torch.empty((n, 27), dtype=torch.int32, device=dev)
+        ws = F.NeighborMapWorkspace(dev).get(n)
+        ms = events_ms(lambda: F.neighbor_map_build_into(mcfg, cd, nbr, ws), steps, 2)
+        F.neighbor_map_check(ws)
+        gbps = (n * 16 + n * 27 * 4) / (ms * 1e-3) / 1e9
+        return {"coords": what, "voxels": n, "table": F.neighbor_map_table_mode(ws), "map_build_ms": ms,
+                "gbps": gbps, "frac_hbm": gbps / PEAK_HBM_GBPS}
+    c3 = synth.config3_coords()
+    shuffled = c3[np.random.default_rng(11).permutation(len(c3))]
+    children = coords5
+    for m in masks:
+        children = synth.child_expand(children, m)
+    out["map_modes"] = {"config3_shuffled": map_mode(shuffled, "config 3 coords in a random row order"),
+                        "config5_children": map_mode(children, "config 5's last child set (C2S order)")}
     return out
 
 

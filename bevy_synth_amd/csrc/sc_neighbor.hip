@@ -82,11 +82,14 @@ __device__ inline Plan make_plan(const NbrHeader *h, Limits lim)
 {
     Plan p;
     p.mode = 0;
+    p.levels = 0;
     p.total = 0;
     for (int j = 0; j < 4; ++j) {
         p.lo[j] = h->bmin[j];
         p.hi[j] = h->bmax[j];
         p.ext[j] = (uint64_t)((int64_t)h->bmax[j] - (int64_t)h->bmin[j] + 1);
+        p.rlo[j] = p.lo[j];
+        p.rext[j] = p.ext[j];
     }
     if (h->status & kStatusNegative) return p;
     uint64_t total = 1;
@@ -96,12 +99,38 @@ __device__ inline Plan make_plan(const NbrHeader *h, Limits lim)
         total *= p.ext[j];
     }
     p.total = total;
-    if (ovf)
+    if (ovf) {
         p.mode = 3;
-    else if (h->unsorted == 0 && total <= lim.bitmap_cells)
+        return p;
+    }
+    if (!(h->unsorted & 1u) && total <= lim.bitmap_cells) {
         p.mode = 5;
-    else
-        p.mode = total <= lim.dense_cells ? 4 : (total <= 0xffffffffull ? 1 : 2);
+        return p;
+    }
+    // Rows in C2S order below a sorted root set: the rank bitmap over the
+    // fewest octree levels whose key they follow (coords are non-negative
+    // here, so >> is the parent index).
+    for (int L = 1; L < kRankLevels; ++L) {
+        if ((h->unsorted >> L) & 1u) continue;
+        uint64_t t = p.ext[0];
+        uint64_t re[4] = {p.ext[0], 0, 0, 0};
+        int32_t rl[4] = {p.lo[0], 0, 0, 0};
+        for (int j = 1; j < 4; ++j) {
+            rl[j] = p.lo[j] >> L;
+            re[j] = (uint64_t)((p.hi[j] >> L) - rl[j] + 1);
+            t = t * re[j];  // <= ext product, no overflow
+        }
+        if (t > (lim.bitmap_cells >> (3 * L))) continue;
+        p.mode = 5;
+        p.levels = L;
+        p.total = t << (3 * L);
+        for (int j = 0; j < 4; ++j) {
+            p.rlo[j] = rl[j];
+            p.rext[j] = re[j];
+        }
+        return p;
+    }
+    p.mode = total <= lim.dense_cells ? 4 : (total <= 0xffffffffull ? 1 : 2);
     return p;
 }
 
@@ -139,15 +168,21 @@ __device__ inline int32_t rank_lookup(const uint64_t *__restrict__ words, uint64
     return (int32_t)(uint32_t)(w >> 32) + __builtin_popcount(bits & ((1u << b) - 1u));
 }
 
-__device__ inline bool coord_less(const int4 a, const int4 b)
+__device__ inline uint32_t wave_or_u32(uint32_t v)
 {
-    if (a.x != b.x) return a.x < b.x;
-    if (a.y != b.y) return a.y < b.y;
-    if (a.z != b.z) return a.z < b.z;
-    return a.w < b.w;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v |= __shfl_xor(v, off, 64);
+    return v;
 }
 
-// Per-block bbox partials (4 min, 4 max, negative flag, order flag), no atomics;
+// Combines entry j of two bbox partials: min of the lower corner, max of the
+// upper corner and of the negative flag, OR of the order bits.
+__device__ inline int reduce_partial(int j, int a, int b)
+{
+    return j < 4 ? min(a, b) : (j < 9 ? max(a, b) : (a | b));
+}
+
+// Per-block bbox partials (4 min, 4 max, negative flag, order bits), no atomics;
 // at most 256 blocks of 1024 threads, so that every block of the next launch
 // can reduce the partials.
 constexpr int kBboxBlocks = 256;
@@ -186,7 +221,7 @@ __global__ __launch_bounds__(kBboxThreads) void nm_bbox_partial_kernel(const int
                     mx[j] = max(mx[j], v[j]);
                     neg |= v[j] < 0;
                 }
-                if (i > 0) uns |= !coord_less(prev, cu);
+                if (i > 0) uns |= (int)unsorted_levels(prev, cu);
             }
         }
     }
@@ -197,7 +232,7 @@ __global__ __launch_bounds__(kBboxThreads) void nm_bbox_partial_kernel(const int
         mx[j] = wave_max_i32(mx[j]);
     }
     neg = wave_max_i32(neg);
-    uns = wave_max_i32(uns);
+    uns = (int)wave_or_u32((uint32_t)uns);
     if (lane == 0) {
         for (int j = 0; j < 4; ++j) {
             s_red[wave][j] = mn[j];
@@ -211,7 +246,7 @@ __global__ __launch_bounds__(kBboxThreads) void nm_bbox_partial_kernel(const int
         const int j = threadIdx.x;
         const int nw = blockDim.x >> 6;
         int v = s_red[0][j];
-        for (int w = 1; w < nw; ++w) v = j < 4 ? min(v, s_red[w][j]) : max(v, s_red[w][j]);
+        for (int w = 1; w < nw; ++w) v = reduce_partial(j, v, s_red[w][j]);
         partials[blockIdx.x * kPartialInts + j] = v;
     }
 }
@@ -250,7 +285,7 @@ __global__ __launch_bounds__(256) void nm_plan_init_kernel(const int32_t *__rest
         mx[j] = wave_max_i32(mx[j]);
     }
     neg = wave_max_i32(neg);
-    uns = wave_max_i32(uns);
+    uns = (int)wave_or_u32((uint32_t)uns);
     if (lane == 0) {
         for (int j = 0; j < 4; ++j) {
             s_red[wave][j] = mn[j];
@@ -263,7 +298,7 @@ __global__ __launch_bounds__(256) void nm_plan_init_kernel(const int32_t *__rest
     if (threadIdx.x < kPartialInts) {
         const int j = threadIdx.x;
         int v = s_red[0][j];
-        for (int w = 1; w < (int)(blockDim.x >> 6); ++w) v = j < 4 ? min(v, s_red[w][j]) : max(v, s_red[w][j]);
+        for (int w = 1; w < (int)(blockDim.x >> 6); ++w) v = reduce_partial(j, v, s_red[w][j]);
         if (j < 4)
             s_h.bmin[j] = v;
         else if (j < 8)
@@ -331,7 +366,7 @@ __global__ __launch_bounds__(256) void nm_insert_kernel(const int4 *__restrict__
             uint32_t q = 0, w = 0xffffffffu;  // total <= 2^32 - 1 cells: 32-bit keys
             if (valid) {
                 const int4 c = coords[r];
-                q = (uint32_t)pack_key(p, c.x, c.y, c.z, c.w);
+                q = (uint32_t)rank_key(p, c.x, c.y, c.z, c.w);
                 w = q >> 5;
             }
             uint32_t wp = __shfl_up(w, 1);
@@ -339,7 +374,7 @@ __global__ __launch_bounds__(256) void nm_insert_kernel(const int4 *__restrict__
                 wp = 0xfffffffeu;  // no predecessor: differs from every word
                 if (r > 0) {
                     const int4 cp = coords[r - 1];
-                    wp = (uint32_t)pack_key(p, cp.x, cp.y, cp.z, cp.w) >> 5;
+                    wp = (uint32_t)rank_key(p, cp.x, cp.y, cp.z, cp.w) >> 5;
                 }
             }
             uint32_t bits = valid ? 1u << (q & 31u) : 0u;
@@ -484,12 +519,45 @@ inline int query_lds_ints(int64_t K, int rows_per_block)
     return staged > rowwise ? staged : rowwise;
 }
 
-template <bool kRank, bool kCube3>
+// Rank bitmap with octree levels on the 3x3x3 path: the key (rank_key) is
+// not linear in the coords, but it is a sum of per-axis terms, so each row
+// keeps, per kernel axis j and step e in {-1, 0, +1}, the term T[j][e + 1]
+// of its neighbour's coordinate along that axis (root index times its stride,
+// shifted past the digits, plus the axis's octree digits), and base the
+// batch term; a neighbour's key is base + three terms.
+__device__ inline void levels_terms(const int4 c, const Cube3 &cube, const Plan &p, uint32_t &base,
+                                    uint32_t (&T)[3][3])
+{
+    const int L = uniform_i32(p.levels);
+    const uint32_t e1 = (uint32_t)uniform_i32((int)(uint32_t)p.rext[1]);
+    const uint32_t e2 = (uint32_t)uniform_i32((int)(uint32_t)p.rext[2]);
+    const uint32_t e3 = (uint32_t)uniform_i32((int)(uint32_t)p.rext[3]);
+    const int l0 = uniform_i32(p.rlo[0]), l1 = uniform_i32(p.rlo[1]), l2 = uniform_i32(p.rlo[2]),
+              l3 = uniform_i32(p.rlo[3]);
+    const uint32_t sx = e2 * e3, sy = e3;  // root strides of x, y (z: 1)
+    base = ((uint32_t)(c.x - l0) * (e1 * sx)) << (3 * L);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        const int a = cube.a[j];
+        const int ca = a == 0 ? c.y : (a == 1 ? c.z : c.w);
+        const int rl = a == 0 ? l1 : (a == 1 ? l2 : l3);
+        const uint32_t st = a == 0 ? sx : (a == 1 ? sy : 1u);
+        const uint32_t m = (1u << L) - 1u;
+#pragma unroll
+        for (int e = 0; e < 3; ++e) {
+            const int v = ca + (e - 1) * cube.s[j];
+            T[j][e] = (((uint32_t)((v >> L) - rl) * st) << (3 * L)) + (spread3((uint32_t)v & m) << a);
+        }
+    }
+}
+
+template <bool kRank, bool kCube3, bool kLevels = false>
 __device__ inline void query_cells(const int4 *__restrict__ coords, int64_t row0, int nrows, int K,
                                    const int4 *__restrict__ otab, const Cube3 &cube, const Plan &p,
                                    const uint64_t *__restrict__ table, uint32_t table_bytes, int *s_out,
                                    int32_t *__restrict__ out)
 {
+    static_assert(!kLevels || (kRank && kCube3), "octree levels: rank bitmap, 3x3x3 path");
     const __amdgpu_buffer_rsrc_t rt = cell_table_rsrc(table, table_bytes);
     const int rw = (int)threadIdx.x;  // row within the block
     const bool valid = rw < nrows;
@@ -497,10 +565,12 @@ __device__ inline void query_cells(const int4 *__restrict__ coords, int64_t row0
     uint32_t base = 0;
     if (valid) {
         c = coords[row0 + rw];
-        base = (uint32_t)pack_key(p, c.x, c.y, c.z, c.w);
+        if (!kLevels) base = (uint32_t)pack_key(p, c.x, c.y, c.z, c.w);
     }
     bool up[3] = {false, false, false}, dn[3] = {false, false, false};
     if (kCube3) cube3_flags(c, cube, up, dn);
+    uint32_t T[3][3];
+    if (kLevels) levels_terms(c, cube, p, base, T);
     const int KK = kCube3 ? 27 : K;
     int *so = s_out + rw * KK;
     for (int k0 = 0; k0 < KK; k0 += kCellChunk) {
@@ -511,7 +581,18 @@ __device__ inline void query_cells(const int4 *__restrict__ coords, int64_t row0
             const int k = k0 + u;
             if (k >= KK) break;
             bool inside;
-            q[u] = neighbour_cell<kCube3>(k, c, valid, base, up, dn, cube, p, otab, inside);
+            if (kLevels) {
+                const int e[3] = {k / 9, (k / 3) % 3, k % 3};  // step + 1 along kernel axis j
+                inside = valid;
+#pragma unroll
+                for (int j = 0; j < 3; ++j) {
+                    if (e[j] == 2) inside = inside && up[j];
+                    if (e[j] == 0) inside = inside && dn[j];
+                }
+                q[u] = base + T[0][e[0]] + T[1][e[1]] + T[2][e[2]];
+            } else {
+                q[u] = neighbour_cell<kCube3>(k, c, valid, base, up, dn, cube, p, otab, inside);
+            }
             if (kRank)
                 raw[u] = bload8(rt, cell_offset<true>(q[u], inside));
             else
@@ -566,15 +647,21 @@ __global__ __launch_bounds__(256) void nm_query_kernel(const int4 *__restrict__ 
     const Plan p = h->plan;
     const bool staged = ks.K <= kMaxStagedOffsets;
     const bool cellwise = p.mode == 4 || p.mode == 5;
+    // octree-level keys are not linear in the coords: only the 3x3x3 row-wise
+    // path handles them specially, other shapes take the per-entry path below
+    const bool levels = p.mode == 5 && p.levels > 0;
     // table bytes, addressed through a buffer descriptor on the row-wise path
     const uint64_t tbytes = cell_table_bytes(p);
+    const bool cube3 = is_cube3(ks);
     const bool rowwise = cellwise && ks.K <= kCellwiseMaxK && rows_per_block == (int)blockDim.x &&
-                         tbytes <= kOobOffset;
+                         tbytes <= kOobOffset && (!levels || cube3);
     int32_t *out = map + row0 * ks.K;
     if (rowwise) {
-        const bool cube3 = is_cube3(ks);
         const Cube3 cube = cube3_of(ks, p);
-        if (p.mode == 5 && cube3)
+        if (levels)
+            query_cells<true, true, true>(coords, row0, nrows, ks.K, otab, cube, p, keys, (uint32_t)tbytes, s_dyn,
+                                          out);
+        else if (p.mode == 5 && cube3)
             query_cells<true, true>(coords, row0, nrows, ks.K, otab, cube, p, keys, (uint32_t)tbytes, s_dyn,
                                      out);
         else if (p.mode == 5)
@@ -602,7 +689,7 @@ __global__ __launch_bounds__(256) void nm_query_kernel(const int4 *__restrict__ 
             s_delta[k] = o.w;
         }
     __syncthreads();
-    if (cellwise && staged) {
+    if (cellwise && staged && !levels) {
         if (p.mode == 5)
             query_dense<true>(s_coord, s_off, s_base, s_delta, nrows, ks.K, p, keys, out);
         else
@@ -630,7 +717,7 @@ __global__ __launch_bounds__(256) void nm_query_kernel(const int4 *__restrict__ 
         const bool inside = p.mode != 0 && nx >= p.lo[1] && nx <= p.hi[1] && ny >= p.lo[2] &&
                             ny <= p.hi[2] && nz >= p.lo[3] && nz <= p.hi[3];
         if (inside && p.mode == 5) {
-            found = rank_lookup(keys, pack_key(p, c.x, (int32_t)nx, (int32_t)ny, (int32_t)nz));
+            found = rank_lookup(keys, rank_key(p, c.x, (int32_t)nx, (int32_t)ny, (int32_t)nz));
         } else if (inside && p.mode == 4) {
             found = (int32_t)~grid[pack_key(p, c.x, (int32_t)nx, (int32_t)ny, (int32_t)nz)];
         } else if (inside && p.mode == 3) {

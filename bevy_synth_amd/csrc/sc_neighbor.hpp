@@ -19,21 +19,27 @@ struct Limits {
     uint64_t bitmap_cells;
 };
 
+// Octree levels the rank bitmap's key may interleave (see rank_key).
+constexpr int kRankLevels = 8;
+
 struct Plan {
     int mode;  // 0: no table (error), 1: 32-bit keys packed with rows, 2: 64-bit keys,
                // 3: row-only table compared through the coords, 4: dense grid,
-               // 5: rank bitmap (rows strictly increasing in (b, x, y, z))
-    uint64_t total;  // bbox cells (valid for modes 1, 2, 4, 5)
+               // 5: rank bitmap (rows strictly increasing in rank_key)
+    int levels;      // mode 5: octree levels of the key (0: the plain (b, x, y, z) order)
+    uint64_t total;  // table cells (valid for modes 1, 2, 4, 5)
     int32_t lo[4];
     int32_t hi[4];
     uint64_t ext[4];
+    int32_t rlo[4];   // mode 5: the root cells' bbox (lo >> levels; batch unchanged)
+    uint64_t rext[4]; //         and its extents
 };
 
 struct alignas(16) NbrHeader {
     int32_t bmin[4];
     int32_t bmax[4];
     uint32_t status;
-    uint32_t unsorted;  // nonzero unless the rows are strictly increasing in (b, x, y, z)
+    uint32_t unsorted;  // bit L set unless the rows are strictly increasing in the L-level key
     int32_t mode;       // the table mode chosen (Plan::mode), a diagnostic for callers
     uint32_t pad0;
     Plan plan;          // derived once from the fields above, read by every later kernel
@@ -52,6 +58,67 @@ __device__ inline uint64_t pack_key(const Plan &p, int32_t b, int32_t x, int32_t
     k = k * p.ext[2] + (uint64_t)(y - p.lo[2]);
     k = k * p.ext[3] + (uint64_t)(z - p.lo[3]);
     return k;
+}
+
+// Bits 0..9 of v spread to every third bit (bit i -> bit 3i).
+__device__ inline uint32_t spread3(uint32_t v)
+{
+    v &= 0x3FFu;
+    v = (v | (v << 16)) & 0x030000FFu;
+    v = (v | (v << 8)) & 0x0300F00Fu;
+    v = (v | (v << 4)) & 0x030C30C3u;
+    v = (v | (v << 2)) & 0x09249249u;
+    return v;
+}
+
+// Octree digits of the low `levels` bits of (x, y, z): per level one 3-bit
+// digit x | y << 1 | z << 2 (a C2S child index), the coarsest level most
+// significant.
+__device__ inline uint32_t octree_digits(int32_t x, int32_t y, int32_t z, int levels)
+{
+    const uint32_t m = (1u << levels) - 1u;
+    return spread3((uint32_t)x & m) | spread3((uint32_t)y & m) << 1 | spread3((uint32_t)z & m) << 2;
+}
+
+// The rank bitmap's cell key with L = p.levels octree levels: the
+// lexicographic index of the root cell (coords >> L, inside the root bbox)
+// times 8^L plus the octree digits of the low L bits.  Children that C2S
+// subdivision emits (parent-major, child index ascending) L times below a
+// lexicographically sorted set are strictly increasing in this key, so a
+// decoder stage after an upsample keeps the rank bitmap.  L = 0 is pack_key.
+__device__ inline uint64_t rank_key(const Plan &p, int32_t b, int32_t x, int32_t y, int32_t z)
+{
+    const int L = p.levels;
+    if (L == 0) return pack_key(p, b, x, y, z);
+    uint64_t k = (uint64_t)(b - p.rlo[0]);
+    k = k * p.rext[1] + (uint64_t)((x >> L) - p.rlo[1]);
+    k = k * p.rext[2] + (uint64_t)((y >> L) - p.rlo[2]);
+    k = k * p.rext[3] + (uint64_t)((z >> L) - p.rlo[3]);
+    return (k << (3 * L)) | octree_digits(x, y, z, L);
+}
+
+// Bit L set unless a precedes c strictly in the L-level key, for every L <
+// kRankLevels, without building the keys: with h_a the highest bit in which
+// the two coords differ along axis a, the root cells (coords >> L) differ
+// along x iff h_x >= L, and then the key order is the order of x, and so on
+// for y and z; with equal roots, the most significant differing octree digit
+// is the one at bit p = max(h_x, h_y, h_z), and within a digit z weighs
+// most, then y, then x.
+__device__ inline uint32_t unsorted_levels(const int4 a, const int4 c)
+{
+    constexpr uint32_t kAll = (1u << kRankLevels) - 1u;
+    if (a.x != c.x) return a.x < c.x ? 0u : kAll;  // batch
+    const int hx = 31 - __clz(a.y ^ c.y), hy = 31 - __clz(a.z ^ c.z), hz = 31 - __clz(a.w ^ c.w);
+    const bool lx = a.y < c.y, ly = a.z < c.z, lz = a.w < c.w;
+    const int p = max(hx, max(hy, hz));
+    const bool digit_less = p >= 0 && (hz == p ? lz : (hy == p ? ly : lx));  // equal coords: not less
+    uint32_t bad = 0;
+#pragma unroll
+    for (int L = 0; L < kRankLevels; ++L) {
+        const bool less = hx >= L ? lx : (hy >= L ? ly : (hz >= L ? lz : digit_less));
+        bad |= (uint32_t)!less << L;
+    }
+    return bad;
 }
 
 // The 3x3x3 kernel with unit axis signs (the decoder's submanifold conv):

@@ -161,6 +161,13 @@ def neighbor_map_table_mode(workspace: torch.Tensor) -> str:
     return NEIGHBOR_TABLE_MODES.get(mode, "none")
 
 
+def neighbor_map_rank_levels(workspace: torch.Tensor) -> int:
+    """Octree levels of the rank bitmap's key in the last build into
+    ``workspace`` (0: rows sorted in (b, x, y, z); L: rows in the order L C2S
+    subdivisions below such a set emit them); syncs the current stream."""
+    return int(workspace[52:56].view(torch.int32).item())
+
+
 def neighbor_map_check(workspace: torch.Tensor) -> None:
     """Syncs the current stream and raises on device-detected coord errors."""
     check(_capi.load().sc_neighbor_map_check(_ptr(workspace), _stream()))

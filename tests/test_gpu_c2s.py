@@ -75,12 +75,15 @@ def _parents_and_mask(n=6000, frac=0.45, seed=3):
     return coords, mask
 
 
-@pytest.mark.parametrize("cchild,ln", [(16, True), (64, True), (128, True), (256, True), (64, False)])
+@pytest.mark.parametrize("cchild,ln", [(16, True), (64, True), (128, True), (256, True), (64, False),
+                                       (24, True), (96, False)])
 @pytest.mark.parametrize("planned", [False, True])
 def test_conv1_child_scatter(oracle, cchild, ln, planned):
     """conv1 (Cin -> 8*C) on the parents writes child c of parent p to row
     child_rows[p, c], normalised over its C channels: in the tile epilogue
-    (C = 64: one wave half; C = 128: the tile) or on f32 staging (C = 16, 256)."""
+    (C = 64: one wave half; C = 128: the tile) or on f32 staging (C = 16, 24,
+    256); C = 24 and 96 take the epilogue's division form (C not a power of
+    two)."""
     coords, mask = _parents_and_mask()
     rng = np.random.default_rng(cchild)
     cin, cout = 64, 8 * cchild
@@ -106,10 +109,12 @@ def test_conv1_child_scatter(oracle, cchild, ln, planned):
     assert_close(host(got), exp, TOL_BF16, f"child scatter C={cchild}")
 
 
-@pytest.mark.parametrize("cp,cout", [(512, 256), (128, 64), (64, 128)])
+@pytest.mark.parametrize("cp,cout", [(512, 256), (128, 64), (64, 128), (256, 32), (128, 32), (256, 96)])
 def test_conv2_parent_skip(oracle, cp, cout):
     """conv2 on the children + the channel-repeated parent skip in its epilogue
-    (S = Cp/8 parent channels per child, each repeated Cout/S times)."""
+    (S = Cp/8 parent channels per child, each repeated R = Cout/S times):
+    R = 4, 4, 16 (one parent load per 4 channels), R = 1, 2 (a load per
+    channel) and R = 3 (the division form)."""
     coords, mask = _parents_and_mask(3000, 0.5, seed=cp)
     rng = np.random.default_rng(cp + cout)
     cd = dev(coords)

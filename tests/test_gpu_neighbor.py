@@ -221,6 +221,71 @@ def test_table_modes_by_row_order(oracle):
     assert mode == "rank_bitmap" and np.array_equal(got, exp[:777])
 
 
+def _c2s_children(coords, levels, frac, seed):
+    """`levels` C2S subdivisions below coords, each child kept with
+    probability frac (parent-major, child index ascending: the order the
+    decoder's subdivision emits)."""
+    rng = np.random.default_rng(seed)
+    for _ in range(levels):
+        mask = (rng.random((len(coords), 8)) < frac).astype(np.uint8)
+        coords = synth.child_expand(coords, mask)
+    return coords
+
+
+@pytest.mark.parametrize("levels", [1, 2, 3])
+def test_rank_bitmap_c2s_order(oracle, levels):
+    """Children in C2S order below a sorted set are strictly increasing in the
+    rank bitmap's key with that many octree levels: they keep the rank bitmap
+    (not the dense grid), and the map equals the oracle's -- on the 3x3x3
+    path (per-axis key terms) and with a permuted, sign-flipped 3x3x1 kernel
+    (the per-entry path).  Two batches, one of them offset so that the root
+    bbox starts at odd coordinates."""
+    base = synth.config1_coords()[::2]
+    shifted = base.copy()
+    shifted[:, 0] = 1
+    shifted[:, 1:] += (3, 5, 1)
+    roots = np.concatenate([base, shifted])                         # sorted: batch 0, then batch 1
+    # 45 % of the children kept: the set stays within the bitmap's budget of
+    # 512 cells per row (a sparser set legitimately takes a hash table)
+    coords = _c2s_children(roots, levels, 0.45, seed=levels)
+    for cfg in (F.SparseSubmConvConfig(1, 1),
+                F.SparseSubmConvConfig(1, 1, 3, 3, 1, axis_order=(2, 0, 1), axis_sign=(1, -1, 1))):
+        c = dev(coords.astype(np.int32))
+        ws = F.NeighborMapWorkspace(c.device).get(len(coords))
+        out = torch.empty((len(coords), F.kernel_rows(cfg)), dtype=torch.int32, device=c.device)
+        F.neighbor_map_build_into(cfg, c, out, ws)
+        F.neighbor_map_check(ws)
+        assert F.neighbor_map_table_mode(ws) == "rank_bitmap"
+        assert F.neighbor_map_rank_levels(ws) == levels
+        assert np.array_equal(out.cpu().numpy(), oracle.build_neighbor_rows(ocfg(oracle, cfg), coords))
+    # the same children through the device subdivision (the decoder's path)
+    cur = dev(roots.astype(np.int32))
+    rng = np.random.default_rng(levels)
+    for _ in range(levels):
+        mask = (rng.random((cur.shape[0], 8)) < 0.45).astype(np.uint8)
+        cur, _, _ = F.subdivision_build(cur, mask=dev(mask), with_pairs=False)
+    got, mode = _map_and_mode(F.SparseSubmConvConfig(1, 1), cur.cpu().numpy())
+    assert mode == "rank_bitmap"
+    assert np.array_equal(got, oracle.build_neighbor_rows(ocfg(oracle, F.SparseSubmConvConfig(1, 1)),
+                                                          cur.cpu().numpy()))
+
+
+def test_c2s_order_broken_falls_back(oracle):
+    """One pair of children out of C2S order: no octree level fits, the map
+    takes the dense grid or a hash table (by density) and still equals the
+    oracle's."""
+    coords = _c2s_children(synth.config1_coords(), 2, 0.4, seed=5)
+    c = coords.copy()
+    i = len(c) // 2
+    c[[i, i + 1]] = c[[i + 1, i]]
+    cfg = F.SparseSubmConvConfig(1, 1)
+    got, mode = _map_and_mode(cfg, c)
+    assert mode in ("dense_grid", "hash32")
+    assert np.array_equal(got, oracle.build_neighbor_rows(ocfg(oracle, cfg), c))
+    got, mode = _map_and_mode(cfg, coords)  # the intact order keeps the bitmap
+    assert mode == "rank_bitmap"
+
+
 def test_rank_bitmap_sparse_bbox(oracle):
     """Sorted unique coords over a bbox of more than 32 cells per row (beyond
     the dense grid's budget) still take the rank bitmap; two batches, words
