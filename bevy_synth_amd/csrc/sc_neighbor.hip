@@ -36,7 +36,11 @@
 // then a rank bitmap: per 32 cells, 32 occupancy bits and the row of the first
 // occupied cell (8 B per 32 cells, 1/16 of the dense grid, small enough to stay
 // in L2), built by one writer per word with no atomics; a query is one 8-byte
-// load and a popcount. Any other row order takes the modes above.
+// load and a popcount. The same holds for rows in the order C2S subdivision
+// emits children (parent-major, child index ascending) L times below such a
+// set: they are strictly increasing in a key with L octree levels (rank_key),
+// which the bbox pass also checks, for L < 8. Any other row order takes the
+// modes above.
 #include <climits>
 
 #include "sc_common.hpp"
