@@ -466,7 +466,10 @@ __global__ __launch_bounds__(256) void linear_skinny_kernel(const Tin *__restric
                         for (int e = 0; e < VEC; ++e) a += f[e] * wr[v * VEC + e];
                     }
                 } else {
-                    for (int i = 0; i < 64 && c0 + i < cin; ++i) a += load_as_f32<Tin>(xr, i) * wr[i];
+                    // static indices keep wr in registers (a runtime bound put it in scratch)
+#pragma unroll
+                    for (int i = 0; i < 64; ++i)
+                        if (c0 + i < cin) a += load_as_f32<Tin>(xr, i) * wr[i];
                 }
                 acc[r] = a;
             }

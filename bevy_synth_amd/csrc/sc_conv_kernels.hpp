@@ -1635,15 +1635,21 @@ __global__ __launch_bounds__(256) void conv_scalar_kernel(ConvArgs args)
     }
 }
 
-// bf16 activations through the v2 tile: 128-byte stages when the group's
+// 16-bit activations through the v2 tile: 128-byte stages when the group's
 // input channels allow it, else 64-byte stages with a deeper A prefetch.
+// int8 weights always take the 64-byte stages: their register staging of the
+// widened pieces does not fit beside the 128-byte stage's operands (the
+// 128-byte int8 variant spilled), so it is not instantiated.
 template <typename TA, typename TW, typename TO, bool PERM>
 void launch_v2(const ConvArgs &a, dim3 grid, hipStream_t s)
 {
-    if (sizeof(TW) == 2 && a.cin_g % 64 == 0)
-        conv_v2_kernel<TA, TW, TO, 128, 1, PERM><<<grid, kThreads, 0, s>>>(a);
-    else
-        conv_v2_kernel<TA, TW, TO, 64, 2, PERM><<<grid, kThreads, 0, s>>>(a);
+    if constexpr (sizeof(TW) == 2) {
+        if (a.cin_g % 64 == 0) {
+            conv_v2_kernel<TA, TW, TO, 128, 1, PERM><<<grid, kThreads, 0, s>>>(a);
+            return;
+        }
+    }
+    conv_v2_kernel<TA, TW, TO, 64, 2, PERM><<<grid, kThreads, 0, s>>>(a);
 }
 
 template <typename TA, typename TW, typename TO>

@@ -30,6 +30,30 @@ def test_library_exports_every_header_symbol():
     assert L.sc_abi_version() == 2
 
 
+def test_no_kernel_uses_scratch():
+    """Every kernel of the build keeps its state in registers and LDS: the
+    compiler's resource report of each object (kept beside it by the
+    Makefile) shows ScratchSize 0 -- a spilled or dynamically indexed array
+    would cost hidden HBM traffic on every wave."""
+    import glob
+    reports = sorted(glob.glob(os.path.join(ROOT, "bevy_synth_amd", "csrc", "_build", "*.o.res")))
+    if not reports:
+        pytest.skip("no build reports: run __graft_entry__.build()")
+    kernels, spilled = 0, []
+    for path in reports:
+        name = None
+        for line in open(path):
+            m = re.search(r"remark: Function Name: (\S+)", line)
+            if m:
+                name = m.group(1)
+                kernels += 1
+            m = re.search(r"remark:\s+ScratchSize \[bytes/lane\]: (\d+)", line)
+            if m and int(m.group(1)) > 0:
+                spilled.append((os.path.basename(path), name, int(m.group(1))))
+    assert kernels >= 100, kernels
+    assert not spilled, spilled
+
+
 def test_status_strings():
     L = _capi.load()
     for code in range(10):
