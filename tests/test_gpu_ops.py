@@ -251,7 +251,7 @@ def test_fused_conv_ln_silu_residual(oracle, cin, cout, groups, dtype, affine, p
     row kernel; Cin = 6 takes the scalar conv.  Every case is held to the
     plain bar against LN of the fp64 conv: one rounding, at the end."""
     if planned and (dtype != torch.bfloat16 or cin % 32):
-        pytest.skip("the plan serves bf16 activations with Cin_g a multiple of 32")
+        pytest.skip("the planned kernel takes 16-bit activations with Cin_g a multiple of 32")
     coords = synth.config1_coords()[:5000]
     rng = np.random.default_rng(cin + cout + groups)
     n = len(coords)
