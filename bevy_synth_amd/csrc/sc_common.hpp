@@ -235,6 +235,49 @@ __device__ inline int wave_max_i32(int v)
     return v;
 }
 
+// Octree levels of the row-order test below: C2S subdivision emits children
+// parent-major, child index ascending, so after L subdivisions below a set
+// sorted in (b, x, y, z) the rows are strictly increasing in the key
+// (lexicographic index of coords >> L) * 8^L + octree digits of the low L
+// bits (coarsest level most significant, a digit x | y << 1 | z << 2).  The
+// neighbour map's rank bitmap and the conv plan's row order use it.
+constexpr int kRankLevels = 8;
+
+// Bit L set unless a precedes c strictly in the L-level key, for every L <
+// kRankLevels, without building the keys.  With h_a the highest bit in which
+// the two coords differ along axis a (-1: equal), the root cells (coords >>
+// L) differ along x exactly for L <= h_x, and the key order is then the
+// order of x; failing that along y for L <= h_y, then z; with equal roots the
+// most significant differing octree digit is the one at bit max(h_x, h_y,
+// h_z), and within a digit z weighs most, then y, then x.  So the levels
+// split into four ranges, each taking one comparison.  (Host and device:
+// tests/cpp/test_order_levels.cpp checks it against the keys themselves.)
+__host__ __device__ inline int high_bit(uint32_t v) { return v ? 31 - __builtin_clz(v) : -1; }
+
+// Levels 0 .. h as a mask (empty for h < 0, all for h >= kRankLevels - 1).
+__host__ __device__ inline uint32_t levels_upto(int h)
+{
+    constexpr uint32_t kAll = (1u << kRankLevels) - 1u;
+    return h < 0 ? 0u : (h >= kRankLevels - 1 ? kAll : (2u << h) - 1u);
+}
+
+__host__ __device__ inline uint32_t unsorted_levels(const int4 a, const int4 c)
+{
+    constexpr uint32_t kAll = (1u << kRankLevels) - 1u;
+    if (a.x != c.x) return a.x < c.x ? 0u : kAll;  // batch
+    const int hx = high_bit((uint32_t)(a.y ^ c.y)), hy = high_bit((uint32_t)(a.z ^ c.z)),
+              hz = high_bit((uint32_t)(a.w ^ c.w));
+    const uint32_t rx = levels_upto(hx);            // x roots differ
+    const uint32_t ry = levels_upto(hy) & ~rx;      // else y roots differ
+    const uint32_t rz = levels_upto(hz) & ~rx & ~ry;
+    const uint32_t rd = kAll & ~rx & ~ry & ~rz;     // equal roots: the digits decide
+    const int p = hx > hy ? (hx > hz ? hx : hz) : (hy > hz ? hy : hz);
+    const bool digit_less = p >= 0 && (hz == p ? a.w < c.w : (hy == p ? a.z < c.z : a.y < c.y));
+    const uint32_t less = (a.y < c.y ? rx : 0u) | (a.z < c.z ? ry : 0u) | (a.w < c.w ? rz : 0u) |
+                          (digit_less ? rd : 0u);
+    return kAll & ~less;
+}
+
 __device__ inline int tile_for_block(int b, int G)
 {
     // Dispatch assigns workgroup b to XCD b % 8; give each XCD a contiguous

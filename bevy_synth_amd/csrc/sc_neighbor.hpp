@@ -19,9 +19,6 @@ struct Limits {
     uint64_t bitmap_cells;
 };
 
-// Octree levels the rank bitmap's key may interleave (see rank_key).
-constexpr int kRankLevels = 8;
-
 struct Plan {
     int mode;  // 0: no table (error), 1: 32-bit keys packed with rows, 2: 64-bit keys,
                // 3: row-only table compared through the coords, 4: dense grid,
@@ -95,30 +92,6 @@ __device__ inline uint64_t rank_key(const Plan &p, int32_t b, int32_t x, int32_t
     k = k * p.rext[2] + (uint64_t)((y >> L) - p.rlo[2]);
     k = k * p.rext[3] + (uint64_t)((z >> L) - p.rlo[3]);
     return (k << (3 * L)) | octree_digits(x, y, z, L);
-}
-
-// Bit L set unless a precedes c strictly in the L-level key, for every L <
-// kRankLevels, without building the keys: with h_a the highest bit in which
-// the two coords differ along axis a, the root cells (coords >> L) differ
-// along x iff h_x >= L, and then the key order is the order of x, and so on
-// for y and z; with equal roots, the most significant differing octree digit
-// is the one at bit p = max(h_x, h_y, h_z), and within a digit z weighs
-// most, then y, then x.
-__device__ inline uint32_t unsorted_levels(const int4 a, const int4 c)
-{
-    constexpr uint32_t kAll = (1u << kRankLevels) - 1u;
-    if (a.x != c.x) return a.x < c.x ? 0u : kAll;  // batch
-    const int hx = 31 - __clz(a.y ^ c.y), hy = 31 - __clz(a.z ^ c.z), hz = 31 - __clz(a.w ^ c.w);
-    const bool lx = a.y < c.y, ly = a.z < c.z, lz = a.w < c.w;
-    const int p = max(hx, max(hy, hz));
-    const bool digit_less = p >= 0 && (hz == p ? lz : (hy == p ? ly : lx));  // equal coords: not less
-    uint32_t bad = 0;
-#pragma unroll
-    for (int L = 0; L < kRankLevels; ++L) {
-        const bool less = hx >= L ? lx : (hy >= L ? ly : (hz >= L ? lz : digit_less));
-        bad |= (uint32_t)!less << L;
-    }
-    return bad;
 }
 
 // The 3x3x3 kernel with unit axis signs (the decoder's submanifold conv):

@@ -24,7 +24,10 @@
 //   7. fix     : rows of duplicated coords appended after the distinct ones
 // The order is a pure function of the coords (no sort, no atomics whose
 // interleaving shows): bricks in (batch, x, y, z) order, lexicographic inside
-// a brick.  A bounding box too large for the grid falls back to a counting
+// a brick.  Rows that already come in the order of 3 or more C2S
+// subdivisions below a sorted set (the bbox pass tests it, as the map build
+// does) keep their own order: they are grouped by aligned 8^3 root cells,
+// Morton order inside, which is as compact, so steps 3-7 are skipped.  A bounding box too large for the grid falls back to a counting
 // sort by brick (brick edge 2^s, the smallest s >= 3 with at most brick_cap
 // bricks): count, scan, scatter with wave-aggregated atomics, then each
 // brick's segment sorted by row index so that the order is deterministic.
@@ -107,27 +110,54 @@ __device__ inline void plan_init(const PlanArgs &a)
 // otherwise plan_bbox_kernel does it).
 __global__ void plan_init_kernel(PlanArgs a) { plan_init(a); }
 
-// Per-block min/max of the query coords -> partials (in the brick-offset
-// array, which the scan overwrites later); every block of plan_prep_kernel
-// reduces them (atomic-free, and no launch of its own).
-constexpr int kBboxBlocks = 512;
+// Per-block min/max of the query coords and the octree-order bits
+// (unsorted_levels of each row against its predecessor, ORed) -> partials of
+// kPartial ints (in the brick-offset array, which the scan overwrites later:
+// kBboxBlocks * kPartial <= 4096 <= brick_cap); every block of
+// plan_prep_kernel reduces them (atomic-free, and no launch of its own).
+constexpr int kBboxBlocks = 448;
+constexpr int kPartial = 9;
+static_assert(kBboxBlocks * kPartial <= 4096, "partials fit the smallest brick-offset array");
+// Rows in octree order over at least this many levels keep their order.
+constexpr int kOwnOrderLevels = 3;
 
 __global__ __launch_bounds__(kThreads) void plan_bbox_kernel(PlanArgs a)
 {
     __shared__ int s_mn[4][4], s_mx[4][4];
+    __shared__ uint32_t s_uns[4];
     plan_init(a);  // header and order padding (read by no kernel before the next launch)
     int mn[4] = {INT_MAX, INT_MAX, INT_MAX, INT_MAX}, mx[4] = {INT_MIN, INT_MIN, INT_MIN, INT_MIN};
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n_q;
-         i += (int64_t)gridDim.x * blockDim.x) {
-        const int4 c = a.coords[i];
-        const int v[4] = {c.x, c.y, c.z, c.w};
+    uint32_t uns = 0;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // Wave-uniform loop, four rows per lane in flight: in each of them lane l
+    // holds row w0 + u * stride + l, so lane l - 1 holds its predecessor
+    // (lane 0 loads its own).
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t w0 = (int64_t)blockIdx.x * blockDim.x + wave * 64; w0 < a.n_q; w0 += 4 * stride) {
+        int4 c[4], pl[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            mn[j] = min(mn[j], v[j]);
-            mx[j] = max(mx[j], v[j]);
+        for (int u = 0; u < 4; ++u) {
+            const int64_t i = w0 + u * stride + lane;
+            c[u] = i < a.n_q ? a.coords[i] : make_int4(0, 0, 0, 0);
+            pl[u] = lane == 0 && i < a.n_q && i > 0 ? a.coords[i - 1] : make_int4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t i = w0 + u * stride + lane;
+            const int4 cu = c[u];
+            int4 prev = make_int4(__shfl_up(cu.x, 1), __shfl_up(cu.y, 1), __shfl_up(cu.z, 1), __shfl_up(cu.w, 1));
+            if (lane == 0) prev = pl[u];
+            if (i < a.n_q) {
+                const int v[4] = {cu.x, cu.y, cu.z, cu.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    mn[j] = min(mn[j], v[j]);
+                    mx[j] = max(mx[j], v[j]);
+                }
+                if (i > 0) uns |= unsorted_levels(prev, cu);
+            }
         }
     }
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         mn[j] = wave_min_i32(mn[j]);
@@ -137,6 +167,9 @@ __global__ __launch_bounds__(kThreads) void plan_bbox_kernel(PlanArgs a)
             s_mx[wave][j] = mx[j];
         }
     }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) uns |= __shfl_xor(uns, off, 64);
+    if (lane == 0) s_uns[wave] = uns;
     __syncthreads();
     if (threadIdx.x < 4) {
         const int j = threadIdx.x;
@@ -145,8 +178,13 @@ __global__ __launch_bounds__(kThreads) void plan_bbox_kernel(PlanArgs a)
             lo = min(lo, s_mn[w][j]);
             hi = max(hi, s_mx[w][j]);
         }
-        a.offsets[blockIdx.x * 8 + j] = lo;
-        a.offsets[blockIdx.x * 8 + 4 + j] = hi;
+        a.offsets[blockIdx.x * kPartial + j] = lo;
+        a.offsets[blockIdx.x * kPartial + 4 + j] = hi;
+    }
+    if (threadIdx.x == 0) {
+        uint32_t u = 0;
+        for (int w = 0; w < (int)blockDim.x / 64; ++w) u |= s_uns[w];
+        a.offsets[blockIdx.x * kPartial + 8] = (int32_t)u;
     }
 }
 
@@ -257,7 +295,7 @@ __device__ inline int64_t grid_cell(const GridGeom &g, int4 c)
     return brick * 512 + ((x & 7) * 64 + (y & 7) * 8 + (z & 7));
 }
 
-// Every block reduces the bbox partials of plan_bbox_kernel (nbb blocks x 8
+// Every block reduces the bbox partials of plan_bbox_kernel (nbb blocks x kPartial
 // ints, from L2; block 0 writes the bbox to the header) and chooses the
 // ordering mode; grid mode: grid := EMPTY, block flags := 0; fallback: brick
 // counts := 0.
@@ -265,23 +303,32 @@ __global__ __launch_bounds__(kThreads) void plan_prep_kernel(PlanArgs a, int nbb
 {
     __shared__ PlanHeader s_h;  // only bmin / bmax are set
     __shared__ int s_v[8][kThreads / 64];
+    __shared__ uint32_t s_uns[kThreads / 64];
+    uint32_t uns = 0;
     {
         const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
         int v[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = j < 4 ? INT_MAX : INT_MIN;
-        for (int b = threadIdx.x; b < nbb; b += blockDim.x)
+        for (int b = threadIdx.x; b < nbb; b += blockDim.x) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                v[j] = min(v[j], a.offsets[b * 8 + j]);
-                v[4 + j] = max(v[4 + j], a.offsets[b * 8 + 4 + j]);
+                v[j] = min(v[j], a.offsets[b * kPartial + j]);
+                v[4 + j] = max(v[4 + j], a.offsets[b * kPartial + 4 + j]);
             }
+            uns |= (uint32_t)a.offsets[b * kPartial + 8];
+        }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             v[j] = j < 4 ? wave_min_i32(v[j]) : wave_max_i32(v[j]);
             if (lane == 0) s_v[j][wave] = v[j];
         }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) uns |= __shfl_xor(uns, off, 64);
+        if (lane == 0) s_uns[wave] = uns;
         __syncthreads();
+        uns = 0;
+        for (int w = 0; w < kThreads / 64; ++w) uns |= s_uns[w];
         if (threadIdx.x < 8) {
             const int j = threadIdx.x;
             int r = s_v[j][0];
@@ -298,6 +345,19 @@ __global__ __launch_bounds__(kThreads) void plan_prep_kernel(PlanArgs a, int nbb
     }
     const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    // Rows in octree order over kOwnOrderLevels or more levels keep their
+    // order (no grid, no sort): grid_mode 2, and the later order kernels exit.
+    const uint32_t deep = ((1u << kRankLevels) - 1u) & ~((1u << kOwnOrderLevels) - 1u);
+    if ((~uns & deep) != 0u && a.n_q > 0) {
+        if (tid == 0) {
+            a.hdr->grid_mode = 2;
+            a.hdr->brick_shift = -1;
+            a.hdr->n_bricks = 0;
+            a.hdr->n_unique = (int32_t)a.n_q;
+        }
+        for (int64_t i = tid; i < a.n_q; i += stride) a.order[i] = (int32_t)i;
+        return;
+    }
     const GridGeom gg = grid_geom(&s_h, a.grid_cap);
     if (gg.ok) {
         if (tid == 0) {
@@ -325,7 +385,8 @@ __global__ __launch_bounds__(kThreads) void plan_prep_kernel(PlanArgs a, int nbb
 // coord keeps it, the others go to the extras list); fallback: brick counts.
 __global__ __launch_bounds__(kThreads) void plan_place_kernel(PlanArgs a)
 {
-    if (a.hdr->grid_mode) {
+    if (a.hdr->grid_mode == 2) return;  // rows keep their own order
+    if (a.hdr->grid_mode == 1) {
         const GridGeom gg = grid_geom(a.hdr, a.grid_cap);
         for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n_q;
              i += (int64_t)gridDim.x * blockDim.x) {
@@ -397,7 +458,8 @@ __device__ inline int extras_in(const PlanArgs &a, const GridGeom &gg, int64_t r
 __global__ __launch_bounds__(kThreads) void plan_scan1_kernel(PlanArgs a)
 {
     __shared__ int s_wave[kThreads / 64];
-    if (a.hdr->grid_mode) {
+    if (a.hdr->grid_mode == 2) return;
+    if (a.hdr->grid_mode == 1) {
         const int64_t nblk = a.grid_cap / kPlanGridBlock;
         const GridGeom gg = grid_geom(a.hdr, a.grid_cap);
         if ((int64_t)blockIdx.x >= nblk) {  // rows of duplicated coords per 2048-row block
@@ -464,7 +526,8 @@ __device__ inline int block_scan_array(int32_t *arr, int64_t n, int *s_wave)
 __global__ __launch_bounds__(kThreads) void plan_scan2_kernel(PlanArgs a)
 {
     __shared__ int s_wave[kThreads / 64];
-    const bool grid = a.hdr->grid_mode != 0;
+    if (a.hdr->grid_mode == 2) return;
+    const bool grid = a.hdr->grid_mode == 1;
     if (!grid && a.hdr->brick_shift < 0) return;
     int32_t *arr = grid ? a.gsum : a.bsum;
     const int64_t n = grid ? grid_geom(a.hdr, a.grid_cap).blocks : a.n_bsum;
@@ -485,7 +548,8 @@ __device__ inline int64_t brick_start(const PlanArgs &a, uint32_t br)
 __global__ __launch_bounds__(kThreads) void plan_emit_kernel(PlanArgs a)
 {
     __shared__ int s_wave[kThreads / 64];
-    if (a.hdr->grid_mode) {
+    if (a.hdr->grid_mode == 2) return;
+    if (a.hdr->grid_mode == 1) {
         const int64_t nblk = a.grid_cap / kPlanGridBlock;
         const GridGeom gg = grid_geom(a.hdr, a.grid_cap);
         if ((int64_t)blockIdx.x >= nblk) {  // rows of duplicated coords, in row order
@@ -552,7 +616,7 @@ __global__ __launch_bounds__(kThreads) void plan_fix_kernel(PlanArgs a)
 {
     __shared__ __attribute__((aligned(16))) int32_t s_seg[kThreads / 64][kSegWave];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (a.hdr->grid_mode) return;
+    if (a.hdr->grid_mode) return;  // grid mode places everything; own order needs nothing
     if (a.hdr->brick_shift < 0) return;
     const uint64_t nb = a.hdr->n_bricks;
     int32_t *seg_lds = s_seg[wave];

@@ -13,6 +13,7 @@ import torch
 
 from bevy_synth_amd import flex_gmm as F
 from bevy_synth_amd import synth
+from tests.sampling import sample_rows
 from tests.tolerance import TOL_BF16, assert_close
 
 pytestmark = pytest.mark.gpu
@@ -80,8 +81,18 @@ def check_plan(plan, nbr, n_in):
     return h
 
 
+def c2s_children(levels, frac=0.5, seed=4):
+    """Children of `levels` C2S subdivisions below config 1's sorted shell,
+    in the order the subdivision emits them."""
+    rng = np.random.default_rng(seed)
+    coords = synth.config1_coords()
+    for _ in range(levels):
+        coords = synth.child_expand(coords, (rng.random((len(coords), 8)) < frac).astype(np.uint8))
+    return coords
+
+
 @pytest.mark.parametrize("which", ["config1", "random_batches", "clusters", "query_subset", "duplicates",
-                                   "wide_bbox"])
+                                   "wide_bbox", "c2s_3_levels", "c2s_2_levels"])
 def test_plan_structure(which):
     rng = np.random.default_rng(11)
     cfg = F.SparseSubmConvConfig(32, 32)
@@ -111,6 +122,12 @@ def test_plan_structure(which):
         c[:4000] = c[4000:8000] + np.array([0, 1, 0, 0], np.int32)       # neighbours in x
         c[-300:] = c[:300]                                               # duplicates
         coords = c[rng.permutation(len(c))]
+    elif which == "c2s_3_levels":
+        # octree order over 3 levels: the rows keep their own order
+        coords = c2s_children(3, frac=0.3)
+        q = len(coords) - 1000
+    elif which == "c2s_2_levels":
+        coords = c2s_children(2)
     else:
         coords = synth.config1_coords()
         q = 9000
@@ -118,7 +135,12 @@ def test_plan_structure(which):
     nbr = F.neighbor_rows_tensor_from_coords_tensor(cfg, cd, query_rows=q)
     plan = F.build_conv_plan(cfg, cd, nbr)
     h = check_plan(plan, nbr.cpu().numpy(), len(coords))
-    assert h["grid_mode"] == (0 if which == "wide_bbox" else 1)
+    # 2 C2S levels over config 1 (234 k rows in a 256^3 box) exceed the grid's
+    # 16 cells per row: the counting-sort order
+    assert h["grid_mode"] == {"wide_bbox": 0, "c2s_2_levels": 0, "c2s_3_levels": 2}.get(which, 1)
+    if which == "c2s_3_levels":
+        n_q = nbr.shape[0]
+        assert np.array_equal(h["order"].ravel()[:n_q], np.arange(n_q))
     if which == "clusters":
         assert h["n_overflow"] == h["n_tiles"]
     if which in ("duplicates", "config1"):
@@ -269,6 +291,31 @@ def test_planned_ln_silu_and_residual(oracle, affine, cin, cout):
     out2, _, _ = planned(cfg, coords, x, w, b, residual=dev(res), out_dtype=torch.float32)
     exp2 = oracle.conv_ref_f64(ocfg_, w, b, x, nbr) + res
     assert_close(out2.cpu().numpy(), exp2, 2e-5, "planned residual")
+
+
+def test_planned_conv_on_own_order(oracle):
+    """The planned conv on rows that keep their own order (3 levels of C2S
+    children, 170 k rows) equals the oracle on 2,000 sampled rows and the
+    unplanned conv."""
+    coords = c2s_children(3, frac=0.45)
+    rng = np.random.default_rng(31)
+    C = 64
+    cfg = F.SparseSubmConvConfig(C, C)
+    x = rbf(synth.normal_f32(rng, (len(coords), C)))
+    w = rbf(synth.conv_weight(rng, C, 27, C, 1 / np.sqrt(27 * C)))
+    b = synth.normal_f32(rng, C, 0.1)
+    cd = dev(coords)
+    nbr = F.neighbor_rows_tensor_from_coords_tensor(cfg, cd)
+    plan = F.build_conv_plan(cfg, cd, nbr)
+    assert plan.to_host()["grid_mode"] == 2
+    wd = bf16_dev(w)
+    got = F.sparse_subm_conv_forward(cfg, bf16_dev(x), nbr, wd, dev(b), plan=plan,
+                                     packed_weight=F.pack_conv_weight(cfg, wd)).float().cpu().numpy()
+    ref = F.sparse_subm_conv_forward(cfg, bf16_dev(x), nbr, wd, dev(b)).float().cpu().numpy()
+    rows = sample_rows(len(coords), rng, 2000, plan=plan)
+    exp = oracle.conv_gemm_f64(ocfg(oracle, cfg), w, b, x, nbr.cpu().numpy()[rows])
+    assert_close(got[rows], exp, TOL_BF16, "planned conv, own order")
+    assert_close(got, ref, TOL_BF16, "planned vs unplanned")
 
 
 def test_planned_overflow_tiles_and_query_subset(oracle):
