@@ -687,9 +687,21 @@ __device__ inline int tile_scan_excl(int x, int *s_wave, int &total)
 //  * bitmap path (the neighbours span at most kBitmapBits row indices, the
 //    usual case for brick-ordered rows): one bit per row index in LDS, then
 //    a per-word prefix of popcounts; rank = prefix + popcount below the bit.
+//  * paged bitmap (a wider span, but within kPages pages of kPageRows rows):
+//    the same over the tile's pages laid side by side in page order.
 //  * otherwise: an LDS hash table of the distinct rows, sorted (bitonic).
 constexpr int kBitmapWords = 4096;  // 131072 row indices
 constexpr int kBitmapBits = kBitmapWords * 32;
+// Paged bitmap: neighbour rows wider apart than kBitmapBits (rows in octree
+// or coarse-brick order put the x-adjacent neighbours ~100,000 rows away)
+// but inside at most kPages pages of kPageRows rows get those pages of the
+// bitmap side by side in page order instead of one contiguous window; an
+// LDS hash of the page ids finds them, and a page's rank is the number of
+// smaller ids among them.
+constexpr int kPageShift = 12;
+constexpr int kPageRows = 1 << kPageShift;               // 128 bitmap words
+constexpr int kPages = kBitmapBits / kPageRows;          // 32
+constexpr int kPageSlots = 2 * kPages;                   // page-id hash table
 
 __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
 {
@@ -700,6 +712,10 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
     __shared__ int32_t s_halo[kPlanHaloMax];        // the halo rows (bitmap path)
     __shared__ int s_wave[kTileThreads / 64];
     __shared__ int s_mm[2][kTileThreads / 64];
+    __shared__ int32_t s_pkey[kPageSlots];  // paged: page ids (relative to lo), -1 empty
+    __shared__ int32_t s_prank[kPageSlots]; // rank of the slot's page among the tile's pages
+    __shared__ int32_t s_pid[kPages];       // page id of rank r
+    __shared__ int s_npages, s_pfull;
     int32_t *s_key = reinterpret_cast<int32_t *>(s_bits);
     uint64_t *s_list = reinterpret_cast<uint64_t *>(s_pre);  // up to 1024 sorted entries
     static_assert(kHashSlots <= kBitmapWords, "hash table fits the bitmap array");
@@ -767,16 +783,84 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
     }
     int32_t *halo = a.halo + t * kPlanHaloMax;
     uint16_t *lm = a.lmap + t * K * kPlanTileRows + p;
-    const bool bitmap = hi < lo || (int64_t)hi - lo < (int64_t)kBitmapBits;
+    const bool window = hi < lo || (int64_t)hi - lo < (int64_t)kBitmapBits;
+    bool paged = false;
+    int np = 0;
+    if (!window) {
+        // The tile's distinct pages: an LDS hash of page ids (bounded probes;
+        // a page that finds no slot sends the tile to the hash path).
+        if (p < kPageSlots) s_pkey[p] = -1;
+        if (p == 0) {
+            s_npages = 0;
+            s_pfull = 0;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 32; ++k) {
+            if (v[k] < 0) continue;
+            const int32_t pg = (int32_t)((uint32_t)(v[k] - lo) >> kPageShift);
+            uint32_t h = ((uint32_t)pg * 0x9E3779B1u) >> 26;  // 6 bits: kPageSlots slots
+            bool placed = false;
+            for (int probe = 0; probe < kPageSlots && !placed; ++probe) {
+                int32_t cur = s_pkey[h];
+                if (cur == -1) {
+                    cur = atomicCAS(&s_pkey[h], -1, pg);
+                    if (cur == -1) atomicAdd(&s_npages, 1);
+                }
+                if (cur == -1 || cur == pg) placed = true;
+                h = (h + 1) & (kPageSlots - 1);
+            }
+            if (!placed) s_pfull = 1;
+        }
+        __syncthreads();
+        np = s_npages;
+        paged = !s_pfull && np <= kPages;
+        if (paged) {
+            // pages in increasing id order: rank = occupied slots with a smaller id
+            if (p < kPageSlots) {
+                const int32_t key = s_pkey[p];
+                if (key >= 0) {
+                    int r = 0;
+                    for (int q = 0; q < kPageSlots; ++q) {
+                        const int32_t o = s_pkey[q];
+                        r += (o >= 0 && o < key);
+                    }
+                    s_prank[p] = r;
+                    s_pid[r] = key;
+                }
+            }
+            __syncthreads();
+            // position: page rank * kPageRows + the row's offset in its page
+#pragma unroll
+            for (int k = 0; k < 32; ++k) {
+                if (v[k] < 0) continue;
+                const uint32_t d = (uint32_t)(v[k] - lo);
+                const int32_t pg = (int32_t)(d >> kPageShift);
+                uint32_t h = ((uint32_t)pg * 0x9E3779B1u) >> 26;
+                for (int probe = 0; probe < kPageSlots && s_pkey[h] != pg; ++probe) h = (h + 1) & (kPageSlots - 1);
+                v[k] = (s_prank[h] << kPageShift) | (int32_t)(d & (kPageRows - 1));
+            }
+        }
+    }
 
-    if (bitmap) {
+    if (window || paged) {
+        // v[k] := the neighbour's position in the bitmap (row - lo in one
+        // window; the paged position already); row_of inverts it.
+        if (window) {
+#pragma unroll
+            for (int k = 0; k < 32; ++k)
+                if (v[k] >= 0) v[k] -= lo;
+        }
+        auto row_of = [&](int32_t pos) {
+            return paged ? lo + (s_pid[pos >> kPageShift] << kPageShift) + (pos & (kPageRows - 1)) : lo + pos;
+        };
         // Only words [0, nw) can hold bits.
-        const int nw = hi < lo ? 0 : (int)(((int64_t)hi - lo) >> 5) + 1;
+        const int nw = paged ? np * (kPageRows / 32) : (hi < lo ? 0 : (int)(((int64_t)hi - lo) >> 5) + 1);
         for (int i = p; i < nw; i += kTileThreads) s_bits[i] = 0u;
         __syncthreads();
 #pragma unroll
         for (int k = 0; k < 32; ++k)
-            if (v[k] >= 0) atomicOr(&s_bits[(v[k] - lo) >> 5], 1u << ((v[k] - lo) & 31));
+            if (v[k] >= 0) atomicOr(&s_bits[v[k] >> 5], 1u << (v[k] & 31));
         __syncthreads();
         // Thread p owns `chunk` consecutive words, chunk odd so that the lanes
         // of a wave (stride chunk words) hit distinct LDS banks; first the
@@ -805,9 +889,9 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
             if (k >= K) break;
             uint16_t out = kPlanAbsent;
             if (v[k] >= 0) {
-                const int d = v[k] - lo, w = d >> 5;
+                const int d = v[k], w = d >> 5;
                 out = (uint16_t)(s_pre[w] + __builtin_popcount(s_bits[w] & ((1u << (d & 31)) - 1u)));
-                s_halo[out] = v[k];
+                s_halo[out] = row_of(d);
             }
             lm[k * kPlanTileRows] = out;
         }

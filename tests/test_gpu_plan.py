@@ -92,7 +92,7 @@ def c2s_children(levels, frac=0.5, seed=4):
 
 
 @pytest.mark.parametrize("which", ["config1", "random_batches", "clusters", "query_subset", "duplicates",
-                                   "wide_bbox", "c2s_3_levels", "c2s_2_levels"])
+                                   "wide_bbox", "c2s_3_levels", "c2s_2_levels", "slab"])
 def test_plan_structure(which):
     rng = np.random.default_rng(11)
     cfg = F.SparseSubmConvConfig(32, 32)
@@ -128,6 +128,13 @@ def test_plan_structure(which):
         q = len(coords) - 1000
     elif which == "c2s_2_levels":
         coords = c2s_children(2)
+    elif which == "slab":
+        # x-planes of 67,600 rows in (b, x, y, z) order: a tile's x-1 and x+1
+        # neighbours lie more than the LDS bitmap's 131,072 rows apart, in a
+        # few pages (the paged bitmap); some cells empty
+        g = np.stack(np.meshgrid(np.arange(4), np.arange(260), np.arange(260), indexing="ij"), -1).reshape(-1, 3)
+        g = g[rng.random(len(g)) < 0.9]
+        coords = np.concatenate([np.zeros((len(g), 1), np.int32), g.astype(np.int32)], 1)
     else:
         coords = synth.config1_coords()
         q = 9000
@@ -141,6 +148,10 @@ def test_plan_structure(which):
     if which == "c2s_3_levels":
         n_q = nbr.shape[0]
         assert np.array_equal(h["order"].ravel()[:n_q], np.arange(n_q))
+    if which == "slab":
+        spans = [h["halo"][t, h["tile_u"][t] - 1] - h["halo"][t, 0] for t in range(h["n_tiles"])
+                 if 0 < h["tile_u"][t] <= F.PLAN_HALO_MAX]
+        assert max(spans) > 131072 and h["n_overflow"] == 0
     if which == "clusters":
         assert h["n_overflow"] == h["n_tiles"]
     if which in ("duplicates", "config1"):
