@@ -27,7 +27,11 @@
 // a brick.  Rows that already come in the order of 3 or more C2S
 // subdivisions below a sorted set (the bbox pass tests it, as the map build
 // does) keep their own order: they are grouped by aligned 8^3 root cells,
-// Morton order inside, which is as compact, so steps 3-7 are skipped.  A bounding box too large for the grid falls back to a counting
+// Morton order inside, which is as compact, so steps 3-7 are skipped.
+// Rows sorted and unique in (b, x, y, z) (no duplicate to place) take one
+// occupancy bit per cell instead of the grid's row per cell: the bitmap
+// stays in L2, and each row finds its own position by popcounts.
+// A bounding box too large for the grid falls back to a counting
 // sort by brick (brick edge 2^s, the smallest s >= 3 with at most brick_cap
 // bricks): count, scan, scatter with wave-aggregated atomics, then each
 // brick's segment sorted by row index so that the order is deterministic.
@@ -266,6 +270,8 @@ struct GridGeom {
     int64_t blocks;  // 2048-cell blocks holding cells
 };
 
+// grid_cap: the most cells the layout holds (the u32 grid's capacity, or
+// bitmap_cells below for the occupancy bitmap).
 __device__ inline GridGeom grid_geom(const PlanHeader *h, int64_t grid_cap)
 {
     GridGeom g;
@@ -285,6 +291,21 @@ __device__ inline GridGeom grid_geom(const PlanHeader *h, int64_t grid_cap)
     g.cells = g.nb[0] * g.nb[1] * g.nb[2] * g.nb[3] * 512;
     g.blocks = (g.cells + kPlanGridBlock - 1) / kPlanGridBlock;
     return g;
+}
+
+// Occupancy-bitmap order (rows sorted and unique in (b, x, y, z)): one bit
+// per cell of the same brick-major layout, in the grid's words; a row's
+// position in the order is the number of occupied cells before its own,
+// from a prefix per 256-cell block (in the brick-count array) and one per
+// 65,536-cell group (gsum).  It holds 32 cells per grid word, as far as the
+// block prefixes fit the brick-count array.
+constexpr int kBitBlock = 256;      // cells per block prefix (8 words)
+constexpr int kBitGroup = 65536;    // cells per group prefix (256 blocks, one scan1 workgroup)
+
+__device__ inline int64_t bitmap_cells(const PlanArgs &a)
+{
+    const int64_t by_words = 32 * a.grid_cap, by_prefix = kBitBlock * a.brick_cap;
+    return by_words < by_prefix ? by_words : by_prefix;
 }
 
 __device__ inline int64_t grid_cell(const GridGeom &g, int4 c)
@@ -358,6 +379,21 @@ __global__ __launch_bounds__(kThreads) void plan_prep_kernel(PlanArgs a, int nbb
         for (int64_t i = tid; i < a.n_q; i += stride) a.order[i] = (int32_t)i;
         return;
     }
+    if (!(uns & 1u)) {
+        // sorted, unique rows: the occupancy bitmap (bits := 0, group flags := 0)
+        const GridGeom bg = grid_geom(&s_h, bitmap_cells(a));
+        if (bg.ok) {
+            if (tid == 0) {
+                a.hdr->grid_mode = 3;
+                a.hdr->brick_shift = 3;
+                a.hdr->n_bricks = (uint64_t)(bg.cells / 512);
+            }
+            uint4 *w4 = reinterpret_cast<uint4 *>(a.grid);  // cells / 32 words, a multiple of 16
+            for (int64_t i = tid; i < bg.cells / 128; i += stride) w4[i] = make_uint4(0, 0, 0, 0);
+            for (int64_t i = tid; i < (bg.cells + kBitGroup - 1) / kBitGroup; i += stride) a.gsum[i] = 0;
+            return;
+        }
+    }
     const GridGeom gg = grid_geom(&s_h, a.grid_cap);
     if (gg.ok) {
         if (tid == 0) {
@@ -386,6 +422,34 @@ __global__ __launch_bounds__(kThreads) void plan_prep_kernel(PlanArgs a, int nbb
 __global__ __launch_bounds__(kThreads) void plan_place_kernel(PlanArgs a)
 {
     if (a.hdr->grid_mode == 2) return;  // rows keep their own order
+    if (a.hdr->grid_mode == 3) {
+        // Sorted rows put runs of consecutive lanes on one word (a z-run
+        // inside a brick): a segmented OR over the lanes of each run, then
+        // one atomic per run (same-address atomics serialise).  A word seen
+        // again in a later run of the wave gets a second OR; ORs commute.
+        const GridGeom bg = grid_geom(a.hdr, bitmap_cells(a));
+        const int lane = threadIdx.x & 63;
+        const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+        for (int64_t w0 = (int64_t)blockIdx.x * blockDim.x + (threadIdx.x & ~63); w0 < a.n_q; w0 += stride) {
+            const int64_t i = w0 + lane;
+            const bool valid = i < a.n_q;
+            const int64_t cell = valid ? grid_cell(bg, a.coords[i]) : -1;
+            const int64_t w = valid ? cell >> 5 : -2 - lane;  // invalid lanes match nothing
+            uint32_t bits = valid ? 1u << (cell & 31) : 0u;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const uint32_t ob = __shfl_down(bits, d, 64);
+                const int64_t ow = __shfl_down(w, d, 64);
+                if (lane + d < 64 && ow == w) bits |= ob;
+            }
+            const int64_t wp = __shfl_up(w, 1, 64);
+            if (valid && (lane == 0 || wp != w)) {
+                atomicOr(&a.grid[w], bits);
+                a.gsum[cell / kBitGroup] = 1;  // the group holds a cell: scan1 reads it
+            }
+        }
+        return;
+    }
     if (a.hdr->grid_mode == 1) {
         const GridGeom gg = grid_geom(a.hdr, a.grid_cap);
         for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n_q;
@@ -459,6 +523,28 @@ __global__ __launch_bounds__(kThreads) void plan_scan1_kernel(PlanArgs a)
 {
     __shared__ int s_wave[kThreads / 64];
     if (a.hdr->grid_mode == 2) return;
+    if (a.hdr->grid_mode == 3) {
+        // group g (one workgroup): thread t counts block 256 g + t (8 words),
+        // block prefixes within the group -> counts, the group total -> gsum
+        static_assert(kBitGroup == kBitBlock * kThreads, "one block per thread");
+        const GridGeom bg = grid_geom(a.hdr, bitmap_cells(a));
+        const int64_t g = blockIdx.x;
+        if (g * kBitGroup >= bg.cells || a.gsum[g] == 0) return;  // no cell placed: stays 0
+        const int64_t b = g * kThreads + threadIdx.x;
+        int cnt = 0;
+        if (b * kBitBlock < bg.cells) {
+            const uint4 *w4 = reinterpret_cast<const uint4 *>(a.grid + b * (kBitBlock / 32));
+            const uint4 u0 = w4[0], u1 = w4[1];
+            cnt = __builtin_popcount(u0.x) + __builtin_popcount(u0.y) + __builtin_popcount(u0.z) +
+                  __builtin_popcount(u0.w) + __builtin_popcount(u1.x) + __builtin_popcount(u1.y) +
+                  __builtin_popcount(u1.z) + __builtin_popcount(u1.w);
+        }
+        int total;
+        const int ex = block_scan_excl(cnt, s_wave, total);
+        if (b * kBitBlock < bg.cells) a.counts[b] = ex;
+        if (threadIdx.x == 0) a.gsum[g] = total;
+        return;
+    }
     if (a.hdr->grid_mode == 1) {
         const int64_t nblk = a.grid_cap / kPlanGridBlock;
         const GridGeom gg = grid_geom(a.hdr, a.grid_cap);
@@ -527,6 +613,12 @@ __global__ __launch_bounds__(kThreads) void plan_scan2_kernel(PlanArgs a)
 {
     __shared__ int s_wave[kThreads / 64];
     if (a.hdr->grid_mode == 2) return;
+    if (a.hdr->grid_mode == 3) {
+        const GridGeom bg = grid_geom(a.hdr, bitmap_cells(a));
+        const int total = block_scan_array(a.gsum, (bg.cells + kBitGroup - 1) / kBitGroup, s_wave);
+        if (threadIdx.x == 0) a.hdr->n_unique = total;
+        return;
+    }
     const bool grid = a.hdr->grid_mode == 1;
     if (!grid && a.hdr->brick_shift < 0) return;
     int32_t *arr = grid ? a.gsum : a.bsum;
@@ -549,6 +641,25 @@ __global__ __launch_bounds__(kThreads) void plan_emit_kernel(PlanArgs a)
 {
     __shared__ int s_wave[kThreads / 64];
     if (a.hdr->grid_mode == 2) return;
+    if (a.hdr->grid_mode == 3) {
+        // each row's position: group prefix + block prefix + the occupied
+        // cells before its own in the block (at most 8 words)
+        const GridGeom bg = grid_geom(a.hdr, bitmap_cells(a));
+        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n_q;
+             i += (int64_t)gridDim.x * blockDim.x) {
+            const int64_t cell = grid_cell(bg, a.coords[i]);
+            const int64_t b = cell / kBitBlock;
+            const uint32_t *bw = a.grid + b * (kBitBlock / 32);
+            const int wi = (int)((cell >> 5) & (kBitBlock / 32 - 1));
+            int before = 0;
+#pragma unroll
+            for (int w = 0; w < kBitBlock / 32; ++w)
+                if (w < wi) before += __builtin_popcount(bw[w]);
+            before += __builtin_popcount(bw[wi] & ((1u << (cell & 31)) - 1u));
+            a.order[(int64_t)a.gsum[cell / kBitGroup] + a.counts[b] + before] = (int32_t)i;
+        }
+        return;
+    }
     if (a.hdr->grid_mode == 1) {
         const int64_t nblk = a.grid_cap / kPlanGridBlock;
         const GridGeom gg = grid_geom(a.hdr, a.grid_cap);

@@ -55,7 +55,8 @@ struct alignas(16) PlanHeader {
     uint64_t n_bricks;
     uint32_t status;
     int32_t grid_mode;  // 1: occupancy-grid order, 0: counting-sort fallback,
-                        // 2: the rows' own order (octree order of >= 3 levels)
+                        // 2: the rows' own order (octree order of >= 3 levels),
+                        // 3: occupancy-bitmap order (sorted, unique rows)
     int32_t n_unique;   // grid mode: occupied cells (distinct coords)
     int32_t n_extras;   // grid mode: rows of duplicated coords
     uint32_t pad[42];

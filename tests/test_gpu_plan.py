@@ -142,9 +142,16 @@ def test_plan_structure(which):
     nbr = F.neighbor_rows_tensor_from_coords_tensor(cfg, cd, query_rows=q)
     plan = F.build_conv_plan(cfg, cd, nbr)
     h = check_plan(plan, nbr.cpu().numpy(), len(coords))
-    # 2 C2S levels over config 1 (234 k rows in a 256^3 box) exceed the grid's
-    # 16 cells per row: the counting-sort order
-    assert h["grid_mode"] == {"wide_bbox": 0, "c2s_2_levels": 0, "c2s_3_levels": 2}.get(which, 1)
+    # rows sorted and unique in (b, x, y, z): the occupancy bitmap (3); other
+    # orders the grid (1); 2 C2S levels over config 1 (234 k rows in a 256^3
+    # box) exceed the grid's 16 cells per row: the counting sort (0); 3 levels
+    # keep their own order (2)
+    qc = coords[:nbr.shape[0]].astype(np.int64)
+    key = ((qc[:, 0] * 4096 + qc[:, 1]) * 4096 + qc[:, 2]) * 4096 + qc[:, 3]
+    sorted_unique = bool(np.all(np.diff(key) > 0))
+    expect = {"wide_bbox": 0, "c2s_2_levels": 0, "c2s_3_levels": 2}.get(which, 3 if sorted_unique else 1)
+    assert h["grid_mode"] == expect, (h["grid_mode"], expect)
+    assert which not in ("config1", "slab", "query_subset") or expect == 3
     if which == "c2s_3_levels":
         n_q = nbr.shape[0]
         assert np.array_equal(h["order"].ravel()[:n_q], np.arange(n_q))
