@@ -161,14 +161,16 @@ def cpu_baseline(coords, x_f32, w1, w2, sample_rows):
     }
 
 
-def config_components(dev, steps: int = 5):
+def config_components(dev, st=None, steps: int = 5):
     """The other BASELINE configs on this GPU, for the record (parity cases,
     not the headline): config 2's planned 3x3x3 conv (C = 256, bf16), config
     4's 2x2x2 transposed upsample (a 1x1x1 conv with the child scatter) then
     the children's map + plan + 3x3x3 conv (C = 256), and config 5's int8
     decoder stack (3 stages of 2 residual blocks + fused C2S upsample,
-    512 -> 64 channels), and the neighbour map in its dense-grid and hash
-    table modes.  ms per call, after one untimed call."""
+    512 -> 64 channels); the neighbour map in its other table modes; the C2S
+    compaction of config 4's parents; a ConvNeXt block at config 2's shape;
+    and config 3's conv in f16 (st: the config-3 step, whose map and plan
+    it reuses).  ms per call, after one untimed call."""
     import numpy as np
     import torch
 
@@ -240,6 +242,52 @@ def config_components(dev, steps: int = 5):
                       "note": "18 convs (int8 weights, bf16 activations), 4 maps + plans, fused C2S upsamples; "
                               "includes the host syncs of the child counts"}
     del stack, res, x5
+
+    # C2S compaction (sc_subdivision_build_indexed) of config 4's parents:
+    # HBM-bound; algorithmic bytes = mask + parent coords read, child coords,
+    # linear_idx and the [P, 8] child-row table written
+    A = int(cc.shape[0])
+    P = len(parents)
+    ms_sub = events_ms(lambda: F.subdivision_build_indexed(pc, mask=mask), steps, 2)
+    sub_bytes = P * 8 + P * 16 + A * (16 + 4) + P * 32
+    out["c2s_compaction"] = {"parents": P, "children": A, "ms": ms_sub,
+                             "gbps": sub_bytes / (ms_sub * 1e-3) / 1e9,
+                             "note": "device kernels only (events); the call also reads the child count back"}
+
+    # ConvNeXt block (conv -> LN(affine) -> mlp_0 -> SiLU -> mlp_2 + x) at
+    # config 2's shape, C = 256, hidden 4C, bf16
+    C, H = 256, 1024
+    blk = D.ConvNeXtBlock(
+        D.ConvLayer(F.SparseSubmConvConfig(C, C), bf(synth.conv_weight(rng, C, 27, C, 1 / np.sqrt(27 * C))),
+                    torch.zeros(C, dtype=torch.float32, device=dev)),
+        torch.ones(C, dtype=torch.float32, device=dev), torch.zeros(C, dtype=torch.float32, device=dev),
+        D.LinearLayer(bf(synth.normal_f32(rng, (H, C), 1 / np.sqrt(C))), torch.zeros(H, dtype=torch.float32,
+                                                                                    device=dev)),
+        D.LinearLayer(bf(synth.normal_f32(rng, (C, H), 1 / np.sqrt(H))), torch.zeros(C, dtype=torch.float32,
+                                                                                    device=dev)))
+    ms_cn = events_ms(lambda: blk(x2, nb), steps, 2)
+    fl_cn = 2.0 * P2 * C * C + 2 * 2.0 * len(c2) * C * H
+    out["convnext_block"] = {"voxels": len(c2), "channels": C, "hidden": H, "ms": ms_cn,
+                             "useful_tflops": fl_cn / (ms_cn * 1e-3) / 1e12}
+
+    # config 3's conv (-> LN -> SiLU, planned) in f16 on the step's map and plan
+    if st is not None:
+        x16 = st.x.to(torch.float16)
+        w16 = st.w1_d.to(torch.float16)
+        wp16 = F.pack_conv_weight(st.cfg, w16)
+        h16 = torch.empty_like(x16)
+        P3 = int((st.nbr >= 0).sum().item())
+        ms16 = events_ms(lambda: F.sparse_subm_conv_forward(st.cfg, x16, st.nbr, w16, st.bias, out=h16,
+                                                            layer_norm=True, ln_eps=1e-6, silu=True,
+                                                            plan=st.plan, packed_weight=wp16), steps, 2)
+        # the bf16 conv under the same protocol (back to back, outside the
+        # step: sustained MFMA load lowers the clock, so both run slower here
+        # than the conv inside the step)
+        ms_bf = events_ms(st.conv1, steps, 2)
+        out["config3_f16_conv"] = {"ms": ms16, "useful_tflops": 2.0 * P3 * st.C * st.C / (ms16 * 1e-3) / 1e12,
+                                   "frac_of_fp16_peak": 2.0 * P3 * st.C * st.C / (ms16 * 1e-3) / 1e12 /
+                                   PEAK_BF16_TFLOPS, "bf16_ms_same_protocol": ms_bf,
+                                   "note": "conv -> LN -> SiLU, planned, back to back outside the step"}
 
     # The neighbour map in its other table modes: config 3's coords shuffled
     # (unsorted rows: the dense grid) and config 5's last C2S child set
@@ -398,6 +446,9 @@ def main():
         e[3].record()
     torch.cuda.synchronize()
     part = [sum(e[j].elapsed_time(e[j + 1]) for e in ev) / args.steps for j in range(3)]
+    per_step = sorted(e[0].elapsed_time(e[3]) for e in ev)
+    step_median = per_step[len(per_step) // 2]
+    step_p90 = per_step[min(len(per_step) - 1, int(0.9 * len(per_step)))]
     ms_map_plan, ms_conv1, ms_conv2 = part
     ms_conv = (ms_conv1 + ms_conv2) / 2.0
     # the map and the plan on their own (the map's GB/s), then the unfused LN
@@ -424,7 +475,7 @@ def main():
     configs = None
     if not args.no_configs:
         print("[bench] configs 2 / 4 / 5 ...", file=sys.stderr, flush=True)
-        configs = config_components(dev)
+        configs = config_components(dev, st)
         print(f"[bench] configs: {json.dumps(configs)}", file=sys.stderr, flush=True)
     cpu = None
     if args.cpu_sample > 0:
@@ -453,6 +504,7 @@ def main():
                      "frac": conv_tflops / PEAK_BF16_TFLOPS, "traffic": traffic,
                      "traffic_source": f"profile-time figure, not measured in this run: {traffic_source}"},
         "components": {
+            "step_ms_median": step_median, "step_ms_p90": step_p90,
             "map_and_plan_ms": ms_map_plan, "map_build_ms": ms_map, "plan_build_ms": ms_plan,
             "conv_ms": ms_conv,
             "conv1_ln_silu_ms": ms_conv1, "conv2_residual_ms": ms_conv2,
