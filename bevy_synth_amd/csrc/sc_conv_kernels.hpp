@@ -1531,6 +1531,244 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
     }
 }
 
+// ----------------------------------------------------------- dense linear
+//
+// The dense layer out = x W^T + b (the decoder's linear layers: a 1x1x1 conv
+// without a map, query row r reading input row r) as an LDS-pipelined GEMM.
+// A tile of 256 rows x 128 output channels steps through the input channels
+// 32 at a time: each k-step's rows (256 x 64 B) and weights (128 channels x
+// 64 B of W [Cout][Cin], the reference layout) are DMA'd into one of three
+// LDS buffers two k-steps ahead, one barrier per k-step; waves 2 x 2 (128
+// rows x 64 channels each) read their MFMA fragments from LDS, 16-byte pieces
+// XOR-swizzled per row (wslot) so that the reads of 8 consecutive rows hit
+// distinct banks.  Same epilogue layout as the halo kernel: lane (l16, q4)
+// holds channels oc0 + 16 j + 4 q4 .. +4 of row row0 + 16 i + l16.
+template <typename TA, typename TO, bool kLN>
+__global__ __launch_bounds__(kThreads, 2) void dense_gemm_kernel(ConvArgs args)
+{
+    constexpr int kI = 8;                          // 16-row MFMA blocks per wave
+    constexpr int kRowsBytes = kTileRows * 64;     // one k-step of rows
+    constexpr int kWBytes = kBN * 64;              // one k-step of weights
+    constexpr int kStage = kRowsBytes + kWBytes;   // 24 KB
+    constexpr int kBuf = 3;
+    constexpr int kAInstr = kRowsBytes / 1024 / 4;  // 1 KB DMA instructions per wave and k-step
+    constexpr int kWInstr = kWBytes / 1024 / 4;
+    __shared__ __attribute__((aligned(16))) unsigned char s_buf[kBuf * kStage];
+    __shared__ float s_red[2][kTileRows];          // LayerNorm: per channel half, per tile row
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, q4 = lane >> 4;
+    const int rh = wave >> 1, ch = wave & 1;
+    // Block b (dealt to the XCDs in contiguous ranges) is column tile b % n_ct
+    // of row tile b / n_ct: a row tile's column tiles run together on one
+    // XCD, so its rows come from HBM once and from L2 for the other columns
+    // (otherwise each column tile re-reads every row from HBM).
+    const int n_ct = (args.cout_g + kBN - 1) / kBN;
+    const int b = tile_for_block(blockIdx.x, gridDim.x);
+    const int tile = b / n_ct;
+    const int64_t trow0 = (int64_t)tile * kTileRows;   // the tile's first row
+    const int o0 = (b % n_ct) * kBN;                   // the tile's first channel
+    const int cin = (int)args.cin;
+    const int nk = cin / 32;
+    const __amdgpu_buffer_rsrc_t a_rsrc =
+        make_rsrc(args.input, (uint32_t)(args.n_q * (int64_t)cin * (int64_t)sizeof(TA)));
+    const __amdgpu_buffer_rsrc_t w_rsrc =
+        make_rsrc(args.weight, (uint32_t)((int64_t)args.cout_g * cin * (int64_t)sizeof(TA)));
+
+    // DMA sources: instruction t of this wave fills LDS bytes [1 KB * (wave +
+    // 4 t), +1 KB) of the rows (or weights) region: 16 rows (channels) x 4
+    // slots; lane L writes row 16 (wave + 4 t) + L / 4, slot L % 4, and loads
+    // the logical piece stored there.  Rows past n_q and channels past Cout
+    // read zero.
+    uint32_t a_src[kAInstr], w_src[kWInstr];
+#pragma unroll
+    for (int t = 0; t < kAInstr; ++t) {
+        const int r = 16 * (wave + 4 * t) + (lane >> 2);
+        const int piece = wslot<64>(r, lane & 3);
+        const int64_t row = trow0 + r;
+        a_src[t] = row < args.n_q ? (uint32_t)((row * cin + 8 * piece) * (int64_t)sizeof(TA)) : kOobOffset;
+    }
+#pragma unroll
+    for (int t = 0; t < kWInstr; ++t) {
+        const int c = 16 * (wave + 4 * t) + (lane >> 2);
+        const int piece = wslot<64>(c, lane & 3);
+        const int o = o0 + c;
+        w_src[t] = o < args.cout_g ? (uint32_t)(((int64_t)o * cin + 8 * piece) * (int64_t)sizeof(TA)) : kOobOffset;
+    }
+    auto dma = [&](int k, int buf) {
+        const uint32_t step = (uint32_t)(k * 32 * (int)sizeof(TA));  // an out-of-range offset stays out of range
+        unsigned char *base = s_buf + buf * kStage;
+#pragma unroll
+        for (int t = 0; t < kAInstr; ++t)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                a_rsrc, (__attribute__((address_space(3))) void *)(base + 1024 * (wave + 4 * t)), 16,
+                a_src[t] + step, 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < kWInstr; ++t)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                w_rsrc, (__attribute__((address_space(3))) void *)(base + kRowsBytes + 1024 * (wave + 4 * t)), 16,
+                w_src[t] + step, 0, 0, 0);
+    };
+
+    f32x4 acc[kI][4];
+#pragma unroll
+    for (int i = 0; i < kI; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[i][j][e] = 0.f;
+
+    auto compute = [&](int buf) {
+        const unsigned char *base = s_buf + buf * kStage;
+        uint4 x[kI], w[4];
+#pragma unroll
+        for (int i = 0; i < kI; ++i) {
+            const int r = 128 * rh + 16 * i + l16;
+            x[i] = *reinterpret_cast<const uint4 *>(base + r * 64 + wslot<64>(r, q4) * 16);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int c = 64 * ch + 16 * j + l16;
+            w[j] = *reinterpret_cast<const uint4 *>(base + kRowsBytes + c * 64 + wslot<64>(c, q4) * 16);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < kI; ++i) acc[i][j] = mfma_16x16x32<TA>(w[j], x[i], acc[i][j]);
+    };
+    constexpr int kPerStep = kAInstr + kWInstr;  // DMA instructions per wave and k-step
+    // k-step k: buffer k % 3.  Top of step k: k and k + 1 are in flight;
+    // wait for k, barrier (every wave is done with k - 1's buffer and every
+    // DMA of k has landed), start k + 2 into k - 1's buffer, compute k.
+    if (nk > 0) dma(0, 0);
+    if (nk > 1) dma(1, 1);
+    for (int k0 = 0; k0 < nk; k0 += kBuf) {
+#pragma unroll
+        for (int u = 0; u < kBuf; ++u) {
+            const int k = k0 + u;
+            if (k >= nk) break;
+            if (k + 1 < nk)
+                wait_vmcnt<kPerStep>();
+            else
+                wait_vmcnt<0>();
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+            __builtin_amdgcn_s_barrier();
+            if (k + 2 < nk) dma(k + 2, (u + 2) % kBuf);
+            compute(u);
+        }
+    }
+
+    // ---- epilogue: bias, LayerNorm over the row (the two channel halves meet
+    //      in LDS), SiLU, residual, stores.
+    const int oc0 = o0 + 64 * ch;
+    const int64_t row0 = trow0 + 128 * rh;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int o = oc0 + j * 16 + 4 * q4 + e;
+            const bool ok = o < args.cout_g;
+            const float bias = (args.bias && ok) ? args.bias[o] : 0.f;
+#pragma unroll
+            for (int i = 0; i < kI; ++i) acc[i][j][e] = ok ? acc[i][j][e] + bias : 0.f;
+        }
+    if constexpr (kLN) {
+        const int trow = 128 * rh + l16;  // tile row of block 0
+        auto row_total = [&](float(&part)[kI]) {
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < kI; ++i)
+                if (q4 == 0) s_red[ch][trow + 16 * i] = part[i];
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < kI; ++i) part[i] = s_red[0][trow + 16 * i] + s_red[1][trow + 16 * i];
+        };
+        const float inv_c = 1.0f / (float)args.cout_g;
+        float mean[kI], inv_std[kI], part[kI];
+#pragma unroll
+        for (int i = 0; i < kI; ++i) {
+            float sum = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) sum += acc[i][j][e];
+            sum += __shfl_xor(sum, 16, 64);
+            sum += __shfl_xor(sum, 32, 64);
+            part[i] = sum;
+        }
+        row_total(part);
+#pragma unroll
+        for (int i = 0; i < kI; ++i) mean[i] = part[i] * inv_c;
+#pragma unroll
+        for (int i = 0; i < kI; ++i) {
+            float qv = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int o = oc0 + j * 16 + 4 * q4 + e;
+                    const float d = acc[i][j][e] - mean[i];
+                    qv += o < args.cout_g ? d * d : 0.f;
+                }
+            qv += __shfl_xor(qv, 16, 64);
+            qv += __shfl_xor(qv, 32, 64);
+            part[i] = qv;
+        }
+        row_total(part);
+#pragma unroll
+        for (int i = 0; i < kI; ++i) inv_std[i] = rsqrt_f32(part[i] * inv_c + args.ln_eps);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int o = oc0 + j * 16 + 4 * q4 + e;
+                const bool ok = o < args.cout_g;
+                const float lw = (args.ln_w && ok) ? args.ln_w[o] : 1.f;
+                const float lb = (args.ln_b && ok) ? args.ln_b[o] : 0.f;
+#pragma unroll
+                for (int i = 0; i < kI; ++i) acc[i][j][e] = (acc[i][j][e] - mean[i]) * inv_std[i] * lw + lb;
+            }
+    }
+    TO *__restrict__ out = static_cast<TO *>(args.out);
+    const TO *__restrict__ res = static_cast<const TO *>(args.residual);
+    const bool vec_ok = args.vec_out != 0;
+#pragma unroll
+    for (int i = 0; i < kI; ++i) {
+        const int64_t r = row0 + 16 * i + l16;
+        if (r >= args.n_q) continue;
+        const int64_t rowbase = r * args.cout;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int oc = oc0 + j * 16 + 4 * q4;
+            if (oc >= args.cout_g) continue;
+            float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+            if (args.silu) {
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc) v[cc] = silu_f32(v[cc]);
+            }
+            if (vec_ok && oc + 3 < args.cout_g) {
+                if (res) {
+                    float r4[4];
+                    Out4<TO>::unpack(*reinterpret_cast<const typename Out4<TO>::V *>(res + rowbase + oc), r4);
+#pragma unroll
+                    for (int cc = 0; cc < 4; ++cc) v[cc] += r4[cc];
+                }
+                *reinterpret_cast<typename Out4<TO>::V *>(out + rowbase + oc) = Out4<TO>::pack(v);
+            } else {
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc) {
+                    if (oc + cc >= args.cout_g) continue;
+                    float t = v[cc];
+                    if (res) t += load_as_f32<TO>(res, rowbase + oc + cc);
+                    store_from_f32<TO>(out, rowbase + oc + cc, t);
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
 // --------------------------------------------------------- weight packing
 //
 // The halo-staged kernel's weight layout: per (group g, 128-channel output
@@ -1694,6 +1932,17 @@ int launch_conv(const ConvArgs &a, int groups, bool mfma, const void *plan, hipS
                 b.tile_count = &pv.hdr->n_overflow;
                 dim3 fgrid((unsigned)(L.n_tiles * kSubTiles), (unsigned)ntile, (unsigned)groups);
                 launch_v2<TA, TW, TO, true>(b, fgrid, s);
+            } else if (sizeof(TW) == 2 && !a.map && a.K == 1 && groups == 1 && a.cin % 32 == 0 && !a.scatter_rows &&
+                       !a.skip_idx) {
+                // the dense linear: contiguous rows, reference-layout weights;
+                // row tile x column tile flattened, column tile fastest
+                if (tiles * ntile > INT32_MAX) return fail(SC_ERR_OVERFLOW, "dense linear grid overflow");
+                const dim3 dgrid((unsigned)(tiles * ntile), 1, 1);
+                if (a.ln)
+                    dense_gemm_kernel<TA, TO, true><<<dgrid, kThreads, 0, s>>>(a);
+                else
+                    dense_gemm_kernel<TA, TO, false><<<dgrid, kThreads, 0, s>>>(a);
+                SC_LAUNCH_CHECK("dense_gemm_kernel launch");
             } else {
                 launch_v2<TA, TW, TO, false>(a, grid, s);
             }
