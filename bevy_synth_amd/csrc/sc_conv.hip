@@ -284,8 +284,8 @@ extern "C" int sc_linear_forward(int act_dtype, const void *d_input, int64_t row
                                  sc_stream stream)
 {
     clear_error();
-    if (epi && (epi->child_rows || epi->skip_index))
-        return fail(SC_ERR_UNSUPPORTED, "linear: the C2S epilogue forms belong to the sparse conv");
+    if (epi && epi->skip_index)
+        return fail(SC_ERR_UNSUPPORTED, "linear: the parent skip belongs to the sparse conv");
     sc_conv_config c{};
     c.in_channels = in_channels;
     c.out_channels = out_channels;

@@ -1533,8 +1533,10 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
 
 // ----------------------------------------------------------- dense linear
 //
-// The dense layer out = x W^T + b (the decoder's linear layers: a 1x1x1 conv
-// without a map, query row r reading input row r) as an LDS-pipelined GEMM.
+// The dense layer out = x W^T + b (the decoder's linear layers, and the 2x2x2
+// transposed upsample as a linear Cin -> 8 Cout with the child scatter: a
+// 1x1x1 conv without a map, query row r reading input row r) as an
+// LDS-pipelined GEMM.
 // A tile of 256 rows x 128 output channels steps through the input channels
 // 32 at a time: each k-step's rows (256 x 64 B) and weights (128 channels x
 // 64 B of W [Cout][Cin], the reference layout) are DMA'd into one of three
@@ -1659,8 +1661,9 @@ __global__ __launch_bounds__(kThreads, 2) void dense_gemm_kernel(ConvArgs args)
         }
     }
 
-    // ---- epilogue: bias, LayerNorm over the row (the two channel halves meet
-    //      in LDS), SiLU, residual, stores.
+    // ---- epilogue: bias, LayerNorm (over the row or one child; the two
+    //      channel halves meet in LDS), SiLU, residual, stores (row-major, or
+    //      each child's slice to its row in the child scatter).
     const int oc0 = o0 + 64 * ch;
     const int64_t row0 = trow0 + 128 * rh;
 #pragma unroll
@@ -1684,7 +1687,10 @@ __global__ __launch_bounds__(kThreads, 2) void dense_gemm_kernel(ConvArgs args)
 #pragma unroll
             for (int i = 0; i < kI; ++i) part[i] = s_red[0][trow + 16 * i] + s_red[1][trow + 16 * i];
         };
-        const float inv_c = 1.0f / (float)args.cout_g;
+        // ln_group channels per normalised row: the whole row (<= 128), or in
+        // the child scatter one child's 128 (the tile) or 64 (one wave's half)
+        const float inv_c = 1.0f / (float)args.ln_group;
+        const bool pair = args.ln_group > 64;  // the two channel halves meet
         float mean[kI], inv_std[kI], part[kI];
 #pragma unroll
         for (int i = 0; i < kI; ++i) {
@@ -1697,7 +1703,7 @@ __global__ __launch_bounds__(kThreads, 2) void dense_gemm_kernel(ConvArgs args)
             sum += __shfl_xor(sum, 32, 64);
             part[i] = sum;
         }
-        row_total(part);
+        if (pair) row_total(part);
 #pragma unroll
         for (int i = 0; i < kI; ++i) mean[i] = part[i] * inv_c;
 #pragma unroll
@@ -1715,7 +1721,7 @@ __global__ __launch_bounds__(kThreads, 2) void dense_gemm_kernel(ConvArgs args)
             qv += __shfl_xor(qv, 32, 64);
             part[i] = qv;
         }
-        row_total(part);
+        if (pair) row_total(part);
 #pragma unroll
         for (int i = 0; i < kI; ++i) inv_std[i] = rsqrt_f32(part[i] * inv_c + args.ln_eps);
 #pragma unroll
@@ -1724,8 +1730,9 @@ __global__ __launch_bounds__(kThreads, 2) void dense_gemm_kernel(ConvArgs args)
             for (int e = 0; e < 4; ++e) {
                 const int o = oc0 + j * 16 + 4 * q4 + e;
                 const bool ok = o < args.cout_g;
-                const float lw = (args.ln_w && ok) ? args.ln_w[o] : 1.f;
-                const float lb = (args.ln_b && ok) ? args.ln_b[o] : 0.f;
+                const int og = o % args.ln_group;  // channel within the LayerNorm group
+                const float lw = (args.ln_w && ok) ? args.ln_w[og] : 1.f;
+                const float lb = (args.ln_b && ok) ? args.ln_b[og] : 0.f;
 #pragma unroll
                 for (int i = 0; i < kI; ++i) acc[i][j][e] = (acc[i][j][e] - mean[i]) * inv_std[i] * lw + lb;
             }
@@ -1747,7 +1754,9 @@ __global__ __launch_bounds__(kThreads, 2) void dense_gemm_kernel(ConvArgs args)
 #pragma unroll
                 for (int cc = 0; cc < 4; ++cc) v[cc] = silu_f32(v[cc]);
             }
-            if (vec_ok && oc + 3 < args.cout_g) {
+            if (args.scatter_rows) {
+                c2s_store4<TO, false>(args, C2SRow{nullptr}, r, oc, min(4, args.cout_g - oc), v, vec_ok);
+            } else if (vec_ok && oc + 3 < args.cout_g) {
                 if (res) {
                     float r4[4];
                     Out4<TO>::unpack(*reinterpret_cast<const typename Out4<TO>::V *>(res + rowbase + oc), r4);
@@ -1932,8 +1941,7 @@ int launch_conv(const ConvArgs &a, int groups, bool mfma, const void *plan, hipS
                 b.tile_count = &pv.hdr->n_overflow;
                 dim3 fgrid((unsigned)(L.n_tiles * kSubTiles), (unsigned)ntile, (unsigned)groups);
                 launch_v2<TA, TW, TO, true>(b, fgrid, s);
-            } else if (sizeof(TW) == 2 && !a.map && a.K == 1 && groups == 1 && a.cin % 32 == 0 && !a.scatter_rows &&
-                       !a.skip_idx) {
+            } else if (sizeof(TW) == 2 && !a.map && a.K == 1 && groups == 1 && a.cin % 32 == 0 && !a.skip_idx) {
                 // the dense linear: contiguous rows, reference-layout weights;
                 // row tile x column tile flattened, column tile fastest
                 if (tiles * ntile > INT32_MAX) return fail(SC_ERR_OVERFLOW, "dense linear grid overflow");

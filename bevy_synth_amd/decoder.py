@@ -223,17 +223,16 @@ def transposed_upsample(parent_coords: torch.Tensor, parent_feats: torch.Tensor,
                         conv1x1: ConvLayer, mask: torch.Tensor
                         ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """2x2x2 stride-2 transposed sparse conv as C2S: a 1x1x1 conv Cin -> 8*Cout
-    on the parents whose epilogue writes each active child's Cout slice to the
-    child's row (no [P, 8*Cout] tensor).  Returns (child coords, child feats,
-    linear_idx)."""
-    K = conv1x1.cfg.kernel_d * conv1x1.cfg.kernel_h * conv1x1.cfg.kernel_w
-    if K != 1:
-        raise ValueError("transposed_upsample needs a 1x1x1 conv")
+    on the parents (parent p's own row: the dense linear, no map) whose
+    epilogue writes each active child's Cout slice to the child's row (no
+    [P, 8*Cout] tensor).  Returns (child coords, child feats, linear_idx)."""
+    cfg = conv1x1.cfg
+    if cfg.kernel_d * cfg.kernel_h * cfg.kernel_w != 1 or cfg.groups != 1:
+        raise ValueError("transposed_upsample needs a 1x1x1 conv with groups == 1")
     child_coords, linear_idx, child_rows = subdivision_build_indexed(parent_coords, mask=mask)
-    P = parent_coords.shape[0]
-    ident = torch.arange(P, dtype=torch.int32, device=parent_coords.device).reshape(P, 1)
-    h_up = conv1x1(parent_feats, ident, out_dtype=parent_feats.dtype, child_rows=child_rows,
-                   n_child_rows=child_coords.shape[0])
+    w = conv1x1.weight.reshape(cfg.out_channels, cfg.in_channels)
+    h_up = linear_forward(parent_feats, w, conv1x1.bias, conv1x1.w_scale, out_dtype=parent_feats.dtype,
+                          child_rows=child_rows, n_child_rows=child_coords.shape[0])
     return child_coords, h_up, linear_idx
 
 

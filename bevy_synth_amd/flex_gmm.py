@@ -503,30 +503,53 @@ def linear_forward(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.T
                    out_dtype: Optional[torch.dtype] = None, silu: bool = False, layer_norm: bool = False,
                    ln_weight: Optional[torch.Tensor] = None, ln_bias: Optional[torch.Tensor] = None,
                    ln_eps: float = 1e-6, out: Optional[torch.Tensor] = None,
-                   workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                   workspace: Optional[torch.Tensor] = None, child_rows: Optional[torch.Tensor] = None,
+                   n_child_rows: Optional[int] = None) -> torch.Tensor:
     """linear_forward_wgpu (burn_trellis sparse_decoder_wgpu_ops.rs:79-160) through
     sc_linear_forward: x [rows, Cin] @ weight[Cout, Cin]^T + bias, with the conv
     epilogue (LayerNorm over the row, SiLU, + residual) fused.  Same dtype rules
-    as sparse_subm_conv_forward."""
+    as sparse_subm_conv_forward.
+    ``child_rows`` [rows, 8] int32 (subdivision_build_indexed) makes this the
+    2x2x2 transposed upsample: row r's channels [c*C, (c+1)*C), C = Cout/8,
+    land in row child_rows[r, c] of an [n_child_rows, C] output (LayerNorm
+    per child, ln_weight / ln_bias then [C])."""
     _require_cuda("x", x)
     _require_cuda("weight", weight)
     rows, cin = x.shape
     if weight.dim() != 2 or weight.shape[1] != cin:
         raise SparseConvError(2, f"linear: invalid input channels {cin}, weight {tuple(weight.shape)}")
     cout = weight.shape[0]
-    for name, t in (("bias", bias), ("w_scale", w_scale), ("ln_weight", ln_weight), ("ln_bias", ln_bias)):
+    out_shape = (rows, cout)
+    if child_rows is not None:
+        _require_cuda("child_rows", child_rows)
+        if child_rows.dtype != torch.int32 or child_rows.shape != (rows, 8):
+            raise SparseConvError(2, "child_rows must be int32 [rows, 8]")
+        if n_child_rows is None or cout % 8:
+            raise SparseConvError(2, "child scatter needs n_child_rows and Cout = 8 * C")
+        if residual is not None:
+            raise SparseConvError(2, "linear: the child scatter takes no residual")
+        out_shape = (int(n_child_rows), cout // 8)
+    for name, t, n in (("bias", bias, cout), ("w_scale", w_scale, cout), ("ln_weight", ln_weight, out_shape[1]),
+                       ("ln_bias", ln_bias, out_shape[1])):
         if t is not None:
             _require_cuda(name, t)
-            if t.dtype != torch.float32 or t.numel() != cout:
-                raise SparseConvError(2, f"linear: {name} must be f32 [{cout}]")
+            if t.dtype != torch.float32 or t.numel() != n:
+                raise SparseConvError(2, f"linear: {name} must be f32 [{n}]")
     od = x.dtype if out_dtype is None else out_dtype
     if out is None:
-        out = torch.empty((rows, cout), dtype=od, device=x.device)
+        out = torch.empty(out_shape, dtype=od, device=x.device)
+    else:
+        _require_cuda("out", out)
+        if tuple(out.shape) != out_shape or out.dtype != od:
+            raise SparseConvError(2, "linear: out has the wrong shape or dtype")
     if residual is not None:
         _require_cuda("residual", residual)
         if residual.shape != (rows, cout) or residual.dtype != od:
             raise SparseConvError(2, "linear: residual must be [rows, Cout] in the output dtype")
     epi = _capi.ScConvEpilogue()
+    if child_rows is not None:
+        epi.child_rows = child_rows.data_ptr()
+        epi.n_child_rows = int(n_child_rows)
     epi.residual = None if residual is None else residual.data_ptr()
     epi.layer_norm = int(layer_norm)
     epi.ln_weight = None if ln_weight is None else ln_weight.data_ptr()

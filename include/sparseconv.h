@@ -232,8 +232,11 @@ int sc_conv_epilogue_workspace_size(const sc_conv_config *cfg, int act_dtype, in
  * LinearLayer layout), b [out_channels] f32 or NULL; dtypes as for
  * sc_subm_conv_forward_fused (bf16 / f16 / f32 activations; int8 weights
  * with d_w_scale).  It is that conv with a 1x1x1 kernel and no map (row r
- * reads row r), on the same MFMA tiles.  epi may be NULL; the C2S forms are
- * refused.
+ * reads row r), on the same MFMA tiles.  epi may be NULL.  epi->child_rows
+ * (no residual) makes it the 2x2x2 transposed upsample: rows are parents,
+ * out_channels = 8 x C, and slice c of row r lands in row child_rows[r * 8 +
+ * c] of an [n_child_rows][C] output (LayerNorm, when asked, per child);
+ * epi->skip_index, the conv2 form, is refused.
  */
 int sc_linear_forward(int act_dtype, const void *d_input, int64_t rows, int64_t in_channels,
                       int64_t out_channels, int w_dtype, const void *d_weight, const float *d_w_scale,

@@ -109,6 +109,38 @@ def test_conv1_child_scatter(oracle, cchild, ln, planned):
     assert_close(host(got), exp, TOL_BF16, f"child scatter C={cchild}")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("cin,cchild,ln", [(512, 256, False), (64, 64, True), (96, 128, True), (64, 256, True),
+                                           (32, 24, False)])
+def test_linear_child_scatter(oracle, dtype, cin, cchild, ln):
+    """The 2x2x2 transposed upsample's linear form (sc_linear_forward with
+    child_rows): row p's slice c of x W^T + b lands in row child_rows[p, c],
+    normalised over its C channels with a [C] affine when asked (C = 64 and
+    128 in the dense tile's epilogue for bf16 / f16, else on f32 staging)."""
+    coords, mask = _parents_and_mask(n=5000, frac=0.45, seed=cin + cchild)
+    rng = np.random.default_rng(cin * cchild)
+    cout = 8 * cchild
+    rnd = {torch.bfloat16: oracle.bf16_round, torch.float16: oracle.f16_round,
+           torch.float32: lambda a: np.asarray(a, np.float32)}[dtype]
+    x = rnd(synth.normal_f32(rng, (len(coords), cin)))
+    w = rnd(synth.normal_f32(rng, (cout, cin), 1 / np.sqrt(cin)))
+    b = synth.normal_f32(rng, cout, 0.5)
+    lw = synth.normal_f32(rng, cchild) if ln else None
+    lb = synth.normal_f32(rng, cchild) if ln else None
+    cc, li, rows = F.subdivision_build_indexed(dev(coords), mask=dev(mask))
+    A = cc.shape[0]
+    got = F.linear_forward(dev(x).to(dtype), dev(w).to(dtype), dev(b), layer_norm=ln,
+                           ln_weight=None if lw is None else dev(lw), ln_bias=None if lb is None else dev(lb),
+                           child_rows=rows, n_child_rows=A)
+    assert tuple(got.shape) == (A, cchild) and got.dtype == dtype
+    dense = x.astype(np.float64) @ w.T.astype(np.float64) + b
+    lin = li.cpu().numpy()
+    sl = dense.reshape(len(coords), 8, cchild)[lin // 8, lin % 8].astype(np.float32)
+    exp = oracle.layer_norm(sl, lw, lb, 1e-6) if ln else sl
+    tol = TOL_F32 if dtype == torch.float32 else TOL_BF16
+    assert_close(host(got), exp, tol, f"linear child scatter {cin}->8x{cchild}")
+
+
 @pytest.mark.parametrize("cp,cout", [(512, 256), (128, 64), (64, 128), (256, 32), (128, 32), (256, 96)])
 def test_conv2_parent_skip(oracle, cp, cout):
     """conv2 on the children + the channel-repeated parent skip in its epilogue
