@@ -179,6 +179,30 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t by
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
 }
 
+// The same buffer resource as make_rsrc as four raw words (base address low
+// 32 bits, high 16 bits with stride 0, size in bytes, the same format word),
+// for the inline-asm DMA below.
+typedef int32_t i32x4_rsrc __attribute__((ext_vector_type(4)));
+__device__ inline i32x4_rsrc rsrc_words(const void *base, uint32_t bytes)
+{
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    return i32x4_rsrc{(int32_t)(uint32_t)a, (int32_t)((a >> 32) & 0xFFFF), (int32_t)bytes, 0x00020000};
+}
+
+// One LDS DMA: lane L loads 16 bytes at byte offset voff of the buffer
+// (zero when out of range) into LDS bytes [lds + 16 L, +16); lds is uniform
+// (it goes to m0; the s_nop covers the m0-write-to-DMA hazard).  Written as
+// inline asm because the compiler, which cannot separate the DMA's LDS
+// writes from reads of other buffers, otherwise waits for every pending DMA
+// before each LDS read.  The compiler does not count these loads: the caller
+// waits for them (s_waitcnt vmcnt) before reading what they wrote, and
+// before the wave's end.
+__device__ inline void lds_dma16(i32x4_rsrc rsrc, uint32_t voff, uint32_t lds)
+{
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "{m0}"(lds)
+                 : "memory");
+}
+
 __device__ inline uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off)
 {
     const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);

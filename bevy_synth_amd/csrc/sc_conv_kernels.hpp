@@ -1537,80 +1537,99 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
 // transposed upsample as a linear Cin -> 8 Cout with the child scatter: a
 // 1x1x1 conv without a map, query row r reading input row r) as an
 // LDS-pipelined GEMM.
-// A tile of 256 rows x 128 output channels steps through the input channels
-// 32 at a time: each k-step's rows (256 x 64 B) and weights (128 channels x
-// 64 B of W [Cout][Cin], the reference layout) are DMA'd into one of three
-// LDS buffers two k-steps ahead, one barrier per k-step; waves 2 x 2 (128
-// rows x 64 channels each) read their MFMA fragments from LDS, 16-byte pieces
-// XOR-swizzled per row (wslot) so that the reads of 8 consecutive rows hit
-// distinct banks.  Same epilogue layout as the halo kernel: lane (l16, q4)
+// A tile of 256 rows x 64 kQ output channels steps through the input
+// channels 32 at a time: each k-step's rows (256 x 64 B) and weights (64 kQ
+// channels x 64 B of W [Cout][Cin], the reference layout) are DMA'd into one
+// of kBuf LDS buffers kBuf - 1 k-steps ahead, one barrier per k-step; waves
+// 2 x kQ (128 rows x 64 channels each) read their MFMA fragments from LDS,
+// 16-byte pieces XOR-swizzled per row (wslot) so that the reads of 8
+// consecutive rows hit distinct banks.  kQ = 2: 128-channel tiles, 3
+// buffers (72 KB), two workgroups per CU; kQ = 4 (Cout > 128): 256-channel
+// tiles, 4 buffers (128 KB), one workgroup of 8 waves per CU -- a third fewer
+// load bytes per MFMA, and the load path's rate here is set by the bytes in
+// flight per CU (under load an L2 access takes microseconds), which the LDS
+// budget fixes (the LayerNorm epilogue takes kQ = 2).  Same epilogue layout
+// as the halo kernel: lane (l16, q4)
 // holds channels oc0 + 16 j + 4 q4 .. +4 of row row0 + 16 i + l16.
-template <typename TA, typename TO, bool kLN>
-__global__ __launch_bounds__(kThreads, 2) void dense_gemm_kernel(ConvArgs args)
+template <int kQ>
+struct DenseShape {
+    static constexpr int kThreads = 128 * kQ;
+    static constexpr int kWaves = 2 * kQ;
+    static constexpr int kCols = 64 * kQ;         // output channels per tile
+    static constexpr int kBuf = kQ == 2 ? 3 : 4;  // LDS stage buffers
+    static constexpr int kBlocksPerCU = kQ == 2 ? 2 : 1;
+};
+
+template <typename TA, typename TO, bool kLN, int kQ>
+__global__ __launch_bounds__(DenseShape<kQ>::kThreads, DenseShape<kQ>::kBlocksPerCU) void dense_gemm_kernel(
+    ConvArgs args)
 {
-    constexpr int kI = 8;                          // 16-row MFMA blocks per wave
-    constexpr int kRowsBytes = kTileRows * 64;     // one k-step of rows
-    constexpr int kWBytes = kBN * 64;              // one k-step of weights
-    constexpr int kStage = kRowsBytes + kWBytes;   // 24 KB
-    constexpr int kBuf = 3;
-    constexpr int kAInstr = kRowsBytes / 1024 / 4;  // 1 KB DMA instructions per wave and k-step
-    constexpr int kWInstr = kWBytes / 1024 / 4;
-    __shared__ __attribute__((aligned(16))) unsigned char s_buf[kBuf * kStage];
-    __shared__ float s_red[2][kTileRows];          // LayerNorm: per channel half, per tile row
+    using S = DenseShape<kQ>;
+    constexpr int kI = 8;                             // 16-row MFMA blocks per wave
+    constexpr int kBuf = S::kBuf;
+    constexpr int kRowsBytes = kTileRows * 64;        // one k-step of rows
+    constexpr int kWBytes = S::kCols * 64;            // one k-step of weights
+    constexpr int kStage = kRowsBytes + kWBytes;      // 24 or 32 KB
+    constexpr int kAInstr = kRowsBytes / 1024 / S::kWaves;  // 1 KB DMA instructions per wave and k-step
+    constexpr int kWInstr = kWBytes / 1024 / S::kWaves;
+    constexpr int kPerStep = kAInstr + kWInstr;
+    static_assert(kAInstr * 1024 * S::kWaves == kRowsBytes && kWInstr * 1024 * S::kWaves == kWBytes, "DMA split");
+    // Separate LDS objects per buffer (the last unused when kBuf = 3).
+    __shared__ __attribute__((aligned(16))) unsigned char s_b0[kStage], s_b1[kStage], s_b2[kStage],
+        s_b3[kBuf > 3 ? kStage : 16];
+    __shared__ float s_red[kQ][kTileRows];            // LayerNorm: per channel quarter, per tile row
+    auto stage = [&](int u) -> unsigned char * {      // buffer u (a constant after unrolling)
+        return u == 0 ? s_b0 : (u == 1 ? s_b1 : (u == 2 ? s_b2 : s_b3));
+    };
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, q4 = lane >> 4;
-    const int rh = wave >> 1, ch = wave & 1;
+    const int rh = wave / kQ, qc = wave % kQ;         // row half, channel quarter
     // Block b (dealt to the XCDs in contiguous ranges) is column tile b % n_ct
     // of row tile b / n_ct: a row tile's column tiles run together on one
     // XCD, so its rows come from HBM once and from L2 for the other columns
     // (otherwise each column tile re-reads every row from HBM).
-    const int n_ct = (args.cout_g + kBN - 1) / kBN;
+    const int n_ct = (args.cout_g + S::kCols - 1) / S::kCols;
     const int b = tile_for_block(blockIdx.x, gridDim.x);
     const int tile = b / n_ct;
-    const int64_t trow0 = (int64_t)tile * kTileRows;   // the tile's first row
-    const int o0 = (b % n_ct) * kBN;                   // the tile's first channel
+    const int64_t trow0 = (int64_t)tile * kTileRows;  // the tile's first row
+    const int o0 = (b % n_ct) * S::kCols;             // the tile's first channel
     const int cin = (int)args.cin;
     const int nk = cin / 32;
-    const __amdgpu_buffer_rsrc_t a_rsrc =
-        make_rsrc(args.input, (uint32_t)(args.n_q * (int64_t)cin * (int64_t)sizeof(TA)));
-    const __amdgpu_buffer_rsrc_t w_rsrc =
-        make_rsrc(args.weight, (uint32_t)((int64_t)args.cout_g * cin * (int64_t)sizeof(TA)));
+    const i32x4_rsrc a_rsrc = rsrc_words(args.input, (uint32_t)(args.n_q * (int64_t)cin * (int64_t)sizeof(TA)));
+    const i32x4_rsrc w_rsrc = rsrc_words(args.weight, (uint32_t)((int64_t)args.cout_g * cin * (int64_t)sizeof(TA)));
 
     // DMA sources: instruction t of this wave fills LDS bytes [1 KB * (wave +
-    // 4 t), +1 KB) of the rows (or weights) region: 16 rows (channels) x 4
-    // slots; lane L writes row 16 (wave + 4 t) + L / 4, slot L % 4, and loads
-    // the logical piece stored there.  Rows past n_q and channels past Cout
-    // read zero.
+    // kWaves t), +1 KB) of the rows (or weights) region: 16 rows (channels) x
+    // 4 slots; lane L writes row 16 (wave + kWaves t) + L / 4, slot L % 4, and
+    // loads the logical piece stored there.  Rows past n_q and channels past
+    // Cout read zero.
     uint32_t a_src[kAInstr], w_src[kWInstr];
 #pragma unroll
     for (int t = 0; t < kAInstr; ++t) {
-        const int r = 16 * (wave + 4 * t) + (lane >> 2);
+        const int r = 16 * (wave + S::kWaves * t) + (lane >> 2);
         const int piece = wslot<64>(r, lane & 3);
         const int64_t row = trow0 + r;
         a_src[t] = row < args.n_q ? (uint32_t)((row * cin + 8 * piece) * (int64_t)sizeof(TA)) : kOobOffset;
     }
 #pragma unroll
     for (int t = 0; t < kWInstr; ++t) {
-        const int c = 16 * (wave + 4 * t) + (lane >> 2);
+        const int c = 16 * (wave + S::kWaves * t) + (lane >> 2);
         const int piece = wslot<64>(c, lane & 3);
         const int o = o0 + c;
         w_src[t] = o < args.cout_g ? (uint32_t)(((int64_t)o * cin + 8 * piece) * (int64_t)sizeof(TA)) : kOobOffset;
     }
+    const uint32_t wave_kb = (uint32_t)__builtin_amdgcn_readfirstlane(1024 * wave);  // uniform
     auto dma = [&](int k, int buf) {
         const uint32_t step = (uint32_t)(k * 32 * (int)sizeof(TA));  // an out-of-range offset stays out of range
-        unsigned char *base = s_buf + buf * kStage;
+        const uint32_t lds =
+            (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)stage(buf) + wave_kb;
 #pragma unroll
-        for (int t = 0; t < kAInstr; ++t)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                a_rsrc, (__attribute__((address_space(3))) void *)(base + 1024 * (wave + 4 * t)), 16,
-                a_src[t] + step, 0, 0, 0);
+        for (int t = 0; t < kAInstr; ++t) lds_dma16(a_rsrc, a_src[t] + step, lds + 1024 * S::kWaves * t);
 #pragma unroll
         for (int t = 0; t < kWInstr; ++t)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                w_rsrc, (__attribute__((address_space(3))) void *)(base + kRowsBytes + 1024 * (wave + 4 * t)), 16,
-                w_src[t] + step, 0, 0, 0);
+            lds_dma16(w_rsrc, w_src[t] + step, lds + kRowsBytes + 1024 * S::kWaves * t);
     };
 
     f32x4 acc[kI][4];
@@ -1621,50 +1640,73 @@ __global__ __launch_bounds__(kThreads, 2) void dense_gemm_kernel(ConvArgs args)
 #pragma unroll
             for (int e = 0; e < 4; ++e) acc[i][j][e] = 0.f;
 
-    auto compute = [&](int buf) {
-        const unsigned char *base = s_buf + buf * kStage;
+    // This lane's fragment offsets in a stage: row 128 rh + 16 i + l16 and
+    // weight channel 64 qc + 16 j + l16 sit 1 KB apart per i (j), their
+    // swizzled slot fixed (wslot reads bits 1-3 of the row).  Kept opaque,
+    // so each fragment address is this offset plus a constant (otherwise the
+    // compiler holds every buffer's addresses in registers, and spills).
+    int xoff = (128 * rh + l16) * 64 + wslot<64>(128 * rh + l16, q4) * 16;
+    int woff = kRowsBytes + (64 * qc + l16) * 64 + wslot<64>(64 * qc + l16, q4) * 16;
+    asm("" : "+v"(xoff));
+    asm("" : "+v"(woff));
+    // k-step k on buffer u: read its fragments, start the DMA of k + kBuf - 1
+    // (into the buffer every wave finished at k - 1), then the MFMAs.
+    auto step = [&](int u, int k) {
+        const unsigned char *base = stage(u);
         uint4 x[kI], w[4];
 #pragma unroll
-        for (int i = 0; i < kI; ++i) {
-            const int r = 128 * rh + 16 * i + l16;
-            x[i] = *reinterpret_cast<const uint4 *>(base + r * 64 + wslot<64>(r, q4) * 16);
-        }
+        for (int i = 0; i < kI; ++i) x[i] = *reinterpret_cast<const uint4 *>(base + xoff + 1024 * i);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int c = 64 * ch + 16 * j + l16;
-            w[j] = *reinterpret_cast<const uint4 *>(base + kRowsBytes + c * 64 + wslot<64>(c, q4) * 16);
-        }
+        for (int j = 0; j < 4; ++j) w[j] = *reinterpret_cast<const uint4 *>(base + woff + 1024 * j);
+        __builtin_amdgcn_sched_barrier(0);
+        if (k + kBuf - 1 < nk) dma(k + kBuf - 1, (u + kBuf - 1) % kBuf);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int i = 0; i < kI; ++i) acc[i][j] = mfma_16x16x32<TA>(w[j], x[i], acc[i][j]);
     };
-    constexpr int kPerStep = kAInstr + kWInstr;  // DMA instructions per wave and k-step
-    // k-step k: buffer k % 3.  Top of step k: k and k + 1 are in flight;
-    // wait for k, barrier (every wave is done with k - 1's buffer and every
-    // DMA of k has landed), start k + 2 into k - 1's buffer, compute k.
-    if (nk > 0) dma(0, 0);
-    if (nk > 1) dma(1, 1);
-    for (int k0 = 0; k0 < nk; k0 += kBuf) {
+    // k-step k uses buffer k % kBuf.  At its top, steps k .. min(k + kBuf -
+    // 2, nk - 1) are in flight: wait until only the younger ones are (the
+    // DMAs complete in issue order; no other vector memory operation is
+    // outstanding in the loop), barrier (every wave's DMA of k has landed and
+    // every wave is done with k - 1's buffer), then step.  The DMAs are inline
+    // asm, which the compiler does not track: these waits are the only ones.
+    // The main loop runs the k-steps that have kBuf - 2 younger steps in
+    // flight, unrolled by kBuf so the buffers are constants; the tail (fewer
+    // than 2 kBuf - 2 steps) waits for what is left.
+    for (int k = 0; k < kBuf - 1; ++k)
+        if (k < nk) dma(k, k);
+    int k0 = 0;
+    for (; k0 + 2 * kBuf - 2 <= nk; k0 += kBuf) {
 #pragma unroll
         for (int u = 0; u < kBuf; ++u) {
-            const int k = k0 + u;
-            if (k >= nk) break;
-            if (k + 1 < nk)
-                wait_vmcnt<kPerStep>();
-            else
-                wait_vmcnt<0>();
+            wait_vmcnt<(kBuf - 2) * kPerStep>();
             __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
             __builtin_amdgcn_s_barrier();
-            if (k + 2 < nk) dma(k + 2, (u + 2) % kBuf);
-            compute(u);
+            step(u, k0 + u);
         }
     }
+#pragma unroll
+    for (int u = 0; u < 2 * kBuf - 2; ++u) {
+        const int k = k0 + u;
+        if (k >= nk) break;
+        const int younger = min(kBuf - 2, nk - 1 - k);  // steps after k already issued
+        if (younger >= 2)
+            wait_vmcnt<2 * kPerStep>();
+        else if (younger == 1)
+            wait_vmcnt<kPerStep>();
+        else
+            wait_vmcnt<0>();
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        step(u % kBuf, k);
+    }
 
-    // ---- epilogue: bias, LayerNorm (over the row or one child; the two
-    //      channel halves meet in LDS), SiLU, residual, stores (row-major, or
-    //      each child's slice to its row in the child scatter).
-    const int oc0 = o0 + 64 * ch;
+    // ---- epilogue: bias, LayerNorm (over the row or one child; the channel
+    //      quarters of a group meet in LDS), SiLU, residual, stores
+    //      (row-major, or each child's slice to its row in the child scatter).
+    const int oc0 = o0 + 64 * qc;
     const int64_t row0 = trow0 + 128 * rh;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -1677,20 +1719,27 @@ __global__ __launch_bounds__(kThreads, 2) void dense_gemm_kernel(ConvArgs args)
             for (int i = 0; i < kI; ++i) acc[i][j][e] = ok ? acc[i][j][e] + bias : 0.f;
         }
     if constexpr (kLN) {
-        const int trow = 128 * rh + l16;  // tile row of block 0
+        // ln_group channels per normalised row: the whole row (<= 128), or in
+        // the child scatter one child's 64 (one wave's quarter) or 128 (two
+        // quarters); the gq quarters of a group add their partial sums in a
+        // fixed order, so they all hold the same statistics.
+        const int gq = (args.ln_group + 63) / 64;
+        const int g0 = qc - qc % gq;                 // first quarter of this wave's group
+        const int trow = 128 * rh + l16;             // tile row of block 0
         auto row_total = [&](float(&part)[kI]) {
             __syncthreads();
 #pragma unroll
             for (int i = 0; i < kI; ++i)
-                if (q4 == 0) s_red[ch][trow + 16 * i] = part[i];
+                if (q4 == 0) s_red[qc][trow + 16 * i] = part[i];
             __syncthreads();
 #pragma unroll
-            for (int i = 0; i < kI; ++i) part[i] = s_red[0][trow + 16 * i] + s_red[1][trow + 16 * i];
+            for (int i = 0; i < kI; ++i) {
+                float t = 0.f;
+                for (int q = 0; q < gq; ++q) t += s_red[g0 + q][trow + 16 * i];
+                part[i] = t;
+            }
         };
-        // ln_group channels per normalised row: the whole row (<= 128), or in
-        // the child scatter one child's 128 (the tile) or 64 (one wave's half)
         const float inv_c = 1.0f / (float)args.ln_group;
-        const bool pair = args.ln_group > 64;  // the two channel halves meet
         float mean[kI], inv_std[kI], part[kI];
 #pragma unroll
         for (int i = 0; i < kI; ++i) {
@@ -1703,7 +1752,7 @@ __global__ __launch_bounds__(kThreads, 2) void dense_gemm_kernel(ConvArgs args)
             sum += __shfl_xor(sum, 32, 64);
             part[i] = sum;
         }
-        if (pair) row_total(part);
+        if (gq > 1) row_total(part);
 #pragma unroll
         for (int i = 0; i < kI; ++i) mean[i] = part[i] * inv_c;
 #pragma unroll
@@ -1721,7 +1770,7 @@ __global__ __launch_bounds__(kThreads, 2) void dense_gemm_kernel(ConvArgs args)
             qv += __shfl_xor(qv, 32, 64);
             part[i] = qv;
         }
-        if (pair) row_total(part);
+        if (gq > 1) row_total(part);
 #pragma unroll
         for (int i = 0; i < kI; ++i) inv_std[i] = rsqrt_f32(part[i] * inv_c + args.ln_eps);
 #pragma unroll
@@ -1943,13 +1992,21 @@ int launch_conv(const ConvArgs &a, int groups, bool mfma, const void *plan, hipS
                 launch_v2<TA, TW, TO, true>(b, fgrid, s);
             } else if (sizeof(TW) == 2 && !a.map && a.K == 1 && groups == 1 && a.cin % 32 == 0 && !a.skip_idx) {
                 // the dense linear: contiguous rows, reference-layout weights;
-                // row tile x column tile flattened, column tile fastest
-                if (tiles * ntile > INT32_MAX) return fail(SC_ERR_OVERFLOW, "dense linear grid overflow");
-                const dim3 dgrid((unsigned)(tiles * ntile), 1, 1);
-                if (a.ln)
-                    dense_gemm_kernel<TA, TO, true><<<dgrid, kThreads, 0, s>>>(a);
-                else
-                    dense_gemm_kernel<TA, TO, false><<<dgrid, kThreads, 0, s>>>(a);
+                // row tile x column tile flattened, column tile fastest;
+                // 256-channel tiles above 128 output channels (not with
+                // LayerNorm, whose statistics do not fit its registers)
+                const bool wide_tile = a.cout_g > 128 && !a.ln;
+                const int64_t ncol = (a.cout_g + (wide_tile ? 255 : 127)) / (wide_tile ? 256 : 128);
+                if (tiles * ncol > INT32_MAX) return fail(SC_ERR_OVERFLOW, "dense linear grid overflow");
+                const dim3 dgrid((unsigned)(tiles * ncol), 1, 1);
+                if (wide_tile) {
+                    dense_gemm_kernel<TA, TO, false, 4><<<dgrid, DenseShape<4>::kThreads, 0, s>>>(a);
+                } else {
+                    if (a.ln)
+                        dense_gemm_kernel<TA, TO, true, 2><<<dgrid, DenseShape<2>::kThreads, 0, s>>>(a);
+                    else
+                        dense_gemm_kernel<TA, TO, false, 2><<<dgrid, DenseShape<2>::kThreads, 0, s>>>(a);
+                }
                 SC_LAUNCH_CHECK("dense_gemm_kernel launch");
             } else {
                 launch_v2<TA, TW, TO, false>(a, grid, s);
