@@ -1544,13 +1544,11 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
 // 2 x kQ (128 rows x 64 channels each) read their MFMA fragments from LDS,
 // 16-byte pieces XOR-swizzled per row (wslot) so that the reads of 8
 // consecutive rows hit distinct banks.  kQ = 2: 128-channel tiles, 3
-// buffers (72 KB), two workgroups per CU; kQ = 4 (Cout > 128): 256-channel
-// tiles, 4 buffers (128 KB), one workgroup of 8 waves per CU -- a third fewer
-// load bytes per MFMA, and the load path's rate here is set by the bytes in
-// flight per CU (under load an L2 access takes microseconds), which the LDS
-// budget fixes (the LayerNorm epilogue takes kQ = 2).  Same epilogue layout
-// as the halo kernel: lane (l16, q4)
-// holds channels oc0 + 16 j + 4 q4 .. +4 of row row0 + 16 i + l16.
+// buffers (72 KB), two workgroups per CU; kQ = 4 (129-256 output channels,
+// no LayerNorm): one 256-channel tile per row, 4 buffers (128 KB), one
+// workgroup of 8 waves per CU.  Same epilogue layout as the halo kernel:
+// lane (l16, q4) holds channels oc0 + 16 j + 4 q4 .. +4 of row
+// row0 + 16 i + l16.
 template <int kQ>
 struct DenseShape {
     static constexpr int kThreads = 128 * kQ;
@@ -1560,7 +1558,7 @@ struct DenseShape {
     static constexpr int kBlocksPerCU = kQ == 2 ? 2 : 1;
 };
 
-template <typename TA, typename TO, bool kLN, int kQ>
+template <typename TA, typename TO, bool kLN, int kQ, bool kStaged>
 __global__ __launch_bounds__(DenseShape<kQ>::kThreads, DenseShape<kQ>::kBlocksPerCU) void dense_gemm_kernel(
     ConvArgs args)
 {
@@ -1574,13 +1572,9 @@ __global__ __launch_bounds__(DenseShape<kQ>::kThreads, DenseShape<kQ>::kBlocksPe
     constexpr int kWInstr = kWBytes / 1024 / S::kWaves;
     constexpr int kPerStep = kAInstr + kWInstr;
     static_assert(kAInstr * 1024 * S::kWaves == kRowsBytes && kWInstr * 1024 * S::kWaves == kWBytes, "DMA split");
-    // Separate LDS objects per buffer (the last unused when kBuf = 3).
-    __shared__ __attribute__((aligned(16))) unsigned char s_b0[kStage], s_b1[kStage], s_b2[kStage],
-        s_b3[kBuf > 3 ? kStage : 16];
+    __shared__ __attribute__((aligned(16))) unsigned char s_buf[kBuf * kStage];  // stages; then the output tile
     __shared__ float s_red[kQ][kTileRows];            // LayerNorm: per channel quarter, per tile row
-    auto stage = [&](int u) -> unsigned char * {      // buffer u (a constant after unrolling)
-        return u == 0 ? s_b0 : (u == 1 ? s_b1 : (u == 2 ? s_b2 : s_b3));
-    };
+    auto stage = [&](int u) -> unsigned char * { return s_buf + u * kStage; };
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -1787,6 +1781,66 @@ __global__ __launch_bounds__(DenseShape<kQ>::kThreads, DenseShape<kQ>::kBlocksPe
             }
     }
     TO *__restrict__ out = static_cast<TO *>(args.out);
+    if constexpr (kStaged) {
+        // 16-bit output, counts and pointers 16-byte aligned (host): the
+        // tile goes through the idle stage buffers, rounded once (after the
+        // residual, added here in f32), so that every store instruction
+        // writes whole 16-byte pieces of consecutive rows (a lane's own
+        // layout scatters 8-byte pieces over 16 rows per store, which costs
+        // the store path several times the bytes' time).  Tile row rl sits at
+        // rl * kRB, its 16-byte piece c in slot c ^ (rl % kNC), so neither
+        // phase has more bank conflicts than its bytes need.
+        static_assert(sizeof(TO) == 2, "16-bit output");
+        constexpr int kRB = S::kCols * 2;  // bytes of a tile row
+        constexpr int kNC = kRB / 16;      // 16-byte pieces per tile row
+        static_assert(kTileRows * kRB <= kBuf * kStage, "output tile fits the stage buffers");
+        const TO *__restrict__ res = static_cast<const TO *>(args.residual);
+        __syncthreads();  // every wave is done with the last stage's fragments
+#pragma unroll
+        for (int i = 0; i < kI; ++i) {
+            const int rl = 128 * rh + 16 * i + l16;
+            const int64_t r = trow0 + rl;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+                if (args.silu) {
+#pragma unroll
+                    for (int cc = 0; cc < 4; ++cc) v[cc] = silu_f32(v[cc]);
+                }
+                const int oc = oc0 + j * 16 + 4 * q4;
+                if (res && r < args.n_q && oc < args.cout_g) {
+                    float r4[4];
+                    Out4<TO>::unpack(*reinterpret_cast<const typename Out4<TO>::V *>(res + r * args.cout + oc), r4);
+#pragma unroll
+                    for (int cc = 0; cc < 4; ++cc) v[cc] += r4[cc];
+                }
+                const int c = 8 * qc + 2 * j + (q4 >> 1);
+                *reinterpret_cast<typename Out4<TO>::V *>(s_buf + rl * kRB + ((c ^ (rl & (kNC - 1))) << 4) +
+                                                          8 * (q4 & 1)) = Out4<TO>::pack(v);
+            }
+        }
+        __syncthreads();
+#pragma unroll 4
+        for (int it = 0; it < kTileRows * kNC / S::kThreads; ++it) {
+            const int idx = it * S::kThreads + tid;
+            const int rl = idx / kNC, c = idx % kNC;
+            const int64_t r = trow0 + rl;
+            const int col = o0 + 8 * c;  // first of the piece's 8 channels
+            if (r >= args.n_q || col >= args.cout_g) continue;
+            const uint4 val = *reinterpret_cast<const uint4 *>(s_buf + rl * kRB + ((c ^ (rl & (kNC - 1))) << 4));
+            int64_t off;
+            if (args.scatter_rows) {
+                const int child = args.scatter_shift >= 0 ? col >> args.scatter_shift : col / args.scatter_ch;
+                const int32_t cr = args.scatter_rows[r * 8 + child];
+                if (cr < 0 || cr >= args.scatter_n) continue;
+                off = (int64_t)cr * args.scatter_ch + (col - child * args.scatter_ch);
+            } else {
+                off = r * args.cout + col;
+            }
+            *reinterpret_cast<uint4 *>(out + off) = val;
+        }
+        return;
+    }
     const TO *__restrict__ res = static_cast<const TO *>(args.residual);
     const bool vec_ok = args.vec_out != 0;
 #pragma unroll
@@ -1993,19 +2047,35 @@ int launch_conv(const ConvArgs &a, int groups, bool mfma, const void *plan, hipS
             } else if (sizeof(TW) == 2 && !a.map && a.K == 1 && groups == 1 && a.cin % 32 == 0 && !a.skip_idx) {
                 // the dense linear: contiguous rows, reference-layout weights;
                 // row tile x column tile flattened, column tile fastest;
-                // 256-channel tiles above 128 output channels (not with
-                // LayerNorm, whose statistics do not fit its registers)
-                const bool wide_tile = a.cout_g > 128 && !a.ln;
+                // one 256-channel tile for 129-256 output channels (the rows
+                // are read once); 128-channel tiles otherwise, two workgroups
+                // per CU, so one's epilogue stores overlap the other's
+                // MFMAs (measured faster once a row spans several column
+                // tiles); never with LayerNorm, whose statistics do not fit
+                // the wide tile's registers
+                const bool wide_tile = a.cout_g > 128 && a.cout_g <= 256 && !a.ln;
                 const int64_t ncol = (a.cout_g + (wide_tile ? 255 : 127)) / (wide_tile ? 256 : 128);
                 if (tiles * ncol > INT32_MAX) return fail(SC_ERR_OVERFLOW, "dense linear grid overflow");
                 const dim3 dgrid((unsigned)(tiles * ncol), 1, 1);
+                // row-contiguous stores through LDS: 16-bit output, 8-channel
+                // pieces aligned in the output rows, residual aligned
+                const bool staged = sizeof(TO) == 2 && a.cout % 8 == 0 && (uintptr_t)a.out % 16 == 0 &&
+                                    (uintptr_t)a.residual % 16 == 0 && (!a.scatter_rows || a.scatter_ch % 8 == 0);
                 if (wide_tile) {
-                    dense_gemm_kernel<TA, TO, false, 4><<<dgrid, DenseShape<4>::kThreads, 0, s>>>(a);
-                } else {
-                    if (a.ln)
-                        dense_gemm_kernel<TA, TO, true, 2><<<dgrid, DenseShape<2>::kThreads, 0, s>>>(a);
+                    if (staged)
+                        dense_gemm_kernel<TA, TO, false, 4, sizeof(TO) == 2><<<dgrid, DenseShape<4>::kThreads, 0, s>>>(a);
                     else
-                        dense_gemm_kernel<TA, TO, false, 2><<<dgrid, DenseShape<2>::kThreads, 0, s>>>(a);
+                        dense_gemm_kernel<TA, TO, false, 4, false><<<dgrid, DenseShape<4>::kThreads, 0, s>>>(a);
+                } else if (a.ln) {
+                    if (staged)
+                        dense_gemm_kernel<TA, TO, true, 2, sizeof(TO) == 2><<<dgrid, DenseShape<2>::kThreads, 0, s>>>(a);
+                    else
+                        dense_gemm_kernel<TA, TO, true, 2, false><<<dgrid, DenseShape<2>::kThreads, 0, s>>>(a);
+                } else {
+                    if (staged)
+                        dense_gemm_kernel<TA, TO, false, 2, sizeof(TO) == 2><<<dgrid, DenseShape<2>::kThreads, 0, s>>>(a);
+                    else
+                        dense_gemm_kernel<TA, TO, false, 2, false><<<dgrid, DenseShape<2>::kThreads, 0, s>>>(a);
                 }
                 SC_LAUNCH_CHECK("dense_gemm_kernel launch");
             } else {
