@@ -46,8 +46,16 @@ def dense_f64(oracle, w, b, x):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("cin,cout,epi", [(128, 512, "silu"), (512, 128, "residual"), (96, 64, "ln"),
-                                          (128, 256, "ln"), (64, 40, "none")])
+                                          (128, 256, "ln"), (64, 40, "none"),
+                                          # 256-channel tiles (129-256 channels): a k-loop of 3 steps
+                                          # and a residual through the staged stores, one k-step with
+                                          # SiLU, a partial tile, and 196 channels (direct stores)
+                                          (96, 200, "residual"), (32, 136, "silu"), (64, 196, "none"),
+                                          (1024, 256, "residual")])
 def test_linear_forward(oracle, dtype, cin, cout, epi):
+    """x W^T + b with each epilogue, on both tile widths (128 and 256 channels), k-loops from 1
+    to 32 steps, whole and partial column tiles, and row-contiguous (staged) and direct
+    stores; 70,001 rows, so the last row tile is partial."""
     rnd, tol = TYPES[dtype]
     rng = np.random.default_rng(cin + cout)
     rows = 70001
