@@ -181,73 +181,116 @@ __device__ inline float seg_sum(float v)
     return v;
 }
 
-template <typename Tin, typename Tout, int LPR, int NV>
+// VEC consecutive Tout values (16-byte aligned group) as f32.
+template <typename Tout, int VEC>
+__device__ inline void load_vec_f32(const Tout *p, float *f)
+{
+    constexpr int kBytes = VEC * (int)sizeof(Tout);
+    if constexpr (kBytes == 16) {
+        unpack16<Tout>(*reinterpret_cast<const uint4 *>(p), f);
+    } else if constexpr (kBytes == 32) {
+        unpack16<Tout>(reinterpret_cast<const uint4 *>(p)[0], f);
+        unpack16<Tout>(reinterpret_cast<const uint4 *>(p)[1], f + 4);
+    } else {
+        static_assert(kBytes == 8 && sizeof(Tout) == 2, "4 16-bit values");
+        const uint2 u = *reinterpret_cast<const uint2 *>(p);
+        f[0] = half_lo<Tout>(u.x);
+        f[1] = half_hi<Tout>(u.x);
+        f[2] = half_lo<Tout>(u.y);
+        f[3] = half_hi<Tout>(u.y);
+    }
+}
+
+// NR rows per lane segment, all their loads issued before any statistic, so
+// that a wave keeps NR x 1 KB in flight (one row per segment left a 128- or
+// 256-channel row kernel at a quarter of HBM bandwidth: latency-bound).
+template <typename Tin, typename Tout, int LPR, int NV, int NR>
 __global__ __launch_bounds__(256) void layer_norm_vec_kernel(const Tin *in, int64_t rows, int channels,
                                                              const float *__restrict__ w,
                                                              const float *__restrict__ b, float eps,
                                                              int apply_silu, const Tout *res, Tout *out)
 {
     constexpr int VEC = Vec16<Tin>::N;
-    constexpr int RPW = 64 / LPR;  // rows per wave
+    constexpr int RPW = 64 / LPR;  // rows per wave and load
     const int lane = threadIdx.x & 63;
     const int seg = lane / LPR, sl = lane % LPR;
-    const int64_t row = ((int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * RPW + seg;
-    const bool live = row < rows;
-    const int64_t rr = live ? row : 0;
-    const uint4 *x = reinterpret_cast<const uint4 *>(in + rr * channels);
-    float v[NV][VEC];
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const uint4 u = x[sl + i * LPR];
-        unpack16<Tin>(u, v[i]);
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) s += v[i][e];
-    }
-    const float inv_c = 1.0f / (float)channels;
-    const float mean = seg_sum<LPR>(s) * inv_c;
-    float q = 0.f;
-#pragma unroll
-    for (int i = 0; i < NV; ++i)
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-            const float d = v[i][e] - mean;
-            q += d * d;
-        }
-    const float inv_std = rsqrt_f32(seg_sum<LPR>(q) * inv_c + eps);
-    if (!live) return;
-    Tout *y = out + row * channels;
+    // the wave's NR * RPW consecutive rows; load r covers rows row0 + r RPW + [0, RPW)
+    const int64_t row0 = ((int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * (RPW * NR) + seg;
+    float v[NR][NV][VEC];
+    // the lane's channels are the same in every row: its affine weights once,
+    // as 16-byte loads
+    float wv[NV][VEC], bv[NV][VEC];
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const int c0 = (sl + i * LPR) * VEC;
-        float t[VEC];
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-            float z = (v[i][e] - mean) * inv_std;
-            if (w) z *= w[c0 + e];
-            if (b) z += b[c0 + e];
-            if (apply_silu) z = silu_f32(z);
-            if (res) z += load_as_f32<Tout>(res + row * channels, c0 + e);
-            t[e] = z;
+        for (int e = 0; e < VEC; e += 4) {
+            const float4 w4 = w ? *reinterpret_cast<const float4 *>(w + c0 + e) : make_float4(1.f, 1.f, 1.f, 1.f);
+            const float4 b4 = b ? *reinterpret_cast<const float4 *>(b + c0 + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+            wv[i][e] = w4.x, wv[i][e + 1] = w4.y, wv[i][e + 2] = w4.z, wv[i][e + 3] = w4.w;
+            bv[i][e] = b4.x, bv[i][e + 1] = b4.y, bv[i][e + 2] = b4.z, bv[i][e + 3] = b4.w;
         }
-        if constexpr (sizeof(Tout) == 2) {
-            if constexpr (VEC == 8) {
-                uint4 o;
-                o.x = pack_half2<Tout>(t[0], t[1]);
-                o.y = pack_half2<Tout>(t[2], t[3]);
-                o.z = pack_half2<Tout>(t[4], t[5]);
-                o.w = pack_half2<Tout>(t[6], t[7]);
-                *reinterpret_cast<uint4 *>(y + c0) = o;
-            } else {
-                uint2 o;
-                o.x = pack_half2<Tout>(t[0], t[1]);
-                o.y = pack_half2<Tout>(t[2], t[3]);
-                *reinterpret_cast<uint2 *>(y + c0) = o;
-            }
-        } else {
+    }
 #pragma unroll
-            for (int e = 0; e < VEC; e += 4)
-                *reinterpret_cast<float4 *>(y + c0 + e) = make_float4(t[e], t[e + 1], t[e + 2], t[e + 3]);
+    for (int r = 0; r < NR; ++r) {
+        const int64_t row = row0 + r * RPW;
+        const int64_t rr = row < rows ? row : 0;
+        const uint4 *x = reinterpret_cast<const uint4 *>(in + rr * channels);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) unpack16<Tin>(x[sl + i * LPR], v[r][i]);
+    }
+    const float inv_c = 1.0f / (float)channels;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        const int64_t row = row0 + r * RPW;
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) s += v[r][i][e];
+        const float mean = seg_sum<LPR>(s) * inv_c;
+        float q = 0.f;
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+                const float d = v[r][i][e] - mean;
+                q += d * d;
+            }
+        const float inv_std = rsqrt_f32(seg_sum<LPR>(q) * inv_c + eps);
+        if (row >= rows) continue;
+        Tout *y = out + row * channels;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int c0 = (sl + i * LPR) * VEC;
+            float t[VEC], rv[VEC];
+            if (res) load_vec_f32<Tout, VEC>(res + row * channels + c0, rv);
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+                float z = (v[r][i][e] - mean) * inv_std * wv[i][e] + bv[i][e];
+                if (apply_silu) z = silu_f32(z);
+                if (res) z += rv[e];
+                t[e] = z;
+            }
+            if constexpr (sizeof(Tout) == 2) {
+                if constexpr (VEC == 8) {
+                    uint4 o;
+                    o.x = pack_half2<Tout>(t[0], t[1]);
+                    o.y = pack_half2<Tout>(t[2], t[3]);
+                    o.z = pack_half2<Tout>(t[4], t[5]);
+                    o.w = pack_half2<Tout>(t[6], t[7]);
+                    *reinterpret_cast<uint4 *>(y + c0) = o;
+                } else {
+                    uint2 o;
+                    o.x = pack_half2<Tout>(t[0], t[1]);
+                    o.y = pack_half2<Tout>(t[2], t[3]);
+                    *reinterpret_cast<uint2 *>(y + c0) = o;
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < VEC; e += 4)
+                    *reinterpret_cast<float4 *>(y + c0 + e) = make_float4(t[e], t[e + 1], t[e + 2], t[e + 3]);
+            }
         }
     }
 }
@@ -365,23 +408,26 @@ int launch_layer_norm(const void *in, int64_t rows, int64_t ch, const float *w,
     const Tout *res = (const Tout *)res_;
     const int C = (int)ch;
     constexpr int VEC = Vec16<Tin>::N;
-    const bool aligned = ((uintptr_t)in % 16 == 0) && ((uintptr_t)out % 16 == 0);
+    const bool aligned = ((uintptr_t)in % 16 == 0) && ((uintptr_t)out % 16 == 0) && ((uintptr_t)res % 16 == 0) &&
+                         ((uintptr_t)w % 16 == 0) && ((uintptr_t)b % 16 == 0);
     if (aligned && C % (VEC * 8) == 0) {
         const int V = C / VEC;  // 16-byte vectors per row, a multiple of 8
         int lpr = 8;
         while (lpr < 64 && V % (lpr * 2) == 0) lpr *= 2;
         const int nv = V / lpr;
-        const int64_t rows_per_block = 4 * (64 / lpr);
+        const int nr = nv == 1 ? 4 : (nv == 2 ? 2 : 1);  // rows per lane segment: ~4 vectors per lane
+        const int64_t rows_per_block = 4 * (64 / lpr) * nr;
         const unsigned gv = grid_for(rows, (int)rows_per_block, INT32_MAX);
-#define LN_VEC(L, N) layer_norm_vec_kernel<Tin, Tout, L, N><<<gv, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y)
+#define LN_VEC(L, N, R) \
+    layer_norm_vec_kernel<Tin, Tout, L, N, R><<<gv, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y)
         bool launched = true;
-        if (lpr == 8 && nv == 1) LN_VEC(8, 1);
-        else if (lpr == 16 && nv == 1) LN_VEC(16, 1);
-        else if (lpr == 32 && nv == 1) LN_VEC(32, 1);
-        else if (lpr == 64 && nv == 1) LN_VEC(64, 1);
-        else if (lpr == 64 && nv == 2) LN_VEC(64, 2);
-        else if (lpr == 64 && nv == 3) LN_VEC(64, 3);
-        else if (lpr == 64 && nv == 4) LN_VEC(64, 4);
+        if (lpr == 8 && nv == 1) LN_VEC(8, 1, 4);
+        else if (lpr == 16 && nv == 1) LN_VEC(16, 1, 4);
+        else if (lpr == 32 && nv == 1) LN_VEC(32, 1, 4);
+        else if (lpr == 64 && nv == 1) LN_VEC(64, 1, 4);
+        else if (lpr == 64 && nv == 2) LN_VEC(64, 2, 2);
+        else if (lpr == 64 && nv == 3) LN_VEC(64, 3, 1);
+        else if (lpr == 64 && nv == 4) LN_VEC(64, 4, 1);
         else launched = false;
 #undef LN_VEC
         if (launched) {
