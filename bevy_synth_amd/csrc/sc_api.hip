@@ -415,16 +415,21 @@ int launch_layer_norm(const void *in, int64_t rows, int64_t ch, const float *w,
         int lpr = 8;
         while (lpr < 64 && V % (lpr * 2) == 0) lpr *= 2;
         const int nv = V / lpr;
-        const int nr = nv == 1 ? 4 : (nv == 2 ? 2 : 1);  // rows per lane segment: ~4 vectors per lane
+        // rows per lane segment: ~4 vectors per lane (8 for f32 rows of one vector per lane)
+        const int nr = nv == 1 ? (sizeof(Tin) == 4 ? 8 : 4) : (nv == 2 ? 2 : 1);
         const int64_t rows_per_block = 4 * (64 / lpr) * nr;
         const unsigned gv = grid_for(rows, (int)rows_per_block, INT32_MAX);
 #define LN_VEC(L, N, R) \
     layer_norm_vec_kernel<Tin, Tout, L, N, R><<<gv, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y)
         bool launched = true;
-        if (lpr == 8 && nv == 1) LN_VEC(8, 1, 4);
-        else if (lpr == 16 && nv == 1) LN_VEC(16, 1, 4);
-        else if (lpr == 32 && nv == 1) LN_VEC(32, 1, 4);
-        else if (lpr == 64 && nv == 1) LN_VEC(64, 1, 4);
+        if (lpr == 8 && nv == 1 && nr == 4) LN_VEC(8, 1, 4);
+        else if (lpr == 16 && nv == 1 && nr == 4) LN_VEC(16, 1, 4);
+        else if (lpr == 32 && nv == 1 && nr == 4) LN_VEC(32, 1, 4);
+        else if (lpr == 64 && nv == 1 && nr == 4) LN_VEC(64, 1, 4);
+        else if (lpr == 8 && nv == 1) LN_VEC(8, 1, 8);
+        else if (lpr == 16 && nv == 1) LN_VEC(16, 1, 8);
+        else if (lpr == 32 && nv == 1) LN_VEC(32, 1, 8);
+        else if (lpr == 64 && nv == 1) LN_VEC(64, 1, 8);
         else if (lpr == 64 && nv == 2) LN_VEC(64, 2, 2);
         else if (lpr == 64 && nv == 3) LN_VEC(64, 3, 1);
         else if (lpr == 64 && nv == 4) LN_VEC(64, 4, 1);
