@@ -1193,11 +1193,24 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
     // ---- prologue: local map (as LDS offsets, thread = tile row), zero
     //      row, halo source offsets, mask of the offsets the tile uses.
     {
+        // Every load first -- the row's K local-map entries and this
+        // thread's halo rows -- so the prologue costs one memory round trip
+        // (a loop over k waits once per few offsets: ~10 round trips a tile).
         const uint16_t *src = plan.lmap + (int64_t)tile * K * kPlanTileRows + tid;
+        const int32_t *hrows = plan.halo + (int64_t)tile * kPlanHaloMax;
+        constexpr int kHPer = (kPlanHaloMax + kThreads - 1) / kThreads;  // halo rows per thread
+        uint32_t jv[kHaloK];
+        int32_t hv[kHPer];
+#pragma unroll
+        for (int k = 0; k < kHaloK; ++k) jv[k] = k < K ? src[k * kPlanTileRows] : (uint32_t)kPlanAbsent;
+#pragma unroll
+        for (int u = 0; u < kHPer; ++u) hv[u] = tid + u * kThreads < U ? hrows[tid + u * kThreads] : 0;
         uint16_t *dst = &s_lmap[0][tid >> 7][tid & 15][(tid >> 4) & 7];
         uint32_t m = 0;
-        for (int k = 0; k < K; ++k) {
-            const int j = src[k * kPlanTileRows];
+#pragma unroll
+        for (int k = 0; k < kHaloK; ++k) {
+            if (k >= K) break;
+            const int j = (int)jv[k];
             m |= (uint32_t)(j != kPlanAbsent) << k;
             dst[k * kPlanTileRows] =
                 (uint16_t)(j == kPlanAbsent ? kZeroRow * CB : j * CB + 16 * (((j >> 1) ^ (j >> 2)) & 3));
@@ -1206,8 +1219,9 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
         for (int off = 32; off > 0; off >>= 1) m |= __shfl_xor(m, off, 64);
         if (lane == 0) s_wmask[wave] = m;
         if (tid < CB / 16) reinterpret_cast<uint4 *>(s_halo + kZeroRow * CB)[tid] = make_uint4(0, 0, 0, 0);
-        const int32_t *hrows = plan.halo + (int64_t)tile * kPlanHaloMax;
-        for (int j = tid; j < U; j += kThreads) s_hoff[j] = (uint32_t)hrows[j] * row_bytes;
+#pragma unroll
+        for (int u = 0; u < kHPer; ++u)
+            if (tid + u * kThreads < U) s_hoff[tid + u * kThreads] = (uint32_t)hv[u] * row_bytes;
     }
     __syncthreads();
     const uint32_t tmask = __builtin_amdgcn_readfirstlane(s_wmask[0] | s_wmask[1] | s_wmask[2] | s_wmask[3]);
