@@ -649,14 +649,21 @@ __global__ __launch_bounds__(kThreads) void plan_emit_kernel(PlanArgs a)
              i += (int64_t)gridDim.x * blockDim.x) {
             const int64_t cell = grid_cell(bg, a.coords[i]);
             const int64_t b = cell / kBitBlock;
-            const uint32_t *bw = a.grid + b * (kBitBlock / 32);
+            // the block's 8 words (32 aligned bytes) and both prefixes in one
+            // round trip (word-by-word conditional loads waited one by one)
+            static_assert(kBitBlock == 256, "a block is two 16-byte loads");
+            const uint4 *bw4 = reinterpret_cast<const uint4 *>(a.grid + b * (kBitBlock / 32));
+            const uint4 lo = bw4[0], hi = bw4[1];
+            const int32_t gp = a.gsum[cell / kBitGroup], bp = a.counts[b];
+            const uint32_t bw[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
             const int wi = (int)((cell >> 5) & (kBitBlock / 32 - 1));
             int before = 0;
 #pragma unroll
-            for (int w = 0; w < kBitBlock / 32; ++w)
-                if (w < wi) before += __builtin_popcount(bw[w]);
-            before += __builtin_popcount(bw[wi] & ((1u << (cell & 31)) - 1u));
-            a.order[(int64_t)a.gsum[cell / kBitGroup] + a.counts[b] + before] = (int32_t)i;
+            for (int w = 0; w < kBitBlock / 32; ++w) {
+                const uint32_t m = w < wi ? 0xFFFFFFFFu : (w == wi ? (1u << (cell & 31)) - 1u : 0u);
+                before += __builtin_popcount(bw[w] & m);
+            }
+            a.order[(int64_t)gp + bp + before] = (int32_t)i;
         }
         return;
     }
