@@ -38,6 +38,20 @@ def test_layer_norm_silu_f32(oracle, ch, affine, silu):
     assert_close(got, exp, TOL_F32, "layer_norm")
 
 
+@pytest.mark.parametrize("ch", [64, 128, 256, 512, 1024])
+def test_layer_norm_bf16_affine(oracle, ch):
+    """bf16 rows with the affine weights and SiLU: each width takes a different lane-segment
+    shape of the vectorised kernel (8 to 64 lanes per row, 1 to 2 vectors per lane, 2 to 4
+    rows per segment); 3,001 rows leave a partial last block."""
+    rng = np.random.default_rng(ch + 7)
+    x = rbf((rng.standard_normal((3001, ch)) * 2 + 0.5).astype(np.float32))
+    w = rng.standard_normal(ch).astype(np.float32)
+    b = rng.standard_normal(ch).astype(np.float32)
+    got = F.layer_norm(bf16_dev(x), dev(w), dev(b), eps=1e-6, silu=True)
+    exp = oracle.silu(oracle.layer_norm(x, w, b, 1e-6))
+    assert_close(got.float().cpu().numpy(), exp, TOL_BF16, f"layer_norm bf16 affine C={ch}")
+
+
 def test_layer_norm_bf16_in_place(oracle):
     rng = np.random.default_rng(1)
     x = rbf(rng.standard_normal((5000, 128)).astype(np.float32))
