@@ -40,8 +40,9 @@ def parse():
                     help="untimed steps right before the timed ones (the GPU's clocks need ~20 steps)")
     ap.add_argument("--cpu-sample", type=int, default=262144,
                     help="query rows of the CPU baseline sample (0 = skip)")
-    ap.add_argument("--only", choices=["map", "plan", "mapplan", "conv", "ln"], default=None,
-                    help="run just this part of the step --steps times (for rocprofv3) and exit")
+    ap.add_argument("--only", choices=["map", "plan", "mapplan", "conv", "ln", "config5"], default=None,
+                    help="run just this part of the step (or config 5's decoder stack) --steps times "
+                         "(for rocprofv3) and exit")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the config 2 / 4 / 5 component timings")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -161,6 +162,30 @@ def cpu_baseline(coords, x_f32, w1, w2, sample_rows):
     }
 
 
+def config5_stack(dev, rng):
+    """Config 5's int8 decoder stack (3 stages of 2 residual blocks + fused
+    C2S upsample, 512 -> 64 channels) on synthetic bf16 features.  Returns
+    (run, res, start voxels): run() executes the stack once and leaves the
+    children's neighbourhood and features in res["nb"], res["y"]."""
+    import numpy as np
+    import torch
+
+    from bevy_synth_amd import decoder as D
+    from bevy_synth_amd import synth
+
+    coords5, masks = synth.config5_stack_inputs()
+    stack = D.int8_stack([512, 256, 128, 64], 2, seed=5, device=dev)
+    x5 = torch.from_numpy(synth.bf16_bits(synth.normal_f32(rng, (len(coords5), 512))).view(np.int16)) \
+        .to(dev).view(torch.bfloat16)
+    c5 = torch.from_numpy(coords5).to(dev)
+    m5 = [torch.from_numpy(m).to(dev) for m in masks]
+    res = {}
+
+    def run():
+        res["nb"], res["y"] = stack(c5, x5, m5)
+    return run, res, len(coords5)
+
+
 def config_components(dev, st=None, steps: int = 5):
     """The other BASELINE configs on this GPU, for the record (parity cases,
     not the headline): config 2's planned 3x3x3 conv (C = 256, bf16), config
@@ -228,20 +253,12 @@ def config_components(dev, st=None, steps: int = 5):
                       "child_map_plus_plan_ms": wall_ms(lambda: D.Neighborhood.build(ccfg, cc), steps),
                       "conv_ms": t_conv, "conv_useful_tflops": 2.0 * P4 * cout * cout / (t_conv * 1e-3) / 1e12}
     # config 5
-    coords5, masks = synth.config5_stack_inputs()
-    stack = D.int8_stack([512, 256, 128, 64], 2, seed=5, device=dev)
-    x5 = bf(synth.normal_f32(rng, (len(coords5), 512)))
-    c5 = torch.from_numpy(coords5).to(dev)
-    m5 = [torch.from_numpy(m).to(dev) for m in masks]
-    res = {}
-
-    def run5():
-        res["nb"], res["y"] = stack(c5, x5, m5)
+    run5, res, n5 = config5_stack(dev, rng)
     t5 = wall_ms(run5, max(2, steps // 2))
-    out["config5"] = {"start_voxels": len(coords5), "end_voxels": int(res["y"].shape[0]), "stack_ms": t5,
+    out["config5"] = {"start_voxels": n5, "end_voxels": int(res["y"].shape[0]), "stack_ms": t5,
                       "note": "18 convs (int8 weights, bf16 activations), 4 maps + plans, fused C2S upsamples; "
                               "includes the host syncs of the child counts"}
-    del stack, res, x5
+    del run5, res
 
     # C2S compaction (sc_subdivision_build_indexed) of config 4's parents:
     # HBM-bound; algorithmic bytes = mask + parent coords read, child coords,
@@ -396,6 +413,13 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.only == "config5":
+        run5, _, _ = config5_stack(dev, np.random.default_rng(7))
+        for _ in range(max(args.warmup, 1)):
+            run5()
+        ms = events_ms(run5, args.steps)
+        print(f"[bench] only=config5 {ms:.3f} ms per call", file=sys.stderr, flush=True)
+        return
     st = Config3Step(dev)
     n, C, coords, x_f32, w1, w2 = st.n, st.C, st.coords, st.x_f32, st.w1, st.w2
     nbr, ws, h, out = st.nbr, st.ws, st.h, st.out
