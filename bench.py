@@ -322,8 +322,8 @@ def config_components(dev, st=None, steps: int = 5):
                 "gbps": gbps, "frac_hbm": gbps / PEAK_HBM_GBPS}
     c3 = synth.config3_coords()
     shuffled = c3[np.random.default_rng(11).permutation(len(c3))]
-    children = coords5
-    for m in masks:
+    children, masks5 = synth.config5_stack_inputs()
+    for m in masks5:
         children = synth.child_expand(children, m)
     out["map_modes"] = {"config3_shuffled": map_mode(shuffled, "config 3 coords in a random row order"),
                         "config5_children": map_mode(children, "config 5's last child set (C2S order)")}
