@@ -1237,8 +1237,10 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
     const int nkc = args.cin_g / (CB / 2);
     if (tmask != 0u && nkc > 0) {
         const uint16_t *input = static_cast<const uint16_t *>(args.input);
-        const __amdgpu_buffer_rsrc_t a_rsrc =
-            make_rsrc(input + in_col0, (uint32_t)(args.n_in * row_bytes - in_col0 * (int64_t)sizeof(uint16_t)));
+        const i32x4_rsrc a_rsrc =
+            rsrc_words(input + in_col0, (uint32_t)(args.n_in * row_bytes - in_col0 * (int64_t)sizeof(uint16_t)));
+        const uint32_t halo_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)s_halo;
+        const int wave_u = __builtin_amdgcn_readfirstlane(wave);  // uniform: scalar DMA branches
         const int n_ot = (args.cout_g + kBN - 1) / kBN;  // 128-channel tiles of the packing
         // Packed weights (sc_conv_weight_pack): per (group, 128-channel tile)
         // a block of K x nkc x 8 fragments; fragment (k, c, jj) is 64 lanes x
@@ -1278,7 +1280,10 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
             for (int jj = 0; jj < 4; ++jj) f[jj] = bload16(w_rsrc, live ? wk + (uint32_t)jj * kFrag : kOobOffset);
         };
         // Halo DMA: instruction wave + 4*ii fills halo rows 16*(wave + 4*ii) + lane/4;
-        // the lane moves logical piece hslot(j, lane%4) of row j.
+        // the lane moves logical piece hslot(j, lane%4) of row j.  Issued as
+        // lds_dma16 (the compiler does not count it): the caller's
+        // wait_vmcnt<0> is the wait, and no other vector-memory load is
+        // issued between a halo load and that wait.
         auto load_halo = [&](int c) {
             const uint32_t cb = (uint32_t)(c * CB) + (uint32_t)(hslot(lane >> 2, lane & 3) * 16);
             // All source offsets first (rows < kPlanHaloMax, in bounds; those
@@ -1288,13 +1293,11 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
             for (int ii = 0; ii < kHaloPerWave; ++ii) hv[ii] = s_hoff[16 * (wave + 4 * ii) + (lane >> 2)];
 #pragma unroll
             for (int ii = 0; ii < kHaloPerWave; ++ii) {
-                const int instr = wave + 4 * ii;
+                const int instr = wave_u + 4 * ii;
                 if (instr < n_halo_instr) {
                     const int j = 16 * instr + (lane >> 2);
                     const uint32_t off = j < U ? hv[ii] + cb : kOobOffset;
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                        a_rsrc, (__attribute__((address_space(3))) void *)(s_halo + instr * 1024), 16, off, 0,
-                        0, 0);
+                    lds_dma16(a_rsrc, off, halo_lds + (uint32_t)instr * 1024u);
                 }
             }
         };
