@@ -272,6 +272,26 @@ def test_planned_conv_shapes(oracle, cin, cout, groups, out_dtype):
                  "planned conv")
 
 
+@pytest.mark.parametrize("kernel", [(1, 1, 1), (3, 1, 1), (1, 3, 3), (3, 3, 1)])
+@pytest.mark.parametrize("cout", [64, 128])
+def test_planned_small_kernels(oracle, kernel, cout):
+    """Plans over fewer than 27 offsets (K = 1, 3, 9): a tile's used-offset
+    mask has a few bits, down to one (K = 1: the halo is the tile's own rows);
+    64 output channels take the 64-channel tile, 128 the 128-channel one."""
+    coords = synth.config1_coords()
+    rng = np.random.default_rng(sum(kernel) * 31 + cout)
+    n, cin = len(coords), 64
+    K = kernel[0] * kernel[1] * kernel[2]
+    x = rbf(synth.normal_f32(rng, (n, cin)))
+    w = rbf(synth.conv_weight(rng, cout, K, cin, 1.0 / np.sqrt(K * cin)))
+    b = synth.normal_f32(rng, cout, 0.1)
+    cfg = F.SparseSubmConvConfig(cin, cout, *kernel)
+    out, nbr, _ = planned(cfg, coords, x, w, b, out_dtype=torch.bfloat16)
+    assert nbr.shape == (n, K)
+    exp = oracle.conv_ref_f64(ocfg(oracle, cfg), w, b, x, nbr)
+    assert_close(out.float().cpu().numpy(), exp, TOL_BF16, f"planned conv, kernel {kernel}")
+
+
 def test_planned_int8_weights(oracle):
     coords = synth.config1_coords()
     rng = np.random.default_rng(5)
