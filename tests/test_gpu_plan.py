@@ -292,6 +292,27 @@ def test_planned_small_kernels(oracle, kernel, cout):
     assert_close(out.float().cpu().numpy(), exp, TOL_BF16, f"planned conv, kernel {kernel}")
 
 
+@pytest.mark.parametrize("n", [0, 1, 2, 257])
+@pytest.mark.parametrize("cout", [64, 128])
+def test_planned_tiny_inputs(oracle, n, cout):
+    """Planned convs on 0, 1, 2 and 257 rows: the empty map and plan, a lone
+    row whose only neighbour is itself (its tile is 255 padding rows), and a
+    full tile followed by a one-row tile."""
+    coords = np.ascontiguousarray(synth.config1_coords()[:n])
+    rng = np.random.default_rng(n + cout)
+    cin = 64
+    x = rbf(synth.normal_f32(rng, (n, cin)))
+    w = rbf(synth.conv_weight(rng, cout, 27, cin, 1.0 / np.sqrt(27 * cin)))
+    b = synth.normal_f32(rng, cout, 0.1)
+    cfg = F.SparseSubmConvConfig(cin, cout)
+    out, nbr, _ = planned(cfg, coords, x, w, b, out_dtype=torch.bfloat16)
+    assert tuple(out.shape) == (n, cout)
+    if n == 0:
+        return
+    exp = oracle.conv_ref_f64(ocfg(oracle, cfg), w, b, x, nbr)
+    assert_close(out.float().cpu().numpy(), exp, TOL_BF16, f"planned conv on {n} rows")
+
+
 def test_planned_int8_weights(oracle):
     coords = synth.config1_coords()
     rng = np.random.default_rng(5)
