@@ -145,6 +145,9 @@ static int conv_forward_impl(const sc_conv_config *cfg, int act_dtype, const voi
     rc = c2s_forms(cfg, epi, c2s);
     if (rc) return rc;
     if (n_q == 0) return SC_OK;
+    // A child scatter with no active child writes nothing (the reference's
+    // select of an empty index); its output may be an empty (NULL) buffer.
+    if (c2s.scatter && c2s.scatter_n == 0) return SC_OK;
     if (!d_input || (!d_map && !dense) || !d_weight || !d_out) return fail(SC_ERR_NULL, "sparse conv: NULL pointer");
 
     ConvArgs a;

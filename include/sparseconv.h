@@ -181,7 +181,8 @@ typedef struct sc_conv_epilogue {
      *    4): parent row r's channels [c*C, (c+1)*C) are child c's features
      *    and go to row child_rows[8r + c] of d_out ([n_child_rows][C]); -1
      *    (inactive child) drops them.  LayerNorm then runs over each child's
-     *    C channels.  This is conv1 + reshape [P, 8C] -> [8P, C] + select
+     *    C channels.  With n_child_rows == 0 the call writes nothing and
+     *    d_out may be NULL.  This is conv1 + reshape [P, 8C] -> [8P, C] + select
      *    (sparse_decoder_runtime_impl.rs:2240-2255) without the [P, 8C]
      *    tensor; child_rows comes from sc_subdivision_build_indexed.
      *  - parent skip, conv2 on the children: with S = skip_parent_channels/8

@@ -170,6 +170,57 @@ def test_conv2_parent_skip(oracle, cp, cout):
     assert_close(host(got), exp, TOL_BF16, "conv + parent skip")
 
 
+def test_linear_child_scatter_no_active_child():
+    """The dense linear's child scatter with no active child (a transposed
+    upsample whose mask is all zero) returns an empty [0, C] output."""
+    coords, _ = _parents_and_mask(n=500, seed=9)
+    rng = np.random.default_rng(9)
+    cin, cchild = 64, 32
+    x = rbf(synth.normal_f32(rng, (len(coords), cin)))
+    w = rbf(synth.normal_f32(rng, (8 * cchild, cin), 1 / np.sqrt(cin)))
+    cc, _, rows = F.subdivision_build_indexed(dev(coords), mask=dev(np.zeros((len(coords), 8), np.uint8)))
+    assert cc.shape[0] == 0
+    got = F.linear_forward(bf16_dev(x), bf16_dev(w), dev(synth.normal_f32(rng, 8 * cchild)),
+                           child_rows=rows, n_child_rows=0)
+    assert tuple(got.shape) == (0, cchild)
+
+
+@pytest.mark.parametrize("which", ["none", "one", "all"])
+@pytest.mark.parametrize("cout", [64, 128])
+def test_c2s_block_degenerate_masks(which, cout):
+    """The fused block with no active child (the children's map, plan and
+    conv2 run on zero rows), one active child, and every child active,
+    against the reference's unfused composition within 2^-5."""
+    coords, _ = _parents_and_mask(n=700, seed=5)
+    rng = np.random.default_rng(cout + len(which))
+    P, cin = len(coords), 64
+    mask = np.zeros((P, 8), np.uint8)
+    if which == "one":
+        mask[P // 2, 5] = 1
+    elif which == "all":
+        mask[:] = 1
+
+    def layer(ci, co):
+        w = rbf(synth.conv_weight(rng, co, 27, ci, 1 / np.sqrt(27 * ci)))
+        return D.ConvLayer(F.SparseSubmConvConfig(ci, co), bf16_dev(w), dev(synth.normal_f32(rng, co, 0.1)))
+    up = D.C2SUpsampleBlock(cin, cout, dev((1 + 0.1 * rng.standard_normal(cin)).astype(np.float32)),
+                            dev((0.1 * rng.standard_normal(cin)).astype(np.float32)),
+                            layer(cin, 8 * cout), layer(cout, cout))
+    pnb = D.Neighborhood.build(up.conv1.cfg, dev(coords))
+    x = bf16_dev(synth.normal_f32(rng, (P, cin)))
+    md = dev(mask)
+    cnb, y = up.forward(pnb, x, mask=md)
+    A = int(mask.sum())
+    assert tuple(y.shape) == (A, cout) and tuple(cnb.coords.shape) == (A, 4)
+    assert np.array_equal(cnb.coords.cpu().numpy(), synth.child_expand(coords, mask).reshape(-1, 4))
+    up.fused = False
+    _, y_ref = up.forward(pnb, x, mask=md)
+    assert tuple(y_ref.shape) == (A, cout)
+    if A:
+        d = (y.float() - y_ref.float()).abs().max().item()
+        assert d <= 2 ** -5 * max(1.0, y_ref.float().abs().max().item()), d
+
+
 def test_c2s_block_fused_config4_parents(oracle):
     """The fused block on config 4's parent set (the config-2 shell + cube,
     113,857 parents at 512 channels, near-surface children at 256 channels):
