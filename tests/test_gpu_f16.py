@@ -69,6 +69,29 @@ def test_config1_conv_f16(oracle, planned, out_dtype):
     assert e <= (1e-3 if out_dtype == torch.float16 else 1e-4), e
 
 
+@pytest.mark.parametrize("kernel,n", [((3, 3, 1), 14648), ((1, 1, 1), 14648), ((3, 3, 3), 257)])
+@pytest.mark.parametrize("cout", [64, 128])
+def test_f16_planned_few_offsets_and_rows(oracle, kernel, n, cout):
+    """The planned f16 tile on plans over 9 and 1 offsets, and on 257 rows
+    (a full tile then a one-row tile), at both tile widths."""
+    coords = np.ascontiguousarray(synth.config1_coords()[:n])
+    rng = np.random.default_rng(n + cout + sum(kernel))
+    cin = 64
+    K = kernel[0] * kernel[1] * kernel[2]
+    x = _fence(oracle, synth.normal_f32(rng, (n, cin)))
+    w = _fence(oracle, synth.conv_weight(rng, cout, K, cin, 1 / np.sqrt(K * cin)))
+    b = synth.normal_f32(rng, cout, 0.1)
+    cfg = F.SparseSubmConvConfig(cin, cout, *kernel)
+    cd = dev(coords)
+    nbr = F.neighbor_rows_tensor_from_coords_tensor(cfg, cd)
+    wd = f16_dev(w)
+    got = F.sparse_subm_conv_forward(cfg, f16_dev(x), nbr, wd, dev(b), out_dtype=torch.float16,
+                                     plan=F.build_conv_plan(cfg, cd, nbr),
+                                     packed_weight=F.pack_conv_weight(cfg, wd))
+    exp = oracle.conv_gemm_f64(oracle.OracleConfig(cin, cout, *kernel), w, b, x, nbr.cpu().numpy())
+    assert_close(host(got), exp, TOL_BF16, f"f16 planned conv, kernel {kernel}, {n} rows")
+
+
 def test_config2_conv_f16_planned(oracle):
     """Config 2's shape (113,857 voxels, C = 256) in f16 through the planned
     conv, 2,000 sampled rows (first / last / overflow tiles included)."""
