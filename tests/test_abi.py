@@ -138,6 +138,25 @@ def test_argument_errors_before_device_work():
     assert L.sc_add(0, None, None, 0, None, None) == 0
 
 
+def test_child_scatter_without_children_is_a_no_op():
+    """A child scatter with n_child_rows == 0 (no active child) returns OK
+    before any device work, with a NULL output, through the conv and the
+    linear entries; a negative child count is a shape error."""
+    L = _capi.load()
+    fake = ctypes.c_void_p(256)  # never dereferenced: the call returns first
+    cfg = F.SparseSubmConvConfig(64, 8 * 32).to_c()
+    epi = _capi.ScConvEpilogue()
+    epi.child_rows = 256
+    epi.n_child_rows = 0
+    assert L.sc_subm_conv_forward_fused(ctypes.byref(cfg), 1, fake, 10, fake, 10, 1, fake, None, None,
+                                        ctypes.byref(epi), 1, None, None) == 0
+    assert L.sc_linear_forward(1, fake, 10, 64, 8 * 32, 1, fake, None, None, ctypes.byref(epi), 1,
+                               None, None) == 0
+    epi.n_child_rows = -1
+    rc = L.sc_linear_forward(1, fake, 10, 64, 8 * 32, 1, fake, None, None, ctypes.byref(epi), 1, None, None)
+    assert rc == 2 and b"negative child row count" in L.sc_last_error()
+
+
 def test_plan_size_matches_layout():
     """sc_conv_plan_size equals the section layout the Python reader mirrors."""
     for n_q, K in ((0, 27), (1, 27), (1000, 27), (1040679, 27), (4097, 1), (300, 8)):
