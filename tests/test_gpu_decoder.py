@@ -91,6 +91,23 @@ def test_config5_int8_decoder_stack(config5_run):
     assert len(trace) == 9 and all(e[2].plan is not None for e in trace), "every resolution got a conv plan"
 
 
+def test_stack_stage_without_children():
+    """A stack whose first upsample activates no child: the next stage's
+    residual blocks, map, plan and upsample all run on zero rows and the
+    stack returns [0, C] features and [0, 4] coords."""
+    coords = np.ascontiguousarray(synth.config1_coords()[:3000])
+    rng = np.random.default_rng(77)
+    stack = D.int8_stack([64, 64, 32], 1, seed=7)
+    x = dev(synth.bf16_bits(synth.normal_f32(rng, (len(coords), 64))).view(np.int16)).view(torch.bfloat16)
+    masks = [dev(np.zeros((len(coords), 8), np.uint8)), dev(np.zeros((0, 8), np.uint8))]
+    trace = []
+    nb, y = stack(dev(coords), x, masks, trace=trace)
+    torch.cuda.synchronize()
+    assert tuple(y.shape) == (0, 32) and tuple(nb.coords.shape) == (0, 4)
+    assert [e[1] for e in trace] == ["block", "up", "block", "up"]
+    assert tuple(trace[2][4].shape) == (0, 64)  # the second stage's residual block output
+
+
 @pytest.mark.parametrize("idx", range(9))
 def test_config5_layer_parity(oracle, config5_run, idx):
     """Each residual block and fused upsample of the config-5 stack at 2,000
