@@ -31,6 +31,7 @@ EXPORTED = (
     "sc_conv_weight_pack_size", "sc_conv_weight_pack",
     "sc_subdivision_build_static", "sc_conv_plan_check", "sc_conv_epilogue_workspace_size",
     "sc_subdivision_build_indexed", "sc_linear_skinny", "sc_linear_forward",
+    "sc_subdivision_logits_finish",
 )
 
 
@@ -129,6 +130,7 @@ def load() -> ctypes.CDLL:
     L.sc_linear_forward.argtypes = [i32, P, i64, i64, i64, i32, P, P, P, ctypes.POINTER(ScConvEpilogue), i32,
                                     P, P]
     L.sc_linear_skinny.argtypes = [i32, P, i64, i64, P, P, i64, P, P]
+    L.sc_subdivision_logits_finish.argtypes = [P, i64, i32, i32, P]
     L.sc_subdivision_build_static.argtypes = [P, P, P, P, i64, P, P, P, P, P]
     L.sc_gather_rows.argtypes = [i32, P, i64, i64, i64, P, i64, P, P]
     L.sc_c2s_skip_add.argtypes = [i32, P, i64, i64, i32, P, i64, i64, P, P]

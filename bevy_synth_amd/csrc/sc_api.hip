@@ -107,8 +107,10 @@ template <typename Tin, typename Tout, int VPL>
 __global__ __launch_bounds__(256) void layer_norm_kernel(const Tin *in, int64_t rows, int channels,
                                                          const float *__restrict__ w,
                                                          const float *__restrict__ b, float eps,
-                                                         int apply_silu, const Tout *res, Tout *out)
+                                                         int apply_silu, const Tout *res, Tout *out,
+                                                         const uint32_t *gate)
 {
+    if (gate && *gate) return;  // see launch_layer_norm
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (row >= rows) return;
@@ -208,8 +210,10 @@ template <typename Tin, typename Tout, int LPR, int NV, int NR>
 __global__ __launch_bounds__(256) void layer_norm_vec_kernel(const Tin *in, int64_t rows, int channels,
                                                              const float *__restrict__ w,
                                                              const float *__restrict__ b, float eps,
-                                                             int apply_silu, const Tout *res, Tout *out)
+                                                             int apply_silu, const Tout *res, Tout *out,
+                                                             const uint32_t *gate)
 {
+    if (gate && *gate) return;  // see launch_layer_norm
     constexpr int VEC = Vec16<Tin>::N;
     constexpr int RPW = 64 / LPR;  // rows per wave and load
     const int lane = threadIdx.x & 63;
@@ -303,8 +307,9 @@ __global__ __launch_bounds__(256) void layer_norm_wide_kernel(const Tin *in, int
                                                               const float *__restrict__ w,
                                                               const float *__restrict__ b,
                                                               float eps, int apply_silu, const Tout *res,
-                                                              Tout *out)
+                                                              Tout *out, const uint32_t *gate)
 {
+    if (gate && *gate) return;  // see launch_layer_norm
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (row >= rows) return;
@@ -398,9 +403,13 @@ __global__ void c2s_skip_add_vec_kernel(uint16_t *h, int n, int vpr, const Tp *_
     }
 }
 
+// gate: NULL, or a device word read by every workgroup before anything
+// else -- nonzero, the kernel writes nothing (the planned conv's plan status,
+// when this kernel normalises what that conv stored).
 template <typename Tin, typename Tout>
 int launch_layer_norm(const void *in, int64_t rows, int64_t ch, const float *w,
-                             const float *b, float eps, int silu, const void *res_, void *out, hipStream_t s)
+                             const float *b, float eps, int silu, const void *res_, void *out, hipStream_t s,
+                             const uint32_t *gate)
 {
     const unsigned g = grid_for(rows, 4, INT32_MAX);
     const Tin *x = (const Tin *)in;
@@ -420,7 +429,7 @@ int launch_layer_norm(const void *in, int64_t rows, int64_t ch, const float *w,
         const int64_t rows_per_block = 4 * (64 / lpr) * nr;
         const unsigned gv = grid_for(rows, (int)rows_per_block, INT32_MAX);
 #define LN_VEC(L, N, R) \
-    layer_norm_vec_kernel<Tin, Tout, L, N, R><<<gv, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y)
+    layer_norm_vec_kernel<Tin, Tout, L, N, R><<<gv, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y, gate)
         bool launched = true;
         if (lpr == 8 && nv == 1 && nr == 4) LN_VEC(8, 1, 4);
         else if (lpr == 16 && nv == 1 && nr == 4) LN_VEC(16, 1, 4);
@@ -442,17 +451,17 @@ int launch_layer_norm(const void *in, int64_t rows, int64_t ch, const float *w,
     }
     const int vpl = (C + 63) / 64;
     if (vpl <= 1)
-        layer_norm_kernel<Tin, Tout, 1><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y);
+        layer_norm_kernel<Tin, Tout, 1><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y, gate);
     else if (vpl <= 2)
-        layer_norm_kernel<Tin, Tout, 2><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y);
+        layer_norm_kernel<Tin, Tout, 2><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y, gate);
     else if (vpl <= 4)
-        layer_norm_kernel<Tin, Tout, 4><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y);
+        layer_norm_kernel<Tin, Tout, 4><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y, gate);
     else if (vpl <= 8)
-        layer_norm_kernel<Tin, Tout, 8><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y);
+        layer_norm_kernel<Tin, Tout, 8><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y, gate);
     else if (vpl <= 16)
-        layer_norm_kernel<Tin, Tout, 16><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y);
+        layer_norm_kernel<Tin, Tout, 16><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y, gate);
     else
-        layer_norm_wide_kernel<Tin, Tout><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y);
+        layer_norm_wide_kernel<Tin, Tout><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y, gate);
     SC_LAUNCH_CHECK("layer_norm_kernel launch");
     return SC_OK;
 }
@@ -537,7 +546,7 @@ __global__ __launch_bounds__(256) void linear_skinny_kernel(const Tin *__restric
 
 int layer_norm_rows(int in_dtype, const void *d_in, int64_t rows, int64_t channels, const float *d_w,
                     const float *d_b, float eps, int apply_silu, int out_dtype, const void *d_res, void *d_out,
-                    hipStream_t s)
+                    hipStream_t s, const uint32_t *d_gate)
 {
     if (rows < 0 || channels <= 0 || channels > INT32_MAX)
         return fail(SC_ERR_SHAPE, "layer_norm: invalid rows/channels");
@@ -545,7 +554,7 @@ int layer_norm_rows(int in_dtype, const void *d_in, int64_t rows, int64_t channe
     if (!d_in || !d_out) return fail(SC_ERR_NULL, "layer_norm: NULL pointer");
 #define LN_CASE(DI, TI, DO, TO)                                                                          \
     if (in_dtype == DI && out_dtype == DO)                                                              \
-        return launch_layer_norm<TI, TO>(d_in, rows, channels, d_w, d_b, eps, apply_silu, d_res, d_out, s);
+        return launch_layer_norm<TI, TO>(d_in, rows, channels, d_w, d_b, eps, apply_silu, d_res, d_out, s, d_gate);
     LN_CASE(SC_DTYPE_F32, float, SC_DTYPE_F32, float)
     LN_CASE(SC_DTYPE_F32, float, SC_DTYPE_BF16, uint16_t)
     LN_CASE(SC_DTYPE_F32, float, SC_DTYPE_F16, _Float16)
@@ -555,6 +564,35 @@ int layer_norm_rows(int in_dtype, const void *d_in, int64_t rows, int64_t channe
     LN_CASE(SC_DTYPE_F16, _Float16, SC_DTYPE_F16, _Float16)
 #undef LN_CASE
     return fail(SC_ERR_DTYPE, "layer_norm: unsupported dtype pair (f32 / bf16 / f16)");
+}
+
+// The decoder's post-processing of the to_subdiv logits [rows][8] in place,
+// one thread per row: round each logit to f16 and back (quantize_f16 under
+// compute_fp16, sparse_decoder_runtime_impl.rs:871-873, host :1205-1207),
+// then subtract the row's mean (center_subdivision_logits; row_center_logits,
+// sparse_decoder_wgpu_ops.rs:1728-1745: the f32 sum in child order / 8).
+__global__ __launch_bounds__(256) void logits_finish_kernel(float *__restrict__ logits, int64_t rows, int round_f16,
+                                                           int center)
+{
+    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= rows) return;
+    float4 *q = reinterpret_cast<float4 *>(logits + r * 8);
+    const float4 a = q[0], b = q[1];
+    float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    if (round_f16) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) v[c] = f16_bits_to_f32(f32_to_f16_bits(v[c]));
+    }
+    if (center) {
+        float sum = 0.f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) sum += v[c];
+        const float mean = sum / 8.0f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) v[c] -= mean;
+    }
+    q[0] = make_float4(v[0], v[1], v[2], v[3]);
+    q[1] = make_float4(v[4], v[5], v[6], v[7]);
 }
 
 }  // namespace sc
@@ -711,6 +749,19 @@ int sc_linear_skinny(int in_dtype, const void *d_x, int64_t rows, int64_t in_cha
     else
         return fail(SC_ERR_DTYPE, "skinny linear input must be f32, bf16 or f16");
     SC_LAUNCH_CHECK("linear_skinny_kernel launch");
+    return SC_OK;
+}
+
+int sc_subdivision_logits_finish(float *d_logits, int64_t rows, int round_f16, int center, sc_stream stream)
+{
+    clear_error();
+    if (rows < 0) return fail(SC_ERR_SHAPE, "subdivision logits: invalid rows");
+    if (rows == 0 || (!round_f16 && !center)) return SC_OK;
+    if (!d_logits) return fail(SC_ERR_NULL, "subdivision logits: NULL pointer");
+    if ((uintptr_t)d_logits % 16 != 0) return fail(SC_ERR_SHAPE, "subdivision logits must be 16-byte aligned");
+    logits_finish_kernel<<<grid_for(rows, 256, INT32_MAX), 256, 0, as_stream(stream)>>>(d_logits, rows, round_f16 != 0,
+                                                                                     center != 0);
+    SC_LAUNCH_CHECK("logits_finish_kernel launch");
     return SC_OK;
 }
 

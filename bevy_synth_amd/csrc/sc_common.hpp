@@ -36,9 +36,11 @@ int validate_config(const sc_conv_config *cfg);
 int silu_inplace(int dtype, void *d, int64_t n, hipStream_t s);
 // Row LayerNorm (+ SiLU) (+ a residual in the output dtype, added before the
 // one rounding to the output dtype); d_res may be NULL.  Stream-ordered.
+// d_gate: NULL, or a device word that, when nonzero as the kernel starts,
+// makes it write nothing (a planned conv's plan status).
 int layer_norm_rows(int in_dtype, const void *d_in, int64_t rows, int64_t channels, const float *d_w,
                     const float *d_b, float eps, int apply_silu, int out_dtype, const void *d_res, void *d_out,
-                    hipStream_t s);
+                    hipStream_t s, const uint32_t *d_gate = nullptr);
 
 inline bool mul_ok(int64_t a, int64_t b, int64_t *out)
 {

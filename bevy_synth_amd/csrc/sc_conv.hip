@@ -253,8 +253,12 @@ static int conv_forward_impl(const sc_conv_config *cfg, int act_dtype, const voi
     const void *plan = (d_plan && (act_bf16 || act_f16) && mfma && K <= kHaloK) ? d_plan : nullptr;
     int rc2 = launch_conv_typed(a, act_f32, w_dtype, conv_out_dtype, groups, mfma, plan, s);
     if (rc2 != SC_OK || !split_ln) return rc2;
+    // After a planned conv, the row kernel is gated on the plan's status: a
+    // conv that found a mismatch stored nothing to normalise, and nothing
+    // may reach d_out.
     return layer_norm_rows(SC_DTYPE_F32, conv_out, ln_rows, ln_ch, epi->ln_weight, epi->ln_bias, epi->ln_eps,
-                           want_silu, out_dtype, d_residual, d_out, s);
+                           want_silu, out_dtype, d_residual, d_out, s,
+                           plan ? &static_cast<const PlanHeader *>(plan)->status : nullptr);
 }
 
 

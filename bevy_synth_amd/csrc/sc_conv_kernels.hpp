@@ -755,9 +755,11 @@ __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
     int tile;
     if (args.tile_list) {
         // Plan tile tile_list[b / kSubTiles], part b % kSubTiles.  The plan's
-        // header is checked first (the halo kernel flags a mismatch), and a
-        // listed tile must lie inside the order.
-        if (!plan_matches(args.plan_hdr, args)) return;
+        // header is checked first, and its status: the halo kernel before
+        // this launch flags a map or packed-weight mismatch there (and a
+        // flagged plan stays flagged until rebuilt).  A listed tile must lie
+        // inside the order.
+        if (!plan_matches(args.plan_hdr, args) || args.plan_hdr->status != 0u) return;
         const int b = (int)blockIdx.x / kSubTiles;
         if (b >= *args.tile_count) return;
         const int lt = args.tile_list[b];
@@ -1180,6 +1182,9 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
             flag_plan_status(plan.hdr, (plan_ok ? 0u : kPlanStatusMapMismatch) | (w_ok ? 0u : kPlanStatusWeightMismatch));
             return;
         }
+        // a plan flagged by an earlier call stays flagged until it is
+        // rebuilt: nothing is written meanwhile
+        if (plan.hdr->status != 0u) return;
     }
     const int tile = tile_for_block(blockIdx.x, gridDim.x);
     const int U = plan.tile_u[tile];

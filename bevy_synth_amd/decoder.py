@@ -17,6 +17,11 @@
 * ``DecoderStack``    : config 5's decoder-shaped stack: per stage, residual
                         blocks then a C2S 2x upsample, int8 weights, bf16
                         activations.
+* ``TrellisDecoderStage``: one stage of TRELLIS2's sparse structured-latent
+                        decoder (sparse_decoder_runtime_impl.rs:522-1171):
+                        ConvNeXt blocks, then the C2S upsample whose children
+                        the to_subdiv logits choose; loaded from a checkpoint
+                        by ``loading.load_decoder_stage``.
 """
 from __future__ import annotations
 
@@ -28,7 +33,8 @@ import torch
 from .flex_gmm import (ConvPlan, NeighborMapWorkspace, SparseSubmConvConfig, build_conv_plan,
                        c2s_skip_add, gather_rows, kernel_rows, layer_norm, linear_forward, linear_skinny,
                        neighbor_rows_tensor_from_coords_tensor, pack_conv_weight,
-                       sparse_subm_conv_forward, subdivision_build, subdivision_build_indexed)
+                       sparse_subm_conv_forward, subdivision_build, subdivision_build_indexed,
+                       subdivision_logits_finish)
 
 LAYER_NORM32_EPS = 1e-6  # sparse_decoder.rs:43
 
@@ -164,6 +170,11 @@ class C2SUpsampleBlock:
     # Unfused: the reference's composition (conv1 [P, 8*Cout] -> select ->
     # LayerNorm -> conv2 -> skip add), kept as the comparison path.
     fused: bool = True
+    # the decoder's logits options: f16 rounding of the logits under
+    # compute_fp16 (the to_subdiv weights are then f16-rounded too, by the
+    # loader), and centering each row (center_subdivision_logits)
+    compute_fp16: bool = False
+    center_logits: bool = False
 
     def __call__(self, parent_coords: torch.Tensor, parent_feats: torch.Tensor,
                  logits: Optional[torch.Tensor] = None, mask: Optional[torch.Tensor] = None,
@@ -215,8 +226,10 @@ class C2SUpsampleBlock:
     def subdivision_logits(self, parent_feats: torch.Tensor) -> torch.Tensor:
         """to_subdiv: [P, 8] f32 logits of the parent features (the skinny
         linear, linear_skinny_forward_wgpu, crates/burn_flex_gmm/src/wgpu/
-        ops.rs:1390-1410)."""
-        return linear_skinny(parent_feats, self.to_subdiv_weight, self.to_subdiv_bias)
+        ops.rs:1390-1410), then rounded to f16 under compute_fp16 and
+        centered per row when asked (sparse_decoder_runtime_impl.rs:859-878)."""
+        logits = linear_skinny(parent_feats, self.to_subdiv_weight, self.to_subdiv_bias)
+        return subdivision_logits_finish(logits, round_f16=self.compute_fp16, center=self.center_logits)
 
 
 def transposed_upsample(parent_coords: torch.Tensor, parent_feats: torch.Tensor,
@@ -274,6 +287,77 @@ class DecoderStack:
                 trace.append((s, "up", nb, x, y, child_nb))
             nb, x = child_nb, y
         return nb, x
+
+
+# decoder_subdivision_child_thresholds (sparse_decoder_wgpu_ops.rs:1813-1822)
+# with DecoderRuntimeConfig's defaults (sparse_decoder.rs:182-190): every
+# child's threshold is the global 0.0.
+DEFAULT_SUBDIVISION_THRESHOLDS = (0.0,) * 8
+
+
+def subdivision_child_thresholds(threshold: float = 0.0,
+                                 child_thresholds: Optional[Sequence[float]] = None) -> Tuple[float, ...]:
+    """decoder_subdivision_child_thresholds: the global threshold, replaced
+    per child by a finite child threshold."""
+    import math
+    out = [float(threshold)] * 8
+    if child_thresholds is not None:
+        for c, t in enumerate(child_thresholds):
+            if math.isfinite(t):
+                out[c] = float(t)
+    return tuple(out)
+
+
+@dataclass
+class TrellisDecoderStage:
+    """One stage of TRELLIS2's sparse structured-latent decoder
+    (SparseStructuredLatentDecoder, sparse_decoder_runtime_impl.rs:522-1171;
+    DecoderStage, sparse_decoder.rs): the stage's ConvNeXt blocks on one
+    Neighborhood, then -- every stage but the last -- the C2S upsample, whose
+    children the to_subdiv logits select against the thresholds
+    (logits_to_mask: logit > threshold, sparse_decoder_wgpu_ops.rs:1759-1811).
+    Built from a checkpoint by ``loading.load_decoder_stage``."""
+
+    convnext_blocks: List[ConvNeXtBlock]
+    upsample: Optional[C2SUpsampleBlock] = None
+
+    def forward(self, nb: Neighborhood, feats: torch.Tensor,
+                thresholds: Sequence[float] = DEFAULT_SUBDIVISION_THRESHOLDS,
+                mask: Optional[torch.Tensor] = None, workspace: Optional[NeighborMapWorkspace] = None,
+                trace: Optional[list] = None) -> Tuple[Neighborhood, torch.Tensor]:
+        """feats [N, C] at ``nb``'s coords -> (the next resolution's
+        Neighborhood, its features); the last stage returns ``nb`` itself.
+        ``mask`` [P, 8] (the reference's guide subdivisions) replaces the
+        logits.  ``trace`` (a list) receives ("convnext", b, input, output),
+        ("logits", parent feats, logits) and ("up", parent feats, output)."""
+        x = feats
+        for b, blk in enumerate(self.convnext_blocks):
+            y = blk(x, nb)
+            if trace is not None:
+                trace.append(("convnext", b, x, y))
+            x = y
+        if self.upsample is None:
+            return nb, x
+        logits = None
+        if mask is None:
+            if self.upsample.to_subdiv_weight is None:
+                raise ValueError("decoder stage requires guide_subdivisions but none were provided")
+            logits = self.upsample.subdivision_logits(x)
+            if trace is not None:
+                trace.append(("logits", x, logits))
+        child_nb, out = self.upsample.forward(nb, x, logits=logits, mask=mask, thresholds=thresholds,
+                                              workspace=workspace)
+        if trace is not None:
+            trace.append(("up", x, out))
+        return child_nb, out
+
+    def __call__(self, coords: torch.Tensor, feats: torch.Tensor, **kw) -> Tuple[torch.Tensor, torch.Tensor]:
+        """coords [N, 4] i32 -> (child coords, child features)."""
+        cfg = (self.convnext_blocks[0].conv.cfg if self.convnext_blocks
+               else self.upsample.conv1.cfg)
+        nb = Neighborhood.build(cfg, coords, kw.get("workspace"))
+        out_nb, out = self.forward(nb, feats, **kw)
+        return out_nb.coords, out
 
 
 def int8_stack(channels: Sequence[int], blocks_per_stage: int, seed: int,

@@ -702,6 +702,20 @@ def linear_skinny(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Te
     return out
 
 
+def subdivision_logits_finish(logits: torch.Tensor, round_f16: bool = False, center: bool = False
+                              ) -> torch.Tensor:
+    """The decoder's to_subdiv logits post-processing, in place on [P, 8] f32:
+    f16 rounding under compute_fp16 (sparse_decoder_runtime_impl.rs:871-873),
+    then row centering (center_subdivision_logits, sparse_decoder_wgpu_ops.rs
+    :1728-1745).  Returns ``logits``."""
+    _require_cuda("logits", logits)
+    if logits.dtype != torch.float32 or logits.dim() != 2 or logits.shape[1] != 8 or not logits.is_contiguous():
+        raise SparseConvError(2, "decoder subdivision logits tensor must be f32 [P, 8]")
+    check(_capi.load().sc_subdivision_logits_finish(_ptr(logits), logits.shape[0], int(round_f16), int(center),
+                                                    _stream()))
+    return logits
+
+
 def gather_rows(src: torch.Tensor, split: int, idx: torch.Tensor) -> torch.Tensor:
     """select(0, idx) on the [rows*split, cols/split] view of src (conv1 child
     selection, sparse_decoder_runtime_impl.rs:2249-2255)."""

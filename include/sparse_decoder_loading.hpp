@@ -9,8 +9,15 @@
 //                                groups from the expected input channels,
 //                                the same shape checks and messages
 //   load_linear        :1-48     weight [Cout, Cin] + bias [Cout]
+//   load_linear_dynamic:50-91    the same, output width taken from the file
 //   load_vector        :210-229
-//   round_vec_to_f16   :202-208  (the compute_fp16 copies)
+//   round_vec_to_f16   :202-208  (the compute_fp16 copies: weights and
+//                                biases alike, sparse_decoder.rs:780-793)
+// and the per-stage part of SparseStructuredLatentDecoder::from_safetensors
+// (sparse_decoder_runtime_impl.rs:94-190): load_decoder_stage reads stage s's
+// ConvNeXt blocks blocks.{s}.{b}.{conv, norm, mlp.0, mlp.2} and, unless s is
+// the last stage, its C2S upsample blocks.{s}.{N}.{norm1, to_subdiv, conv1,
+// conv2}, with the reference's expected shapes.
 // The layers land on the device in the compute dtype (f32, bf16 with the
 // reference's round-to-nearest-even, or f16), and a conv's weights are packed
 // once for the planned conv (sc_conv_weight_pack), the role pack_flex_weight
@@ -425,9 +432,22 @@ inline Result<DeviceTensor> upload_as(const std::vector<float> &v, std::vector<s
     return DeviceTensor::from_host(h.data(), std::move(shape), dt, stream);
 }
 
+// A bias on the device, f32: rounded to f16 first for the f16 compute dtype
+// (the reference's bias_fp16, sparse_decoder_loading.rs:195 and :38, used
+// whenever compute_fp16 is on, sparse_decoder.rs:780-793).
+inline Result<DeviceTensor> upload_bias(const std::vector<float> &b, DType compute, hipStream_t stream = nullptr)
+{
+    if (compute == DType::F16) {
+        const std::vector<float> r = round_vec_to_f16(b);
+        return DeviceTensor::from_host(r.data(), {b.size()}, DType::F32, stream);
+    }
+    return DeviceTensor::from_host(b.data(), {b.size()}, DType::F32, stream);
+}
+
 // A decoder conv layer on the device: the config, the weight in the
 // reference layout [Cout, KD, KH, KW, Cin_g] and its packed copy (16-bit
-// compute dtypes with Cin_g a multiple of 32) in the compute dtype, bias f32.
+// compute dtypes with Cin_g a multiple of 32) in the compute dtype, bias f32
+// (f16-rounded values for the f16 compute dtype).
 struct SparseConvLayerHip {
     SparseSubmConvConfig config;
     DeviceTensor weight;
@@ -485,7 +505,7 @@ inline Result<SparseConvLayerHip> load_sparse_conv(const SafeTensors &st, const 
     auto wd = upload_as(layer.weight_host, {out_channels, kd, kh, kw, in_pg}, compute, stream);
     if (wd.is_err()) return R::err(wd.error());
     layer.weight = wd.take();
-    auto bd = DeviceTensor::from_host(layer.bias_host.data(), {out_channels}, DType::F32, stream);
+    auto bd = upload_bias(layer.bias_host, compute, stream);
     if (bd.is_err()) return R::err(bd.error());
     layer.bias = bd.take();
     if ((compute == DType::BF16 || compute == DType::F16) && in_pg % 32 == 0) {
@@ -507,10 +527,13 @@ struct LinearLayerHip {
     std::vector<float> weight_host, bias_host;
 };
 
-// load_linear, sparse_decoder_loading.rs:1-48.
-inline Result<LinearLayerHip> load_linear(const SafeTensors &st, const std::string &weight_key,
-                                          const std::string &bias_key, size_t expected_in, size_t expected_out,
-                                          DType compute, hipStream_t stream = nullptr)
+namespace detail {
+// The body of load_linear and load_linear_dynamic (expected_out 0: any).
+// f32_weight: the weight stays an f32 operand like the bias (f16-rounded for
+// the f16 compute dtype) -- the to_subdiv head, whose skinny linear takes f32.
+inline Result<LinearLayerHip> load_linear_impl(const SafeTensors &st, const std::string &weight_key,
+                                               const std::string &bias_key, size_t expected_in, size_t expected_out,
+                                               DType compute, hipStream_t stream, bool f32_weight = false)
 {
     using R = Result<LinearLayerHip>;
     auto w = st.load_tensor_f32(weight_key);
@@ -534,13 +557,129 @@ inline Result<LinearLayerHip> load_linear(const SafeTensors &st, const std::stri
     layer.out_channels = out_channels;
     layer.weight_host = std::move(w.value().second);
     layer.bias_host = std::move(b.value().second);
-    auto wd = upload_as(layer.weight_host, {out_channels, in_channels}, compute, stream);
+    auto wd = f32_weight ? upload_as(compute == DType::F16 ? round_vec_to_f16(layer.weight_host) : layer.weight_host,
+                                     {out_channels, in_channels}, DType::F32, stream)
+                         : upload_as(layer.weight_host, {out_channels, in_channels}, compute, stream);
     if (wd.is_err()) return R::err(wd.error());
     layer.weight = wd.take();
-    auto bd = DeviceTensor::from_host(layer.bias_host.data(), {out_channels}, DType::F32, stream);
+    auto bd = upload_bias(layer.bias_host, compute, stream);
     if (bd.is_err()) return R::err(bd.error());
     layer.bias = bd.take();
     return R::ok(std::move(layer));
+}
+}  // namespace detail
+
+// load_linear, sparse_decoder_loading.rs:1-48.
+inline Result<LinearLayerHip> load_linear(const SafeTensors &st, const std::string &weight_key,
+                                          const std::string &bias_key, size_t expected_in, size_t expected_out,
+                                          DType compute, hipStream_t stream = nullptr)
+{
+    return detail::load_linear_impl(st, weight_key, bias_key, expected_in, expected_out, compute, stream);
+}
+
+// load_linear_dynamic, sparse_decoder_loading.rs:50-91: the output width is
+// the file's (the ConvNeXt MLP's hidden width).
+inline Result<LinearLayerHip> load_linear_dynamic(const SafeTensors &st, const std::string &weight_key,
+                                                  const std::string &bias_key, size_t expected_in, DType compute,
+                                                  hipStream_t stream = nullptr)
+{
+    return detail::load_linear_impl(st, weight_key, bias_key, expected_in, 0, compute, stream);
+}
+
+// A vector (SafeTensors::load_vector: rank 1, length checked when
+// expected_len > 0) uploaded as f32: the LayerNorm affine vectors.
+inline Result<DeviceTensor> load_vector_device(const SafeTensors &st, const std::string &key, size_t expected_len,
+                                               hipStream_t stream = nullptr)
+{
+    auto v = st.load_vector(key, expected_len);
+    if (v.is_err()) return Result<DeviceTensor>::err(v.error());
+    return DeviceTensor::from_host(v.value().data(), {v.value().size()}, DType::F32, stream);
+}
+
+// TRELLIS2's sparse ConvNeXt block (sparse_decoder.rs, ConvNeXtBlock):
+// conv3x3x3 -> LayerNorm(norm) -> mlp.0 -> SiLU -> mlp.2 -> + x.
+struct ConvNeXtBlockHip {
+    SparseConvLayerHip conv;
+    DeviceTensor norm_weight, norm_bias;
+    LinearLayerHip mlp_0, mlp_2;
+};
+
+// The C2S upsample block (sparse_decoder.rs, C2SUpsampleBlock): norm1 affine,
+// the to_subdiv head (Linear Cin -> 8, weight and bias f32 for
+// sc_linear_skinny; absent when pred_subdiv is off),
+// conv1 Cin -> 8 Cout on the parents, conv2 Cout -> Cout on the children.
+struct C2SUpsampleBlockHip {
+    size_t in_channels = 0, out_channels = 0;
+    DeviceTensor norm1_weight, norm1_bias;
+    std::optional<LinearLayerHip> to_subdiv;
+    SparseConvLayerHip conv1, conv2;
+};
+
+// One decoder stage: its ConvNeXt blocks, then (all but the last stage) the
+// upsample to the next resolution.
+struct DecoderStageHip {
+    std::vector<ConvNeXtBlockHip> convnext_blocks;
+    std::optional<C2SUpsampleBlockHip> upsample_block;
+};
+
+// Stage stage_idx of the decoder, sparse_decoder_runtime_impl.rs:94-190:
+// num_blocks ConvNeXt blocks at stage_channels (model_channels[s]), then,
+// when next_channels > 0 (model_channels[s + 1]; 0 for the last stage),
+// the upsample blocks.{s}.{num_blocks}.* to next_channels, its to_subdiv
+// head read when pred_subdiv is set (the reference's default).  The same
+// keys, expected shapes and messages as the reference; the first failure
+// is returned.
+inline Result<DecoderStageHip> load_decoder_stage(const SafeTensors &st, size_t stage_idx, size_t num_blocks,
+                                                  size_t stage_channels, size_t next_channels, bool pred_subdiv,
+                                                  DType compute, hipStream_t stream = nullptr)
+{
+    using R = Result<DecoderStageHip>;
+    DecoderStageHip stage;
+    for (size_t b = 0; b < num_blocks; ++b) {
+        const std::string pre = "blocks." + std::to_string(stage_idx) + "." + std::to_string(b);
+        auto conv = load_sparse_conv(st, pre + ".conv.weight", pre + ".conv.bias", stage_channels, stage_channels,
+                                     compute, stream);
+        if (conv.is_err()) return R::err(conv.error());
+        auto nw = load_vector_device(st, pre + ".norm.weight", stage_channels, stream);
+        if (nw.is_err()) return R::err(nw.error());
+        auto nb = load_vector_device(st, pre + ".norm.bias", stage_channels, stream);
+        if (nb.is_err()) return R::err(nb.error());
+        auto m0 = load_linear_dynamic(st, pre + ".mlp.0.weight", pre + ".mlp.0.bias", stage_channels, compute, stream);
+        if (m0.is_err()) return R::err(m0.error());
+        auto m2 = load_linear_dynamic(st, pre + ".mlp.2.weight", pre + ".mlp.2.bias", 0, compute, stream);
+        if (m2.is_err()) return R::err(m2.error());
+        stage.convnext_blocks.push_back(
+            ConvNeXtBlockHip{conv.take(), nw.take(), nb.take(), m0.take(), m2.take()});
+    }
+    if (next_channels > 0) {
+        const std::string pre = "blocks." + std::to_string(stage_idx) + "." + std::to_string(num_blocks);
+        if (next_channels > SIZE_MAX / 8) return R::err("conv1_out channels overflow");
+        C2SUpsampleBlockHip up;
+        up.in_channels = stage_channels;
+        up.out_channels = next_channels;
+        if (pred_subdiv) {
+            auto ts = detail::load_linear_impl(st, pre + ".to_subdiv.weight", pre + ".to_subdiv.bias",
+                                               stage_channels, 8, compute, stream, true);
+            if (ts.is_err()) return R::err(ts.error());
+            up.to_subdiv = ts.take();
+        }
+        auto n1w = load_vector_device(st, pre + ".norm1.weight", stage_channels, stream);
+        if (n1w.is_err()) return R::err(n1w.error());
+        up.norm1_weight = n1w.take();
+        auto n1b = load_vector_device(st, pre + ".norm1.bias", stage_channels, stream);
+        if (n1b.is_err()) return R::err(n1b.error());
+        up.norm1_bias = n1b.take();
+        auto c1 = load_sparse_conv(st, pre + ".conv1.weight", pre + ".conv1.bias", stage_channels, 8 * next_channels,
+                                   compute, stream);
+        if (c1.is_err()) return R::err(c1.error());
+        up.conv1 = c1.take();
+        auto c2 = load_sparse_conv(st, pre + ".conv2.weight", pre + ".conv2.bias", next_channels, next_channels,
+                                   compute, stream);
+        if (c2.is_err()) return R::err(c2.error());
+        up.conv2 = c2.take();
+        stage.upsample_block = std::move(up);
+    }
+    return R::ok(std::move(stage));
 }
 
 }  // namespace loading

@@ -323,8 +323,11 @@ int sc_conv_weight_pack(const sc_conv_config *cfg, int w_dtype, const void *d_we
  * The kernels compare the plan's header (n_q, n_in, K) and the packed
  * weights' header (groups, Cout_g, Cin_g, K) with this call before they
  * read anything else from either buffer: on a mismatch d_out is left
- * untouched and the plan's status records it (sc_conv_plan_check).  A plan
- * from another map of the same n_q / n_in / K is not detected.
+ * untouched (the epilogue workspace of a LayerNorm wider than one tile too
+ * is then not normalised into d_out) and the plan's status records it
+ * (sc_conv_plan_check).  A flagged plan stays flagged until it is rebuilt:
+ * every planned conv on it leaves d_out untouched meanwhile.  A plan from
+ * another map of the same n_q / n_in / K is not detected.
  */
 int sc_subm_conv_forward_planned(const sc_conv_config *cfg, int act_dtype, const void *d_input,
                                  int64_t n_in, const int32_t *d_map, int64_t n_q, int w_dtype,
@@ -363,6 +366,15 @@ int sc_layer_norm(int in_dtype, const void *d_in, int64_t rows, int64_t channels
  * accumulation in a fixed order. */
 int sc_linear_skinny(int in_dtype, const void *d_x, int64_t rows, int64_t in_channels, const float *d_w,
                      const float *d_b, int64_t out_channels, float *d_out, sc_stream stream);
+
+/* Post-processing of the to_subdiv logits [rows][8] f32 in place (16-byte
+ * aligned), in the reference's order: with round_f16, each logit is rounded
+ * to f16 and back (quantize_f16 under compute_fp16,
+ * sparse_decoder_runtime_impl.rs:871-873); with center, the row's mean (f32
+ * sum in child order / 8) is subtracted (center_subdivision_logits,
+ * row_center_logits, sparse_decoder_wgpu_ops.rs:1728-1745).  Both off: no
+ * launch. */
+int sc_subdivision_logits_finish(float *d_logits, int64_t rows, int round_f16, int center, sc_stream stream);
 
 /* out = a + b elementwise over n values (add_inplace, sparse_decoder_wgpu_ops.rs
  * :1747-1757).  All three share `dtype`; d_out may alias d_a. */

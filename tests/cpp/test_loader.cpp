@@ -5,6 +5,12 @@
 //   test_loader device FILE OUTDIR   load the layers onto the device and
 //                                    download the weights (compute dtype
 //                                    bits) and the packed copies
+//   test_loader stage FILE OUTDIR S N C C2 DTYPE
+//                                    load_decoder_stage(S, N blocks, C -> C2;
+//                                    DTYPE bf16 | f16 | f32) and download
+//                                    every tensor of the stage as stored on
+//                                    the device (stage.<key>.bin), or record
+//                                    the refusal in errors.txt
 // Output files: <name>.f32 / <name>.bin raw little-endian, errors.txt with
 // one "key: message" line per refused layer, config.txt one line per layer.
 #include <cstdio>
@@ -25,10 +31,68 @@ static bool write_raw(const std::string &path, const void *p, size_t n)
     return ok;
 }
 
+static bool dump(const std::string &path, const DeviceTensor &t)
+{
+    std::vector<uint8_t> b(t.bytes());
+    if (!b.empty() && hipMemcpy(b.data(), t.data(), b.size(), hipMemcpyDeviceToHost) != hipSuccess) return false;
+    return write_raw(path, b.data(), b.size());
+}
+
+// The stage mode: every tensor of the loaded stage under its checkpoint key.
+static int run_stage(const SafeTensors &st, const std::string &out, char **argv)
+{
+    const size_t s = std::stoul(argv[4]), n = std::stoul(argv[5]), c = std::stoul(argv[6]),
+                 c2 = std::stoul(argv[7]);
+    const std::string dt = argv[8];
+    const DType d = dt == "f16" ? DType::F16 : (dt == "f32" ? DType::F32 : DType::BF16);
+    auto r = load_decoder_stage(st, s, n, c, c2, true, d);
+    std::FILE *errs = std::fopen((out + "/errors.txt").c_str(), "w");
+    if (!errs) return 1;
+    if (r.is_err()) {
+        std::fprintf(errs, "stage: %s\n", r.error().c_str());
+        std::fclose(errs);
+        std::printf("loader stage refused\n");
+        return 0;
+    }
+    std::fclose(errs);
+    const DecoderStageHip &g = r.value();
+    bool ok = true;
+    auto conv = [&](const std::string &key, const SparseConvLayerHip &L) {
+        ok &= dump(out + "/stage." + key + ".weight.bin", L.weight);
+        ok &= dump(out + "/stage." + key + ".bias.bin", L.bias);
+        if (L.packed) ok &= dump(out + "/stage." + key + ".packed.bin", *L.packed);
+    };
+    auto lin = [&](const std::string &key, const LinearLayerHip &L) {
+        ok &= dump(out + "/stage." + key + ".weight.bin", L.weight);
+        ok &= dump(out + "/stage." + key + ".bias.bin", L.bias);
+    };
+    for (size_t b = 0; b < g.convnext_blocks.size(); ++b) {
+        const std::string pre = "blocks." + std::to_string(s) + "." + std::to_string(b);
+        const ConvNeXtBlockHip &k = g.convnext_blocks[b];
+        conv(pre + ".conv", k.conv);
+        ok &= dump(out + "/stage." + pre + ".norm.weight.bin", k.norm_weight);
+        ok &= dump(out + "/stage." + pre + ".norm.bias.bin", k.norm_bias);
+        lin(pre + ".mlp.0", k.mlp_0);
+        lin(pre + ".mlp.2", k.mlp_2);
+    }
+    if (g.upsample_block) {
+        const std::string pre = "blocks." + std::to_string(s) + "." + std::to_string(n);
+        const C2SUpsampleBlockHip &u = *g.upsample_block;
+        ok &= dump(out + "/stage." + pre + ".norm1.weight.bin", u.norm1_weight);
+        ok &= dump(out + "/stage." + pre + ".norm1.bias.bin", u.norm1_bias);
+        if (u.to_subdiv) lin(pre + ".to_subdiv", *u.to_subdiv);
+        conv(pre + ".conv1", u.conv1);
+        conv(pre + ".conv2", u.conv2);
+    }
+    if (!ok) return 1;
+    std::printf("loader stage ok: %zu blocks, upsample %d\n", g.convnext_blocks.size(), g.upsample_block ? 1 : 0);
+    return 0;
+}
+
 int main(int argc, char **argv)
 {
-    if (argc != 4) {
-        std::fprintf(stderr, "usage: %s host|device FILE OUTDIR\n", argv[0]);
+    if (argc != 4 && !(argc == 9 && std::string(argv[1]) == "stage")) {
+        std::fprintf(stderr, "usage: %s host|device FILE OUTDIR | stage FILE OUTDIR S N C C2 DTYPE\n", argv[0]);
         return 2;
     }
     const std::string mode = argv[1], path = argv[2], out = argv[3];
@@ -37,6 +101,7 @@ int main(int argc, char **argv)
         std::fprintf(stderr, "open: %s\n", st.error().c_str());
         return 1;
     }
+    if (mode == "stage") return run_stage(st.value(), out, argv);
     std::FILE *errs = std::fopen((out + "/errors.txt").c_str(), "w");
     std::FILE *cfgs = std::fopen((out + "/config.txt").c_str(), "w");
     if (!errs || !cfgs) return 1;

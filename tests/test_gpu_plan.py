@@ -461,9 +461,10 @@ def test_plan_argument_errors():
     assert e.value.status == 5
 
 
-def _raw_planned(cfg, x, nbr, w, packed, out, plan_buf):
+def _raw_planned(cfg, x, nbr, w, packed, out, plan_buf, ln_workspace=None):
     """sc_subm_conv_forward_planned straight through the C ABI (no host-side
-    shape checks of the plan or the packed weights)."""
+    shape checks of the plan or the packed weights); with ``ln_workspace``,
+    LayerNorm over the row (wider than one tile: the f32 staging path)."""
     import ctypes
 
     from bevy_synth_amd import _capi
@@ -471,6 +472,9 @@ def _raw_planned(cfg, x, nbr, w, packed, out, plan_buf):
     def p(t):
         return ctypes.c_void_p(t.data_ptr())
     epi = _capi.ScConvEpilogue()
+    if ln_workspace is not None:
+        epi.layer_norm, epi.ln_eps = 1, 1e-6
+        epi.workspace, epi.workspace_bytes = p(ln_workspace), ln_workspace.numel()
     c = cfg.to_c()
     return _capi.load().sc_subm_conv_forward_planned(
         ctypes.byref(c), 1, p(x), x.shape[0], p(nbr), nbr.shape[0], 1, p(w), p(packed), None, None,
@@ -520,3 +524,42 @@ def test_raw_abi_rejects_plan_and_weights_of_another_shape(oracle):
     F.conv_plan_check(plan_big)
     exp = oracle.conv_ref_f64(ocfg(oracle, cfg), w, np.zeros(64, np.float32), x, nbr_big.cpu().numpy())
     assert_close(out.float().cpu().numpy(), exp, TOL_BF16, "planned conv after rebuild")
+
+
+def test_raw_abi_mismatch_leaves_wide_layer_norm_output_untouched(oracle):
+    """Cout = 256 with LayerNorm: the conv stores f32 into the epilogue
+    workspace and a row kernel normalises it into d_out.  With packed weights
+    of another config the conv writes nothing, and neither does the row
+    kernel (it is gated on the plan's status); the flagged plan then keeps a
+    matching call from writing too, until it is rebuilt."""
+    coords = synth.config1_coords()
+    rng = np.random.default_rng(72)
+    n = len(coords)
+    cfg = F.SparseSubmConvConfig(64, 256)
+    cd = dev(coords)
+    nbr = F.neighbor_rows_tensor_from_coords_tensor(cfg, cd)
+    plan = F.build_conv_plan(cfg, cd, nbr)
+    x = rbf(synth.normal_f32(rng, (n, 64)))
+    w = rbf(synth.conv_weight(rng, 256, 27, 64, 1 / np.sqrt(27 * 64)))
+    xd, wd = bf16_dev(x), bf16_dev(w)
+    pw = F.pack_conv_weight(cfg, wd)
+    pw128 = F.pack_conv_weight(F.SparseSubmConvConfig(64, 128), bf16_dev(w[:128]))
+    ws = torch.zeros(n * 256 * 4, dtype=torch.uint8, device="cuda")
+    sentinel = torch.full((n, 256), 7.0, dtype=torch.bfloat16, device="cuda")
+
+    out = sentinel.clone()
+    assert _raw_planned(cfg, xd, nbr, wd, pw128, out, plan.buf, ln_workspace=ws) == 0
+    with pytest.raises(F.SparseConvError) as e:
+        F.conv_plan_check(plan)
+    assert e.value.status == 2 and "packed weights" in e.value.message
+    assert torch.equal(out, sentinel)
+    # the flagged plan: a matching call writes nothing until the rebuild
+    assert _raw_planned(cfg, xd, nbr, wd, pw, out, plan.buf, ln_workspace=ws) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(out, sentinel)
+    plan = F.build_conv_plan(cfg, cd, nbr)
+    assert _raw_planned(cfg, xd, nbr, wd, pw, out, plan.buf, ln_workspace=ws) == 0
+    F.conv_plan_check(plan)
+    conv = oracle.conv_ref_f64(ocfg(oracle, cfg), w, np.zeros(256, np.float32), x, nbr.cpu().numpy())
+    exp = oracle.layer_norm(conv.astype(np.float32), None, None, 1e-6)
+    assert_close(out.float().cpu().numpy(), exp, TOL_BF16, "planned conv + wide LayerNorm after rebuild")

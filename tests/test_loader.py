@@ -151,3 +151,25 @@ def test_loader_device_layers(tmp_path, oracle):
     assert errs["7_conv_f32"] == "tensor 'conv_f32.weight' expected out_channels=65, got 64"
     assert errs["8_bias_len"] == "tensor 'bias_len.bias' expected shape=[8]"
     assert errs["lin_bad"] == "tensor 'lin.weight' expected in_channels=31, got 32"
+
+
+def test_python_loader_host_decode(tmp_path, oracle):
+    """bevy_synth_amd.loading.SafeTensors (the Python twin) decodes the same
+    values as the C++ header and refuses with the same messages."""
+    from bevy_synth_amd import loading as Ld
+    ref, errs = _run("host", tmp_path)
+    st = Ld.SafeTensors.open(str(tmp_path / "layers.safetensors"))
+    for k in ("conv_f32.weight", "conv_f16.weight", "conv_bf16.weight", "conv_f32.bias", "lin.weight", "edge_f16"):
+        shape, v = st.load_tensor_f32(k)
+        assert shape == tuple(ref["T"][k][1]), k
+        assert np.array_equal(v.ravel().view(np.uint32), _f32(tmp_path, k + ".f32").view(np.uint32)), k
+    for k in ("bad_dtype.weight", "missing.weight"):
+        with pytest.raises(Ld.LoadError) as e:
+            st.load_tensor_f32(k)
+        assert str(e.value) == errs[k]
+    with pytest.raises(Ld.LoadError) as e:
+        st.load_vector("conv_f32.bias", 63)
+    assert str(e.value) == errs["vector_len"]
+    with pytest.raises(Ld.LoadError) as e:
+        Ld.SafeTensors.open(str(tmp_path / "absent.safetensors"))
+    assert str(e.value).startswith("cannot open safetensors file")
