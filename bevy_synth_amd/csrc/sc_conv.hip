@@ -108,7 +108,8 @@ static int conv_forward_impl(const sc_conv_config *cfg, int act_dtype, const voi
                              int64_t n_in, const int32_t *d_map, int64_t n_q, int w_dtype,
                              const void *d_weight, const float *d_w_scale, const float *d_bias,
                              const sc_conv_epilogue *epi, int out_dtype, void *d_out,
-                             const void *d_plan, const void *d_wpack, sc_stream stream, bool dense = false)
+                             const void *d_plan, const void *d_wpack, sc_stream stream, bool dense = false,
+                             bool child_plan = false)
 {
     clear_error();
     const void *d_residual = epi ? epi->residual : nullptr;
@@ -192,6 +193,9 @@ static int conv_forward_impl(const sc_conv_config *cfg, int act_dtype, const voi
     };
     a.scatter_shift = log2_or_neg(c2s.scatter_ch);
     a.skip_shift = log2_or_neg(c2s.skip_R);
+    a.tile_child = nullptr;
+    a.child_ch = (int)c2s.scatter_ch;
+    a.child_plan = child_plan ? 1 : 0;
     if (c2s.scatter) a.ln_group = a.scatter_ch;
 
     const size_t asz = dtype_size(act_dtype);
@@ -251,6 +255,13 @@ static int conv_forward_impl(const sc_conv_config *cfg, int act_dtype, const voi
     if (d_wpack && (uintptr_t)d_wpack % 16 != 0)
         return fail(SC_ERR_SHAPE, "packed weights must be 16-byte aligned");
     const void *plan = (d_plan && (act_bf16 || act_f16) && mfma && K <= kHaloK) ? d_plan : nullptr;
+    if (child_plan) {
+        // a child plan's tiles hold parents, not query rows: only the
+        // halo-staged kernel on packed weights can run it
+        if (!plan || !d_wpack || groups != 1)
+            return fail(SC_ERR_UNSUPPORTED, "sparse conv child plan needs 16-bit activations, packed weights, "
+                                            "one group and a kernel of at most 27 offsets");
+    }
     int rc2 = launch_conv_typed(a, act_f32, w_dtype, conv_out_dtype, groups, mfma, plan, s);
     if (rc2 != SC_OK || !split_ln) return rc2;
     // After a planned conv, the row kernel is gated on the plan's status: a
@@ -318,6 +329,27 @@ extern "C" int sc_subm_conv_forward_planned(const sc_conv_config *cfg, int act_d
 {
     return conv_forward_impl(cfg, act_dtype, d_input, n_in, d_map, n_q, w_dtype, d_weight, d_w_scale,
                              d_bias, epi, out_dtype, d_out, d_plan, d_packed_weight, stream);
+}
+
+extern "C" int sc_subm_conv_forward_child_planned(const sc_conv_config *cfg, int act_dtype,
+                                                  const void *d_input, int64_t n_in, const int32_t *d_map,
+                                                  int64_t n_q, int w_dtype, const void *d_weight,
+                                                  const void *d_packed_weight, const float *d_w_scale,
+                                                  const float *d_bias, const sc_conv_epilogue *epi,
+                                                  int out_dtype, void *d_out, const void *d_child_plan,
+                                                  sc_stream stream)
+{
+    clear_error();
+    if (!epi || !epi->child_rows)
+        return fail(SC_ERR_NULL, "sparse conv child plan: the epilogue's child_rows (the child scatter) is required");
+    if (!d_child_plan || !d_packed_weight) return fail(SC_ERR_NULL, "sparse conv child plan: NULL plan or weights");
+    // children of 64 channels or a multiple of 128: the halo tiles then cover
+    // one child each
+    if (cfg && cfg->out_channels != 512 && cfg->out_channels % 1024 != 0)
+        return fail(SC_ERR_UNSUPPORTED, "sparse conv child plan needs children of 64 channels or a multiple of 128 "
+                                        "(Cout 512 or a multiple of 1024)");
+    return conv_forward_impl(cfg, act_dtype, d_input, n_in, d_map, n_q, w_dtype, d_weight, d_w_scale, d_bias, epi,
+                             out_dtype, d_out, d_child_plan, d_packed_weight, stream, false, true);
 }
 
 static int weight_pack_bytes(const sc_conv_config *cfg, int w_dtype, size_t *bytes)
@@ -389,6 +421,9 @@ extern "C" int sc_conv_plan_check(const void *d_plan, sc_stream stream)
     if (status & kPlanStatusWeightMismatch)
         return fail(SC_ERR_SHAPE, "sparse conv: the packed weights were packed for another config; "
                                   "the conv wrote nothing");
+    if (status & kPlanStatusChildRows)
+        return fail(SC_ERR_SHAPE, "child plan: the parent plan was built for another row count, or the child "
+                                  "rows name more active children than n_children; the plan is empty");
     return SC_OK;
 }
 

@@ -77,6 +77,12 @@ struct ConvArgs {
     int skip_R;
     int scatter_shift;  // log2(scatter_ch), or -1 when not a power of two
     int skip_shift;     // log2(skip_R), or -1 when not a power of two
+    // Child plan (C2S conv1 over the active children only): the plan's tiles
+    // each belong to one child c, tile_child[t], and compute its output
+    // channels [c * child_ch, (c + 1) * child_ch); child_plan marks the call.
+    const int32_t *tile_child;
+    int child_ch;
+    int child_plan;
 };
 
 // Header of a packed weight buffer (its first 256 bytes): the shape the
@@ -752,7 +758,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
     const int l16 = lane & 15, q4 = lane >> 4;
     const int K = args.K;
 
-    int tile;
+    int tile, child = 0;
     if (args.tile_list) {
         // Plan tile tile_list[b / kSubTiles], part b % kSubTiles.  The plan's
         // header is checked first, and its status: the halo kernel before
@@ -763,13 +769,19 @@ __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
         const int b = (int)blockIdx.x / kSubTiles;
         if (b >= *args.tile_count) return;
         const int lt = args.tile_list[b];
-        if (lt < 0 || (int64_t)lt * kPlanTileRows >= args.n_q) return;
+        if (lt < 0 || (int64_t)lt * kPlanTileRows >= (args.tile_child ? args.plan_hdr->n_tiles * (int64_t)kPlanTileRows
+                                                                       : args.n_q))
+            return;
+        if (args.tile_child) {  // a child plan's tile: its child's channel block
+            child = args.tile_child[lt];
+            if (child < 0) return;
+        }
         tile = lt * kSubTiles + (int)blockIdx.x % kSubTiles;
     } else {
         tile = tile_for_block(blockIdx.x, gridDim.x);
     }
     const int64_t row0 = (int64_t)tile * kRows;
-    const int o0 = blockIdx.y * kBN;
+    const int o0 = child * args.child_ch + blockIdx.y * kBN;
     const int g = blockIdx.z;
     const int64_t in_col0 = (int64_t)g * args.cin_g;
     const int64_t out_col0 = (int64_t)g * args.cout_g;
@@ -1076,8 +1088,10 @@ __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
             const int oc = o0 + j * 16 + 4 * q4;
             float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
             if (c2s) {
-                if (oc < args.cout_g)
-                    c2s_store4<TO>(args, crow, qrow, (int)(out_col0 + oc), min(4, args.cout_g - oc), v, vec_ok);
+                // a child plan's tile stores its own child's channels only
+                // (its 128-channel tile may reach into the next child)
+                const int cend = args.tile_child ? min(args.cout_g, (child + 1) * args.child_ch) : args.cout_g;
+                if (oc < cend) c2s_store4<TO>(args, crow, qrow, (int)(out_col0 + oc), min(4, cend - oc), v, vec_ok);
                 continue;
             }
             if (vec_ok && oc + 3 < args.cout_g) {
@@ -1127,6 +1141,17 @@ __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
 // reads.  Absent neighbours read a zero row.  Per-row accumulation order is
 // fixed (chunk-major, offsets ascending).
 //
+// Tiles of 64 output channels (layers of at most 64 per group, and C2S
+// children of 64) keep the 128 x 64 wave block: the two waves of a row half
+// split the stages instead of the channels (in chunk c the wave of parity p
+// takes the offsets at even or odd positions of the tile's offset list,
+// alternating per chunk when the list is odd, so the halves differ by at
+// most one stage per two chunks), and add their partial sums through LDS
+// after the loop, each keeping 64 rows.  A wave of 64 rows x 64 channels
+// would load a weight fragment per 4 MFMAs instead of per 8 and be bound by
+// the texture path at about 0.6 PFLOP/s.  Per value the sum is (stages of
+// parity 0) + (stages of parity 1), each in stage order.
+//
 // LDS: halo (960 + 1) x 64 B + source offsets 960 x 4 B + lmap 27 x 256 x 2 B
 // = 77 KB.
 constexpr int kHaloK = 27;
@@ -1147,9 +1172,12 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
     constexpr int kWS = SC_HALO_WS;             // weight register sets: stages t .. t+kWS-1
     static_assert(kPlanTileRows == kTileRows, "plan tile = 256 rows");
     // kNT = 128: waves 2 x 2 (128 rows x 64 channels each); kNT = 64 (layers
-    // of at most 64 output channels): waves 4 x 1 (64 rows x 64 channels).
+    // of at most 64 output channels): waves 2 (row halves) x 2 (stage
+    // parity) in the loop, 64 rows x 64 channels each in the epilogue.
     static_assert(kNT == 128 || kNT == 64, "output tile of 128 or 64 channels");
-    constexpr int kI = kNT == 128 ? 8 : 4;      // 16-row MFMA blocks per wave
+    constexpr bool kKS = kNT == 64;             // stages split between the waves of a row half
+    constexpr int kIM = 8;                      // 16-row MFMA blocks per wave in the loop
+    constexpr int kI = kNT == 128 ? 8 : 4;      // ... and in the epilogue
 
     __shared__ __attribute__((aligned(16))) unsigned char s_halo[(kPlanHaloMax + 1) * CB];
     // s_lmap[k][rh][l16][i]: LDS byte offset of the halo row feeding tile row
@@ -1165,7 +1193,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
     const int l16 = lane & 15, q4 = lane >> 4;
     const int rh = wave >> 1;                              // lmap half of the wave's rows
     const int ch = kNT == 128 ? (wave & 1) : 0;            // channel half
-    const int row0 = kNT == 128 ? 128 * rh : 64 * wave;    // first tile row of the wave
+    const int row0 = kNT == 128 ? 128 * rh : 64 * wave;    // first tile row of the wave (epilogue)
     const int K = args.K;
 
     // The plan must be the one built for this map shape and the packed
@@ -1189,7 +1217,10 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
     const int tile = tile_for_block(blockIdx.x, gridDim.x);
     const int U = plan.tile_u[tile];
     if (U > kPlanHaloMax) return;  // listed in plan.overflow; the direct kernel takes it
-    const int o0 = blockIdx.y * kNT;
+    // a child plan's tile computes its child's channel block (an unused tile nothing)
+    const int child = plan.tile_child ? plan.tile_child[tile] : 0;
+    if (child < 0) return;
+    const int o0 = child * args.child_ch + blockIdx.y * kNT;
     const int g = blockIdx.z;
     const int64_t in_col0 = (int64_t)g * args.cin_g;
     const int64_t out_col0 = (int64_t)g * args.cout_g;
@@ -1230,10 +1261,31 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
     }
     __syncthreads();
     const uint32_t tmask = __builtin_amdgcn_readfirstlane(s_wmask[0] | s_wmask[1] | s_wmask[2] | s_wmask[3]);
+    // The wave's offsets in even and odd chunks (all of them without the
+    // stage split; a tile with one offset leaves the parity-1 waves idle).
+    uint32_t m_even = tmask, m_odd = tmask;
+    const int kpar = kKS ? (__builtin_amdgcn_readfirstlane(wave) & 1) : 0;
+    if constexpr (kKS) {
+        uint32_t ev = 0u, r = tmask;
+        for (bool take = true; r != 0u; take = !take) {
+            const uint32_t b = r & (0u - r);
+            if (take) ev |= b;
+            r ^= b;
+        }
+        const uint32_t od = tmask ^ ev;
+        if (od == 0u) {
+            m_even = m_odd = kpar ? 0u : tmask;
+        } else if ((__builtin_popcount(tmask) & 1) == 0) {
+            m_even = m_odd = kpar ? od : ev;
+        } else {
+            m_even = kpar ? od : ev;
+            m_odd = kpar ? ev : od;
+        }
+    }
 
-    f32x4 acc[kI][4];
+    f32x4 acc[kIM][4];
 #pragma unroll
-    for (int i = 0; i < kI; ++i)
+    for (int i = 0; i < kIM; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -1265,15 +1317,21 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
             int k, c;
         };
         auto cur_init = [&](Cursor &u) {
-            u.rem = tmask;
-            u.k = __builtin_ctz(tmask);
+            u.rem = m_even;
+            u.k = __builtin_ctz(m_even);
             u.c = 0;
         };
         auto cur_next = [&](Cursor &u) {
             u.rem &= u.rem - 1u;
             if (u.rem == 0u) {
-                u.rem = tmask;
                 ++u.c;
+                if constexpr (kKS) {
+                    // bit arithmetic, not a select: the compiler would make a
+                    // two-entry table of the masks in scratch memory
+                    u.rem = m_even ^ ((m_even ^ m_odd) & (0u - (uint32_t)(u.c & 1)));
+                } else {
+                    u.rem = tmask;
+                }
             }
             u.k = __builtin_ctz(u.rem);
         };
@@ -1310,20 +1368,13 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
             __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
             __builtin_amdgcn_s_barrier();
         };
-        auto read_lm = [&](int k) {
-            if constexpr (kNT == 128) {
-                return *reinterpret_cast<const uint4 *>(&s_lmap[k][rh][l16][0]);
-            } else {
-                const uint2 v = *reinterpret_cast<const uint2 *>(&s_lmap[k][rh][l16][4 * (wave & 1)]);
-                return make_uint4(v.x, v.y, 0u, 0u);
-            }
-        };
+        auto read_lm = [&](int k) { return *reinterpret_cast<const uint4 *>(&s_lmap[k][rh][l16][0]); };
         auto compute = [&](const uint4 &lm, const uint4(&f)[4]) {
             const uint32_t lw[4] = {lm.x, lm.y, lm.z, lm.w};
             const uint32_t qx = (uint32_t)q4 << 4;
-            uint4 x[kI];
+            uint4 x[kIM];
 #pragma unroll
-            for (int i = 0; i < kI; ++i) {
+            for (int i = 0; i < kIM; ++i) {
                 const uint32_t off = ((i & 1) ? (lw[i >> 1] >> 16) : (lw[i >> 1] & 0xFFFFu)) ^ qx;
                 x[i] = *reinterpret_cast<const uint4 *>(s_halo + off);
             }
@@ -1331,51 +1382,94 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
             for (int jj = 0; jj < 4; ++jj) {
                 const uint4 w = f[jj];
 #pragma unroll
-                for (int i = 0; i < kI; ++i)
+                for (int i = 0; i < kIM; ++i)
                     acc[i][jj] = mfma_16x16x32<TA>(w, x[i], acc[i][jj]);
             }
         };
 
-        Cursor cur, pre;
-        cur_init(cur);
-        cur_init(pre);
-        uint4 lm[kWS];
-#pragma unroll
-        for (int s0 = 0; s0 < kWS - 1; ++s0) {
-            load_w(pre, wf[s0]);
-            lm[s0] = read_lm(pre.k);
-            cur_next(pre);
-        }
-        load_halo(0);
-        wait_vmcnt<0>();
-        barrier();
-        // Stage t uses weight set t % 2 and issues the loads of stage t + 1
-        // into the other set; the body covers two stages so the sets are
-        // compile-time constants.
-        int prev_c = 0;
-        while (true) {
-            bool done = false;
-#pragma unroll
-            for (int u = 0; u < kWS; ++u) {
-                if (!done && cur.c >= nkc) done = true;
-                if (!done) {
-                    if (cur.c != prev_c) {  // next chunk: every wave is done with the halo
-                        barrier();
-                        load_halo(cur.c);
-                        wait_vmcnt<0>();
-                        barrier();
-                    }
-                    load_w(pre, wf[(u + kWS - 1) % kWS]);
-                    lm[(u + kWS - 1) % kWS] = read_lm(pre.k);
-                    cur_next(pre);
-                    compute(lm[u], wf[u]);
-                    prev_c = cur.c;
-                    cur_next(cur);
-                }
+        if (m_even == 0u) {
+            // idle wave (stage split, one offset): its share of every halo
+            // load and the same barriers as the others
+            for (int c = 0; c < nkc; ++c) {
+                if (c > 0) barrier();
+                load_halo(c);
+                wait_vmcnt<0>();
+                barrier();
             }
-            if (done) break;
+        } else {
+            Cursor cur, pre;
+            cur_init(cur);
+            cur_init(pre);
+            uint4 lm[kWS];
+#pragma unroll
+            for (int s0 = 0; s0 < kWS - 1; ++s0) {
+                load_w(pre, wf[s0]);
+                lm[s0] = read_lm(pre.k);
+                cur_next(pre);
+            }
+            load_halo(0);
+            wait_vmcnt<0>();
+            barrier();
+            // Stage t uses weight set t % 2 and issues the loads of stage t + 1
+            // into the other set; the body covers two stages so the sets are
+            // compile-time constants.
+            int prev_c = 0;
+            while (true) {
+                bool done = false;
+#pragma unroll
+                for (int u = 0; u < kWS; ++u) {
+                    if (!done && cur.c >= nkc) done = true;
+                    if (!done) {
+                        if (cur.c != prev_c) {  // next chunk: every wave is done with the halo
+                            barrier();
+                            load_halo(cur.c);
+                            wait_vmcnt<0>();
+                            barrier();
+                        }
+                        load_w(pre, wf[(u + kWS - 1) % kWS]);
+                        lm[(u + kWS - 1) % kWS] = read_lm(pre.k);
+                        cur_next(pre);
+                        compute(lm[u], wf[u]);
+                        prev_c = cur.c;
+                        cur_next(cur);
+                    }
+                }
+                if (done) break;
+            }
+            wait_vmcnt<0>();
         }
-        wait_vmcnt<0>();
+    }
+    if constexpr (kKS) {
+        // The two waves of a row half add their partial sums: the wave of
+        // parity p keeps row blocks [4p, 4p + 4) (tile rows 128 rh + 64 p ..,
+        // its epilogue rows) and hands the other four to its partner, two
+        // 16-channel blocks per round (32 KB of the halo's LDS).
+        f32x4 *xb = reinterpret_cast<f32x4 *>(s_halo);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            __syncthreads();
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii)
+                    xb[((wave * 2 + jj) * 4 + ii) * 64 + lane] = kpar ? acc[ii][2 * r + jj] : acc[ii + 4][2 * r + jj];
+            __syncthreads();
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii) {
+                    const f32x4 v = xb[(((wave ^ 1) * 2 + jj) * 4 + ii) * 64 + lane];
+                    const f32x4 own = kpar ? acc[ii + 4][2 * r + jj] : acc[ii][2 * r + jj];
+                    acc[ii][2 * r + jj] = own + v;
+                    // computed here: sunk into the epilogue's branches, the
+                    // sum would keep both halves and v live there
+                    asm volatile("" : "+v"(acc[ii][2 * r + jj]));
+                }
+        }
+        // nothing of the epilogue moves above the exchange (its loads would
+        // be live beside the whole accumulator)
+        __builtin_amdgcn_sched_barrier(0);
     }
 
     // ---- epilogue: lane l holds channels oc0 + 16 j + 4 q4 + e of tile row
@@ -2041,14 +2135,28 @@ int launch_conv(const ConvArgs &a, int groups, bool mfma, const void *plan, hipS
                 // order, each plan tile as kPlanTileRows / kTileRows tiles.
                 // Packed weights are bf16 for either weight type; int8
                 // weights keep their per-channel scales for the epilogue.
-                const PlanLayout L = plan_layout(a.n_q, a.K);
-                const PlanView pv = plan_view(plan, L);
-                dim3 hgrid((unsigned)L.n_tiles, (unsigned)ntile, (unsigned)groups);
+                // A child plan (C2S conv1 over the active children): its own
+                // tile count, and one tile per child and column block of the
+                // child's channels.
+                PlanView pv;
+                int64_t n_tiles;
+                if (a.child_plan) {
+                    const ChildPlanLayout CL = child_plan_layout(a.n_q, a.scatter_n, a.K);
+                    pv = child_plan_view(plan, CL);
+                    n_tiles = CL.n_tiles;
+                } else {
+                    const PlanLayout L = plan_layout(a.n_q, a.K);
+                    pv = plan_view(plan, L);
+                    n_tiles = L.n_tiles;
+                }
+                const int64_t cols = a.child_plan ? a.child_ch : a.cout_g;  // channels one tile row spans
+                dim3 hgrid((unsigned)n_tiles, (unsigned)((cols + kBN - 1) / kBN), (unsigned)groups);
                 ConvArgs h = a;
                 h.plan_hdr = pv.hdr;
+                h.tile_child = pv.tile_child;
                 if (sizeof(TW) != 1) h.w_scale = nullptr;
-                if (a.cout_g <= 64) {  // 64-channel tiles: no half-empty MFMA tile
-                    hgrid.y = (unsigned)((a.cout_g + 63) / 64);
+                if (cols <= 64) {  // 64-channel tiles: no half-empty MFMA tile
+                    hgrid.y = (unsigned)((cols + 63) / 64);
                     if (a.ln)
                         conv_halo_kernel<TA, TO, true, 64><<<hgrid, kThreads, 0, s>>>(h, pv);
                     else
@@ -2064,7 +2172,8 @@ int launch_conv(const ConvArgs &a, int groups, bool mfma, const void *plan, hipS
                 b.perm = pv.order;
                 b.tile_list = pv.overflow;
                 b.tile_count = &pv.hdr->n_overflow;
-                dim3 fgrid((unsigned)(L.n_tiles * kSubTiles), (unsigned)ntile, (unsigned)groups);
+                b.tile_child = pv.tile_child;
+                dim3 fgrid((unsigned)(n_tiles * kSubTiles), (unsigned)((cols + kBN - 1) / kBN), (unsigned)groups);
                 launch_v2<TA, TW, TO, true>(b, fgrid, s);
             } else if (sizeof(TW) == 2 && !a.map && a.K == 1 && groups == 1 && a.cin % 32 == 0 && !a.skip_idx) {
                 // the dense linear: contiguous rows, reference-layout weights;

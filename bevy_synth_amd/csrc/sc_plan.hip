@@ -81,6 +81,11 @@ struct PlanArgs {
     int64_t brick_cap;
     int64_t n_bsum;
     int64_t grid_cap;
+    // plan_tiles_kernel on listed tiles only (a child plan's split tiles):
+    // workgroup b takes tile_list[b] when b < *tile_list_n; the overflow
+    // list is then not appended to (the caller rebuilds it)
+    const int32_t *tile_list;
+    const int32_t *tile_list_n;
 };
 
 constexpr uint32_t kGridEmpty = 0xFFFFFFFFu;
@@ -839,7 +844,13 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
     static_assert(kHashSlots <= kBitmapWords, "hash table fits the bitmap array");
     static_assert(kPlanHaloMax <= 1024 && 1024 * 8 <= kBitmapWords * 2, "sort list fits the prefix array");
     // XCD-contiguous tiles: neighbouring tiles read neighbouring map rows.
-    const int64_t t = tile_for_block((int)blockIdx.x, (int)gridDim.x);
+    int64_t t;
+    if (a.tile_list) {
+        if ((int)blockIdx.x >= *a.tile_list_n) return;
+        t = a.tile_list[blockIdx.x];
+    } else {
+        t = tile_for_block((int)blockIdx.x, (int)gridDim.x);
+    }
     const int p = threadIdx.x;
     const int lane = p & 63, wave = p >> 6;
     const int K = a.K;
@@ -996,7 +1007,7 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
         }
         if (p == 0) {
             a.tile_u[t] = U;
-            if (U > kPlanHaloMax) a.overflow[atomicAdd(&a.hdr->n_overflow, 1)] = (int32_t)t;
+            if (U > kPlanHaloMax && !a.tile_list) a.overflow[atomicAdd(&a.hdr->n_overflow, 1)] = (int32_t)t;
         }
         if (U > kPlanHaloMax) return;  // handled by the direct-gather kernel
         __syncthreads();
@@ -1050,7 +1061,7 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
     int id = tile_scan_excl(cnt, s_wave, U);
     if (p == 0) {
         a.tile_u[t] = U;
-        if (U > kPlanHaloMax) a.overflow[atomicAdd(&a.hdr->n_overflow, 1)] = (int32_t)t;
+        if (U > kPlanHaloMax && !a.tile_list) a.overflow[atomicAdd(&a.hdr->n_overflow, 1)] = (int32_t)t;
     }
     if (U > kPlanHaloMax) return;
     for (int i = 0; i < kPer; ++i) {
@@ -1089,6 +1100,296 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
         if (k >= K) break;
         lm[k * kPlanTileRows] = v[k] >= 0 ? (uint16_t)s_key[v[k] & (kHashSlots - 1)] : kPlanAbsent;
     }
+}
+
+// ------------------------------------------------------------ child plans
+//
+// For C2S conv1 over the active children only (sc_conv_child_plan_build):
+// per child index c, the entries of the parent plan's order whose child c is
+// active, in that order, compacted into tiles of their own (sc_plan.hpp,
+// ChildPlanLayout):
+//   count  : one workgroup per parent-plan tile, a ballot per child
+//   chunk  : per 256 parent tiles, the counts scanned per child (exclusive)
+//   layout : one workgroup: the chunk totals scanned, the children's tile
+//            ranges, the header and tile_child
+//   emit   : every entry to its slot (chunk offset + in-chunk offset + the
+//            wave's ballot prefix)
+//   pad    : -1 in every slot no entry takes
+//   tiles  : plan_tiles_kernel on the child order (the parents' map rows)
+//   split  : each list tile whose halo overflows gives its rows 128..255 to
+//            a spare tile (in tile order), then both are rebuilt, and the
+//            overflow list is rebuilt in tile order
+// The plan is a pure function of the inputs (no atomics whose order shows).
+
+struct ChildArgs {
+    const PlanHeader *phdr;     // the parent plan
+    const int32_t *porder;      // its order [n_ptiles * 256]
+    const int32_t *child_rows;  // [P][8]: row of child (p, c), or -1
+    int64_t n_parents;
+    int64_t n_children;
+    int64_t n_ptiles;
+    int64_t n_chunks;
+    int64_t n_main;
+    int64_t n_tiles;
+    int K;
+    PlanHeader *hdr;  // the child plan
+    int32_t *order;
+    int32_t *tile_child;
+    int32_t *tile_u;
+    int32_t *overflow;
+    int32_t *counts;  // [n_ptiles][8]: count, then in-chunk exclusive offset
+    int32_t *chunks;  // [n_chunks][8]: chunk total, then chunk exclusive offset
+    int32_t *child_n;
+    int32_t *child_base;
+    int32_t *split;   // [n_extra][2]: (split tile, spare tile)
+    int32_t *split_n; // 2 x splits: the rebuild's tile count
+};
+
+// Parent-order entry e: its parent row (-1 for padding) and its active
+// children as bits (a row outside [0, n_children) counts as inactive).
+__device__ inline uint32_t child_bits(const ChildArgs &a, int64_t e, int32_t &p)
+{
+    p = a.porder[e];
+    if (p < 0 || p >= a.n_parents) {
+        p = -1;
+        return 0u;
+    }
+    const int4 *r = reinterpret_cast<const int4 *>(a.child_rows + (int64_t)p * 8);
+    const int4 x = r[0], y = r[1];
+    const int32_t v[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+    uint32_t b = 0;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) b |= (uint32_t)(v[c] >= 0 && v[c] < a.n_children) << c;
+    return b;
+}
+
+__global__ __launch_bounds__(kThreads) void child_count_kernel(ChildArgs a)
+{
+    __shared__ int s_c[kThreads / 64][8];
+    int32_t p;
+    const uint32_t bits = child_bits(a, (int64_t)blockIdx.x * kPlanTileRows + threadIdx.x, p);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const uint64_t m = __ballot((bits >> c) & 1u);
+        if (lane == 0) s_c[wave][c] = __popcll(m);
+    }
+    __syncthreads();
+    if (threadIdx.x < 8) {
+        int t = 0;
+        for (int w = 0; w < kThreads / 64; ++w) t += s_c[w][threadIdx.x];
+        a.counts[(int64_t)blockIdx.x * 8 + threadIdx.x] = t;
+    }
+}
+
+// Exclusive scan of 256 per-thread values of 8 children at once (LDS
+// Hillis-Steele over [256][8]); returns the thread's exclusive prefixes and
+// the totals.
+__device__ inline void scan8(int (&v)[8], int (*s)[8], int (&tot)[8])
+{
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) s[tid][c] = v[c];
+    __syncthreads();
+    for (int off = 1; off < kThreads; off <<= 1) {
+        int add[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) add[c] = tid >= off ? s[tid - off][c] : 0;
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < 8; ++c) s[tid][c] += add[c];
+        __syncthreads();
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        tot[c] = s[kThreads - 1][c];
+        v[c] = s[tid][c] - v[c];
+    }
+    __syncthreads();
+}
+
+// Per group of 256 parent tiles: counts -> in-group exclusive offsets, and
+// the group's totals.
+__global__ __launch_bounds__(kThreads) void child_chunk_kernel(ChildArgs a)
+{
+    __shared__ int s[kThreads][8];
+    const int64_t b = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    int v[8], tot[8];
+    if (b < a.n_ptiles) {
+        const int4 *q = reinterpret_cast<const int4 *>(a.counts + b * 8);
+        const int4 x = q[0], y = q[1];
+        v[0] = x.x, v[1] = x.y, v[2] = x.z, v[3] = x.w, v[4] = y.x, v[5] = y.y, v[6] = y.z, v[7] = y.w;
+    } else {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) v[c] = 0;
+    }
+    scan8(v, s, tot);
+    if (b < a.n_ptiles) {
+        int4 *q = reinterpret_cast<int4 *>(a.counts + b * 8);
+        q[0] = make_int4(v[0], v[1], v[2], v[3]);
+        q[1] = make_int4(v[4], v[5], v[6], v[7]);
+    }
+    if (threadIdx.x < 8) a.chunks[(int64_t)blockIdx.x * 8 + threadIdx.x] = tot[threadIdx.x];
+}
+
+// One workgroup: the group totals scanned (loops of 256 groups), the
+// children's tile ranges, the header, tile_child.  A parent plan of
+// another size or more active children than the list tiles hold flags the
+// status; every tile is then empty.
+__global__ __launch_bounds__(kThreads) void child_layout_kernel(ChildArgs a)
+{
+    __shared__ int s[kThreads][8];
+    __shared__ int64_t s_base[9];
+    __shared__ int s_ok;
+    int run[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int64_t k0 = 0; k0 < a.n_chunks; k0 += kThreads) {
+        const int64_t k = k0 + threadIdx.x;
+        int v[8], tot[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) v[c] = k < a.n_chunks ? a.chunks[k * 8 + c] : 0;
+        scan8(v, s, tot);
+        if (k < a.n_chunks)
+#pragma unroll
+            for (int c = 0; c < 8; ++c) a.chunks[k * 8 + c] = v[c] + run[c];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) run[c] += tot[c];
+    }
+    if (threadIdx.x == 0) {
+        int64_t base = 0;
+        for (int c = 0; c < 8; ++c) {
+            s_base[c] = base;
+            base += (run[c] + kPlanTileRows - 1) / kPlanTileRows;
+        }
+        s_base[8] = base;
+        const bool ok = base <= a.n_main && a.phdr->n_q == a.n_parents && a.phdr->K == a.K;
+        s_ok = ok;
+        for (int c = 0; c < 8; ++c) {
+            a.child_n[c] = ok ? run[c] : 0;
+            a.child_base[c] = ok ? (int32_t)s_base[c] : 0;
+        }
+        PlanHeader *h = a.hdr;
+        h->n_q = a.n_parents;
+        h->n_in = a.n_parents;
+        h->n_tiles = (int32_t)a.n_tiles;
+        h->K = a.K;
+        h->brick_shift = -1;
+        h->n_overflow = 0;
+        for (int j = 0; j < 4; ++j) h->bmin[j] = h->bmax[j] = 0;
+        h->n_bricks = 0;
+        h->status = ok ? 0u : kPlanStatusChildRows;
+        h->grid_mode = kPlanModeChild;
+        h->n_unique = ok ? (int32_t)base : 0;  // list tiles in use
+        h->n_extras = 0;                       // splits (the split pass sets it)
+        *a.split_n = 0;
+    }
+    __syncthreads();
+    const bool ok = s_ok != 0;
+    for (int64_t t = threadIdx.x; t < a.n_tiles; t += kThreads) {
+        int ct = -1;
+        if (ok)
+            for (int c = 0; c < 8; ++c)
+                if (t >= s_base[c] && t < s_base[c + 1]) ct = c;
+        a.tile_child[t] = ct;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void child_emit_kernel(ChildArgs a)
+{
+    __shared__ int s_c[kThreads / 64][8];
+    if (a.hdr->status != 0u) return;  // refused by the layout (uniform)
+    int32_t p;
+    const uint32_t bits = child_bits(a, (int64_t)blockIdx.x * kPlanTileRows + threadIdx.x, p);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint64_t below = (1ull << lane) - 1ull;
+    int pos[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const uint64_t m = __ballot((bits >> c) & 1u);
+        pos[c] = __popcll(m & below);
+        if (lane == 0) s_c[wave][c] = __popcll(m);
+    }
+    __syncthreads();
+    const int64_t chunk = (int64_t)blockIdx.x / kThreads;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        if (!((bits >> c) & 1u)) continue;
+        int off = a.chunks[chunk * 8 + c] + a.counts[(int64_t)blockIdx.x * 8 + c] + pos[c];
+        for (int w = 0; w < wave; ++w) off += s_c[w][c];
+        a.order[(int64_t)a.child_base[c] * kPlanTileRows + off] = p;
+    }
+}
+
+// -1 in every order slot no entry takes: past a child's entries in its last
+// tile, and every unused tile (all of them when the build was refused).
+__global__ __launch_bounds__(kThreads) void child_pad_kernel(ChildArgs a)
+{
+    const int64_t t = blockIdx.x;
+    const int c = a.tile_child[t];
+    const int64_t i = t * kPlanTileRows + threadIdx.x;
+    bool pad = c < 0;
+    if (!pad) pad = i >= (int64_t)a.child_base[c] * kPlanTileRows + a.child_n[c];
+    if (pad) a.order[i] = -1;
+}
+
+// One workgroup, after the first tables: list tiles whose halo overflows,
+// in tile order, each paired with the next spare tile while spares last;
+// the spare takes the tile's child.
+__global__ __launch_bounds__(kThreads) void child_split_kernel(ChildArgs a)
+{
+    __shared__ int s_wave[kThreads / 64];
+    if (a.hdr->status != 0u) return;
+    const int64_t n_used = a.hdr->n_unique;
+    const int64_t n_extra = a.n_tiles - a.n_main;
+    int64_t done = 0;
+    for (int64_t t0 = 0; t0 < n_used; t0 += kThreads) {
+        const int64_t t = t0 + threadIdx.x;
+        const bool f = t < n_used && a.tile_u[t] > kPlanHaloMax;
+        int total;
+        const int rank = tile_scan_excl((int)f, s_wave, total);
+        if (f && done + rank < n_extra) {
+            const int64_t j = done + rank, spare = a.n_main + j;
+            a.split[2 * j] = (int32_t)t;
+            a.split[2 * j + 1] = (int32_t)spare;
+            a.tile_child[spare] = a.tile_child[t];
+        }
+        done += total;
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const int64_t ns = done < n_extra ? done : n_extra;
+        *a.split_n = (int32_t)(2 * ns);
+        a.hdr->n_extras = (int32_t)ns;
+    }
+}
+
+// One workgroup per split: rows 128..255 of the tile go to its spare (whose
+// slots are all -1 from the pad pass).
+__global__ __launch_bounds__(kPlanTileRows / 2) void child_move_kernel(ChildArgs a)
+{
+    const int j = blockIdx.x;
+    if (2 * j >= *a.split_n) return;
+    const int64_t t = a.split[2 * j], spare = a.split[2 * j + 1];
+    const int i = threadIdx.x;
+    a.order[spare * kPlanTileRows + i] = a.order[t * kPlanTileRows + kPlanTileRows / 2 + i];
+    a.order[t * kPlanTileRows + kPlanTileRows / 2 + i] = -1;
+}
+
+// One workgroup: the overflow list rebuilt in tile order (tiles whose halo
+// still overflows after the splits, or that found no spare).
+__global__ __launch_bounds__(kThreads) void child_overflow_kernel(ChildArgs a)
+{
+    __shared__ int s_wave[kThreads / 64];
+    int64_t done = 0;
+    for (int64_t t0 = 0; t0 < a.n_tiles; t0 += kThreads) {
+        const int64_t t = t0 + threadIdx.x;
+        const bool f = t < a.n_tiles && a.tile_child[t] >= 0 && a.tile_u[t] > kPlanHaloMax;
+        int total;
+        const int rank = tile_scan_excl((int)f, s_wave, total);
+        if (f) a.overflow[done + rank] = (int32_t)t;
+        done += total;
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) a.hdr->n_overflow = (int32_t)done;
 }
 
 }  // namespace
@@ -1156,6 +1457,8 @@ int plan_args(const sc_conv_config *cfg, const int32_t *d_coords, int64_t n_in, 
     a.brick_cap = L.brick_cap;
     a.n_bsum = L.n_bsum;
     a.grid_cap = L.grid_cap;
+    a.tile_list = nullptr;
+    a.tile_list_n = nullptr;
     return SC_OK;
 }
 
@@ -1240,4 +1543,113 @@ extern "C" int sc_conv_plan_tables(const sc_conv_config *cfg, const int32_t *d_m
     int rc = plan_args(cfg, nullptr, n_in, d_map, n_q, d_plan, plan_bytes, false, true, a, L);
     if (rc) return rc;
     return launch_plan_tables(a, L, as_stream(stream));
+}
+
+extern "C" int sc_conv_child_plan_size(int64_t n_parents, int64_t n_children, int64_t kernel_rows, size_t *bytes)
+{
+    clear_error();
+    if (!bytes) return fail(SC_ERR_NULL, "bytes out-pointer is NULL");
+    if (n_parents < 0 || n_parents > INT32_MAX)
+        return fail(SC_ERR_SHAPE, "child plan parent count must be in [0, i32::MAX]");
+    if (n_children < 0 || n_children > 8 * n_parents)
+        return fail(SC_ERR_SHAPE, "child plan child count must be in [0, 8 * parents]");
+    if (kernel_rows < 1 || kernel_rows > 32)
+        return fail(SC_ERR_UNSUPPORTED, "conv plan supports kernels of 1..32 offsets");
+    *bytes = child_plan_layout(n_parents, n_children, kernel_rows).total;
+    return SC_OK;
+}
+
+extern "C" int sc_conv_child_plan_build(const sc_conv_config *cfg, const void *d_parent_plan, const int32_t *d_map,
+                                        int64_t n_parents, const int32_t *d_child_rows, int64_t n_children,
+                                        void *d_child_plan, size_t child_plan_bytes, sc_stream stream)
+{
+    clear_error();
+    int rc = validate_config(cfg);
+    if (rc) return rc;
+    const int64_t K = cfg->kernel_d * cfg->kernel_h * cfg->kernel_w;
+    if (K > 32) return fail(SC_ERR_UNSUPPORTED, "conv plan supports kernels of 1..32 offsets");
+    if (n_parents < 0 || n_parents > INT32_MAX)
+        return fail(SC_ERR_SHAPE, "child plan parent count must be in [0, i32::MAX]");
+    if (n_children < 0 || n_children > 8 * n_parents)
+        return fail(SC_ERR_SHAPE, "child plan child count must be in [0, 8 * parents]");
+    if (!d_parent_plan || !d_child_plan || (n_parents > 0 && (!d_map || !d_child_rows)))
+        return fail(SC_ERR_NULL, "child plan: NULL pointer");
+    if ((uintptr_t)d_parent_plan % 256 != 0 || (uintptr_t)d_child_plan % 256 != 0)
+        return fail(SC_ERR_WORKSPACE, "conv plans must be 256-byte aligned");
+    if ((uintptr_t)d_child_rows % 16 != 0) return fail(SC_ERR_SHAPE, "child rows must be 16-byte aligned");
+    const ChildPlanLayout CL = child_plan_layout(n_parents, n_children, K);
+    if (child_plan_bytes < CL.total)
+        return fail(SC_ERR_WORKSPACE, "child plan buffer too small: got " + std::to_string(child_plan_bytes) +
+                                          " need " + std::to_string(CL.total));
+    if (CL.n_tiles > INT32_MAX) return fail(SC_ERR_OVERFLOW, "child plan tile count overflow");
+    const PlanLayout PL = plan_layout(n_parents, K);
+    const char *pb = static_cast<const char *>(d_parent_plan);
+    char *b = static_cast<char *>(d_child_plan);
+    ChildArgs c;
+    c.phdr = reinterpret_cast<const PlanHeader *>(pb);
+    c.porder = reinterpret_cast<const int32_t *>(pb + PL.order);
+    c.child_rows = d_child_rows;
+    c.n_parents = n_parents;
+    c.n_children = n_children;
+    c.n_ptiles = CL.n_ptiles;
+    c.n_chunks = CL.n_chunks;
+    c.n_main = CL.n_main;
+    c.n_tiles = CL.n_tiles;
+    c.K = (int)K;
+    c.hdr = reinterpret_cast<PlanHeader *>(b);
+    c.order = reinterpret_cast<int32_t *>(b + CL.order);
+    c.tile_child = reinterpret_cast<int32_t *>(b + CL.tile_child);
+    c.tile_u = reinterpret_cast<int32_t *>(b + CL.tile_u);
+    c.overflow = reinterpret_cast<int32_t *>(b + CL.overflow);
+    c.counts = reinterpret_cast<int32_t *>(b + CL.counts);
+    c.chunks = reinterpret_cast<int32_t *>(b + CL.chunks);
+    c.child_n = reinterpret_cast<int32_t *>(b + CL.child_n);
+    c.child_base = reinterpret_cast<int32_t *>(b + CL.child_base);
+    c.split = reinterpret_cast<int32_t *>(b + CL.split);
+    c.split_n = reinterpret_cast<int32_t *>(b + CL.split_n);
+    hipStream_t s = as_stream(stream);
+    if (CL.n_ptiles > 0) {
+        child_count_kernel<<<(unsigned)CL.n_ptiles, kThreads, 0, s>>>(c);
+        SC_LAUNCH_CHECK("child_count_kernel launch");
+        child_chunk_kernel<<<(unsigned)CL.n_chunks, kThreads, 0, s>>>(c);
+        SC_LAUNCH_CHECK("child_chunk_kernel launch");
+    }
+    child_layout_kernel<<<1, kThreads, 0, s>>>(c);
+    SC_LAUNCH_CHECK("child_layout_kernel launch");
+    if (CL.n_ptiles > 0) {
+        child_emit_kernel<<<(unsigned)CL.n_ptiles, kThreads, 0, s>>>(c);
+        SC_LAUNCH_CHECK("child_emit_kernel launch");
+    }
+    child_pad_kernel<<<(unsigned)CL.n_tiles, kThreads, 0, s>>>(c);
+    SC_LAUNCH_CHECK("child_pad_kernel launch");
+    // the halo tables of the child tiles, from the parents' map rows
+    PlanArgs a{};
+    a.map = d_map;
+    a.n_q = n_parents;
+    a.n_in = n_parents;
+    a.K = (int)K;
+    a.hdr = c.hdr;
+    a.order = c.order;
+    a.tile_u = c.tile_u;
+    a.overflow = c.overflow;
+    a.halo = reinterpret_cast<int32_t *>(b + CL.halo);
+    a.lmap = reinterpret_cast<uint16_t *>(b + CL.lmap);
+    a.n_tiles = CL.n_tiles;
+    a.tile_list = nullptr;
+    a.tile_list_n = nullptr;
+    plan_tiles_kernel<<<(unsigned)CL.n_tiles, kTileThreads, 0, s>>>(a);
+    SC_LAUNCH_CHECK("plan_tiles_kernel launch (child plan)");
+    // overflowing tiles split in two, both rebuilt; the overflow list in tile order
+    child_split_kernel<<<1, kThreads, 0, s>>>(c);
+    SC_LAUNCH_CHECK("child_split_kernel launch");
+    const int64_t n_extra = CL.n_tiles - CL.n_main;
+    child_move_kernel<<<(unsigned)n_extra, kPlanTileRows / 2, 0, s>>>(c);
+    SC_LAUNCH_CHECK("child_move_kernel launch");
+    a.tile_list = c.split;
+    a.tile_list_n = c.split_n;
+    plan_tiles_kernel<<<(unsigned)(2 * n_extra), kTileThreads, 0, s>>>(a);
+    SC_LAUNCH_CHECK("plan_tiles_kernel launch (child plan splits)");
+    child_overflow_kernel<<<1, kThreads, 0, s>>>(c);
+    SC_LAUNCH_CHECK("child_overflow_kernel launch");
+    return SC_OK;
 }

@@ -42,6 +42,8 @@ constexpr int kPlanGridPerRow = 16;   // grid budget: cells per query row
 // were built for another shape; sc_conv_plan_check reads them back.
 constexpr uint32_t kPlanStatusMapMismatch = 1u;     // plan's n_q / n_in / K differ from the call's
 constexpr uint32_t kPlanStatusWeightMismatch = 2u;  // packed weights packed for another config
+constexpr uint32_t kPlanStatusChildRows = 4u;       // child plan: parent plan of another size, or more
+                                                    // active children than the call's child count
 
 struct alignas(16) PlanHeader {
     int64_t n_q;
@@ -56,7 +58,8 @@ struct alignas(16) PlanHeader {
     uint32_t status;
     int32_t grid_mode;  // 1: occupancy-grid order, 0: counting-sort fallback,
                         // 2: the rows' own order (octree order of >= 3 levels),
-                        // 3: occupancy-bitmap order (sorted, unique rows)
+                        // 3: occupancy-bitmap order (sorted, unique rows),
+                        // 4: a child plan (tiles grouped by C2S child index)
     int32_t n_unique;   // grid mode: occupied cells (distinct coords)
     int32_t n_extras;   // grid mode: rows of duplicated coords
     uint32_t pad[42];
@@ -109,7 +112,8 @@ inline PlanLayout plan_layout(int64_t n_q, int64_t K)
     return L;
 }
 
-// Device view of a built plan.
+// Device view of a built plan (tile_child: a child plan's per-tile child
+// index, NULL for a plan of the query rows themselves).
 struct PlanView {
     const PlanHeader *hdr;
     const int32_t *order;
@@ -117,6 +121,7 @@ struct PlanView {
     const int32_t *overflow;
     const int32_t *halo;
     const uint16_t *lmap;
+    const int32_t *tile_child;
 };
 
 inline PlanView plan_view(const void *plan, const PlanLayout &L)
@@ -129,6 +134,78 @@ inline PlanView plan_view(const void *plan, const PlanLayout &L)
     v.overflow = reinterpret_cast<const int32_t *>(b + L.overflow);
     v.halo = reinterpret_cast<const int32_t *>(b + L.halo);
     v.lmap = reinterpret_cast<const uint16_t *>(b + L.lmap);
+    v.tile_child = nullptr;
+    return v;
+}
+
+// Child plan (C2S conv1 over the active children only).  For each child
+// index c, the parents whose child c is active, in the parent plan's order,
+// in 256-row tiles of their own; tile t computes child tile_child[t]'s
+// channel block for its parents.  Same tables as a plan (order holds parent
+// rows), plus tile_child and the build's scratch.  The first n_main tiles
+// take the children's lists (every list but its last tile fills whole
+// tiles, so ceil(A / 256) + 8 suffice for A active children); a tile whose
+// halo overflows is then split, its second 128 rows moved to one of the
+// n_extra spare tiles, so both halves take the halo-staged kernel.  The
+// header's n_unique holds the tiles the lists use, n_extras the splits.
+constexpr int32_t kPlanModeChild = 4;
+
+struct ChildPlanLayout {
+    int64_t n_main, n_extra, n_tiles;  // list tiles, spare tiles for splits, all
+    int64_t n_ptiles;                  // tiles of the parent plan (compaction blocks)
+    int64_t n_chunks;                  // groups of 256 parent tiles (the scan's first level)
+    size_t order, tile_u, overflow, halo, lmap, tile_child, counts, chunks, child_n, child_base, split, split_n,
+        total;
+};
+
+inline ChildPlanLayout child_plan_layout(int64_t n_parents, int64_t n_children, int64_t K)
+{
+    ChildPlanLayout L;
+    L.n_main = (n_children + kPlanTileRows - 1) / kPlanTileRows + 8;
+    L.n_extra = L.n_main / 4 + 8;
+    L.n_tiles = L.n_main + L.n_extra;
+    L.n_ptiles = (n_parents + kPlanTileRows - 1) / kPlanTileRows;
+    L.n_chunks = (L.n_ptiles + 255) / 256;
+    size_t o = plan_align(sizeof(PlanHeader));
+    L.order = o;
+    o = plan_align(o + (size_t)L.n_tiles * kPlanTileRows * 4);
+    L.tile_u = o;
+    o = plan_align(o + (size_t)L.n_tiles * 4);
+    L.overflow = o;
+    o = plan_align(o + (size_t)L.n_tiles * 4);
+    L.halo = o;
+    o = plan_align(o + (size_t)L.n_tiles * kPlanHaloMax * 4);
+    L.lmap = o;
+    o = plan_align(o + (size_t)L.n_tiles * (size_t)K * kPlanTileRows * 2);
+    L.tile_child = o;
+    o = plan_align(o + (size_t)L.n_tiles * 4);
+    L.counts = o;
+    o = plan_align(o + (size_t)L.n_ptiles * 8 * 4);
+    L.chunks = o;
+    o = plan_align(o + (size_t)L.n_chunks * 8 * 4);
+    L.child_n = o;
+    o = plan_align(o + 8 * 4);
+    L.child_base = o;
+    o = plan_align(o + 8 * 4);
+    L.split = o;
+    o = plan_align(o + (size_t)L.n_extra * 2 * 4);
+    L.split_n = o;
+    o = plan_align(o + 4);
+    L.total = o;
+    return L;
+}
+
+inline PlanView child_plan_view(const void *plan, const ChildPlanLayout &L)
+{
+    const char *b = static_cast<const char *>(plan);
+    PlanView v;
+    v.hdr = reinterpret_cast<const PlanHeader *>(b);
+    v.order = reinterpret_cast<const int32_t *>(b + L.order);
+    v.tile_u = reinterpret_cast<const int32_t *>(b + L.tile_u);
+    v.overflow = reinterpret_cast<const int32_t *>(b + L.overflow);
+    v.halo = reinterpret_cast<const int32_t *>(b + L.halo);
+    v.lmap = reinterpret_cast<const uint16_t *>(b + L.lmap);
+    v.tile_child = reinterpret_cast<const int32_t *>(b + L.tile_child);
     return v;
 }
 

@@ -30,7 +30,7 @@ from typing import List, Optional, Sequence, Tuple, Union
 
 import torch
 
-from .flex_gmm import (ConvPlan, NeighborMapWorkspace, SparseSubmConvConfig, build_conv_plan,
+from .flex_gmm import (ConvPlan, NeighborMapWorkspace, SparseSubmConvConfig, build_child_plan, build_conv_plan,
                        c2s_skip_add, gather_rows, kernel_rows, layer_norm, linear_forward, linear_skinny,
                        neighbor_rows_tensor_from_coords_tensor, pack_conv_weight,
                        sparse_subm_conv_forward, subdivision_build, subdivision_build_indexed,
@@ -175,6 +175,10 @@ class C2SUpsampleBlock:
     # loader), and centering each row (center_subdivision_logits)
     compute_fp16: bool = False
     center_logits: bool = False
+    # fused conv1 over the active children only (a child plan of the
+    # parents' plan), when the shapes allow it: else all eight children are
+    # computed and the inactive ones dropped in the store
+    child_plans: bool = True
 
     def __call__(self, parent_coords: torch.Tensor, parent_feats: torch.Tensor,
                  logits: Optional[torch.Tensor] = None, mask: Optional[torch.Tensor] = None,
@@ -206,8 +210,16 @@ class C2SUpsampleBlock:
         if self.fused:
             child_coords, linear_idx, child_rows = subdivision_build_indexed(
                 parent_nb.coords, logits=logits, mask=mask, thresholds=thresholds)
-            h_up = self.conv1(h, parent_nb, out_dtype=dt, layer_norm=True, silu=True, ln_eps=self.eps,
-                              child_rows=child_rows, n_child_rows=child_coords.shape[0])
+            A = child_coords.shape[0]
+            nb1 = parent_nb
+            if (self.child_plans and parent_nb.plan is not None and A > 0 and dt in (torch.bfloat16, torch.float16)
+                    and (self.conv1.cfg.out_channels == 512 or self.conv1.cfg.out_channels % 1024 == 0)
+                    and self.conv1.cfg.groups == 1
+                    and self.conv1.packed_weight() is not None):
+                cp = build_child_plan(self.conv1.cfg, parent_nb.plan, parent_nb.nbr, child_rows, A)
+                nb1 = Neighborhood(parent_nb.coords, parent_nb.nbr, cp)
+            h_up = self.conv1(h, nb1, out_dtype=dt, layer_norm=True, silu=True, ln_eps=self.eps,
+                              child_rows=child_rows, n_child_rows=A)
         else:
             child_coords, linear_idx, _ = subdivision_build(parent_nb.coords, logits=logits, mask=mask,
                                                             thresholds=thresholds, with_pairs=False)

@@ -339,6 +339,77 @@ def build_conv_plan(cfg: SparseSubmConvConfig, coords: torch.Tensor,
     return conv_plan_build_into(cfg, coords, neighbor_rows, buf)
 
 
+class ChildPlan:
+    """A child plan (sc_conv_child_plan_build): per C2S child index, the
+    parents whose child is active, in the parent plan's order, in tiles of
+    their own, so conv1 of the upsample block computes only active children.
+    Built from the parents' ConvPlan, their map and the subdivision's
+    child_rows; ``n_children`` is the child count those rows index."""
+
+    def __init__(self, buf: torch.Tensor, n_parents: int, n_children: int, K: int):
+        self.buf, self.n_in, self.n_q, self.n_children, self.K = buf, n_parents, n_parents, n_children, K
+
+    def to_host(self) -> dict:
+        """Reads the child plan back (syncs): order [tiles, 256], tile_child,
+        tile_u, the overflow list, status, the tiles the lists use, the
+        splits, and the per-child entry counts and first tiles."""
+        n = ctypes.c_size_t()
+        check(_capi.load().sc_conv_child_plan_size(self.n_q, self.n_children, self.K, ctypes.byref(n)))
+        n_main = (self.n_children + PLAN_TILE_ROWS - 1) // PLAN_TILE_ROWS + 8
+        n_extra = n_main // 4 + 8
+        nt = n_main + n_extra
+        npt = (self.n_q + PLAN_TILE_ROWS - 1) // PLAN_TILE_ROWS
+        nch = (npt + 255) // 256
+        al = lambda x: (x + 255) & ~255
+        o = {"order": 256}
+        o["tile_u"] = al(o["order"] + nt * PLAN_TILE_ROWS * 4)
+        o["overflow"] = al(o["tile_u"] + nt * 4)
+        o["halo"] = al(o["overflow"] + nt * 4)
+        o["lmap"] = al(o["halo"] + nt * PLAN_HALO_MAX * 4)
+        o["tile_child"] = al(o["lmap"] + nt * self.K * PLAN_TILE_ROWS * 2)
+        o["counts"] = al(o["tile_child"] + nt * 4)
+        o["chunks"] = al(o["counts"] + npt * 8 * 4)
+        o["child_n"] = al(o["chunks"] + nch * 8 * 4)
+        o["child_base"] = al(o["child_n"] + 32)
+        o["split"] = al(o["child_base"] + 32)
+        o["split_n"] = al(o["split"] + n_extra * 8)
+        assert al(o["split_n"] + 4) == n.value
+        b = self.buf.cpu().numpy()
+        sec = lambda name, cnt: b[o[name]:o[name] + 4 * cnt].view(np.int32)
+        hdr = b[:256].view(np.int32)
+        n_over, n_split = int(hdr[7]), int(hdr[21])
+        return {"n_tiles": int(hdr[4]), "n_main": n_main, "status": int(b[:256].view(np.uint32)[18]),
+                "n_overflow": n_over, "grid_mode": int(hdr[19]), "n_used": int(hdr[20]), "n_split": n_split,
+                "order": sec("order", nt * PLAN_TILE_ROWS).reshape(nt, PLAN_TILE_ROWS),
+                "tile_child": sec("tile_child", nt), "tile_u": sec("tile_u", nt),
+                "overflow": sec("overflow", nt)[:n_over].copy(),
+                "split": sec("split", 2 * n_extra).reshape(n_extra, 2)[:n_split].copy(),
+                "child_n": sec("child_n", 8), "child_base": sec("child_base", 8)}
+
+
+def build_child_plan(cfg: SparseSubmConvConfig, parent_plan: ConvPlan, neighbor_rows: torch.Tensor,
+                     child_rows: torch.Tensor, n_children: int) -> ChildPlan:
+    """sc_conv_child_plan_build: the child plan of conv1 (``cfg``'s kernel)
+    over the parents of ``parent_plan`` / ``neighbor_rows`` [P, K] and the
+    subdivision's ``child_rows`` [P, 8] (n_children active)."""
+    _require_cuda("neighbor_rows", neighbor_rows)
+    _require_cuda("child_rows", child_rows)
+    K = kernel_rows(cfg)
+    P = neighbor_rows.shape[0]
+    if parent_plan.n_q != P or parent_plan.K != K:
+        raise SparseConvError(2, f"child plan: parent plan built for n_q={parent_plan.n_q} K={parent_plan.K}, "
+                                 f"map has {P} rows and K={K}")
+    if child_rows.dtype != torch.int32 or tuple(child_rows.shape) != (P, 8) or not child_rows.is_contiguous():
+        raise SparseConvError(2, "child plan: child_rows must be int32 [P, 8]")
+    n = ctypes.c_size_t()
+    check(_capi.load().sc_conv_child_plan_size(P, int(n_children), K, ctypes.byref(n)))
+    buf = torch.empty(n.value, dtype=torch.uint8, device=neighbor_rows.device)
+    check(_capi.load().sc_conv_child_plan_build(
+        ctypes.byref(cfg.to_c()), _ptr(parent_plan.buf), _ptr(neighbor_rows), P, _ptr(child_rows),
+        int(n_children), _ptr(buf), buf.numel(), _stream()))
+    return ChildPlan(buf, P, int(n_children), K)
+
+
 def conv_weight_pack_bytes(cfg: SparseSubmConvConfig, w_dtype: torch.dtype) -> int:
     out = ctypes.c_size_t()
     dt = {torch.bfloat16: _capi.SC_DTYPE_BF16, torch.int8: _capi.SC_DTYPE_I8,
@@ -480,6 +551,15 @@ def sparse_subm_conv_forward(cfg: SparseSubmConvConfig, input: torch.Tensor,
                 workspace = torch.empty(need.value, dtype=torch.uint8, device=input.device)
             epi.workspace = workspace.data_ptr()
             epi.workspace_bytes = workspace.numel()
+        if isinstance(plan, ChildPlan):
+            if child_rows is None or int(n_child_rows) != plan.n_children:
+                raise SparseConvError(2, "a child plan needs the child scatter it was built for "
+                                         f"({plan.n_children} children)")
+            check(_capi.load().sc_subm_conv_forward_child_planned(
+                ctypes.byref(c), _dt(input), _ptr(input), input.shape[0], _ptr(neighbor_rows), n_q,
+                _dt(weight), _ptr(weight), _ptr(packed_weight), _ptr(w_scale), _ptr(bias), ctypes.byref(epi),
+                _dt(out), _ptr(out), _ptr(plan.buf), _stream()))
+            return out
         if plan is not None:
             check(_capi.load().sc_subm_conv_forward_planned(
                 ctypes.byref(c), _dt(input), _ptr(input), input.shape[0], _ptr(neighbor_rows), n_q,

@@ -336,6 +336,47 @@ int sc_subm_conv_forward_planned(const sc_conv_config *cfg, int act_dtype, const
                                  const sc_conv_epilogue *epi, int out_dtype, void *d_out,
                                  const void *d_plan, sc_stream stream);
 
+/*
+ * Child plan: C2S conv1 over the active children only.  conv1 of the
+ * decoder's upsample block maps Cin -> 8 * Cout_child on the parents and
+ * keeps, per parent, only its active children's slices (the reference
+ * computes all eight and selects, sparse_decoder_runtime_impl.rs:2180-2255).
+ * A child plan groups, per child index c, the parents whose child c is
+ * active (d_child_rows [P][8] from sc_subdivision_build_indexed, 16-byte
+ * aligned; rows outside [0, n_children) count as inactive), in the parent
+ * plan's order (d_parent_plan: sc_conv_plan_build on the parents' map
+ * d_map [P][K]), into 256-row tiles of their own with halo tables; a tile
+ * then computes only its child's Cout_child channels.  Size it with
+ * sc_conv_child_plan_size (it depends on the child count); the build
+ * launches four kernels, stream-ordered, no sync.  A parent plan built for
+ * another row count or K, or more active children than n_children, leaves
+ * the plan empty and flagged (sc_conv_plan_check).  No reference
+ * counterpart: it replaces the [P, 8 * Cout_child] tensor and its select.
+ */
+int sc_conv_child_plan_size(int64_t n_parents, int64_t n_children, int64_t kernel_rows, size_t *bytes);
+int sc_conv_child_plan_build(const sc_conv_config *cfg, const void *d_parent_plan, const int32_t *d_map,
+                             int64_t n_parents, const int32_t *d_child_rows, int64_t n_children,
+                             void *d_child_plan, size_t child_plan_bytes, sc_stream stream);
+
+/*
+ * sc_subm_conv_forward_planned on a child plan: conv1 of the C2S block with
+ * the child scatter (epi->child_rows and epi->n_child_rows required, the same
+ * table and count the child plan was built from), only the active children
+ * computed.  Same results as sc_subm_conv_forward_planned with the parent
+ * plan and the same epilogue (each stored value is the same sum in the same
+ * order), except for children whose tile overflows the halo budget in either
+ * plan: the direct kernel sums those in another fixed order.  Needs 16-bit
+ * activations, packed weights, one group, at most 27
+ * offsets, and children of 64 channels or a multiple of 128 (Cout 512 or a
+ * multiple of 1024); other shapes fail with SC_ERR_UNSUPPORTED.
+ */
+int sc_subm_conv_forward_child_planned(const sc_conv_config *cfg, int act_dtype, const void *d_input,
+                                       int64_t n_in, const int32_t *d_map, int64_t n_q, int w_dtype,
+                                       const void *d_weight, const void *d_packed_weight,
+                                       const float *d_w_scale, const float *d_bias,
+                                       const sc_conv_epilogue *epi, int out_dtype, void *d_out,
+                                       const void *d_child_plan, sc_stream stream);
+
 /* Syncs `stream` and reports whether a planned conv on d_plan found the plan
  * or the packed weights built for another shape (SC_ERR_SHAPE; the conv then
  * wrote nothing).  The status is cleared when the plan is rebuilt (the

@@ -37,6 +37,45 @@ def host(t):
     return t.float().cpu().numpy()
 
 
+@pytest.mark.parametrize("round_f16,center", [(True, False), (False, True), (True, True), (False, False)])
+def test_subdivision_logits_finish(oracle, round_f16, center):
+    """The to_subdiv logits' post-processing in place, bit for bit: f16
+    rounding (the reference's quantize_f16 under compute_fp16; here against
+    the oracle's f16 rounding) and row centering (row_center_logits: the f32
+    sum in child order / 8, subtracted)."""
+    rng = np.random.default_rng(5 + 2 * round_f16 + center)
+    lg = (rng.standard_normal((70001, 8)) * 4).astype(np.float32)
+    lg[0] = [70000.0, -70000.0, 1e-8, -1e-8, 0.0, -0.0, 65504.0, 65520.0]  # f16 overflow / underflow edges
+    t = dev(lg)
+    F.subdivision_logits_finish(t, round_f16=round_f16, center=center)
+    exp = oracle.f16_round(lg) if round_f16 else lg.copy()
+    if center:
+        s = np.zeros(len(exp), np.float32)
+        for c in range(8):
+            s = (s + exp[:, c]).astype(np.float32)
+        exp = (exp - (s / np.float32(8))[:, None]).astype(np.float32)
+    got = t.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), exp.view(np.uint32)) or \
+        np.array_equal(np.isnan(got), np.isnan(exp)) and np.array_equal(got[~np.isnan(got)], exp[~np.isnan(exp)])
+
+
+def test_c2s_f16_logits_pick_children(oracle):
+    """compute_fp16: the block's to_subdiv logits are rounded to f16 before
+    the threshold test, so a logit that is positive in f32 but below f16's
+    smallest subnormal picks no child (the reference rounds, then compares)."""
+    P, C = 3000, 64
+    rng = np.random.default_rng(31)
+    x = synth.normal_f32(rng, (P, C)).astype(np.float16)
+    w = np.zeros((8, C), np.float32)
+    b = np.array([1e-9, -1e-9, 0.5, -0.5, 1e-3, 70000.0, 2.0 ** -25, 2.0 ** -24], np.float32)
+    up = D.C2SUpsampleBlock(C, C, dev(np.ones(C, np.float32)), dev(np.zeros(C, np.float32)), None, None,
+                            to_subdiv_weight=dev(w), to_subdiv_bias=dev(b), compute_fp16=True)
+    lg = up.subdivision_logits(dev(x)).cpu().numpy()
+    exp = np.broadcast_to(oracle.f16_round(b), (P, 8))
+    assert np.array_equal(lg.view(np.uint32), exp.view(np.uint32))
+    assert np.array_equal(lg[0] > 0, [False, False, True, False, True, True, False, True])
+
+
 @pytest.mark.parametrize("P", [1, 1023, 1025, 70001])
 def test_subdivision_indexed_child_rows(P):
     rng = np.random.default_rng(P)
@@ -257,3 +296,147 @@ def test_c2s_block_fused_config4_parents(oracle):
     _, y_ref = up.forward(pnb, x, logits=logits)
     d = (y.float() - y_ref.float()).abs().max().item()
     assert d <= 2 ** -5 * max(1.0, y_ref.float().abs().max().item()), d
+
+
+def _c2s_parents(n=None):
+    parents = synth.ShellCubeGeometry().coords()
+    return parents if n is None else parents[:n]
+
+
+@pytest.mark.parametrize("frac", [0.5, 0.0, 1.0])
+def test_child_plan_lists(frac):
+    """sc_conv_child_plan_build: per child index, the parents whose child is
+    active, in the parent plan's order, tiled from child_base[c]; a tile
+    whose halo overflowed has its rows 128..255 in a spare tile of the same
+    child (the splits listed in tile order); every other slot is -1; the
+    overflow list holds exactly the tiles still over the halo budget, in
+    tile order."""
+    rng = np.random.default_rng(int(frac * 10) + 3)
+    parents = _c2s_parents(50000)
+    P = len(parents)
+    mask = rng.random((P, 8)) < frac
+    cfg = F.SparseSubmConvConfig(128, 512)
+    pc = dev(parents)
+    nbr = F.neighbor_rows_tensor_from_coords_tensor(cfg, pc)
+    plan = F.build_conv_plan(cfg, pc, nbr)
+    cc, _, child_rows = F.subdivision_build_indexed(pc, mask=dev(mask.astype(np.uint8)))
+    A = cc.shape[0]
+    cp = F.build_child_plan(cfg, plan, nbr, child_rows, A)
+    h, ph = cp.to_host(), plan.to_host()
+    n_main = (A + 255) // 256 + 8
+    assert h["status"] == 0 and h["grid_mode"] == 4 and h["n_tiles"] == n_main + n_main // 4 + 8
+    porder = ph["order"].ravel()
+    porder = porder[porder >= 0]
+    order, tc = h["order"], h["tile_child"]
+    spare = {int(t): int(u) for t, u in h["split"]}
+    assert list(spare) == sorted(spare) and all(n_main <= u < h["n_tiles"] for u in spare.values())
+    assert sorted(spare.values()) == list(range(n_main, n_main + len(spare)))
+    base, used = 0, set()
+    for c in range(8):
+        lst = porder[mask[porder, c]]
+        nt = (len(lst) + 255) // 256
+        assert h["child_n"][c] == len(lst) and h["child_base"][c] == base, c
+        seg = []
+        for t in range(base, base + nt):
+            assert tc[t] == c
+            if t in spare:
+                u = spare[t]
+                assert tc[u] == c and (order[t][128:] == -1).all() and (order[u][128:] == -1).all()
+                seg += [order[t][:128], order[u][:128]]
+                used.add(u)
+            else:
+                seg.append(order[t])
+            used.add(t)
+        seg = np.concatenate(seg) if seg else np.zeros(0, np.int32)
+        assert np.array_equal(seg[:len(lst)], lst), c
+        assert (seg[len(lst):] == -1).all(), c
+        base += nt
+    assert h["n_used"] == base
+    rest = np.array(sorted(set(range(h["n_tiles"])) - used), np.int64)
+    assert (tc[rest] == -1).all() and (order[rest] == -1).all()
+    over = [t for t in range(h["n_tiles"]) if tc[t] >= 0 and h["tile_u"][t] > F.PLAN_HALO_MAX]
+    assert h["overflow"].tolist() == over
+    print(f"children {A}: list tiles {base}, splits {len(spare)}, overflow after splits {len(over)}")
+    F.conv_plan_check(cp)
+
+
+@pytest.mark.parametrize("cin,cchild,ln", [(128, 64, True), (256, 128, True), (128, 256, True),
+                                           (128, 64, False)])
+def test_conv1_child_plan_matches_parent_plan(cin, cchild, ln):
+    """conv1 of the C2S block through the child plan (only active children
+    computed) stores exactly what the parent-plan conv1 (all eight children,
+    inactive ones dropped) stores -- the same sum in the same order per value
+    -- wherever both plans take the halo-staged kernel with 128-channel
+    tiles, with the per-child LayerNorm in the tile (128 channels) or
+    through the f32 staging (256).  Children of 64 channels take 64-channel
+    tiles in the child plan, whose two waves per row half split the stages
+    (another order of the same sum): held to the bf16 bar."""
+    rng = np.random.default_rng(cin + cchild + ln)
+    parents = _c2s_parents()
+    P = len(parents)
+    mask = rng.random((P, 8)) < 0.5
+    cfg = F.SparseSubmConvConfig(cin, 8 * cchild)
+    pc = dev(parents)
+    nbr = F.neighbor_rows_tensor_from_coords_tensor(cfg, pc)
+    nb = D.Neighborhood(pc, nbr, F.build_conv_plan(cfg, pc, nbr))
+    cc, _, child_rows = F.subdivision_build_indexed(pc, mask=dev(mask.astype(np.uint8)))
+    A = cc.shape[0]
+    x = bf16_dev(synth.normal_f32(rng, (P, cin)))
+    layer = D.ConvLayer(cfg, bf16_dev(synth.conv_weight(rng, 8 * cchild, 27, cin, 1 / np.sqrt(27 * cin))),
+                        dev(synth.normal_f32(rng, 8 * cchild, 0.1)))
+    kw = dict(out_dtype=torch.bfloat16, layer_norm=ln, silu=ln, child_rows=child_rows, n_child_rows=A)
+    ref = layer(x, nb, **kw)
+    cp = F.build_child_plan(cfg, nb.plan, nbr, child_rows, A)
+    got = layer(x, D.Neighborhood(pc, nbr, cp), **kw)
+    F.conv_plan_check(cp)
+    assert got.shape == (A, cchild)
+    # Children computed by a halo tile in both plans are bit-equal; a tile
+    # whose halo overflows goes to the direct kernel, which sums in another
+    # order, so its children are held to the bf16 bar.
+    cr = child_rows.cpu().numpy()
+    ph, ch = nb.plan.to_host(), cp.to_host()
+    direct = np.zeros(A, bool)
+    for t in ph["overflow"]:
+        ps = ph["order"][t]
+        r = cr[ps[ps >= 0]].ravel()
+        direct[r[r >= 0]] = True
+    for t in np.nonzero(ch["tile_u"] > F.PLAN_HALO_MAX)[0]:
+        ps = ch["order"][t]
+        r = cr[ps[ps >= 0], ch["tile_child"][t]]
+        direct[r[r >= 0]] = True
+    g, r = got.float().cpu().numpy(), ref.float().cpu().numpy()
+    print(f"children {A}, through the direct kernel in either plan: {int(direct.sum())}")
+    if cchild == 64:
+        assert_close(g, r, TOL_BF16, "64-channel children, stage-split tiles")
+        return
+    assert np.array_equal(g[~direct], r[~direct])
+    if direct.any():
+        assert_close(g[direct], r[direct], TOL_BF16, "overflow-tile children")
+
+
+def test_child_plan_refuses_inconsistent_child_rows():
+    """Child rows naming more active children than the plan was sized for
+    (every child of every parent at row 0, with one child declared): the
+    build flags the plan and leaves it empty, and a conv on it writes
+    nothing."""
+    rng = np.random.default_rng(8)
+    parents = _c2s_parents(20000)
+    P = len(parents)
+    cfg = F.SparseSubmConvConfig(128, 512)
+    pc = dev(parents)
+    nbr = F.neighbor_rows_tensor_from_coords_tensor(cfg, pc)
+    plan = F.build_conv_plan(cfg, pc, nbr)
+    child_rows = torch.zeros((P, 8), dtype=torch.int32, device="cuda")
+    cp = F.build_child_plan(cfg, plan, nbr, child_rows, 1)
+    with pytest.raises(F.SparseConvError) as e:
+        F.conv_plan_check(cp)
+    assert e.value.status == 2 and "child plan" in e.value.message
+    h = cp.to_host()
+    assert (h["tile_child"] == -1).all() and (h["order"] == -1).all()
+    x = bf16_dev(synth.normal_f32(rng, (P, 128)))
+    layer = D.ConvLayer(cfg, bf16_dev(synth.conv_weight(rng, 512, 27, 128, 0.01)), dev(np.zeros(512, np.float32)))
+    out = torch.full((1, 64), 7.0, dtype=torch.bfloat16, device="cuda")
+    F.sparse_subm_conv_forward(cfg, x, nbr, layer.weight, layer.bias, out=out, plan=cp,
+                               packed_weight=layer.packed_weight(), child_rows=child_rows, n_child_rows=1)
+    torch.cuda.synchronize()
+    assert (out.float() == 7.0).all()

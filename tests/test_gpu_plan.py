@@ -256,7 +256,7 @@ def planned(cfg, coords, x, w, b, *, wdt="bf16", w_scale=None, q=None, **kw):
 
 
 @pytest.mark.parametrize("cin,cout,groups", [(32, 32, 1), (64, 96, 1), (128, 128, 1), (256, 64, 1),
-                                             (64, 64, 2), (96, 200, 1)])
+                                             (64, 64, 2), (96, 200, 1), (96, 64, 1)])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
 def test_planned_conv_shapes(oracle, cin, cout, groups, out_dtype):
     coords = synth.config1_coords()
