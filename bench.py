@@ -40,7 +40,8 @@ def parse():
                     help="untimed steps right before the timed ones (the GPU's clocks need ~20 steps)")
     ap.add_argument("--cpu-sample", type=int, default=262144,
                     help="query rows of the CPU baseline sample (0 = skip)")
-    ap.add_argument("--only", choices=["map", "plan", "mapplan", "conv", "ln", "config5"], default=None,
+    ap.add_argument("--only", choices=["map", "plan", "mapplan", "conv", "ln", "config5", "map_shuffled",
+                                       "map_spread"], default=None,
                     help="run just this part of the step (or config 5's decoder stack) --steps times "
                          "(for rocprofv3) and exit")
     ap.add_argument("--no-configs", action="store_true",
@@ -87,7 +88,8 @@ def host_cpu():
 
 def _config3_cpu_step(O, coords, x_f32, w1, w2, sample_rows, threads):
     """Seconds for the map over all coords and for the block over the first
-    `sample_rows` query rows, with the flex conv on `threads` threads."""
+    `sample_rows` query rows, with the flex conv (im2col gather + packed FMA
+    sgemm, oracle/sc_fastgemm.c) on `threads` threads."""
     import numpy as np
     O.set_num_threads(threads)
     cfg = O.OracleConfig(128, 128)
@@ -97,17 +99,61 @@ def _config3_cpu_step(O, coords, x_f32, w1, w2, sample_rows, threads):
     t_map = time.perf_counter() - t0
     rows = np.arange(sample_rows)
     t0 = time.perf_counter()
-    h = O.conv_flex_precomputed(cfg, w1, b, x_f32, nbr[rows])
+    h = O.conv_flex_fast(cfg, w1, b, x_f32, nbr[rows], threads=threads)
     h = O.silu(O.layer_norm(h, None, None, 1e-6))
     # conv2 reads conv1 output at neighbour rows; the sample's own rows stand in
     # for the rest of the input (same work per row).
     h_full = np.zeros_like(x_f32)
     h_full[rows] = h
-    y = O.conv_flex_precomputed(cfg, w2, b, h_full, nbr[rows]) + x_f32[rows]
+    y = O.conv_flex_fast(cfg, w2, b, h_full, nbr[rows], threads=threads) + x_f32[rows]
     t_rest = time.perf_counter() - t0
     assert y.shape == (sample_rows, 128)
     O.set_num_threads(1)
     return t_map, t_rest
+
+
+def _reference_bench_shape(O, reps=7):
+    """The reference's own CPU bench (crates/burn_flex_gmm/benches/
+    sparse_subm_conv.rs:37-74: 4,096 line coords [0, x, 0, 0], 3x3x3, Cin 64 ->
+    Cout 128, f32, LCG inputs), one thread, median of `reps`: the flex path
+    (map + pack + im2col + sgemm) with the packed FMA sgemm and with the
+    oracle's separately rounded loop, and the legacy direct loop; beside the
+    published ~22.5 ms (flex) and ~44.1 ms (legacy), whose hardware is not
+    stated (docs/trellis2_gpu_efficiency_roadmap.md:10-13)."""
+    import numpy as np
+    cfg = O.OracleConfig(64, 128)
+    coords = np.zeros((4096, 4), np.int32)
+    coords[:, 1] = np.arange(4096)
+    vals = O.Lcg(7).next_f32(4096 * 64 + 128 * 27 * 64 + 128)  # input, weight, bias in the bench's order
+    x = vals[:4096 * 64].reshape(4096, 64)
+    w = vals[4096 * 64:4096 * 64 + 128 * 27 * 64].reshape(128, 27, 64)
+    b = vals[4096 * 64 + 128 * 27 * 64:]
+    O.set_num_threads(1)
+
+    def med(fn):
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return 1e3 * sorted(ts)[reps // 2]
+
+    def flex_fast():
+        nbr = O.build_neighbor_rows(cfg, coords, lowest_row_on_duplicate=False)
+        return O.conv_flex_fast(cfg, w, b, x, nbr, threads=1)
+
+    ms_fast = med(flex_fast)
+    ms_oracle = med(lambda: O.conv_flex(cfg, w, b, coords, x))
+    ms_legacy = med(lambda: O.conv_legacy(cfg, w, b, coords, x))
+    issued = 2.0 * 4096 * 27 * 64 * 128
+    return {"shape": "4,096 line coords, 3x3x3, Cin 64 -> Cout 128, f32, 1 thread "
+                     "(crates/burn_flex_gmm/benches/sparse_subm_conv.rs:37-74)",
+            "flex_ms": ms_fast, "flex_issued_gflops": issued / (ms_fast * 1e-3) / 1e9,
+            "flex_oracle_loop_ms": ms_oracle, "legacy_ms": ms_legacy,
+            "published_flex_ms": 22.5, "published_legacy_ms": 44.1,
+            "note": "flex_ms: packed FMA sgemm (the kind matrixmultiply 0.3.10 runs); flex_oracle_loop_ms: the "
+                    "parity oracle's separately rounded loop; published figures from the reference's docs, "
+                    "hardware not stated"}
 
 
 def cpu_baseline(coords, x_f32, w1, w2, sample_rows):
@@ -125,6 +171,7 @@ def cpu_baseline(coords, x_f32, w1, w2, sample_rows):
     O.build()
     model, cores, threads = host_cpu()
     n = len(coords)
+    ref_shape = _reference_bench_shape(O)
     t_map1, t_rest1 = _config3_cpu_step(O, coords, x_f32, w1, w2, sample_rows, 1)
     t_mapn, t_restn = _config3_cpu_step(O, coords, x_f32, w1, w2, sample_rows, threads)
     # config 1, every row
@@ -138,7 +185,7 @@ def cpu_baseline(coords, x_f32, w1, w2, sample_rows):
         O.set_num_threads(t)
         t0 = time.perf_counter()
         nb1 = O.build_neighbor_rows(cfg1, c1, lowest_row_on_duplicate=False)
-        y1 = O.conv_flex_precomputed(cfg1, wc1, np.zeros(64, np.float32), x1, nb1)
+        y1 = O.conv_flex_fast(cfg1, wc1, np.zeros(64, np.float32), x1, nb1, threads=t)
         dt = time.perf_counter() - t0
         assert y1.shape == (len(c1), 64)
         pairs = int((nb1 >= 0).sum())
@@ -151,8 +198,10 @@ def cpu_baseline(coords, x_f32, w1, w2, sample_rows):
         "cores": 1,
         "kind": "port",
         "sample": (f"config 3 step: map build over all {n} coords ({t_map1:.2f} s) + conv/LN/SiLU/"
-                   f"conv/add over the first {sample_rows} query rows ({t_rest1:.2f} s), f32, 1 thread, "
-                   f"oracle/sc_oracle.c restating crates/burn_flex_gmm/src/lib.rs:69-109,242-375"),
+                   f"conv/add over the first {sample_rows} query rows ({t_rest1:.2f} s), f32, 1 thread; "
+                   f"map and LN/SiLU from oracle/sc_oracle.c, flex conv = its im2col gather + a packed FMA "
+                   f"sgemm (oracle/sc_fastgemm.c), restating crates/burn_flex_gmm/src/lib.rs:69-109,242-375"),
+        "reference_bench_shape": ref_shape,
         "host": {"cpu_model": model, "cores_available": cores},
         "all_cores": {"value": 1.0 / (t_mapn / n + t_restn / sample_rows), "unit": "voxels/s", "cores": threads,
                       "sample": f"same step; flex conv on {threads} OpenMP threads over row blocks "
@@ -265,11 +314,17 @@ def config_components(dev, st=None, steps: int = 5):
     # linear_idx and the [P, 8] child-row table written
     A = int(cc.shape[0])
     P = len(parents)
-    ms_sub = events_ms(lambda: F.subdivision_build_indexed(pc, mask=mask), steps, 2)
+    mask_u8 = mask.to(torch.uint8).contiguous()
+    sbuf = F.SubdivisionBuffers(P, dev)
+    ms_sub = events_ms(lambda: F.subdivision_launch(pc, mask=mask_u8, buffers=sbuf), steps, 2)
+    ms_call = events_ms(lambda: F.subdivision_build_indexed(pc, mask=mask_u8), steps, 2)
     sub_bytes = P * 8 + P * 16 + A * (16 + 4) + P * 32
     out["c2s_compaction"] = {"parents": P, "children": A, "ms": ms_sub,
                              "gbps": sub_bytes / (ms_sub * 1e-3) / 1e9,
-                             "note": "device kernels only (events); the call also reads the child count back"}
+                             "frac_hbm": sub_bytes / (ms_sub * 1e-3) / 8e12,
+                             "call_ms": ms_call,
+                             "note": "ms: the two launches back to back, buffers preallocated (events); "
+                                     "call_ms: the Python call, which allocates and reads the child count back"}
 
     # ConvNeXt block (conv -> LN(affine) -> mlp_0 -> SiLU -> mlp_2 + x) at
     # config 2's shape, C = 256, hidden 4C, bf16
@@ -307,8 +362,9 @@ def config_components(dev, st=None, steps: int = 5):
                                    "note": "conv -> LN -> SiLU, planned, back to back outside the step"}
 
     # The neighbour map in its other table modes: config 3's coords shuffled
-    # (unsorted rows: the dense grid) and config 5's last C2S child set
-    # (parent-major order over a sparse 512^3 box: the hash table).
+    # (unsorted rows: the dense grid), spread over a wide box (the hash
+    # table) and config 5's last C2S child set (C2S order below a sorted root
+    # set: the rank bitmap over octree levels).
     def map_mode(coords_np, what):
         cd = torch.from_numpy(np.ascontiguousarray(coords_np)).to(dev)
         n = len(coords_np)
@@ -326,6 +382,9 @@ def config_components(dev, st=None, steps: int = 5):
     for m in masks5:
         children = synth.child_expand(children, m)
     out["map_modes"] = {"config3_shuffled": map_mode(shuffled, "config 3 coords in a random row order"),
+                        "config3_spread": map_mode(synth.config3_spread_coords(),
+                                                   "config 3's octants 1024 cells apart in x, random row "
+                                                   "order (bbox beyond the dense grid)"),
                         "config5_children": map_mode(children, "config 5's last child set (C2S order)")}
     return out
 
@@ -419,6 +478,23 @@ def main():
             run5()
         ms = events_ms(run5, args.steps)
         print(f"[bench] only=config5 {ms:.3f} ms per call", file=sys.stderr, flush=True)
+        return
+    if args.only in ("map_shuffled", "map_spread"):
+        # the map alone in its dense-grid / hash-table mode (for rocprofv3)
+        c3 = synth.config3_coords()
+        cm = (c3[np.random.default_rng(11).permutation(len(c3))] if args.only == "map_shuffled"
+              else synth.config3_spread_coords())
+        cd = torch.from_numpy(np.ascontiguousarray(cm)).to(dev)
+        mcfg = F.SparseSubmConvConfig(64, 64)
+        nbr_m = torch.empty((len(cm), 27), dtype=torch.int32, device=dev)
+        ws_m = F.NeighborMapWorkspace(dev).get(len(cm))
+        part = lambda: F.neighbor_map_build_into(mcfg, cd, nbr_m, ws_m)
+        for _ in range(max(args.warmup, 1)):
+            part()
+        ms = events_ms(part, args.steps)
+        F.neighbor_map_check(ws_m)
+        print(f"[bench] only={args.only} table={F.neighbor_map_table_mode(ws_m)} {ms:.3f} ms per call",
+              file=sys.stderr, flush=True)
         return
     st = Config3Step(dev)
     n, C, coords, x_f32, w1, w2 = st.n, st.C, st.coords, st.x_f32, st.w1, st.w2

@@ -856,6 +856,13 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
     const int K = a.K;
     const int32_t n_in = (int32_t)a.n_in;  // <= INT32_MAX
     const int32_t q = a.order[t * kPlanTileRows + p];
+    // A tile of padding only (a child plan's unused list and spare tiles)
+    // records an empty halo and writes nothing else: no conv reads the
+    // other tables of such a tile.
+    if (!__syncthreads_or(q >= 0)) {
+        if (p == 0) a.tile_u[t] = 0;
+        return;
+    }
 
     int32_t v[32];
     if (a.n_q * (int64_t)K * 4 + 256 <= (int64_t)kOobOffset) {
@@ -1331,29 +1338,66 @@ __global__ __launch_bounds__(kThreads) void child_pad_kernel(ChildArgs a)
     if (pad) a.order[i] = -1;
 }
 
-// One workgroup, after the first tables: list tiles whose halo overflows,
-// in tile order, each paired with the next spare tile while spares last;
-// the spare takes the tile's child.
-__global__ __launch_bounds__(kThreads) void child_split_kernel(ChildArgs a)
+// The two passes over the tile list below run in one workgroup of
+// kListThreads threads, kListPer consecutive tiles per thread: a block scan
+// per kListThreads * kListPer tiles (4 rounds for config 5's 14,000 tiles).
+constexpr int kListThreads = 1024;
+constexpr int kListPer = 4;
+
+__device__ inline int list_scan_excl(int x, int *s_wave, int &total)
 {
-    __shared__ int s_wave[kThreads / 64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int inc = x;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(inc, off, 64);
+        if (lane >= off) inc += y;
+    }
+    __syncthreads();
+    if (lane == 63) s_wave[wave] = inc;
+    __syncthreads();
+    int before = 0;
+    total = 0;
+    for (int w = 0; w < kListThreads / 64; ++w) {
+        if (w < wave) before += s_wave[w];
+        total += s_wave[w];
+    }
+    return before + inc - x;
+}
+
+// After the first tables: list tiles whose halo overflows, in tile order,
+// each paired with the next spare tile while spares last; the spare takes
+// the tile's child.
+__global__ __launch_bounds__(kListThreads) void child_split_kernel(ChildArgs a)
+{
+    __shared__ int s_wave[kListThreads / 64];
     if (a.hdr->status != 0u) return;
     const int64_t n_used = a.hdr->n_unique;
     const int64_t n_extra = a.n_tiles - a.n_main;
     int64_t done = 0;
-    for (int64_t t0 = 0; t0 < n_used; t0 += kThreads) {
-        const int64_t t = t0 + threadIdx.x;
-        const bool f = t < n_used && a.tile_u[t] > kPlanHaloMax;
+    for (int64_t t0 = 0; t0 < n_used; t0 += kListThreads * kListPer) {
+        const int64_t tb = t0 + (int64_t)threadIdx.x * kListPer;
+        bool f[kListPer];
+        int cnt = 0;
+#pragma unroll
+        for (int u = 0; u < kListPer; ++u) {
+            f[u] = tb + u < n_used && a.tile_u[tb + u] > kPlanHaloMax;
+            cnt += f[u];
+        }
         int total;
-        const int rank = tile_scan_excl((int)f, s_wave, total);
-        if (f && done + rank < n_extra) {
-            const int64_t j = done + rank, spare = a.n_main + j;
-            a.split[2 * j] = (int32_t)t;
-            a.split[2 * j + 1] = (int32_t)spare;
-            a.tile_child[spare] = a.tile_child[t];
+        int64_t j = done + list_scan_excl(cnt, s_wave, total);
+#pragma unroll
+        for (int u = 0; u < kListPer; ++u) {
+            if (!f[u]) continue;
+            if (j < n_extra) {
+                const int64_t t = tb + u, spare = a.n_main + j;
+                a.split[2 * j] = (int32_t)t;
+                a.split[2 * j + 1] = (int32_t)spare;
+                a.tile_child[spare] = a.tile_child[t];
+            }
+            ++j;
         }
         done += total;
-        __syncthreads();
     }
     if (threadIdx.x == 0) {
         const int64_t ns = done < n_extra ? done : n_extra;
@@ -1374,20 +1418,28 @@ __global__ __launch_bounds__(kPlanTileRows / 2) void child_move_kernel(ChildArgs
     a.order[t * kPlanTileRows + kPlanTileRows / 2 + i] = -1;
 }
 
-// One workgroup: the overflow list rebuilt in tile order (tiles whose halo
-// still overflows after the splits, or that found no spare).
-__global__ __launch_bounds__(kThreads) void child_overflow_kernel(ChildArgs a)
+// The overflow list rebuilt in tile order (tiles whose halo still overflows
+// after the splits, or that found no spare).
+__global__ __launch_bounds__(kListThreads) void child_overflow_kernel(ChildArgs a)
 {
-    __shared__ int s_wave[kThreads / 64];
+    __shared__ int s_wave[kListThreads / 64];
     int64_t done = 0;
-    for (int64_t t0 = 0; t0 < a.n_tiles; t0 += kThreads) {
-        const int64_t t = t0 + threadIdx.x;
-        const bool f = t < a.n_tiles && a.tile_child[t] >= 0 && a.tile_u[t] > kPlanHaloMax;
+    for (int64_t t0 = 0; t0 < a.n_tiles; t0 += kListThreads * kListPer) {
+        const int64_t tb = t0 + (int64_t)threadIdx.x * kListPer;
+        bool f[kListPer];
+        int cnt = 0;
+#pragma unroll
+        for (int u = 0; u < kListPer; ++u) {
+            const int64_t t = tb + u;
+            f[u] = t < a.n_tiles && a.tile_child[t] >= 0 && a.tile_u[t] > kPlanHaloMax;
+            cnt += f[u];
+        }
         int total;
-        const int rank = tile_scan_excl((int)f, s_wave, total);
-        if (f) a.overflow[done + rank] = (int32_t)t;
+        int64_t j = done + list_scan_excl(cnt, s_wave, total);
+#pragma unroll
+        for (int u = 0; u < kListPer; ++u)
+            if (f[u]) a.overflow[j++] = (int32_t)(tb + u);
         done += total;
-        __syncthreads();
     }
     if (threadIdx.x == 0) a.hdr->n_overflow = (int32_t)done;
 }
@@ -1640,7 +1692,7 @@ extern "C" int sc_conv_child_plan_build(const sc_conv_config *cfg, const void *d
     plan_tiles_kernel<<<(unsigned)CL.n_tiles, kTileThreads, 0, s>>>(a);
     SC_LAUNCH_CHECK("plan_tiles_kernel launch (child plan)");
     // overflowing tiles split in two, both rebuilt; the overflow list in tile order
-    child_split_kernel<<<1, kThreads, 0, s>>>(c);
+    child_split_kernel<<<1, kListThreads, 0, s>>>(c);
     SC_LAUNCH_CHECK("child_split_kernel launch");
     const int64_t n_extra = CL.n_tiles - CL.n_main;
     child_move_kernel<<<(unsigned)n_extra, kPlanTileRows / 2, 0, s>>>(c);
@@ -1649,7 +1701,7 @@ extern "C" int sc_conv_child_plan_build(const sc_conv_config *cfg, const void *d
     a.tile_list_n = c.split_n;
     plan_tiles_kernel<<<(unsigned)(2 * n_extra), kTileThreads, 0, s>>>(a);
     SC_LAUNCH_CHECK("plan_tiles_kernel launch (child plan splits)");
-    child_overflow_kernel<<<1, kThreads, 0, s>>>(c);
+    child_overflow_kernel<<<1, kListThreads, 0, s>>>(c);
     SC_LAUNCH_CHECK("child_overflow_kernel launch");
     return SC_OK;
 }

@@ -162,7 +162,7 @@ inline ChildPlanLayout child_plan_layout(int64_t n_parents, int64_t n_children, 
 {
     ChildPlanLayout L;
     L.n_main = (n_children + kPlanTileRows - 1) / kPlanTileRows + 8;
-    L.n_extra = L.n_main / 4 + 8;
+    L.n_extra = L.n_main / 8 + 16;  // splits measured at 3-5 % of the list tiles
     L.n_tiles = L.n_main + L.n_extra;
     L.n_ptiles = (n_parents + kPlanTileRows - 1) / kPlanTileRows;
     L.n_chunks = (L.n_ptiles + 255) / 256;

@@ -2,15 +2,19 @@
 //
 // Replaces subdivision_active_indices_wgpu (argwhere of (logits - thr) > 0
 // on [P,8]) and expand_subdivision_coords_and_linear_indices_wgpu
-// (sparse_decoder_wgpu_ops.rs:885-1054) with a three-launch stream compaction:
-//   count : 1024 parents per block, popcount of each parent's 8-bit child
-//           mask, block total via wave64 reduction
-//   scan  : one block scans the block totals (exclusive) and writes the
-//           child count
-//   emit  : block-exclusive prefix (wave64 shfl scan + LDS wave totals) of
-//           per-thread counts; each thread writes the children of its 4
-//           consecutive parents in child order -> parent-major,
-//           child-ascending output, identical to argwhere's row-major order.
+// (sparse_decoder_wgpu_ops.rs:885-1054) with a two-launch stream compaction.
+// A block takes `rounds` rounds of 256 consecutive parents (rounds chosen so
+// that there are at most kMaxBlocks blocks):
+//   count : per block, the popcount of each parent's 8-bit child mask,
+//           summed
+//   emit  : the block's output offset = the counts of the blocks before it
+//           (at most kMaxBlocks values, read by the whole block); per
+//           round, a block scan of the parents' child counts, child_rows per
+//           parent, then the round's children written one per thread in
+//           output order (the thread finds its parent by binary search of
+//           the round's prefix), so consecutive lanes write consecutive
+//           rows -> parent-major, child-ascending output, identical to
+//           argwhere's row-major order.  The last block writes the count.
 #include "sc_common.hpp"
 
 #include <mutex>
@@ -18,9 +22,9 @@
 namespace sc {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kParentsPerThread = 4;
-constexpr int kParentsPerBlock = kThreads * kParentsPerThread;
+constexpr int kThreads = 256;               // parents per round
+constexpr int64_t kMaxBlocks = 1024;         // blocks while rounds stay under kMaxRounds
+constexpr int64_t kMaxRounds = 64;
 
 struct Thresholds {
     float t[8];
@@ -56,6 +60,7 @@ __device__ inline int block_exclusive_scan(int x, int *s_wave, int &total)
         const int y = __shfl_up(inc, off, 64);
         if (lane >= off) inc += y;
     }
+    __syncthreads();
     if (lane == 63) s_wave[wave] = inc;
     __syncthreads();
     int before = 0;
@@ -68,95 +73,107 @@ __device__ inline int block_exclusive_scan(int x, int *s_wave, int &total)
 }
 
 __global__ __launch_bounds__(kThreads) void subdiv_count_kernel(const float *logits, const uint8_t *mask,
-                                                                Thresholds th, int64_t P,
-                                                                int64_t *block_counts)
+                                                                Thresholds th, int64_t P, int rounds,
+                                                                int32_t *block_counts)
 {
     __shared__ int s_wave[kThreads / 64];
-    const int64_t p0 = (int64_t)blockIdx.x * kParentsPerBlock + (int64_t)threadIdx.x * kParentsPerThread;
+    const int64_t base = (int64_t)blockIdx.x * kThreads * rounds + threadIdx.x;
     int cnt = 0;
-#pragma unroll
-    for (int i = 0; i < kParentsPerThread; ++i)
-        if (p0 + i < P) cnt += __popc(child_mask(logits, mask, th, p0 + i));
+    for (int r = 0; r < rounds; ++r) {
+        const int64_t p = base + (int64_t)r * kThreads;
+        if (p < P) cnt += __popc(child_mask(logits, mask, th, p));
+    }
     int total;
     block_exclusive_scan(cnt, s_wave, total);
     if (threadIdx.x == 0) block_counts[blockIdx.x] = total;
 }
 
-__global__ __launch_bounds__(1024) void subdiv_scan_kernel(const int64_t *block_counts, int64_t nblocks,
-                                                           int64_t *block_offsets, int64_t *count)
-{
-    __shared__ int64_t s_part[1024];
-    int64_t carry = 0;
-    for (int64_t base = 0; base < nblocks; base += 1024) {
-        const int64_t i = base + threadIdx.x;
-        const int64_t v = i < nblocks ? block_counts[i] : 0;
-        s_part[threadIdx.x] = v;
-        __syncthreads();
-        // Hillis-Steele inclusive scan over 1024 entries.
-        for (int off = 1; off < 1024; off <<= 1) {
-            const int64_t y = threadIdx.x >= (unsigned)off ? s_part[threadIdx.x - off] : 0;
-            __syncthreads();
-            s_part[threadIdx.x] += y;
-            __syncthreads();
-        }
-        if (i < nblocks) block_offsets[i] = carry + s_part[threadIdx.x] - v;
-        const int64_t chunk_total = s_part[1023];
-        __syncthreads();
-        carry += chunk_total;
-    }
-    if (threadIdx.x == 0) *count = carry;
-}
-
 __global__ __launch_bounds__(kThreads) void subdiv_emit_kernel(const float *logits, const uint8_t *mask,
-                                                               Thresholds th, int64_t P,
+                                                               Thresholds th, int64_t P, int rounds,
                                                                const int4 *__restrict__ parent_coords,
-                                                               const int64_t *block_offsets,
+                                                               const int32_t *block_counts,
                                                                int4 *child_coords, int32_t *linear_idx,
-                                                               int2 *pairs, int32_t *child_rows)
+                                                               int2 *pairs, int32_t *child_rows,
+                                                               int64_t *count)
 {
     __shared__ int s_wave[kThreads / 64];
-    const int64_t p0 = (int64_t)blockIdx.x * kParentsPerBlock + (int64_t)threadIdx.x * kParentsPerThread;
-    unsigned m[kParentsPerThread];
-    int cnt = 0;
+    __shared__ int s_pre[kThreads];
+    __shared__ uint8_t s_m[kThreads];
+    __shared__ int64_t s_sum[kThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the block's first output row: the counts of the blocks before it
+    int64_t part = 0;
+    for (int64_t i = tid; i < (int64_t)blockIdx.x; i += kThreads) part += block_counts[i];
 #pragma unroll
-    for (int i = 0; i < kParentsPerThread; ++i) {
-        m[i] = p0 + i < P ? child_mask(logits, mask, th, p0 + i) : 0u;
-        cnt += __popc(m[i]);
-    }
-    int total;
-    int64_t out = block_offsets[blockIdx.x] + block_exclusive_scan(cnt, s_wave, total);
-#pragma unroll
-    for (int i = 0; i < kParentsPerThread; ++i) {
-        if (child_rows && p0 + i < P) {
+    for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off, 64);
+    if (lane == 0) s_sum[wave] = part;
+    __syncthreads();
+    int64_t out = 0;
+    for (int w = 0; w < kThreads / 64; ++w) out += s_sum[w];
+    const int64_t base = (int64_t)blockIdx.x * kThreads * rounds;
+    for (int r = 0; r < rounds; ++r) {
+        const int64_t p0 = base + (int64_t)r * kThreads;
+        const int64_t p = p0 + tid;
+        const unsigned m = p < P ? child_mask(logits, mask, th, p) : 0u;
+        int total;
+        const int ex = block_exclusive_scan(__popc(m), s_wave, total);
+        if (child_rows && p < P) {
             // the inverse of linear_idx: child row of (parent, c), -1 if inactive
             int32_t cr[8];
-            int32_t o = (int32_t)out;
+            int32_t o = (int32_t)(out + ex);
 #pragma unroll
-            for (int c = 0; c < 8; ++c) cr[c] = (m[i] >> c) & 1u ? o++ : -1;
-            int4 *dst = reinterpret_cast<int4 *>(child_rows + (p0 + i) * 8);
+            for (int c = 0; c < 8; ++c) cr[c] = (m >> c) & 1u ? o++ : -1;
+            int4 *dst = reinterpret_cast<int4 *>(child_rows + p * 8);
             dst[0] = make_int4(cr[0], cr[1], cr[2], cr[3]);
             dst[1] = make_int4(cr[4], cr[5], cr[6], cr[7]);
         }
-        if (!m[i]) continue;
-        const int64_t p = p0 + i;
-        const int4 pc = parent_coords[p];
-        for (int c = 0; c < 8; ++c) {
-            if (!(m[i] & (1u << c))) continue;
-            child_coords[out] = make_int4(pc.x, 2 * pc.y + (c & 1), 2 * pc.z + ((c >> 1) & 1),
+        s_pre[tid] = ex;
+        s_m[tid] = (uint8_t)m;
+        __syncthreads();
+        for (int j = tid; j < total; j += kThreads) {
+            // the last parent of the round whose prefix is <= j (parents with
+            // no children share the next one's prefix, so it is the owner)
+            int lo = 0, hi = kThreads - 1;
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (s_pre[mid] <= j) lo = mid;
+                else hi = mid - 1;
+            }
+            const unsigned pm = s_m[lo];
+            int k = j - s_pre[lo], c = 0;
+            for (; c < 8; ++c)
+                if ((pm >> c) & 1u) {
+                    if (k == 0) break;
+                    --k;
+                }
+            const int64_t pp = p0 + lo, row = out + j;
+            const int4 pc = parent_coords[pp];
+            child_coords[row] = make_int4(pc.x, 2 * pc.y + (c & 1), 2 * pc.z + ((c >> 1) & 1),
                                           2 * pc.w + ((c >> 2) & 1));
-            linear_idx[out] = (int32_t)(p * 8 + c);
-            if (pairs) pairs[out] = make_int2((int32_t)p, c);
-            ++out;
+            linear_idx[row] = (int32_t)(pp * 8 + c);
+            if (pairs) pairs[row] = make_int2((int32_t)pp, c);
         }
+        out += total;
+        __syncthreads();  // s_pre / s_m are rewritten by the next round
     }
+    if (blockIdx.x == gridDim.x - 1 && tid == 0) *count = out;
 }
 
 __global__ void write_zero_count(int64_t *count) { *count = 0; }
 
-inline int64_t n_blocks(int64_t P) { return (P + kParentsPerBlock - 1) / kParentsPerBlock; }
+inline int rounds_for(int64_t P)
+{
+    const int64_t r = (P + kThreads * kMaxBlocks - 1) / (kThreads * kMaxBlocks);
+    return (int)(r < 1 ? 1 : (r > kMaxRounds ? kMaxRounds : r));
+}
+inline int64_t n_blocks(int64_t P)
+{
+    const int64_t per = (int64_t)kThreads * rounds_for(P);
+    return (P + per - 1) / per;
+}
 
-// Bytes of block counts + offsets for P parents.
-inline size_t workspace_bytes_for(int64_t P) { return (size_t)(2 * n_blocks(P) + 2) * sizeof(int64_t); }
+// Bytes of block counts for P parents.
+inline size_t workspace_bytes_for(int64_t P) { return (size_t)(n_blocks(P) + 4) * sizeof(int32_t); }
 
 // Argument checks shared by both entry points (the workspace is checked by
 // the caller).
@@ -180,14 +197,14 @@ int check_args(const float *d_logits, const uint8_t *d_mask, const float *thresh
     return SC_OK;
 }
 
-// The three launches over a workspace of workspace_bytes_for(parent_rows)
+// The two launches over a workspace of workspace_bytes_for(parent_rows)
 // bytes (the caller's, or the library's static scratch).  count writes every
-// block total and scan every offset, so nothing in the workspace needs to
+// block total before emit reads them, so nothing in the workspace needs to
 // start at zero.
 int launch_subdivision(const float *d_logits, const uint8_t *d_mask, const float *thresholds,
                        const int32_t *d_parent_coords, int64_t parent_rows, int32_t *d_child_coords,
                        int32_t *d_linear_idx, int32_t *d_pairs, int32_t *d_child_rows, int64_t *d_count,
-                       int64_t *ws, hipStream_t s)
+                       int32_t *ws, hipStream_t s)
 {
     if (parent_rows == 0) {
         write_zero_count<<<1, 1, 0, s>>>(d_count);
@@ -196,39 +213,37 @@ int launch_subdivision(const float *d_logits, const uint8_t *d_mask, const float
     }
     Thresholds th;
     for (int c = 0; c < 8; ++c) th.t[c] = thresholds ? thresholds[c] : 0.f;
+    const int rounds = rounds_for(parent_rows);
     const int64_t nb = n_blocks(parent_rows);
-    int64_t *counts = ws;
-    int64_t *offsets = counts + nb;
-    subdiv_count_kernel<<<(unsigned)nb, kThreads, 0, s>>>(d_logits, d_mask, th, parent_rows, counts);
+    int32_t *counts = ws;
+    subdiv_count_kernel<<<(unsigned)nb, kThreads, 0, s>>>(d_logits, d_mask, th, parent_rows, rounds, counts);
     SC_LAUNCH_CHECK("subdiv_count_kernel launch");
-    subdiv_scan_kernel<<<1, 1024, 0, s>>>(counts, nb, offsets, d_count);
-    SC_LAUNCH_CHECK("subdiv_scan_kernel launch");
-    subdiv_emit_kernel<<<(unsigned)nb, kThreads, 0, s>>>(d_logits, d_mask, th, parent_rows,
-                                                         (const int4 *)d_parent_coords, offsets,
+    subdiv_emit_kernel<<<(unsigned)nb, kThreads, 0, s>>>(d_logits, d_mask, th, parent_rows, rounds,
+                                                         (const int4 *)d_parent_coords, counts,
                                                          (int4 *)d_child_coords, d_linear_idx,
-                                                         (int2 *)d_pairs, d_child_rows);
+                                                         (int2 *)d_pairs, d_child_rows, d_count);
     SC_LAUNCH_CHECK("subdiv_emit_kernel launch");
     return SC_OK;
 }
 
 // ------------------------------------------------------ static scratch
-// The workspace of sc_subdivision_build_static: block counts and offsets for
-// up to kStaticMaxParents parents (1 MiB + 16 B), one copy per GPU, held
-// until the process ends.  In host code `scratch` names a host-side stand-in,
+// The workspace of sc_subdivision_build_static: block counts for up to
+// kStaticMaxParents parents (4,096 blocks, 16 KiB + 16 B), one copy per GPU,
+// held until the process ends.  In host code `scratch` names a host-side stand-in,
 // never the device array: every host use goes through the per-device
 // address from hipGetSymbolAddress (static_scratch_for).
 constexpr int64_t kStaticMaxParents = (int64_t)1 << 26;
-constexpr int64_t kStaticMaxBlocks = kStaticMaxParents / kParentsPerBlock;
-static __device__ __align__(256) int64_t scratch[2 * kStaticMaxBlocks + 2];
+constexpr int64_t kStaticMaxBlocks = kStaticMaxParents / (kThreads * kMaxRounds);
+static __device__ __align__(256) int32_t scratch[kStaticMaxBlocks + 4];
 
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
-int64_t *g_scratch_ptr[kMaxDevices] = {};
+int32_t *g_scratch_ptr[kMaxDevices] = {};
 
 // Device address of `scratch` on the device that stream s belongs to (the
 // current device for the NULL stream), looked up once per device with that
 // device current.
-int static_scratch_for(hipStream_t s, int64_t **out)
+int static_scratch_for(hipStream_t s, int32_t **out)
 {
     int dev = 0;
     if (s)
@@ -246,7 +261,7 @@ int static_scratch_for(hipStream_t s, int64_t **out)
         if (cur != dev) SC_HIP_CHECK(hipSetDevice(cur), "hipSetDevice");
         if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
         if (!p || (uintptr_t)p % 256 != 0) return fail(SC_ERR_HIP, "static subdivision scratch is misaligned");
-        g_scratch_ptr[dev] = static_cast<int64_t *>(p);
+        g_scratch_ptr[dev] = static_cast<int32_t *>(p);
     }
     *out = g_scratch_ptr[dev];
     return SC_OK;
@@ -286,7 +301,7 @@ int sc_subdivision_build(const float *d_logits, const uint8_t *d_mask, const flo
             return fail(SC_ERR_WORKSPACE, "subdivision workspace too small");
     }
     return launch_subdivision(d_logits, d_mask, thresholds, d_parent_coords, parent_rows, d_child_coords,
-                              d_linear_idx, d_pairs, nullptr, d_count, static_cast<int64_t *>(d_workspace),
+                              d_linear_idx, d_pairs, nullptr, d_count, static_cast<int32_t *>(d_workspace),
                               as_stream(stream));
 }
 
@@ -308,7 +323,7 @@ int sc_subdivision_build_indexed(const float *d_logits, const uint8_t *d_mask, c
             return fail(SC_ERR_WORKSPACE, "subdivision workspace too small");
     }
     return launch_subdivision(d_logits, d_mask, thresholds, d_parent_coords, parent_rows, d_child_coords,
-                              d_linear_idx, d_pairs, d_child_rows, d_count, static_cast<int64_t *>(d_workspace),
+                              d_linear_idx, d_pairs, d_child_rows, d_count, static_cast<int32_t *>(d_workspace),
                               as_stream(stream));
 }
 
@@ -326,7 +341,7 @@ int sc_subdivision_build_static(const float *d_logits, const uint8_t *d_mask, co
                                           std::to_string(kStaticMaxParents) + " parent rows, got " +
                                           std::to_string(parent_rows) + " (use sc_subdivision_build)");
     hipStream_t s = as_stream(stream);
-    int64_t *ws = nullptr;
+    int32_t *ws = nullptr;
     if (parent_rows > 0) {
         rc = static_scratch_for(s, &ws);
         if (rc) return rc;

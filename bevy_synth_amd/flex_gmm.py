@@ -356,7 +356,7 @@ class ChildPlan:
         n = ctypes.c_size_t()
         check(_capi.load().sc_conv_child_plan_size(self.n_q, self.n_children, self.K, ctypes.byref(n)))
         n_main = (self.n_children + PLAN_TILE_ROWS - 1) // PLAN_TILE_ROWS + 8
-        n_extra = n_main // 4 + 8
+        n_extra = n_main // 8 + 16
         nt = n_main + n_extra
         npt = (self.n_q + PLAN_TILE_ROWS - 1) // PLAN_TILE_ROWS
         nch = (npt + 255) // 256
@@ -727,13 +727,28 @@ def subdivision_build(parent_coords: torch.Tensor, logits: Optional[torch.Tensor
     return child[:a], lin[:a], (pairs[:a] if pairs is not None else None)
 
 
-def subdivision_build_indexed(parent_coords: torch.Tensor, logits: Optional[torch.Tensor] = None,
-                              mask: Optional[torch.Tensor] = None,
-                              thresholds: Optional[Sequence[float]] = None
-                              ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """subdivision_build plus the inverse of linear_idx (sc_subdivision_build_indexed):
-    returns (child_coords [A,4], linear_idx [A], child_rows [P,8] int32 with
-    child_rows[p, c] = the row of child (p, c) or -1).  Syncs once to read A."""
+class SubdivisionBuffers:
+    """Device buffers of one sc_subdivision_build_indexed call over P parents
+    (child capacity 8P), reusable across calls of the same P."""
+
+    def __init__(self, P: int, dev):
+        cap = max(8 * P, 1)
+        self.P = P
+        self.child = torch.empty((cap, 4), dtype=torch.int32, device=dev)
+        self.lin = torch.empty((cap,), dtype=torch.int32, device=dev)
+        self.rows = torch.empty((max(P, 1), 8), dtype=torch.int32, device=dev)
+        self.count = torch.empty((1,), dtype=torch.int64, device=dev)
+        wsb = ctypes.c_size_t()
+        check(_capi.load().sc_subdivision_workspace_size(P, ctypes.byref(wsb)))
+        self.ws = torch.empty(max(wsb.value, 16), dtype=torch.uint8, device=dev)
+
+
+def subdivision_launch(parent_coords: torch.Tensor, logits: Optional[torch.Tensor] = None,
+                       mask: Optional[torch.Tensor] = None, thresholds: Optional[Sequence[float]] = None,
+                       buffers: Optional[SubdivisionBuffers] = None) -> SubdivisionBuffers:
+    """sc_subdivision_build_indexed into `buffers` (new ones when None), on the
+    current stream, without waiting: the child count stays on the device
+    (buffers.count)."""
     _require_cuda("parent_coords", parent_coords)
     P = parent_coords.shape[0]
     dev = parent_coords.device
@@ -748,19 +763,25 @@ def subdivision_build_indexed(parent_coords: torch.Tensor, logits: Optional[torc
             raise SparseConvError(2, "subdivision mask must be u8/bool [P, 8]")
         mask = mask.to(torch.uint8).contiguous()
         th = None
-    cap = max(8 * P, 1)
-    child = torch.empty((cap, 4), dtype=torch.int32, device=dev)
-    lin = torch.empty((cap,), dtype=torch.int32, device=dev)
-    rows = torch.empty((max(P, 1), 8), dtype=torch.int32, device=dev)
-    count = torch.empty((1,), dtype=torch.int64, device=dev)
-    wsb = ctypes.c_size_t()
-    check(_capi.load().sc_subdivision_workspace_size(P, ctypes.byref(wsb)))
-    ws = torch.empty(max(wsb.value, 16), dtype=torch.uint8, device=dev)
+    b = buffers if buffers is not None else SubdivisionBuffers(P, dev)
+    if b.P != P:
+        raise SparseConvError(2, f"subdivision buffers hold {b.P} parents, the call has {P}")
     check(_capi.load().sc_subdivision_build_indexed(
-        _ptr(logits), _ptr(mask), th, _ptr(parent_coords), P, _ptr(child), _ptr(lin), None, _ptr(rows),
-        _ptr(count), _ptr(ws), ws.numel(), _stream()))
-    a = int(count.item())
-    return child[:a], lin[:a], rows[:P]
+        _ptr(logits), _ptr(mask), th, _ptr(parent_coords), P, _ptr(b.child), _ptr(b.lin), None, _ptr(b.rows),
+        _ptr(b.count), _ptr(b.ws), b.ws.numel(), _stream()))
+    return b
+
+
+def subdivision_build_indexed(parent_coords: torch.Tensor, logits: Optional[torch.Tensor] = None,
+                              mask: Optional[torch.Tensor] = None,
+                              thresholds: Optional[Sequence[float]] = None
+                              ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """subdivision_build plus the inverse of linear_idx (sc_subdivision_build_indexed):
+    returns (child_coords [A,4], linear_idx [A], child_rows [P,8] int32 with
+    child_rows[p, c] = the row of child (p, c) or -1).  Syncs once to read A."""
+    b = subdivision_launch(parent_coords, logits, mask, thresholds)
+    a = int(b.count.item())
+    return b.child[:a], b.lin[:a], b.rows[:b.P]
 
 
 def linear_skinny(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:

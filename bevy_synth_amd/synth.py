@@ -150,6 +150,18 @@ def config3_coords(seed: int = 13) -> np.ndarray:
     return EllipsoidShellGeometry(seed=seed).coords()
 
 
+def config3_spread_coords(seed: int = 13, gap: int = 1024, shuffle_seed: int = 11) -> np.ndarray:
+    """Config 3's rows with its eight octants (halves of the 256^3 box per
+    axis) moved gap cells apart along x, in a random row order: the same
+    local neighbourhoods (but across the cuts) in a bounding box far above the
+    dense grid's budget -- the map's hash-table mode."""
+    c = config3_coords(seed).copy()
+    octant = ((c[:, 1] >= 128).astype(np.int32) | ((c[:, 2] >= 128).astype(np.int32) << 1) |
+              ((c[:, 3] >= 128).astype(np.int32) << 2))
+    c[:, 1] += octant * gap
+    return c[np.random.default_rng(shuffle_seed).permutation(len(c))]
+
+
 def ellipsoid_shell_distance(geom: EllipsoidShellGeometry, pts: np.ndarray) -> np.ndarray:
     """min_i |d_i(p)| over the union's ellipsoids, the first-order distance the
     shell set uses, at arbitrary points (grid units of ``geom``)."""

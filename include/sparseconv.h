@@ -462,8 +462,8 @@ int sc_subdivision_build_indexed(const float *d_logits, const uint8_t *d_mask, c
  * sc_subdivision_build without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, serving loops that
  * forbid hipMalloc).  It has no counterpart in the reference.  Same
- * arguments and results as sc_subdivision_build; its scratch (block counts
- * and offsets, 1 MiB + 16 B) is a static device array inside the library,
+ * arguments and results as sc_subdivision_build; its scratch (block counts,
+ * 16 KiB + 16 B) is a static device array inside the library,
  * one copy per GPU, held until the process ends.  parent_rows is limited to
  * 2^26 (67,108,864; larger counts fail with SC_ERR_WORKSPACE and
  * launch nothing).  It calls no allocator.  Every call on one GPU shares that

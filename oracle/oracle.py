@@ -121,6 +121,8 @@ def lib():
         L.orc_c2s_block.argtypes = [P, P, i64, i64, i64, P, P, P, cfgp, P, P, cfgp, P, P,
                                     ctypes.c_float, P, P]
         L.orc_c2s_block.restype = i64
+        L.orc_conv_flex_fast.argtypes = [cfgp, P, P, P, i64, P, i64, P]
+        L.orc_fast_set_num_threads.argtypes = [ctypes.c_int]
         L.orc_lcg_fill.argtypes = [ctypes.c_uint64, i64, P]
         L.orc_lcg_fill.restype = ctypes.c_uint64
         _lib = L
@@ -212,6 +214,23 @@ def conv_flex_precomputed(cfg: OracleConfig, weight, bias, inp, nbr,
     _check(lib().orc_conv_flex_precomputed(ctypes.byref(cfg.c()), _p(w), _p(b), _p(x),
                                            x.shape[0], _p(m), m.shape[0], _p(pk), _p(out)),
            "conv_flex_precomputed")
+    return out
+
+
+def conv_flex_fast(cfg: OracleConfig, weight, bias, inp, nbr, packed: Optional[np.ndarray] = None,
+                   threads: int = 1) -> np.ndarray:
+    """Timing only (the CPU baseline): conv_flex_precomputed's gather with a
+    packed, register-blocked FMA sgemm of matrixmultiply's kind
+    (oracle/sc_fastgemm.c), on `threads` OpenMP threads.  Equal to
+    conv_flex_precomputed up to float rounding; never a parity checker."""
+    b = np.ascontiguousarray(bias, dtype=np.float32).reshape(-1)
+    x = np.ascontiguousarray(inp, dtype=np.float32).reshape(-1, cfg.in_channels)
+    m = np.ascontiguousarray(nbr, dtype=np.int32).reshape(-1, cfg.kernel_rows)
+    pk = pack_flex_weight(cfg, weight) if packed is None else np.ascontiguousarray(packed, dtype=np.float32)
+    out = np.zeros((m.shape[0], cfg.out_channels), dtype=np.float32)
+    lib().orc_fast_set_num_threads(int(threads))
+    _check(lib().orc_conv_flex_fast(ctypes.byref(cfg.c()), _p(pk), _p(b), _p(x), x.shape[0], _p(m), m.shape[0],
+                                    _p(out)), "conv_flex_fast")
     return out
 
 

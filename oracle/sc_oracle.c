@@ -20,29 +20,7 @@
 #include <stdlib.h>
 #include <string.h>
 
-#define ORC_INVALID_NEIGHBOR (-1) /* crates/burn_flex_gmm/src/lib.rs:3 */
-
-/* Mirror of SparseSubmConvConfig, crates/burn_flex_gmm/src/lib.rs:5-17. */
-typedef struct orc_cfg {
-    int64_t in_channels;
-    int64_t out_channels;
-    int64_t kernel_d;
-    int64_t kernel_h;
-    int64_t kernel_w;
-    int64_t in_channels_per_group;
-    int64_t out_channels_per_group;
-    int64_t groups;
-    int32_t axis_order[3];
-    int32_t axis_sign[3];
-} orc_cfg;
-
-enum {
-    ORC_OK = 0,
-    ORC_ERR_CONFIG = 1,
-    ORC_ERR_SHAPE = 2,
-    ORC_ERR_INDEX = 3,
-    ORC_ERR_ALLOC = 4,
-};
+#include "sc_oracle_cfg.h"
 
 /* validate_config, crates/burn_flex_gmm/src/lib.rs:698-725. */
 int orc_validate_config(const orc_cfg *c)

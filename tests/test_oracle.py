@@ -100,6 +100,26 @@ def test_flex_handles_empty_rows(oracle):
     assert out.shape == (0, 2)
 
 
+@pytest.mark.parametrize("groups", [1, 2])
+def test_fast_flex_matches_flex_to_rounding(oracle, groups):
+    """The CPU baseline's timing conv (packed FMA sgemm, oracle/sc_fastgemm.c)
+    computes the oracle's flex conv: equal to float rounding, on 1 and 3
+    threads, with row and column counts off the 6 x 16 register tile."""
+    rng = np.random.default_rng(groups)
+    cfg = oracle.OracleConfig(48 * groups, 40 * groups, groups=groups)
+    c = rng.integers(0, 12, size=(700, 4)).astype(np.int32)
+    c[:, 0] = 0
+    c = np.unique(c, axis=0)
+    x = rng.standard_normal((len(c), cfg.in_channels)).astype(np.float32)
+    w = rng.standard_normal((cfg.out_channels, 27, 48)).astype(np.float32)
+    b = rng.standard_normal(cfg.out_channels).astype(np.float32)
+    nbr = oracle.build_neighbor_rows(cfg, c)
+    ref = oracle.conv_flex_precomputed(cfg, w, b, x, nbr)
+    for t in (1, 3):
+        got = oracle.conv_flex_fast(cfg, w, b, x, nbr, threads=t)
+        assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max(), t
+
+
 def test_flex_precomputed_matches_default(oracle):
     """crates/burn_flex_gmm/src/lib.rs:864-915 (seed 73, groups 2, 32 line coords)."""
     cfg = oracle.OracleConfig(8, 12, 3, 1, 1, groups=2)
