@@ -71,6 +71,7 @@ class ScConvEpilogue(ctypes.Structure):
         ("skip_index", ctypes.c_void_p),
         ("skip_parent_rows", ctypes.c_int64),
         ("skip_parent_channels", ctypes.c_int64),
+        ("child_count", ctypes.c_void_p),
     ]
 
 

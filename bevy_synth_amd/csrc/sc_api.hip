@@ -108,9 +108,10 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const Tin *in, int64_t 
                                                          const float *__restrict__ w,
                                                          const float *__restrict__ b, float eps,
                                                          int apply_silu, const Tout *res, Tout *out,
-                                                         const uint32_t *gate)
+                                                         const uint32_t *gate, const int64_t *row_limit)
 {
     if (gate && *gate) return;  // see launch_layer_norm
+    if (row_limit && *row_limit < rows) rows = *row_limit > 0 ? *row_limit : 0;
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (row >= rows) return;
@@ -211,9 +212,10 @@ __global__ __launch_bounds__(256) void layer_norm_vec_kernel(const Tin *in, int6
                                                              const float *__restrict__ w,
                                                              const float *__restrict__ b, float eps,
                                                              int apply_silu, const Tout *res, Tout *out,
-                                                             const uint32_t *gate)
+                                                             const uint32_t *gate, const int64_t *row_limit)
 {
     if (gate && *gate) return;  // see launch_layer_norm
+    if (row_limit && *row_limit < rows) rows = *row_limit > 0 ? *row_limit : 0;
     constexpr int VEC = Vec16<Tin>::N;
     constexpr int RPW = 64 / LPR;  // rows per wave and load
     const int lane = threadIdx.x & 63;
@@ -307,9 +309,11 @@ __global__ __launch_bounds__(256) void layer_norm_wide_kernel(const Tin *in, int
                                                               const float *__restrict__ w,
                                                               const float *__restrict__ b,
                                                               float eps, int apply_silu, const Tout *res,
-                                                              Tout *out, const uint32_t *gate)
+                                                              Tout *out, const uint32_t *gate,
+                                                              const int64_t *row_limit)
 {
     if (gate && *gate) return;  // see launch_layer_norm
+    if (row_limit && *row_limit < rows) rows = *row_limit > 0 ? *row_limit : 0;
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (row >= rows) return;
@@ -409,7 +413,7 @@ __global__ void c2s_skip_add_vec_kernel(uint16_t *h, int n, int vpr, const Tp *_
 template <typename Tin, typename Tout>
 int launch_layer_norm(const void *in, int64_t rows, int64_t ch, const float *w,
                              const float *b, float eps, int silu, const void *res_, void *out, hipStream_t s,
-                             const uint32_t *gate)
+                             const uint32_t *gate, const int64_t *row_limit)
 {
     const unsigned g = grid_for(rows, 4, INT32_MAX);
     const Tin *x = (const Tin *)in;
@@ -429,7 +433,7 @@ int launch_layer_norm(const void *in, int64_t rows, int64_t ch, const float *w,
         const int64_t rows_per_block = 4 * (64 / lpr) * nr;
         const unsigned gv = grid_for(rows, (int)rows_per_block, INT32_MAX);
 #define LN_VEC(L, N, R) \
-    layer_norm_vec_kernel<Tin, Tout, L, N, R><<<gv, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y, gate)
+    layer_norm_vec_kernel<Tin, Tout, L, N, R><<<gv, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y, gate, row_limit)
         bool launched = true;
         if (lpr == 8 && nv == 1 && nr == 4) LN_VEC(8, 1, 4);
         else if (lpr == 16 && nv == 1 && nr == 4) LN_VEC(16, 1, 4);
@@ -451,17 +455,17 @@ int launch_layer_norm(const void *in, int64_t rows, int64_t ch, const float *w,
     }
     const int vpl = (C + 63) / 64;
     if (vpl <= 1)
-        layer_norm_kernel<Tin, Tout, 1><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y, gate);
+        layer_norm_kernel<Tin, Tout, 1><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y, gate, row_limit);
     else if (vpl <= 2)
-        layer_norm_kernel<Tin, Tout, 2><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y, gate);
+        layer_norm_kernel<Tin, Tout, 2><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y, gate, row_limit);
     else if (vpl <= 4)
-        layer_norm_kernel<Tin, Tout, 4><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y, gate);
+        layer_norm_kernel<Tin, Tout, 4><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y, gate, row_limit);
     else if (vpl <= 8)
-        layer_norm_kernel<Tin, Tout, 8><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y, gate);
+        layer_norm_kernel<Tin, Tout, 8><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y, gate, row_limit);
     else if (vpl <= 16)
-        layer_norm_kernel<Tin, Tout, 16><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y, gate);
+        layer_norm_kernel<Tin, Tout, 16><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y, gate, row_limit);
     else
-        layer_norm_wide_kernel<Tin, Tout><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y, gate);
+        layer_norm_wide_kernel<Tin, Tout><<<g, 256, 0, s>>>(x, rows, C, w, b, eps, silu, res, y, gate, row_limit);
     SC_LAUNCH_CHECK("layer_norm_kernel launch");
     return SC_OK;
 }
@@ -546,7 +550,7 @@ __global__ __launch_bounds__(256) void linear_skinny_kernel(const Tin *__restric
 
 int layer_norm_rows(int in_dtype, const void *d_in, int64_t rows, int64_t channels, const float *d_w,
                     const float *d_b, float eps, int apply_silu, int out_dtype, const void *d_res, void *d_out,
-                    hipStream_t s, const uint32_t *d_gate)
+                    hipStream_t s, const uint32_t *d_gate, const int64_t *d_row_limit)
 {
     if (rows < 0 || channels <= 0 || channels > INT32_MAX)
         return fail(SC_ERR_SHAPE, "layer_norm: invalid rows/channels");
@@ -554,7 +558,8 @@ int layer_norm_rows(int in_dtype, const void *d_in, int64_t rows, int64_t channe
     if (!d_in || !d_out) return fail(SC_ERR_NULL, "layer_norm: NULL pointer");
 #define LN_CASE(DI, TI, DO, TO)                                                                          \
     if (in_dtype == DI && out_dtype == DO)                                                              \
-        return launch_layer_norm<TI, TO>(d_in, rows, channels, d_w, d_b, eps, apply_silu, d_res, d_out, s, d_gate);
+        return launch_layer_norm<TI, TO>(d_in, rows, channels, d_w, d_b, eps, apply_silu, d_res, d_out, s, d_gate, \
+                                         d_row_limit);
     LN_CASE(SC_DTYPE_F32, float, SC_DTYPE_F32, float)
     LN_CASE(SC_DTYPE_F32, float, SC_DTYPE_BF16, uint16_t)
     LN_CASE(SC_DTYPE_F32, float, SC_DTYPE_F16, _Float16)

@@ -40,7 +40,7 @@ int silu_inplace(int dtype, void *d, int64_t n, hipStream_t s);
 // makes it write nothing (a planned conv's plan status).
 int layer_norm_rows(int in_dtype, const void *d_in, int64_t rows, int64_t channels, const float *d_w,
                     const float *d_b, float eps, int apply_silu, int out_dtype, const void *d_res, void *d_out,
-                    hipStream_t s, const uint32_t *d_gate = nullptr);
+                    hipStream_t s, const uint32_t *d_gate = nullptr, const int64_t *d_row_limit = nullptr);
 
 inline bool mul_ok(int64_t a, int64_t b, int64_t *out)
 {

@@ -267,9 +267,12 @@ static int conv_forward_impl(const sc_conv_config *cfg, int act_dtype, const voi
     // After a planned conv, the row kernel is gated on the plan's status: a
     // conv that found a mismatch stored nothing to normalise, and nothing
     // may reach d_out.
+    // With the child scatter, rows at or past the device child count (when
+    // given) were never written: the row kernel stops there.
     return layer_norm_rows(SC_DTYPE_F32, conv_out, ln_rows, ln_ch, epi->ln_weight, epi->ln_bias, epi->ln_eps,
                            want_silu, out_dtype, d_residual, d_out, s,
-                           plan ? &static_cast<const PlanHeader *>(plan)->status : nullptr);
+                           plan ? &static_cast<const PlanHeader *>(plan)->status : nullptr,
+                           c2s.scatter ? epi->child_count : nullptr);
 }
 
 

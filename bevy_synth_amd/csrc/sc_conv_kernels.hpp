@@ -1214,7 +1214,18 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
         // rebuilt: nothing is written meanwhile
         if (plan.hdr->status != 0u) return;
     }
-    const int tile = tile_for_block(blockIdx.x, gridDim.x);
+    int tile;
+    if (plan.tile_child) {
+        // a child plan: its list tiles in use, then its split spares, dealt
+        // to the XCDs as one range (the grid covers the layout's bound; the
+        // other workgroups exit on every XCD alike)
+        const int n_used = plan.hdr->n_unique, n_real = n_used + plan.hdr->n_extras;
+        if ((int)blockIdx.x >= n_real) return;
+        const int l = tile_for_block(blockIdx.x, n_real);
+        tile = l < n_used ? l : plan.hdr->list_tiles + (l - n_used);
+    } else {
+        tile = tile_for_block(blockIdx.x, gridDim.x);
+    }
     const int U = plan.tile_u[tile];
     if (U > kPlanHaloMax) return;  // listed in plan.overflow; the direct kernel takes it
     // a child plan's tile computes its child's channel block (an unused tile nothing)

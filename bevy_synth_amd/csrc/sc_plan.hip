@@ -111,6 +111,7 @@ __device__ inline void plan_init(const PlanArgs &a)
         h->grid_mode = 0;
         h->n_unique = 0;
         h->n_extras = 0;
+        h->list_tiles = 0;
     }
     for (int64_t i = a.n_q + tid; i < a.n_tiles * kPlanTileRows; i += stride) a.order[i] = -1;
 }
@@ -848,6 +849,12 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
     if (a.tile_list) {
         if ((int)blockIdx.x >= *a.tile_list_n) return;
         t = a.tile_list[blockIdx.x];
+    } else if (a.hdr->grid_mode == kPlanModeChild) {
+        // a child plan's list tiles in use (the grid covers the layout's
+        // bound): dealt to the XCDs like any tile range, the rest exit
+        const int n_used = a.hdr->n_unique;
+        if ((int)blockIdx.x >= n_used) return;
+        t = tile_for_block((int)blockIdx.x, n_used);
     } else {
         t = tile_for_block((int)blockIdx.x, (int)gridDim.x);
     }
@@ -1287,6 +1294,7 @@ __global__ __launch_bounds__(kThreads) void child_layout_kernel(ChildArgs a)
         h->grid_mode = kPlanModeChild;
         h->n_unique = ok ? (int32_t)base : 0;  // list tiles in use
         h->n_extras = 0;                       // splits (the split pass sets it)
+        h->list_tiles = (int32_t)a.n_main;     // spare tiles from here
         *a.split_n = 0;
     }
     __syncthreads();

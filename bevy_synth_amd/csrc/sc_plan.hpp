@@ -60,9 +60,10 @@ struct alignas(16) PlanHeader {
                         // 2: the rows' own order (octree order of >= 3 levels),
                         // 3: occupancy-bitmap order (sorted, unique rows),
                         // 4: a child plan (tiles grouped by C2S child index)
-    int32_t n_unique;   // grid mode: occupied cells (distinct coords)
-    int32_t n_extras;   // grid mode: rows of duplicated coords
-    uint32_t pad[42];
+    int32_t n_unique;   // grid mode: occupied cells (distinct coords); child plan: list tiles in use
+    int32_t n_extras;   // grid mode: rows of duplicated coords; child plan: splits
+    int32_t list_tiles; // child plan: list tiles laid out (the first spare tile); 0 otherwise
+    uint32_t pad[41];
 };
 static_assert(sizeof(PlanHeader) == 256, "plan header size");
 

@@ -34,6 +34,7 @@ from .flex_gmm import (ConvPlan, NeighborMapWorkspace, SparseSubmConvConfig, bui
                        c2s_skip_add, gather_rows, kernel_rows, layer_norm, linear_forward, linear_skinny,
                        neighbor_rows_tensor_from_coords_tensor, pack_conv_weight,
                        sparse_subm_conv_forward, subdivision_build, subdivision_build_indexed,
+                       subdivision_launch, count_to_host_async,
                        subdivision_logits_finish)
 
 LAYER_NORM32_EPS = 1e-6  # sparse_decoder.rs:43
@@ -53,9 +54,12 @@ class Neighborhood:
 
     @classmethod
     def build(cls, cfg: SparseSubmConvConfig, coords: torch.Tensor,
-              workspace: Optional[NeighborMapWorkspace] = None, with_plan: bool = True
-              ) -> "Neighborhood":
-        nbr = neighbor_rows_tensor_from_coords_tensor(cfg, coords, workspace=workspace)
+              workspace: Optional[NeighborMapWorkspace] = None, with_plan: bool = True,
+              check_status: bool = True) -> "Neighborhood":
+        """The map (and plan) of ``coords``.  check_status=False skips the
+        map's status read-back (a sync), for coords this library derived from
+        checked ones (C2S children: 2x + c of non-negative, distinct parents)."""
+        nbr = neighbor_rows_tensor_from_coords_tensor(cfg, coords, workspace=workspace, check_status=check_status)
         plan = build_conv_plan(cfg, coords, nbr) if with_plan and kernel_rows(cfg) <= 32 else None
         return cls(coords, nbr, plan)
 
@@ -208,18 +212,28 @@ class C2SUpsampleBlock:
             logits = self.subdivision_logits(parent_feats)
         h = layer_norm(parent_feats, self.norm1_weight, self.norm1_bias, eps=self.eps, silu=True)
         if self.fused:
-            child_coords, linear_idx, child_rows = subdivision_build_indexed(
-                parent_nb.coords, logits=logits, mask=mask, thresholds=thresholds)
-            A = child_coords.shape[0]
+            # conv1 and its child plan are sized by the bound 8P, so they are
+            # enqueued before the child count reaches the host: the count's
+            # read-back overlaps conv1 instead of idling the GPU (conv1 writes
+            # only the rows child_rows names, all below the count)
+            P = parent_nb.coords.shape[0]
+            sb = subdivision_launch(parent_nb.coords, logits=logits, mask=mask, thresholds=thresholds)
+            host_count, count_ready = count_to_host_async(sb.count)
+            child_rows = sb.rows[:P]
+            A_max = 8 * P
             nb1 = parent_nb
-            if (self.child_plans and parent_nb.plan is not None and A > 0 and dt in (torch.bfloat16, torch.float16)
+            if (self.child_plans and parent_nb.plan is not None and A_max > 0
+                    and dt in (torch.bfloat16, torch.float16)
                     and (self.conv1.cfg.out_channels == 512 or self.conv1.cfg.out_channels % 1024 == 0)
                     and self.conv1.cfg.groups == 1
                     and self.conv1.packed_weight() is not None):
-                cp = build_child_plan(self.conv1.cfg, parent_nb.plan, parent_nb.nbr, child_rows, A)
+                cp = build_child_plan(self.conv1.cfg, parent_nb.plan, parent_nb.nbr, child_rows, A_max)
                 nb1 = Neighborhood(parent_nb.coords, parent_nb.nbr, cp)
             h_up = self.conv1(h, nb1, out_dtype=dt, layer_norm=True, silu=True, ln_eps=self.eps,
-                              child_rows=child_rows, n_child_rows=A)
+                              child_rows=child_rows, n_child_rows=A_max, child_count=sb.count)
+            count_ready.synchronize()
+            A = int(host_count[0])
+            child_coords, linear_idx, h_up = sb.child[:A], sb.lin[:A], h_up[:A]
         else:
             child_coords, linear_idx, _ = subdivision_build(parent_nb.coords, logits=logits, mask=mask,
                                                             thresholds=thresholds, with_pairs=False)
@@ -227,7 +241,7 @@ class C2SUpsampleBlock:
             h_up = gather_rows(h1, 8, linear_idx)
             h_up = layer_norm(h_up, eps=self.eps, silu=True, out=h_up)
         child_nb = Neighborhood.build(self.conv2.cfg, child_coords, workspace,
-                                      with_plan=parent_nb.plan is not None)
+                                      with_plan=parent_nb.plan is not None, check_status=not self.fused)
         if self.fused:
             out = self.conv2(h_up, child_nb, out_dtype=dt, skip_parent=parent_feats, skip_index=linear_idx)
         else:

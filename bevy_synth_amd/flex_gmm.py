@@ -309,6 +309,24 @@ def _aux_stream(device: torch.device) -> torch.cuda.Stream:
     return _AUX_STREAMS[key]
 
 
+def count_to_host_async(count: torch.Tensor) -> Tuple[torch.Tensor, "torch.cuda.Event"]:
+    """Copies a device int64 count into pinned host memory on the side stream,
+    ordered after the current stream's work so far but not after anything
+    enqueued on it later: the caller enqueues more GPU work, then waits on
+    the returned event and reads the host tensor, so the read-back overlaps
+    that work instead of idling the GPU."""
+    main = torch.cuda.current_stream(count.device)
+    aux = _aux_stream(count.device)
+    host = torch.empty(count.shape, dtype=count.dtype, pin_memory=True)
+    aux.wait_stream(main)
+    with torch.cuda.stream(aux):
+        host.copy_(count, non_blocking=True)
+        ready = torch.cuda.Event()
+        ready.record(aux)
+    count.record_stream(aux)
+    return host, ready
+
+
 def map_and_plan_into(cfg: SparseSubmConvConfig, coords: torch.Tensor, neighbor_rows: torch.Tensor,
                       workspace: torch.Tensor, plan_buf: torch.Tensor) -> ConvPlan:
     """The neighbour map and its conv plan, with the plan's row order (which
@@ -380,6 +398,7 @@ class ChildPlan:
         n_over, n_split = int(hdr[7]), int(hdr[21])
         return {"n_tiles": int(hdr[4]), "n_main": n_main, "status": int(b[:256].view(np.uint32)[18]),
                 "n_overflow": n_over, "grid_mode": int(hdr[19]), "n_used": int(hdr[20]), "n_split": n_split,
+                "list_tiles": int(hdr[22]),
                 "order": sec("order", nt * PLAN_TILE_ROWS).reshape(nt, PLAN_TILE_ROWS),
                 "tile_child": sec("tile_child", nt), "tile_u": sec("tile_u", nt),
                 "overflow": sec("overflow", nt)[:n_over].copy(),
@@ -447,7 +466,8 @@ def sparse_subm_conv_forward(cfg: SparseSubmConvConfig, input: torch.Tensor,
                              workspace: Optional[torch.Tensor] = None,
                              child_rows: Optional[torch.Tensor] = None, n_child_rows: Optional[int] = None,
                              skip_parent: Optional[torch.Tensor] = None,
-                             skip_index: Optional[torch.Tensor] = None) -> torch.Tensor:
+                             skip_index: Optional[torch.Tensor] = None,
+                             child_count: Optional[torch.Tensor] = None) -> torch.Tensor:
     """sparse_subm_conv_forward_wgpu (crates/burn_flex_gmm/src/wgpu/sparse_conv.rs:310-367).
 
     input [N_in, Cin] f32|bf16; neighbor_rows [N_q, K] int32 (N_q <= N_in);
@@ -467,8 +487,11 @@ def sparse_subm_conv_forward(cfg: SparseSubmConvConfig, input: torch.Tensor,
     ``child_rows`` [N_q, 8] int32 (subdivision_build_indexed) makes this conv1
     of the upsample block -- query row r's channels [c*C, (c+1)*C), C =
     Cout/8, are child c's features and land in row child_rows[r, c] of an
-    [n_child_rows, C] output (LayerNorm then per child); ``skip_parent`` [P,
-    Cp] with ``skip_index`` [N_q] (the children's linear_idx) adds the
+    [n_child_rows, C] output (LayerNorm then per child); ``child_count`` (the
+    subdivision's device int64 count) lets n_child_rows be an upper bound
+    such as 8 N_q, so the call needs no host read of the count: a LayerNorm
+    staged outside the tile stops at that row.  ``skip_parent`` [P, Cp] with
+    ``skip_index`` [N_q] (the children's linear_idx) adds the
     channel-repeated parent skip (conv2).
     Returns [N_q, Cout] in out_dtype (default: the input dtype)."""
     _require_cuda("input", input)
@@ -532,6 +555,11 @@ def sparse_subm_conv_forward(cfg: SparseSubmConvConfig, input: torch.Tensor,
         if child_rows is not None:
             epi.child_rows = child_rows.data_ptr()
             epi.n_child_rows = int(n_child_rows)
+            if child_count is not None:
+                _require_cuda("child_count", child_count)
+                if child_count.dtype != torch.int64 or child_count.numel() != 1:
+                    raise SparseConvError(2, "child_count must be a device int64 [1]")
+                epi.child_count = child_count.data_ptr()
         if skip_index is not None:
             epi.skip_parent = skip_parent.data_ptr()
             epi.skip_index = skip_index.data_ptr()

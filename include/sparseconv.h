@@ -195,6 +195,13 @@ typedef struct sc_conv_epilogue {
     const int32_t *skip_index;
     int64_t skip_parent_rows;
     int64_t skip_parent_channels;
+    /* Child scatter with n_child_rows an upper bound (8P, so that conv1 can
+     * be enqueued before the child count reaches the host): the device int64
+     * count sc_subdivision_build_indexed wrote, or NULL.  A LayerNorm staged
+     * through `workspace` then stops at that row; rows past it are neither
+     * written by the conv nor read.  (Last field: a zero-initialised
+     * epilogue leaves it NULL.) */
+    const int64_t *child_count;
 } sc_conv_epilogue;
 
 /* sc_subm_conv_forward with a fused epilogue (same arguments, epi replaces

@@ -325,6 +325,7 @@ def test_child_plan_lists(frac):
     h, ph = cp.to_host(), plan.to_host()
     n_main = (A + 255) // 256 + 8
     assert h["status"] == 0 and h["grid_mode"] == 4 and h["n_tiles"] == n_main + n_main // 8 + 16
+    assert h["list_tiles"] == n_main
     porder = ph["order"].ravel()
     porder = porder[porder >= 0]
     order, tc = h["order"], h["tile_child"]
