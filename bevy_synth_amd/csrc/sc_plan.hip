@@ -938,10 +938,15 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
             s_pfull = 0;
         }
         __syncthreads();
+        // A row's neighbours come in offset order, z fastest, so runs of
+        // them share a page: each run inserts (and later probes) once.
+        int32_t last_pg = -1;
 #pragma unroll
         for (int k = 0; k < 32; ++k) {
             if (v[k] < 0) continue;
             const int32_t pg = (int32_t)((uint32_t)(v[k] - lo) >> kPageShift);
+            if (pg == last_pg) continue;
+            last_pg = pg;
             uint32_t h = ((uint32_t)pg * 0x9E3779B1u) >> 26;  // 6 bits: kPageSlots slots
             bool placed = false;
             for (int probe = 0; probe < kPageSlots && !placed; ++probe) {
@@ -974,14 +979,19 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
             }
             __syncthreads();
             // position: page rank * kPageRows + the row's offset in its page
+            int32_t run_pg = -1, run_rank = 0;
 #pragma unroll
             for (int k = 0; k < 32; ++k) {
                 if (v[k] < 0) continue;
                 const uint32_t d = (uint32_t)(v[k] - lo);
                 const int32_t pg = (int32_t)(d >> kPageShift);
-                uint32_t h = ((uint32_t)pg * 0x9E3779B1u) >> 26;
-                for (int probe = 0; probe < kPageSlots && s_pkey[h] != pg; ++probe) h = (h + 1) & (kPageSlots - 1);
-                v[k] = (s_prank[h] << kPageShift) | (int32_t)(d & (kPageRows - 1));
+                if (pg != run_pg) {
+                    uint32_t h = ((uint32_t)pg * 0x9E3779B1u) >> 26;
+                    for (int probe = 0; probe < kPageSlots && s_pkey[h] != pg; ++probe) h = (h + 1) & (kPageSlots - 1);
+                    run_pg = pg;
+                    run_rank = s_prank[h];
+                }
+                v[k] = (run_rank << kPageShift) | (int32_t)(d & (kPageRows - 1));
             }
         }
     }
