@@ -19,7 +19,9 @@
 //   4. query  : one row per lane for the dense tables (below), else R rows
 //               per block staged in LDS, one (row, k) entry per lane;
 //               coalesced map writes; neighbours outside the bbox (including
-//               negative ones) are rejected before probing
+//               negative ones) are rejected before probing. A dense grid
+//               over rows in no particular order is swept in cell order
+//               instead (sweep_grid)
 //
 // Linear probing over a power-of-two table with >= 2 slots per row; every
 // probe loop is bounded by the table capacity.
@@ -400,7 +402,8 @@ __global__ __launch_bounds__(256) void nm_insert_kernel(const int4 *__restrict__
         if (p.mode == 4) {
             // cells hold ~row and start at 0 (empty): the unsigned maximum keeps
             // the lowest row, and an empty cell decodes as ~0 = -1
-            atomicMax(&grid[pack_key(p, c.x, c.y, c.z, c.w)], ~(uint32_t)r);
+            const uint32_t old = atomicMax(&grid[pack_key(p, c.x, c.y, c.z, c.w)], ~(uint32_t)r);
+            if (old != 0u) atomicOr(&h->status, kStatusDupCell);
             continue;
         }
         if (p.mode == 3) {
@@ -512,15 +515,167 @@ __device__ inline void query_dense(const int4 *s_coord, const int *s_off, const 
 constexpr int kCellwiseMaxK = 32;
 constexpr int kCellChunk = 27;
 
+// Grid sweep (below): per wave, a ring of (cell, row) entries (< 64 left
+// over + 64 appended) and results for 64 entries.
+constexpr int kSweepRing = 128;
+
+// LDS of the sweep (3x3x3 kernels), in ints: per wave, [entry][27] results,
+// then the ring's cells and rows.
+constexpr int kSweepLdsInts = 4 * (64 * 27 + 2 * kSweepRing);
+
 // Dynamic LDS of the query kernel, in ints: the larger of the row-wise
-// results (rows x K) and the entry-wise staging (3 + 1 ints per offset, then
-// 4 + 1 ints per row).
+// results (rows x K, or the grid sweep's) and the entry-wise staging (3 + 1
+// ints per offset, then 4 + 1 ints per row).
 inline int query_lds_ints(int64_t K, int rows_per_block)
 {
     const int kst = K <= kMaxStagedOffsets ? (int)K : 0;
     const int staged = 4 * kst + 5 * kMaxStagedRows;
-    const int rowwise = K <= kCellwiseMaxK ? rows_per_block * (int)K : 0;
+    int rowwise = K <= kCellwiseMaxK ? rows_per_block * (int)K : 0;
+    if (K == 27 && rows_per_block == 256 && kSweepLdsInts > rowwise) rowwise = kSweepLdsInts;
     return staged > rowwise ? staged : rowwise;
+}
+
+// Dense grid over rows in no particular order (sorted rows take the rank
+// bitmap), 3x3x3 kernels. Row by row, the lookups would go to random cells,
+// a few cache lines per row, so the query sweeps the grid in cell order
+// instead. Each wave takes a contiguous range of cells (XCD-aware, so an
+// XCD's waves cover one region of the grid) in units of 64 cells, one per
+// lane, four units per step with the next four in flight; the occupied cells
+// of query rows are appended, in cell order, to the wave's ring of (cell,
+// row) entries in LDS. Each time it holds 64 entries, one per lane, they are
+// mapped: an entry's 27 neighbour lookups fall in the cache lines of nearby
+// entries' lookups; the results go through LDS ([entry][27]) and leave as
+// runs of 27 consecutive ints, the rows' map rows. Waves need no barrier,
+// only their own LDS order. A cell names one row, so duplicate coords
+// (flagged by the insert) take the row-wise query instead.
+__device__ inline void wave_lds_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The 3x3x3 path: each entry's 27 neighbour cells come from its coord's
+// per-axis up / down flags and the kernel axes' cell deltas (no offset table
+// reads), and all 27 lookups are in flight together.
+__device__ inline void sweep_map_entries(const Plan &p, const Cube3 &cube, const __amdgpu_buffer_rsrc_t rt,
+                                         const int *s_cell, const int *s_rrow, int *s_val, uint32_t head,
+                                         int cnt, int32_t *__restrict__ map)
+{
+    constexpr int K = 27;
+    const int lane = (int)threadIdx.x & 63;
+    if (lane < cnt) {
+        const uint32_t ez = (uint32_t)p.ext[3], ey = (uint32_t)p.ext[2], ex = (uint32_t)p.ext[1];
+        const uint32_t cell = (uint32_t)s_cell[(head + lane) & (kSweepRing - 1)];
+        const uint32_t line = cell / ez, cz = cell - line * ez;
+        const uint32_t xy = line / ey, cy = line - xy * ey, cx = xy % ex;
+        const int4 c = make_int4(0, p.lo[1] + (int)cx, p.lo[2] + (int)cy, p.lo[3] + (int)cz);
+        bool up[3], dn[3];
+        cube3_flags(c, cube, up, dn);
+        uint32_t raw[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            bool inside;
+            const uint32_t q = neighbour_cell<true>(k, c, true, cell, up, dn, cube, p, nullptr, inside);
+            raw[k] = bload4(rt, cell_offset<false>(q, inside));
+        }
+#pragma unroll
+        for (int k = 0; k < K; ++k) s_val[lane * K + k] = decode_grid(raw[k]);
+    }
+    wave_lds_sync();
+    const int n_ent = cnt * K;
+    int r = lane / K, k = lane % K;
+    constexpr int step_r = 64 / K, step_k = 64 % K;
+#pragma unroll 4
+    for (int i = lane; i < n_ent; i += 64) {
+        map[(int64_t)s_rrow[(head + r) & (kSweepRing - 1)] * K + k] = s_val[i];
+        r += step_r;
+        k += step_k;
+        if (k >= K) {
+            k -= K;
+            ++r;
+        }
+    }
+    wave_lds_sync();
+}
+
+__device__ inline void sweep_grid(const Plan &p, const Cube3 &cube, int64_t q_rows,
+                                  const uint64_t *__restrict__ table, uint32_t table_bytes, int *s_dyn,
+                                  int32_t *__restrict__ map)
+{
+    const __amdgpu_buffer_rsrc_t rt = cell_table_rsrc(table, table_bytes);
+    const int lane = (int)threadIdx.x & 63, wave = uniform_i32((int)threadIdx.x >> 6);
+    int *s_val = s_dyn + wave * (64 * 27 + 2 * kSweepRing);
+    int *s_cell = s_val + 64 * 27;
+    int *s_rrow = s_cell + kSweepRing;
+    // total <= 2^32 - 2 cells (dense-grid budget), and table_bytes < 3 GiB
+    // keeps every cell's byte offset in 32 bits
+    const uint64_t total = p.total, n_waves = (uint64_t)gridDim.x * 4;
+    const uint64_t per = (total + n_waves - 1) / n_waves;
+    const uint64_t gw = (uint64_t)tile_for_block((int)blockIdx.x, (int)gridDim.x) * 4 + wave;
+    const uint32_t c0 = (uint32_t)min(gw * per, total), c1 = (uint32_t)min(gw * per + per, total);
+    // Units go in groups of four: a group's cells are read (waited for)
+    // before the next group's loads issue, and the next group's loads are in
+    // flight while this group's entries are mapped. (A wait for a load issued
+    // before the map stores would also wait for those stores.)
+    constexpr int kGroup = 4;
+    uint32_t g[kGroup];
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u) {
+        const uint32_t c = c0 + 64u * u + lane;
+        g[u] = bload4(rt, c < c1 ? c << 2 : kOobOffset);
+    }
+    uint32_t head = 0, tail = 0;
+    for (uint32_t base = c0; base < c1; base += 64u * kGroup) {
+        int32_t row[kGroup];
+        bool occ[kGroup];
+        uint64_t m[kGroup];
+#pragma unroll
+        for (int u = 0; u < kGroup; ++u) {
+            row[u] = decode_grid(g[u]);
+            occ[u] = g[u] != 0u && (int64_t)row[u] < q_rows;  // 0 beyond the range
+            m[u] = __ballot(occ[u]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < kGroup; ++u) {
+            const uint64_t c = (uint64_t)base + 64u * (kGroup + u) + lane;
+            g[u] = bload4(rt, c < c1 ? (uint32_t)c << 2 : kOobOffset);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // one unit per step, its values in slot 0 (the others move down), so
+        // that the mapping step appears once in the code
+#pragma unroll 1
+        for (int u = 0; u < kGroup; ++u) {
+            const uint32_t ub = base + 64u * u;
+            if (ub >= c1) break;
+            const bool o = occ[0];
+            const int32_t r0 = row[0];
+            const uint64_t mu = m[0];
+#pragma unroll
+            for (int i = 0; i + 1 < kGroup; ++i) {
+                occ[i] = occ[i + 1];
+                row[i] = row[i + 1];
+                m[i] = m[i + 1];
+            }
+            if (o) {
+                const uint32_t e = (tail + __builtin_amdgcn_mbcnt_hi((uint32_t)(mu >> 32),
+                                                                     __builtin_amdgcn_mbcnt_lo((uint32_t)mu, 0u))) &
+                                   (kSweepRing - 1);
+                s_cell[e] = (int)(ub + lane);
+                s_rrow[e] = r0;
+            }
+            tail += (uint32_t)__popcll(mu);
+            wave_lds_sync();
+            // map 64 entries at a time; after the range's last cells, the rest
+            const bool last = (uint64_t)ub + 64u >= c1;
+            while (tail - head >= 64u || (last && tail != head)) {
+                const int cnt = (int)min(tail - head, 64u);
+                sweep_map_entries(p, cube, rt, s_cell, s_rrow, s_val, head, cnt, map);
+                head += (uint32_t)cnt;
+            }
+        }
+    }
 }
 
 // Rank bitmap with octree levels on the 3x3x3 path: the key (rank_key) is
@@ -625,7 +780,7 @@ __device__ inline void query_cells(const int4 *__restrict__ coords, int64_t row0
     }
 }
 
-__global__ __launch_bounds__(256) void nm_query_kernel(const int4 *__restrict__ coords,
+__global__ __launch_bounds__(256) void nm_query_kernel(const int4 *__restrict__ coords, int64_t n_rows,
                                                        int64_t q_rows, KernelShape ks,
                                                        int rows_per_block,
                                                        const NbrHeader *__restrict__ h,
@@ -660,6 +815,11 @@ __global__ __launch_bounds__(256) void nm_query_kernel(const int4 *__restrict__ 
     const bool rowwise = cellwise && ks.K <= kCellwiseMaxK && rows_per_block == (int)blockDim.x &&
                          tbytes <= kOobOffset && (!levels || cube3);
     int32_t *out = map + row0 * ks.K;
+    // the sweep covers every cell, so it pays when most rows are queried
+    if (rowwise && cube3 && p.mode == 4 && !(h->status & kStatusDupCell) && 2 * q_rows >= n_rows) {
+        sweep_grid(p, cube3_of(ks, p), q_rows, keys, (uint32_t)tbytes, s_dyn, map);
+        return;
+    }
     if (rowwise) {
         const Cube3 cube = cube3_of(ks, p);
         if (levels)
@@ -853,7 +1013,7 @@ int sc_neighbor_map_build(const sc_conv_config *cfg, const int32_t *d_coords, in
     const int64_t blocks = (query_rows + rpb - 1) / rpb;
     if (blocks > INT32_MAX) return fail(SC_ERR_OVERFLOW, "neighbor map grid overflow");
     const size_t lds = (size_t)query_lds_ints(K, rpb) * sizeof(int);
-    nm_query_kernel<<<(unsigned)blocks, 256, lds, s>>>(c4, query_rows, ks, rpb, h, keys, rows, cap - 1,
+    nm_query_kernel<<<(unsigned)blocks, 256, lds, s>>>(c4, n_rows, query_rows, ks, rpb, h, keys, rows, cap - 1,
                                                        otab, d_map);
     SC_LAUNCH_CHECK("nm_query_kernel launch");
     return SC_OK;

@@ -10,6 +10,9 @@ namespace nbr {
 constexpr size_t kHeaderBytes = 256;
 constexpr uint64_t kEmpty64 = ~0ull;
 constexpr uint32_t kStatusNegative = 1u;
+// Dense grid: some cell received more than one row (duplicate coords). Not an
+// error; the query then maps row by row, since the grid names one row per cell.
+constexpr uint32_t kStatusDupCell = 2u;
 constexpr int kMaxStagedOffsets = 512;
 
 // Table budgets, in bbox cells, that the workspace affords: the dense grid

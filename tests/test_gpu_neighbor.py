@@ -355,3 +355,51 @@ def test_rank_bitmap_small_dense_bboxes(oracle, kernel, seed):
     got, mode = _map_and_mode(cfg, c)
     assert mode == "rank_bitmap"
     assert np.array_equal(got, oracle.build_neighbor_rows(ocfg(oracle, cfg), c))
+
+
+@pytest.mark.parametrize("kernel", [(3, 3, 3), (3, 3, 1), (1, 1, 1), (2, 2, 2), (1, 3, 5), (5, 5, 5)])
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_dense_grid_sweep_shuffled(oracle, kernel, seed):
+    """Unique coords in a random row order take the dense grid, whose query
+    sweeps the grid's cells (64 cells of a z line per wave unit) and writes
+    each row's map row through LDS: z extents below, at and across 64 cells,
+    several batches, every axis order and sign draw, and partial queries on
+    both sides of the sweep's half-the-rows threshold, against the oracle.
+    K = 125 exceeds the sweep's 32 entries and takes the per-entry query."""
+    rng = np.random.default_rng(200 + seed)
+    ext = np.array([rng.integers(1, 9), rng.integers(1, 9), [1, 64, 97][seed]])
+    cells = np.stack(np.meshgrid(*[np.arange(e) for e in ext], indexing="ij"), -1).reshape(-1, 3)
+    parts = []
+    for b in range(1 + seed):
+        keep = rng.random(len(cells)) < rng.uniform(0.2, 0.9)
+        c = np.zeros((int(keep.sum()), 4), np.int32)
+        c[:, 0] = 2 * b
+        c[:, 1:] = cells[keep] + rng.integers(0, 4, 3)
+        parts.append(c)
+    c = np.concatenate(parts)
+    c = c[rng.permutation(len(c))]
+    order = tuple(int(v) for v in rng.permutation(3))
+    sign = tuple(int(v) for v in rng.choice([-1, 1], 3))
+    cfg = F.SparseSubmConvConfig(1, 1, *kernel, axis_order=order, axis_sign=sign)
+    exp = oracle.build_neighbor_rows(ocfg(oracle, cfg), c)
+    got, mode = _map_and_mode(cfg, c)
+    assert mode == "dense_grid"
+    assert np.array_equal(got, exp)
+    for q in (len(c) * 3 // 5, len(c) // 3, 1):
+        got, mode = _map_and_mode(cfg, c, query_rows=q)
+        assert mode == "dense_grid"
+        assert np.array_equal(got, exp[:q]), q
+
+
+def test_dense_grid_sweep_duplicates_fall_back(oracle):
+    """Shuffled coords with duplicated cells: the grid names each cell's
+    lowest row, so the query maps row by row and every duplicate row gets
+    its own map row."""
+    rng = np.random.default_rng(5)
+    c = np.zeros((30000, 4), np.int32)
+    c[:, 1:] = rng.integers(0, 48, (30000, 3))
+    assert len(np.unique(c, axis=0)) < len(c)
+    cfg = F.SparseSubmConvConfig(1, 1)
+    got, mode = _map_and_mode(cfg, c)
+    assert mode == "dense_grid"
+    assert np.array_equal(got, oracle.build_neighbor_rows(ocfg(oracle, cfg), c))
