@@ -1257,14 +1257,13 @@ __global__ __launch_bounds__(kThreads) void child_chunk_kernel(ChildArgs a)
 }
 
 // One workgroup: the group totals scanned (loops of 256 groups), the
-// children's tile ranges, the header, tile_child.  A parent plan of
+// children's tile ranges and the header (tile_child is the pad pass's).  A parent plan of
 // another size or more active children than the list tiles hold flags the
 // status; every tile is then empty.
 __global__ __launch_bounds__(kThreads) void child_layout_kernel(ChildArgs a)
 {
     __shared__ int s[kThreads][8];
     __shared__ int64_t s_base[9];
-    __shared__ int s_ok;
     int run[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     for (int64_t k0 = 0; k0 < a.n_chunks; k0 += kThreads) {
         const int64_t k = k0 + threadIdx.x;
@@ -1286,7 +1285,6 @@ __global__ __launch_bounds__(kThreads) void child_layout_kernel(ChildArgs a)
         }
         s_base[8] = base;
         const bool ok = base <= a.n_main && a.phdr->n_q == a.n_parents && a.phdr->K == a.K;
-        s_ok = ok;
         for (int c = 0; c < 8; ++c) {
             a.child_n[c] = ok ? run[c] : 0;
             a.child_base[c] = ok ? (int32_t)s_base[c] : 0;
@@ -1306,15 +1304,6 @@ __global__ __launch_bounds__(kThreads) void child_layout_kernel(ChildArgs a)
         h->n_extras = 0;                       // splits (the split pass sets it)
         h->list_tiles = (int32_t)a.n_main;     // spare tiles from here
         *a.split_n = 0;
-    }
-    __syncthreads();
-    const bool ok = s_ok != 0;
-    for (int64_t t = threadIdx.x; t < a.n_tiles; t += kThreads) {
-        int ct = -1;
-        if (ok)
-            for (int c = 0; c < 8; ++c)
-                if (t >= s_base[c] && t < s_base[c + 1]) ct = c;
-        a.tile_child[t] = ct;
     }
 }
 
@@ -1344,12 +1333,22 @@ __global__ __launch_bounds__(kThreads) void child_emit_kernel(ChildArgs a)
     }
 }
 
-// -1 in every order slot no entry takes: past a child's entries in its last
-// tile, and every unused tile (all of them when the build was refused).
+// Per tile: its child (tile_child; -1 past the list tiles in use, and for
+// every tile when the build was refused), and -1 in every order slot no entry
+// takes: past a child's entries in its last tile, and every unused tile.
 __global__ __launch_bounds__(kThreads) void child_pad_kernel(ChildArgs a)
 {
     const int64_t t = blockIdx.x;
-    const int c = a.tile_child[t];
+    int c = -1;
+    if (a.hdr->status == 0u) {
+        const int64_t n_used = a.hdr->n_unique;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int64_t hi = k < 7 ? (int64_t)a.child_base[k + 1] : n_used;
+            if (t >= a.child_base[k] && t < hi) c = k;
+        }
+    }
+    if (threadIdx.x == 0) a.tile_child[t] = c;
     const int64_t i = t * kPlanTileRows + threadIdx.x;
     bool pad = c < 0;
     if (!pad) pad = i >= (int64_t)a.child_base[c] * kPlanTileRows + a.child_n[c];
@@ -1437,26 +1436,32 @@ __global__ __launch_bounds__(kPlanTileRows / 2) void child_move_kernel(ChildArgs
 }
 
 // The overflow list rebuilt in tile order (tiles whose halo still overflows
-// after the splits, or that found no spare).
+// after the splits, or that found no spare). Only the tiles in use can: the
+// list tiles [0, n_unique) and the spares taken, [n_main, n_main + n_extras)
+// (none when the build was refused), walked as one index range.
 __global__ __launch_bounds__(kListThreads) void child_overflow_kernel(ChildArgs a)
 {
     __shared__ int s_wave[kListThreads / 64];
+    const int64_t n_used = a.hdr->status == 0u ? a.hdr->n_unique : 0;
+    const int64_t n_live = n_used + (a.hdr->status == 0u ? a.hdr->n_extras : 0);
     int64_t done = 0;
-    for (int64_t t0 = 0; t0 < a.n_tiles; t0 += kListThreads * kListPer) {
-        const int64_t tb = t0 + (int64_t)threadIdx.x * kListPer;
+    for (int64_t v0 = 0; v0 < n_live; v0 += kListThreads * kListPer) {
+        const int64_t vb = v0 + (int64_t)threadIdx.x * kListPer;
         bool f[kListPer];
+        int64_t tt[kListPer];
         int cnt = 0;
 #pragma unroll
         for (int u = 0; u < kListPer; ++u) {
-            const int64_t t = tb + u;
-            f[u] = t < a.n_tiles && a.tile_child[t] >= 0 && a.tile_u[t] > kPlanHaloMax;
+            const int64_t v = vb + u;
+            tt[u] = v < n_used ? v : a.n_main + (v - n_used);
+            f[u] = v < n_live && a.tile_child[tt[u]] >= 0 && a.tile_u[tt[u]] > kPlanHaloMax;
             cnt += f[u];
         }
         int total;
         int64_t j = done + list_scan_excl(cnt, s_wave, total);
 #pragma unroll
         for (int u = 0; u < kListPer; ++u)
-            if (f[u]) a.overflow[j++] = (int32_t)(tb + u);
+            if (f[u]) a.overflow[j++] = (int32_t)tt[u];
         done += total;
     }
     if (threadIdx.x == 0) a.hdr->n_overflow = (int32_t)done;

@@ -23,7 +23,7 @@ namespace sc {
 namespace {
 
 constexpr int kThreads = 256;               // parents per round
-constexpr int64_t kMaxBlocks = 1024;         // blocks while rounds stay under kMaxRounds
+constexpr int64_t kMaxBlocks = 4096;         // blocks while rounds stay under kMaxRounds
 constexpr int64_t kMaxRounds = 64;
 
 struct Thresholds {
@@ -99,6 +99,7 @@ __global__ __launch_bounds__(kThreads) void subdiv_emit_kernel(const float *logi
     __shared__ int s_wave[kThreads / 64];
     __shared__ int s_pre[kThreads];
     __shared__ uint8_t s_m[kThreads];
+    __shared__ int4 s_pc[kThreads];
     __shared__ int64_t s_sum[kThreads / 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // the block's first output row: the counts of the blocks before it
@@ -115,6 +116,9 @@ __global__ __launch_bounds__(kThreads) void subdiv_emit_kernel(const float *logi
         const int64_t p0 = base + (int64_t)r * kThreads;
         const int64_t p = p0 + tid;
         const unsigned m = p < P ? child_mask(logits, mask, th, p) : 0u;
+        // the round's parent coords, fetched with the masks (the emit loop
+        // then reads them from LDS, not through a dependent global load)
+        s_pc[tid] = p < P ? parent_coords[p] : make_int4(0, 0, 0, 0);
         int total;
         const int ex = block_exclusive_scan(__popc(m), s_wave, total);
         if (child_rows && p < P) {
@@ -147,14 +151,14 @@ __global__ __launch_bounds__(kThreads) void subdiv_emit_kernel(const float *logi
                     --k;
                 }
             const int64_t pp = p0 + lo, row = out + j;
-            const int4 pc = parent_coords[pp];
+            const int4 pc = s_pc[lo];
             child_coords[row] = make_int4(pc.x, 2 * pc.y + (c & 1), 2 * pc.z + ((c >> 1) & 1),
                                           2 * pc.w + ((c >> 2) & 1));
             linear_idx[row] = (int32_t)(pp * 8 + c);
             if (pairs) pairs[row] = make_int2((int32_t)pp, c);
         }
         out += total;
-        __syncthreads();  // s_pre / s_m are rewritten by the next round
+        __syncthreads();  // s_pre / s_m / s_pc are rewritten by the next round
     }
     if (blockIdx.x == gridDim.x - 1 && tid == 0) *count = out;
 }
