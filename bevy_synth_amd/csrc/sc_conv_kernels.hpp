@@ -1187,6 +1187,10 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
     __shared__ __attribute__((aligned(16))) uint16_t s_lmap[kHaloK][2][16][8];
     __shared__ uint32_t s_hoff[kPlanHaloMax];
     __shared__ uint32_t s_wmask[kThreads / 64];
+    // fetched in the prologue's round trip for the epilogue: the tile's
+    // output rows (the plan order) and its channels' bias and int8 scale
+    __shared__ int32_t s_order[kPlanTileRows];
+    __shared__ float s_bias[kNT], s_scale[kNT];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -1252,6 +1256,14 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
         for (int k = 0; k < kHaloK; ++k) jv[k] = k < K ? src[k * kPlanTileRows] : (uint32_t)kPlanAbsent;
 #pragma unroll
         for (int u = 0; u < kHPer; ++u) hv[u] = tid + u * kThreads < U ? hrows[tid + u * kThreads] : 0;
+        const int32_t ord = plan.order[(int64_t)tile * kPlanTileRows + tid];
+        float bv = 0.f, sv = 1.f;
+        if (tid < kNT) {
+            const int o = o0 + tid;
+            const bool ok = o < args.cout_g;
+            if (args.bias && ok) bv = args.bias[out_col0 + o];
+            if (args.w_scale && ok) sv = args.w_scale[out_col0 + o];  // int8 weights
+        }
         uint16_t *dst = &s_lmap[0][tid >> 7][tid & 15][(tid >> 4) & 7];
         uint32_t m = 0;
 #pragma unroll
@@ -1269,6 +1281,11 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
 #pragma unroll
         for (int u = 0; u < kHPer; ++u)
             if (tid + u * kThreads < U) s_hoff[tid + u * kThreads] = (uint32_t)hv[u] * row_bytes;
+        s_order[tid] = ord;
+        if (tid < kNT) {
+            s_bias[tid] = bv;
+            s_scale[tid] = sv;
+        }
     }
     __syncthreads();
     const uint32_t tmask = __builtin_amdgcn_readfirstlane(s_wmask[0] | s_wmask[1] | s_wmask[2] | s_wmask[3]);
@@ -1496,8 +1513,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
         for (int e = 0; e < 4; ++e) {
             const int o = oc0 + j * 16 + 4 * q4 + e;
             const bool ok = o < args.cout_g;
-            const float bias = (args.bias && ok) ? args.bias[out_col0 + o] : 0.f;
-            const float scale = (args.w_scale && ok) ? args.w_scale[out_col0 + o] : 1.f;  // int8 weights
+            const float bias = s_bias[o - o0], scale = s_scale[o - o0];
 #pragma unroll
             for (int i = 0; i < kI; ++i)
                 acc[i][j][e] = ok ? acc[i][j][e] * scale + bias : 0.f;
@@ -1583,7 +1599,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
     int32_t qrow[kI];
 #pragma unroll
     for (int i = 0; i < kI; ++i) {
-        const int32_t q = plan.order[(int64_t)tile * kPlanTileRows + row0 + 16 * i + l16];
+        const int32_t q = s_order[row0 + 16 * i + l16];
         qrow[i] = q < args.n_q ? q : -1;  // -1 pads the order; nothing past n_q is written
     }
     if (args.scatter_rows || args.skip_idx) {
