@@ -62,6 +62,19 @@ inline uint64_t table_capacity(int64_t n)
     return cap;
 }
 
+inline uint64_t dense_cells_for(int64_t n);
+
+// Slots the hash modes use: at least table_capacity, and as many as the
+// table region of the minimal workspace holds at 12 bytes per slot (5-10 per
+// row), which keeps the brick-local probe runs short.
+inline uint64_t table_slots(int64_t n)
+{
+    uint64_t cap = table_capacity(n);
+    const uint64_t room = dense_cells_for(n) * 4u / 12u;
+    while (cap * 2 <= room) cap <<= 1;
+    return cap;
+}
+
 // Dense-grid budget: 32 cells per row (at least 2^16 cells).
 inline uint64_t dense_cells_for(int64_t n)
 {
@@ -336,7 +349,10 @@ __global__ __launch_bounds__(256) void nm_plan_init_kernel(const int32_t *__rest
         }
     }
     if (p.mode == 0) return;
-    uint64_t n_words = cap + cap / 2, fill = kEmpty64;
+    // hash modes: mode 1 uses the packed key slots [0, cap), mode 3 the row
+    // slots (words [cap, cap + cap / 2)), mode 2 both
+    uint64_t w0 = p.mode == 3 ? cap : 0;
+    uint64_t n_words = p.mode == 1 ? cap : cap + cap / 2, fill = kEmpty64;
     if (p.mode == 4) {
         n_words = (p.total + 1) / 2;
         fill = 0;
@@ -346,7 +362,8 @@ __global__ __launch_bounds__(256) void nm_plan_init_kernel(const int32_t *__rest
         fill = 0;
     }
     const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_words; i += stride) words[i] = fill;
+    if (p.mode == 4 || p.mode == 5) w0 = 0;
+    for (uint64_t i = w0 + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_words; i += stride) words[i] = fill;
 }
 
 __global__ __launch_bounds__(256) void nm_insert_kernel(const int4 *__restrict__ coords, int64_t n,
@@ -972,7 +989,7 @@ int sc_neighbor_map_build(const sc_conv_config *cfg, const int32_t *d_coords, in
     // Workspace: [header 256 B][bbox partials][offset table][hash table, grid or bitmap].
     NbrHeader *h = (NbrHeader *)d_workspace;
     int32_t *partials = (int32_t *)((char *)d_workspace + kHeaderBytes);
-    const uint64_t cap = table_capacity(n_rows);
+    const uint64_t cap = table_slots(n_rows);
     int4 *otab = (int4 *)((char *)d_workspace + kHeaderBytes + kPartialBytes);
     uint64_t *keys = (uint64_t *)((char *)d_workspace + kFixedBytes);
     uint32_t *rows = (uint32_t *)(keys + cap);
