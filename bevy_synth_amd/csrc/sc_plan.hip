@@ -862,7 +862,10 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
     const int lane = p & 63, wave = p >> 6;
     const int K = a.K;
     const int32_t n_in = (int32_t)a.n_in;  // <= INT32_MAX
-    const int32_t q = a.order[t * kPlanTileRows + p];
+    // rows that keep their own order (grid_mode 2): order[i] = i, so the
+    // tile's rows need no read before their map rows
+    const int64_t slot = t * kPlanTileRows + p;
+    const int32_t q = a.hdr->grid_mode == 2 ? (slot < a.n_q ? (int32_t)slot : -1) : a.order[slot];
     // A tile of padding only (a child plan's unused list and spare tiles)
     // records an empty halo and writes nothing else: no conv reads the
     // other tables of such a tile.
