@@ -32,7 +32,7 @@ EXPORTED = (
     "sc_subdivision_build_static", "sc_conv_plan_check", "sc_conv_epilogue_workspace_size",
     "sc_subdivision_build_indexed", "sc_linear_skinny", "sc_linear_forward",
     "sc_subdivision_logits_finish", "sc_conv_child_plan_size", "sc_conv_child_plan_build",
-    "sc_subm_conv_forward_child_planned",
+    "sc_subm_conv_forward_child_planned", "sc_linear_child_plan_build", "sc_linear_forward_child_planned",
 )
 
 
@@ -137,6 +137,9 @@ def load() -> ctypes.CDLL:
     L.sc_conv_child_plan_build.argtypes = [cfgp, P, P, i64, P, i64, P, ctypes.c_size_t, P]
     L.sc_subm_conv_forward_child_planned.argtypes = [cfgp, i32, P, i64, P, i64, i32, P, P, P, P,
                                                      ctypes.POINTER(ScConvEpilogue), i32, P, P, P]
+    L.sc_linear_child_plan_build.argtypes = [i64, P, i64, P, ctypes.c_size_t, P]
+    L.sc_linear_forward_child_planned.argtypes = [i32, P, i64, i64, i64, i32, P, P, P,
+                                                  ctypes.POINTER(ScConvEpilogue), i32, P, P, P]
     L.sc_subdivision_build_static.argtypes = [P, P, P, P, i64, P, P, P, P, P]
     L.sc_gather_rows.argtypes = [i32, P, i64, i64, i64, P, i64, P, P]
     L.sc_c2s_skip_add.argtypes = [i32, P, i64, i64, i32, P, i64, i64, P, P]

@@ -255,12 +255,18 @@ static int conv_forward_impl(const sc_conv_config *cfg, int act_dtype, const voi
     if (d_wpack && (uintptr_t)d_wpack % 16 != 0)
         return fail(SC_ERR_SHAPE, "packed weights must be 16-byte aligned");
     const void *plan = (d_plan && (act_bf16 || act_f16) && mfma && K <= kHaloK) ? d_plan : nullptr;
-    if (child_plan) {
+    if (child_plan && !dense) {
         // a child plan's tiles hold parents, not query rows: only the
         // halo-staged kernel on packed weights can run it
         if (!plan || !d_wpack || groups != 1)
             return fail(SC_ERR_UNSUPPORTED, "sparse conv child plan needs 16-bit activations, packed weights, "
                                             "one group and a kernel of at most 27 offsets");
+    }
+    if (child_plan && dense) {
+        // a linear child plan: only the dense MFMA tile on 16-bit weights runs it
+        if (!plan || w_dtype == SC_DTYPE_I8 || cfg->in_channels % 32 != 0 || c2s.scatter_ch % 128 != 0)
+            return fail(SC_ERR_UNSUPPORTED, "linear child plan needs 16-bit activations and weights, input channels "
+                                            "a multiple of 32 and children of a multiple of 128 channels");
     }
     int rc2 = launch_conv_typed(a, act_f32, w_dtype, conv_out_dtype, groups, mfma, plan, s);
     if (rc2 != SC_OK || !split_ln) return rc2;
@@ -320,6 +326,34 @@ extern "C" int sc_linear_forward(int act_dtype, const void *d_input, int64_t row
     c.axis_sign[0] = c.axis_sign[1] = c.axis_sign[2] = 1;
     return conv_forward_impl(&c, act_dtype, d_input, rows, nullptr, rows, w_dtype, d_weight, d_w_scale, d_bias,
                              epi, out_dtype, d_out, nullptr, nullptr, stream, true);
+}
+
+extern "C" int sc_linear_forward_child_planned(int act_dtype, const void *d_input, int64_t rows,
+                                               int64_t in_channels, int64_t out_channels, int w_dtype,
+                                               const void *d_weight, const float *d_w_scale, const float *d_bias,
+                                               const sc_conv_epilogue *epi, int out_dtype, void *d_out,
+                                               const void *d_child_plan, sc_stream stream)
+{
+    clear_error();
+    if (!epi || !epi->child_rows)
+        return fail(SC_ERR_NULL, "linear child plan: the epilogue's child_rows (the child scatter) is required");
+    if (epi->skip_index)
+        return fail(SC_ERR_UNSUPPORTED, "linear: the parent skip belongs to the sparse conv");
+    if (!d_child_plan) return fail(SC_ERR_NULL, "linear child plan: NULL plan");
+    if ((uintptr_t)d_child_plan % 256 != 0) return fail(SC_ERR_WORKSPACE, "conv plans must be 256-byte aligned");
+    sc_conv_config c{};
+    c.in_channels = in_channels;
+    c.out_channels = out_channels;
+    c.kernel_d = c.kernel_h = c.kernel_w = 1;
+    c.in_channels_per_group = in_channels;
+    c.out_channels_per_group = out_channels;
+    c.groups = 1;
+    c.axis_order[0] = 0;
+    c.axis_order[1] = 1;
+    c.axis_order[2] = 2;
+    c.axis_sign[0] = c.axis_sign[1] = c.axis_sign[2] = 1;
+    return conv_forward_impl(&c, act_dtype, d_input, rows, nullptr, rows, w_dtype, d_weight, d_w_scale, d_bias,
+                             epi, out_dtype, d_out, d_child_plan, nullptr, stream, true, true);
 }
 
 extern "C" int sc_subm_conv_forward_planned(const sc_conv_config *cfg, int act_dtype,

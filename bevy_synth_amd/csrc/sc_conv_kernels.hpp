@@ -1701,7 +1701,11 @@ struct DenseShape {
     static constexpr int kBlocksPerCU = kQ == 2 ? 2 : 1;
 };
 
-template <typename TA, typename TO, bool kLN, int kQ, bool kStaged>
+// kListed: the rows come from a linear child plan (sc_linear_child_plan_build):
+// tile t holds up to 256 parents whose child tile_child[t] is active (perm, -1
+// pads), and computes only that child's channels, so inactive children cost
+// nothing; a row's values are the same sums as without the plan.
+template <typename TA, typename TO, bool kLN, int kQ, bool kStaged, bool kListed = false>
 __global__ __launch_bounds__(DenseShape<kQ>::kThreads, DenseShape<kQ>::kBlocksPerCU) void dense_gemm_kernel(
     ConvArgs args)
 {
@@ -1717,6 +1721,7 @@ __global__ __launch_bounds__(DenseShape<kQ>::kThreads, DenseShape<kQ>::kBlocksPe
     static_assert(kAInstr * 1024 * S::kWaves == kRowsBytes && kWInstr * 1024 * S::kWaves == kWBytes, "DMA split");
     __shared__ __attribute__((aligned(16))) unsigned char s_buf[kBuf * kStage];  // stages; then the output tile
     __shared__ float s_red[kQ][kTileRows];            // LayerNorm: per channel quarter, per tile row
+    __shared__ int32_t s_rows[kListed ? kTileRows : 1];  // listed: the tile's parents (-1: none)
     auto stage = [&](int u) -> unsigned char * { return s_buf + u * kStage; };
 
     const int tid = threadIdx.x;
@@ -1727,11 +1732,38 @@ __global__ __launch_bounds__(DenseShape<kQ>::kThreads, DenseShape<kQ>::kBlocksPe
     // of row tile b / n_ct: a row tile's column tiles run together on one
     // XCD, so its rows come from HBM once and from L2 for the other columns
     // (otherwise each column tile re-reads every row from HBM).
-    const int n_ct = (args.cout_g + S::kCols - 1) / S::kCols;
-    const int b = tile_for_block(blockIdx.x, gridDim.x);
-    const int tile = b / n_ct;
-    const int64_t trow0 = (int64_t)tile * kTileRows;  // the tile's first row
-    const int o0 = (b % n_ct) * S::kCols;             // the tile's first channel
+    int64_t trow0 = 0;  // the tile's first row (unlisted)
+    int o0;             // the tile's first channel
+    if constexpr (kListed) {
+        // the plan's list tiles in use, each with child_ch / kCols column
+        // tiles of its child, dealt to the XCDs as one range; the plan must
+        // be the one built for these parents
+        if (!plan_matches(args.plan_hdr, args) || args.plan_hdr->status != 0u) return;
+        const int n_ct = args.child_ch / S::kCols;
+        const int n_real = args.plan_hdr->n_unique * n_ct;
+        if ((int)blockIdx.x >= n_real) return;
+        const int b = tile_for_block(blockIdx.x, n_real);
+        const int lt = b / n_ct;
+        const int child = args.tile_child[lt];
+        if (child < 0) return;
+        o0 = child * args.child_ch + (b % n_ct) * S::kCols;
+        if (tid < kTileRows) {
+            const int32_t p = args.perm[(int64_t)lt * kTileRows + tid];
+            s_rows[tid] = p >= 0 && p < args.n_q ? p : -1;
+        }
+        __syncthreads();
+    } else {
+        const int n_ct = (args.cout_g + S::kCols - 1) / S::kCols;
+        const int b = tile_for_block(blockIdx.x, gridDim.x);
+        trow0 = (int64_t)(b / n_ct) * kTileRows;
+        o0 = (b % n_ct) * S::kCols;
+    }
+    // input row of tile row rl (-1: none)
+    auto tile_row = [&](int rl) -> int64_t {
+        if constexpr (kListed) return s_rows[rl];
+        const int64_t r = trow0 + rl;
+        return r < args.n_q ? r : -1;
+    };
     const int cin = (int)args.cin;
     const int nk = cin / 32;
     const i32x4_rsrc a_rsrc = rsrc_words(args.input, (uint32_t)(args.n_q * (int64_t)cin * (int64_t)sizeof(TA)));
@@ -1747,8 +1779,8 @@ __global__ __launch_bounds__(DenseShape<kQ>::kThreads, DenseShape<kQ>::kBlocksPe
     for (int t = 0; t < kAInstr; ++t) {
         const int r = 16 * (wave + S::kWaves * t) + (lane >> 2);
         const int piece = wslot<64>(r, lane & 3);
-        const int64_t row = trow0 + r;
-        a_src[t] = row < args.n_q ? (uint32_t)((row * cin + 8 * piece) * (int64_t)sizeof(TA)) : kOobOffset;
+        const int64_t row = tile_row(r);
+        a_src[t] = row >= 0 ? (uint32_t)((row * cin + 8 * piece) * (int64_t)sizeof(TA)) : kOobOffset;
     }
 #pragma unroll
     for (int t = 0; t < kWInstr; ++t) {
@@ -1844,7 +1876,6 @@ __global__ __launch_bounds__(DenseShape<kQ>::kThreads, DenseShape<kQ>::kBlocksPe
     //      quarters of a group meet in LDS), SiLU, residual, stores
     //      (row-major, or each child's slice to its row in the child scatter).
     const int oc0 = o0 + 64 * qc;
-    const int64_t row0 = trow0 + 128 * rh;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -1942,7 +1973,7 @@ __global__ __launch_bounds__(DenseShape<kQ>::kThreads, DenseShape<kQ>::kBlocksPe
 #pragma unroll
         for (int i = 0; i < kI; ++i) {
             const int rl = 128 * rh + 16 * i + l16;
-            const int64_t r = trow0 + rl;
+            const int64_t r = tile_row(rl);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
@@ -1951,7 +1982,7 @@ __global__ __launch_bounds__(DenseShape<kQ>::kThreads, DenseShape<kQ>::kBlocksPe
                     for (int cc = 0; cc < 4; ++cc) v[cc] = silu_f32(v[cc]);
                 }
                 const int oc = oc0 + j * 16 + 4 * q4;
-                if (res && r < args.n_q && oc < args.cout_g) {
+                if (res && r >= 0 && oc < args.cout_g) {
                     float r4[4];
                     Out4<TO>::unpack(*reinterpret_cast<const typename Out4<TO>::V *>(res + r * args.cout + oc), r4);
 #pragma unroll
@@ -1967,9 +1998,9 @@ __global__ __launch_bounds__(DenseShape<kQ>::kThreads, DenseShape<kQ>::kBlocksPe
         for (int it = 0; it < kTileRows * kNC / S::kThreads; ++it) {
             const int idx = it * S::kThreads + tid;
             const int rl = idx / kNC, c = idx % kNC;
-            const int64_t r = trow0 + rl;
+            const int64_t r = tile_row(rl);
             const int col = o0 + 8 * c;  // first of the piece's 8 channels
-            if (r >= args.n_q || col >= args.cout_g) continue;
+            if (r < 0 || col >= args.cout_g) continue;
             const uint4 val = *reinterpret_cast<const uint4 *>(s_buf + rl * kRB + ((c ^ (rl & (kNC - 1))) << 4));
             int64_t off;
             if (args.scatter_rows) {
@@ -1988,8 +2019,8 @@ __global__ __launch_bounds__(DenseShape<kQ>::kThreads, DenseShape<kQ>::kBlocksPe
     const bool vec_ok = args.vec_out != 0;
 #pragma unroll
     for (int i = 0; i < kI; ++i) {
-        const int64_t r = row0 + 16 * i + l16;
-        if (r >= args.n_q) continue;
+        const int64_t r = tile_row(128 * rh + 16 * i + l16);
+        if (r < 0) continue;
         const int64_t rowbase = r * args.cout;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -2219,6 +2250,33 @@ int launch_conv(const ConvArgs &a, int groups, bool mfma, const void *plan, hipS
                 // pieces aligned in the output rows, residual aligned
                 const bool staged = sizeof(TO) == 2 && a.cout % 8 == 0 && (uintptr_t)a.out % 16 == 0 &&
                                     (uintptr_t)a.residual % 16 == 0 && (!a.scatter_rows || a.scatter_ch % 8 == 0);
+                if (plan && a.child_plan) {
+                    // the transposed upsample over the active children only: a
+                    // linear child plan's list tiles (sc_linear_child_plan_build),
+                    // 128-channel column tiles of each tile's child
+                    const ChildPlanLayout CL = child_plan_layout(a.n_q, a.scatter_n, 1);
+                    const PlanView pv = child_plan_view(plan, CL);
+                    ConvArgs h = a;
+                    h.plan_hdr = pv.hdr;
+                    h.perm = pv.order;
+                    h.tile_child = pv.tile_child;
+                    const int64_t lgrid = CL.n_main * (a.child_ch / 128);
+                    if (lgrid > INT32_MAX) return fail(SC_ERR_OVERFLOW, "dense linear grid overflow");
+                    const dim3 lg((unsigned)lgrid, 1, 1);
+                    if (a.ln) {
+                        if (staged)
+                            dense_gemm_kernel<TA, TO, true, 2, sizeof(TO) == 2, true><<<lg, DenseShape<2>::kThreads, 0, s>>>(h);
+                        else
+                            dense_gemm_kernel<TA, TO, true, 2, false, true><<<lg, DenseShape<2>::kThreads, 0, s>>>(h);
+                    } else {
+                        if (staged)
+                            dense_gemm_kernel<TA, TO, false, 2, sizeof(TO) == 2, true><<<lg, DenseShape<2>::kThreads, 0, s>>>(h);
+                        else
+                            dense_gemm_kernel<TA, TO, false, 2, false, true><<<lg, DenseShape<2>::kThreads, 0, s>>>(h);
+                    }
+                    SC_LAUNCH_CHECK("dense_gemm_kernel launch (child plan)");
+                    return SC_OK;
+                }
                 if (wide_tile) {
                     if (staged)
                         dense_gemm_kernel<TA, TO, false, 4, sizeof(TO) == 2><<<dgrid, DenseShape<4>::kThreads, 0, s>>>(a);

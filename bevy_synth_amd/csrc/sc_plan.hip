@@ -1149,8 +1149,8 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
 // The plan is a pure function of the inputs (no atomics whose order shows).
 
 struct ChildArgs {
-    const PlanHeader *phdr;     // the parent plan
-    const int32_t *porder;      // its order [n_ptiles * 256]
+    const PlanHeader *phdr;     // the parent plan (NULL: parents in row order, a linear child plan)
+    const int32_t *porder;      // its order [n_ptiles * 256] (NULL: row order)
     const int32_t *child_rows;  // [P][8]: row of child (p, c), or -1
     int64_t n_parents;
     int64_t n_children;
@@ -1176,7 +1176,7 @@ struct ChildArgs {
 // children as bits (a row outside [0, n_children) counts as inactive).
 __device__ inline uint32_t child_bits(const ChildArgs &a, int64_t e, int32_t &p)
 {
-    p = a.porder[e];
+    p = a.porder ? a.porder[e] : (int32_t)e;  // no parent plan: parents in row order
     if (p < 0 || p >= a.n_parents) {
         p = -1;
         return 0u;
@@ -1287,7 +1287,7 @@ __global__ __launch_bounds__(kThreads) void child_layout_kernel(ChildArgs a)
             base += (run[c] + kPlanTileRows - 1) / kPlanTileRows;
         }
         s_base[8] = base;
-        const bool ok = base <= a.n_main && a.phdr->n_q == a.n_parents && a.phdr->K == a.K;
+        const bool ok = base <= a.n_main && (!a.phdr || (a.phdr->n_q == a.n_parents && a.phdr->K == a.K));
         for (int c = 0; c < 8; ++c) {
             a.child_n[c] = ok ? run[c] : 0;
             a.child_base[c] = ok ? (int32_t)s_base[c] : 0;
@@ -1634,6 +1634,65 @@ extern "C" int sc_conv_child_plan_size(int64_t n_parents, int64_t n_children, in
     if (kernel_rows < 1 || kernel_rows > 32)
         return fail(SC_ERR_UNSUPPORTED, "conv plan supports kernels of 1..32 offsets");
     *bytes = child_plan_layout(n_parents, n_children, kernel_rows).total;
+    return SC_OK;
+}
+
+extern "C" int sc_linear_child_plan_build(int64_t n_parents, const int32_t *d_child_rows, int64_t n_children,
+                                          void *d_child_plan, size_t child_plan_bytes, sc_stream stream)
+{
+    clear_error();
+    if (n_parents < 0 || n_parents > INT32_MAX)
+        return fail(SC_ERR_SHAPE, "child plan parent count must be in [0, i32::MAX]");
+    if (n_children < 0 || n_children > 8 * n_parents)
+        return fail(SC_ERR_SHAPE, "child plan child count must be in [0, 8 * parents]");
+    if (!d_child_plan || (n_parents > 0 && !d_child_rows)) return fail(SC_ERR_NULL, "linear child plan: NULL pointer");
+    if ((uintptr_t)d_child_plan % 256 != 0) return fail(SC_ERR_WORKSPACE, "conv plans must be 256-byte aligned");
+    if ((uintptr_t)d_child_rows % 16 != 0) return fail(SC_ERR_SHAPE, "child rows must be 16-byte aligned");
+    const ChildPlanLayout CL = child_plan_layout(n_parents, n_children, 1);
+    if (child_plan_bytes < CL.total)
+        return fail(SC_ERR_WORKSPACE, "child plan buffer too small: got " + std::to_string(child_plan_bytes) +
+                                          " need " + std::to_string(CL.total));
+    if (CL.n_tiles > INT32_MAX) return fail(SC_ERR_OVERFLOW, "child plan tile count overflow");
+    char *b = static_cast<char *>(d_child_plan);
+    ChildArgs c;
+    c.phdr = nullptr;  // parents in row order: no parent plan
+    c.porder = nullptr;
+    c.child_rows = d_child_rows;
+    c.n_parents = n_parents;
+    c.n_children = n_children;
+    c.n_ptiles = CL.n_ptiles;
+    c.n_chunks = CL.n_chunks;
+    c.n_main = CL.n_main;
+    c.n_tiles = CL.n_tiles;
+    c.K = 1;
+    c.hdr = reinterpret_cast<PlanHeader *>(b);
+    c.order = reinterpret_cast<int32_t *>(b + CL.order);
+    c.tile_child = reinterpret_cast<int32_t *>(b + CL.tile_child);
+    c.tile_u = reinterpret_cast<int32_t *>(b + CL.tile_u);
+    c.overflow = reinterpret_cast<int32_t *>(b + CL.overflow);
+    c.counts = reinterpret_cast<int32_t *>(b + CL.counts);
+    c.chunks = reinterpret_cast<int32_t *>(b + CL.chunks);
+    c.child_n = reinterpret_cast<int32_t *>(b + CL.child_n);
+    c.child_base = reinterpret_cast<int32_t *>(b + CL.child_base);
+    c.split = reinterpret_cast<int32_t *>(b + CL.split);
+    c.split_n = reinterpret_cast<int32_t *>(b + CL.split_n);
+    hipStream_t s = as_stream(stream);
+    // the child plan's lists and tile_child, without halo tables: the linear
+    // reads each parent's own row
+    if (CL.n_ptiles > 0) {
+        child_count_kernel<<<(unsigned)CL.n_ptiles, kThreads, 0, s>>>(c);
+        SC_LAUNCH_CHECK("child_count_kernel launch");
+        child_chunk_kernel<<<(unsigned)CL.n_chunks, kThreads, 0, s>>>(c);
+        SC_LAUNCH_CHECK("child_chunk_kernel launch");
+    }
+    child_layout_kernel<<<1, kThreads, 0, s>>>(c);
+    SC_LAUNCH_CHECK("child_layout_kernel launch");
+    if (CL.n_ptiles > 0) {
+        child_emit_kernel<<<(unsigned)CL.n_ptiles, kThreads, 0, s>>>(c);
+        SC_LAUNCH_CHECK("child_emit_kernel launch");
+    }
+    child_pad_kernel<<<(unsigned)CL.n_tiles, kThreads, 0, s>>>(c);
+    SC_LAUNCH_CHECK("child_pad_kernel launch");
     return SC_OK;
 }
 

@@ -31,6 +31,7 @@ from typing import List, Optional, Sequence, Tuple, Union
 import torch
 
 from .flex_gmm import (ConvPlan, NeighborMapWorkspace, SparseSubmConvConfig, build_child_plan, build_conv_plan,
+                       build_linear_child_plan,
                        c2s_skip_add, gather_rows, kernel_rows, layer_norm, linear_forward, linear_skinny,
                        neighbor_rows_tensor_from_coords_tensor, pack_conv_weight,
                        sparse_subm_conv_forward, subdivision_build, subdivision_build_indexed,
@@ -259,19 +260,29 @@ class C2SUpsampleBlock:
 
 
 def transposed_upsample(parent_coords: torch.Tensor, parent_feats: torch.Tensor,
-                        conv1x1: ConvLayer, mask: torch.Tensor
+                        conv1x1: ConvLayer, mask: torch.Tensor, active_only: bool = True
                         ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """2x2x2 stride-2 transposed sparse conv as C2S: a 1x1x1 conv Cin -> 8*Cout
     on the parents (parent p's own row: the dense linear, no map) whose
     epilogue writes each active child's Cout slice to the child's row (no
-    [P, 8*Cout] tensor).  Returns (child coords, child feats, linear_idx)."""
+    [P, 8*Cout] tensor).  With ``active_only`` (and 16-bit weights, Cout a
+    multiple of 128, Cin of 32) a linear child plan lists, per child index,
+    the parents whose child is active, and only those (parent, child) pairs
+    are computed; the values are the same.  Returns (child coords, child
+    feats, linear_idx)."""
     cfg = conv1x1.cfg
     if cfg.kernel_d * cfg.kernel_h * cfg.kernel_w != 1 or cfg.groups != 1:
         raise ValueError("transposed_upsample needs a 1x1x1 conv with groups == 1")
     child_coords, linear_idx, child_rows = subdivision_build_indexed(parent_coords, mask=mask)
     w = conv1x1.weight.reshape(cfg.out_channels, cfg.in_channels)
+    n_children = child_coords.shape[0]
+    plan = None
+    if (active_only and n_children > 0 and parent_feats.dtype in (torch.bfloat16, torch.float16)
+            and w.dtype == parent_feats.dtype and (cfg.out_channels // 8) % 128 == 0
+            and cfg.in_channels % 32 == 0):
+        plan = build_linear_child_plan(child_rows, n_children)
     h_up = linear_forward(parent_feats, w, conv1x1.bias, conv1x1.w_scale, out_dtype=parent_feats.dtype,
-                          child_rows=child_rows, n_child_rows=child_coords.shape[0])
+                          child_rows=child_rows, n_child_rows=n_children, child_plan=plan)
     return child_coords, h_up, linear_idx
 
 

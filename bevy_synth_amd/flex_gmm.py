@@ -429,6 +429,24 @@ def build_child_plan(cfg: SparseSubmConvConfig, parent_plan: ConvPlan, neighbor_
     return ChildPlan(buf, P, int(n_children), K)
 
 
+def build_linear_child_plan(child_rows: torch.Tensor, n_children: int) -> ChildPlan:
+    """sc_linear_child_plan_build: for the transposed upsample's linear
+    (linear_forward with ``child_rows``), per child index the parents whose
+    child is active, in row order, in tiles of their own, so that
+    linear_forward(..., child_plan=) computes only active children."""
+    _require_cuda("child_rows", child_rows)
+    if child_rows.dtype != torch.int32 or child_rows.dim() != 2 or child_rows.shape[1] != 8 \
+            or not child_rows.is_contiguous():
+        raise SparseConvError(2, "child plan: child_rows must be int32 [P, 8]")
+    P = child_rows.shape[0]
+    n = ctypes.c_size_t()
+    check(_capi.load().sc_conv_child_plan_size(P, int(n_children), 1, ctypes.byref(n)))
+    buf = torch.empty(n.value, dtype=torch.uint8, device=child_rows.device)
+    check(_capi.load().sc_linear_child_plan_build(P, _ptr(child_rows), int(n_children), _ptr(buf), buf.numel(),
+                                                  _stream()))
+    return ChildPlan(buf, P, int(n_children), 1)
+
+
 def conv_weight_pack_bytes(cfg: SparseSubmConvConfig, w_dtype: torch.dtype) -> int:
     out = ctypes.c_size_t()
     dt = {torch.bfloat16: _capi.SC_DTYPE_BF16, torch.int8: _capi.SC_DTYPE_I8,
@@ -612,7 +630,7 @@ def linear_forward(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.T
                    ln_weight: Optional[torch.Tensor] = None, ln_bias: Optional[torch.Tensor] = None,
                    ln_eps: float = 1e-6, out: Optional[torch.Tensor] = None,
                    workspace: Optional[torch.Tensor] = None, child_rows: Optional[torch.Tensor] = None,
-                   n_child_rows: Optional[int] = None) -> torch.Tensor:
+                   n_child_rows: Optional[int] = None, child_plan: Optional["ChildPlan"] = None) -> torch.Tensor:
     """linear_forward_wgpu (burn_trellis sparse_decoder_wgpu_ops.rs:79-160) through
     sc_linear_forward: x [rows, Cin] @ weight[Cout, Cin]^T + bias, with the conv
     epilogue (LayerNorm over the row, SiLU, + residual) fused.  Same dtype rules
@@ -620,7 +638,10 @@ def linear_forward(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.T
     ``child_rows`` [rows, 8] int32 (subdivision_build_indexed) makes this the
     2x2x2 transposed upsample: row r's channels [c*C, (c+1)*C), C = Cout/8,
     land in row child_rows[r, c] of an [n_child_rows, C] output (LayerNorm
-    per child, ln_weight / ln_bias then [C])."""
+    per child, ln_weight / ln_bias then [C]).  ``child_plan``
+    (build_linear_child_plan over the same child_rows) computes only the
+    active children (sc_linear_forward_child_planned); the stored values are
+    the same."""
     _require_cuda("x", x)
     _require_cuda("weight", weight)
     rows, cin = x.shape
@@ -673,6 +694,15 @@ def linear_forward(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.T
             workspace = torch.empty(need.value, dtype=torch.uint8, device=x.device)
         epi.workspace = workspace.data_ptr()
         epi.workspace_bytes = workspace.numel()
+    if child_plan is not None:
+        if child_rows is None:
+            raise SparseConvError(2, "linear: a child plan needs child_rows")
+        if child_plan.n_q != rows or child_plan.n_children != int(n_child_rows) or child_plan.K != 1:
+            raise SparseConvError(2, "linear: the child plan was built for other parents or children")
+        check(_capi.load().sc_linear_forward_child_planned(
+            _dt(x), _ptr(x), rows, cin, cout, _dt(weight), _ptr(weight), _ptr(w_scale), _ptr(bias),
+            ctypes.byref(epi), _dt(out), _ptr(out), _ptr(child_plan.buf), _stream()))
+        return out
     check(_capi.load().sc_linear_forward(_dt(x), _ptr(x), rows, cin, cout, _dt(weight), _ptr(weight), _ptr(w_scale),
                                          _ptr(bias), ctypes.byref(epi), _dt(out), _ptr(out), _stream()))
     return out

@@ -366,6 +366,36 @@ int sc_conv_child_plan_build(const sc_conv_config *cfg, const void *d_parent_pla
                              void *d_child_plan, size_t child_plan_bytes, sc_stream stream);
 
 /*
+ * A child plan for the dense linear's child scatter (the 2x2x2 transposed
+ * upsample: sc_linear_forward with epi->child_rows): per child index c, the
+ * parents whose child c is active (d_child_rows[p * 8 + c] in
+ * [0, n_children)), in row order, in 256-row tiles of their own, so that
+ * sc_linear_forward_child_planned computes only the active children.  The
+ * buffer is sized by sc_conv_child_plan_size(n_parents, n_children, 1); the
+ * build launches five kernels, stream-ordered, no sync, and has no halo
+ * tables (the linear reads each parent's own row).  More active children
+ * than n_children leaves the plan empty and flagged (sc_conv_plan_check).
+ * No reference counterpart: the reference's transposed upsample computes
+ * every child of every parent.
+ */
+int sc_linear_child_plan_build(int64_t n_parents, const int32_t *d_child_rows, int64_t n_children,
+                               void *d_child_plan, size_t child_plan_bytes, sc_stream stream);
+
+/*
+ * sc_linear_forward with the child scatter (epi->child_rows and
+ * epi->n_child_rows required, the table and count the plan was built from)
+ * over a linear child plan: each tile's parents, one child's channels, so
+ * inactive children cost nothing.  Every stored value is the same sum as
+ * sc_linear_forward's.  Needs 16-bit activations and weights, in_channels a
+ * multiple of 32 and children of a multiple of 128 channels (out_channels /
+ * 8); other shapes fail with SC_ERR_UNSUPPORTED.
+ */
+int sc_linear_forward_child_planned(int act_dtype, const void *d_input, int64_t rows, int64_t in_channels,
+                                    int64_t out_channels, int w_dtype, const void *d_weight,
+                                    const float *d_w_scale, const float *d_bias, const sc_conv_epilogue *epi,
+                                    int out_dtype, void *d_out, const void *d_child_plan, sc_stream stream);
+
+/*
  * sc_subm_conv_forward_planned on a child plan: conv1 of the C2S block with
  * the child scatter (epi->child_rows and epi->n_child_rows required, the same
  * table and count the child plan was built from), only the active children

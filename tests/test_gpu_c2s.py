@@ -441,3 +441,71 @@ def test_child_plan_refuses_inconsistent_child_rows():
                                packed_weight=layer.packed_weight(), child_rows=child_rows, n_child_rows=1)
     torch.cuda.synchronize()
     assert (out.float() == 7.0).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("cin,cchild,ln,frac", [(512, 256, False, 0.74), (128, 128, True, 0.5),
+                                                (256, 256, True, 0.3), (64, 128, False, 1.0)])
+def test_linear_child_plan_matches_unplanned(dtype, cin, cchild, ln, frac):
+    """The transposed upsample's linear over a linear child plan
+    (sc_linear_child_plan_build; only active children computed) stores
+    exactly what sc_linear_forward stores (all eight children, inactive ones
+    dropped): every value the same sum in the same order, with the per-child
+    LayerNorm in the tile (128 channels) or on the f32 staging (256).  The
+    plan's lists: per child, the parents in row order, tiled from
+    child_base[c]; child index 3 is never active; every other slot is -1."""
+    rng = np.random.default_rng(cin + cchild + int(frac * 10))
+    parents = _c2s_parents(30001)
+    P = len(parents)
+    mask = rng.random((P, 8)) < frac
+    mask[:, 3] = False
+    pc = dev(parents)
+    cc, _, child_rows = F.subdivision_build_indexed(pc, mask=dev(mask.astype(np.uint8)))
+    A = cc.shape[0]
+    x = dev(synth.normal_f32(rng, (P, cin))).to(dtype)
+    w = dev(synth.normal_f32(rng, (8 * cchild, cin), 1 / np.sqrt(cin))).to(dtype)
+    b = dev(synth.normal_f32(rng, 8 * cchild, 0.5))
+    kw = dict(layer_norm=ln, child_rows=child_rows, n_child_rows=A)
+    if ln:
+        kw.update(ln_weight=dev(synth.normal_f32(rng, cchild)), ln_bias=dev(synth.normal_f32(rng, cchild)))
+    ref = F.linear_forward(x, w, b, **kw)
+    cp = F.build_linear_child_plan(child_rows, A)
+    got = F.linear_forward(x, w, b, child_plan=cp, **kw)
+    F.conv_plan_check(cp)
+    assert got.shape == (A, cchild) and got.dtype == dtype
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    h = cp.to_host()
+    tc, order = h["tile_child"], h["order"]
+    base = 0
+    for c in range(8):
+        lst = np.nonzero(mask[:, c])[0]
+        nt = (len(lst) + 255) // 256
+        assert h["child_n"][c] == len(lst) and h["child_base"][c] == base, c
+        seg = order[base:base + nt].ravel()
+        assert np.array_equal(seg[:len(lst)], lst) and (seg[len(lst):] == -1).all(), c
+        assert (tc[base:base + nt] == c).all(), c
+        base += nt
+    assert h["n_used"] == base
+    assert (tc[base:] == -1).all() and (order[base:] == -1).all()
+
+
+def test_linear_child_plan_refusals():
+    """The linear child plan takes children of a multiple of 128 channels on
+    16-bit weights; a plan built for other parents or children is refused on
+    the host."""
+    rng = np.random.default_rng(12)
+    parents = _c2s_parents(3000)
+    P = len(parents)
+    mask = rng.random((P, 8)) < 0.5
+    cc, _, child_rows = F.subdivision_build_indexed(dev(parents), mask=dev(mask.astype(np.uint8)))
+    A = cc.shape[0]
+    cp = F.build_linear_child_plan(child_rows, A)
+    x = bf16_dev(synth.normal_f32(rng, (P, 64)))
+    w64 = bf16_dev(synth.normal_f32(rng, (8 * 64, 64), 0.1))
+    with pytest.raises(F.SparseConvError) as e:
+        F.linear_forward(x, w64, child_rows=child_rows, n_child_rows=A, child_plan=cp)
+    assert "multiple of 128" in e.value.message
+    w128 = bf16_dev(synth.normal_f32(rng, (8 * 128, 64), 0.1))
+    with pytest.raises(F.SparseConvError):
+        F.linear_forward(x[:P - 1], w128, child_rows=child_rows[:P - 1].contiguous(), n_child_rows=A,
+                         child_plan=cp)
