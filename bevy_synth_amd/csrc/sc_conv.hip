@@ -14,8 +14,9 @@
 //                     packed weights: the tile's distinct neighbour rows are
 //                     staged in LDS once per 32-channel chunk and every
 //                     operand is read from there (v_mfma_f32_16x16x32_bf16);
-//   conv_v2_kernel    bf16 activations without a plan, and the plan tiles
-//                     whose halo exceeds the LDS budget: neighbour rows
+//                     a tile whose halo exceeds the LDS budget gathers its
+//                     operands from global memory in the same stage order;
+//   conv_v2_kernel    bf16 activations without a plan: neighbour rows
 //                     gathered from global memory per (row, offset), weights
 //                     staged in LDS;
 //   conv_mfma_kernel  f32 activations (v_mfma_f32_32x32x2_f32);
@@ -171,8 +172,6 @@ static int conv_forward_impl(const sc_conv_config *cfg, int act_dtype, const voi
     a.ln_eps = 0.f;
     a.silu = 0;
     a.perm = nullptr;
-    a.tile_list = nullptr;
-    a.tile_count = nullptr;
     a.wpack = d_wpack;
     a.plan_hdr = nullptr;
     a.ln_group = (int)cfg->out_channels_per_group;

@@ -19,7 +19,6 @@ constexpr int kBN = 128;        // output channels per workgroup
 constexpr int kThreads = 256;
 constexpr int kChunkBytes = 64;   // smallest per-stage reduction slice of a row (bytes)
 constexpr int kMaxTableK = 32;    // MFMA tile: kernels with at most 32 offsets
-constexpr int kSubTiles = kPlanTileRows / kTileRows;  // direct tiles per plan tile
 
 struct ConvArgs {
     const void *input;
@@ -47,9 +46,6 @@ struct ConvArgs {
     // Optional row order (a permutation of [0, n_q), padded with -1 to whole
     // tiles): tile row p computes query row perm[p].
     const int32_t *perm;
-    // Optional tile list: workgroup b takes tile tile_list[b] if b < *tile_count.
-    const int32_t *tile_list;
-    const int32_t *tile_count;
     // Weights packed by sc_conv_weight_pack (the halo-staged kernel's layout),
     // starting with their PackHeader.
     const void *wpack;
@@ -678,10 +674,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv_mfma_kernel(ConvArgs args)
 //    operand reads (16 channels x 16 bytes per 16 lanes) hit distinct banks;
 //  * offsets are walked by scalar bit cursors over the tile's offset mask,
 //    and the gathered-row byte offsets of the next A stage are read from LDS
-//    one stage before the loads that use them;
-//  * optional row permutation (args.perm, a plan's row order) and tile list
-//    (args.tile_list: the plan tiles whose halo overflowed the halo kernel's
-//    LDS budget).
+//    one stage before the loads that use them.
 // The stage loop keeps a static number of vector loads per stage, so the
 // explicit vmcnt waits below are exact: W(t) and A(t) have landed when
 // stage t starts.
@@ -725,7 +718,7 @@ struct StageCursor {
     __device__ inline bool live() const { return rem != 0u; }
 };
 
-template <typename TA, typename TW, typename TO, int CB, int DIST, bool PERM>
+template <typename TA, typename TW, typename TO, int CB, int DIST>
 __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
 {
     constexpr bool kI8 = sizeof(TW) == 1;
@@ -758,30 +751,9 @@ __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
     const int l16 = lane & 15, q4 = lane >> 4;
     const int K = args.K;
 
-    int tile, child = 0;
-    if (args.tile_list) {
-        // Plan tile tile_list[b / kSubTiles], part b % kSubTiles.  The plan's
-        // header is checked first, and its status: the halo kernel before
-        // this launch flags a map or packed-weight mismatch there (and a
-        // flagged plan stays flagged until rebuilt).  A listed tile must lie
-        // inside the order.
-        if (!plan_matches(args.plan_hdr, args) || args.plan_hdr->status != 0u) return;
-        const int b = (int)blockIdx.x / kSubTiles;
-        if (b >= *args.tile_count) return;
-        const int lt = args.tile_list[b];
-        if (lt < 0 || (int64_t)lt * kPlanTileRows >= (args.tile_child ? args.plan_hdr->n_tiles * (int64_t)kPlanTileRows
-                                                                       : args.n_q))
-            return;
-        if (args.tile_child) {  // a child plan's tile: its child's channel block
-            child = args.tile_child[lt];
-            if (child < 0) return;
-        }
-        tile = lt * kSubTiles + (int)blockIdx.x % kSubTiles;
-    } else {
-        tile = tile_for_block(blockIdx.x, gridDim.x);
-    }
+    const int tile = tile_for_block(blockIdx.x, gridDim.x);
     const int64_t row0 = (int64_t)tile * kRows;
-    const int o0 = child * args.child_ch + blockIdx.y * kBN;
+    const int o0 = blockIdx.y * kBN;
     const int g = blockIdx.z;
     const int64_t in_col0 = (int64_t)g * args.cin_g;
     const int64_t out_col0 = (int64_t)g * args.cout_g;
@@ -792,15 +764,8 @@ __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
     if (tid == 0) s_tmask = 0u;
     uint32_t m = 0;
     {
-        const int64_t q = row0 + tid;
-        bool rv = q < args.n_q;
-        int64_t qrow = q;
-        if constexpr (PERM) {
-            // the order is padded to whole tiles with -1
-            const int32_t pq = args.perm[q];
-            qrow = pq;
-            rv = pq >= 0 && pq < args.n_q;
-        }
+        const int64_t qrow = row0 + tid;
+        const bool rv = qrow < args.n_q;
         s_qrow[tid] = rv ? (int32_t)qrow : -1;
         // no map: the dense linear (K = 1), query row q reads input row q
         const int32_t *mrow = args.map ? args.map + (rv ? qrow : 0) * K : nullptr;
@@ -1088,10 +1053,8 @@ __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
             const int oc = o0 + j * 16 + 4 * q4;
             float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
             if (c2s) {
-                // a child plan's tile stores its own child's channels only
-                // (its 128-channel tile may reach into the next child)
-                const int cend = args.tile_child ? min(args.cout_g, (child + 1) * args.child_ch) : args.cout_g;
-                if (oc < cend) c2s_store4<TO>(args, crow, qrow, (int)(out_col0 + oc), min(4, cend - oc), v, vec_ok);
+                if (oc < args.cout_g)
+                    c2s_store4<TO>(args, crow, qrow, (int)(out_col0 + oc), min(4, args.cout_g - oc), v, vec_ok);
                 continue;
             }
             if (vec_ok && oc + 3 < args.cout_g) {
@@ -1139,7 +1102,10 @@ __global__ __launch_bounds__(kThreads, 2) void conv_v2_kernel(ConvArgs args)
 // split halves the vector-memory weight traffic of a 1 x 4 row split (the
 // texture path, not the MFMAs, bounds that form) for twice the LDS operand
 // reads.  Absent neighbours read a zero row.  Per-row accumulation order is
-// fixed (chunk-major, offsets ascending).
+// fixed (chunk-major, offsets ascending).  A tile whose halo exceeds
+// kPlanHaloMax rows (no local map or halo is built for it) keeps the byte
+// offsets of its rows' neighbours where the halo would be and loads every
+// operand from global memory, in the same stages and order.
 //
 // Tiles of 64 output channels (layers of at most 64 per group, and C2S
 // children of 64) keep the 128 x 64 wave block: the two waves of a row half
@@ -1231,7 +1197,11 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
         tile = tile_for_block(blockIdx.x, gridDim.x);
     }
     const int U = plan.tile_u[tile];
-    if (U > kPlanHaloMax) return;  // listed in plan.overflow; the direct kernel takes it
+    // A tile whose halo exceeds the LDS budget (listed in plan.overflow; its
+    // local map and halo are not built) gathers its operands straight from
+    // global memory, through the byte offsets of its rows' neighbours held
+    // where the halo would be.
+    const bool direct = U > kPlanHaloMax;
     // a child plan's tile computes its child's channel block (an unused tile nothing)
     const int child = plan.tile_child ? plan.tile_child[tile] : 0;
     if (child < 0) return;
@@ -1247,15 +1217,6 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
         // Every load first -- the row's K local-map entries and this
         // thread's halo rows -- so the prologue costs one memory round trip
         // (a loop over k waits once per few offsets: ~10 round trips a tile).
-        const uint16_t *src = plan.lmap + (int64_t)tile * K * kPlanTileRows + tid;
-        const int32_t *hrows = plan.halo + (int64_t)tile * kPlanHaloMax;
-        constexpr int kHPer = (kPlanHaloMax + kThreads - 1) / kThreads;  // halo rows per thread
-        uint32_t jv[kHaloK];
-        int32_t hv[kHPer];
-#pragma unroll
-        for (int k = 0; k < kHaloK; ++k) jv[k] = k < K ? src[k * kPlanTileRows] : (uint32_t)kPlanAbsent;
-#pragma unroll
-        for (int u = 0; u < kHPer; ++u) hv[u] = tid + u * kThreads < U ? hrows[tid + u * kThreads] : 0;
         const int32_t ord = plan.order[(int64_t)tile * kPlanTileRows + tid];
         float bv = 0.f, sv = 1.f;
         if (tid < kNT) {
@@ -1264,23 +1225,49 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
             if (args.bias && ok) bv = args.bias[out_col0 + o];
             if (args.w_scale && ok) sv = args.w_scale[out_col0 + o];  // int8 weights
         }
-        uint16_t *dst = &s_lmap[0][tid >> 7][tid & 15][(tid >> 4) & 7];
         uint32_t m = 0;
+        if (direct) {
+            // the row's map entries -> byte offsets of its neighbours' input
+            // rows, dof[k][tile row] (absent: an offset past the input)
+            uint32_t *dof = reinterpret_cast<uint32_t *>(s_halo);
+            const bool live = ord >= 0 && ord < args.n_q;
+            int32_t e[kHaloK];
 #pragma unroll
-        for (int k = 0; k < kHaloK; ++k) {
-            if (k >= K) break;
-            const int j = (int)jv[k];
-            m |= (uint32_t)(j != kPlanAbsent) << k;
-            dst[k * kPlanTileRows] =
-                (uint16_t)(j == kPlanAbsent ? kZeroRow * CB : j * CB + 16 * (((j >> 1) ^ (j >> 2)) & 3));
+            for (int k = 0; k < kHaloK; ++k) e[k] = (k < K && live) ? args.map[(int64_t)ord * K + k] : -1;
+#pragma unroll
+            for (int k = 0; k < kHaloK; ++k) {
+                if (k >= K) break;
+                const bool ok = e[k] >= 0 && e[k] < args.n_in;
+                m |= (uint32_t)ok << k;
+                dof[k * kPlanTileRows + tid] = ok ? (uint32_t)e[k] * row_bytes : kOobOffset;
+            }
+        } else {
+            const uint16_t *src = plan.lmap + (int64_t)tile * K * kPlanTileRows + tid;
+            const int32_t *hrows = plan.halo + (int64_t)tile * kPlanHaloMax;
+            constexpr int kHPer = (kPlanHaloMax + kThreads - 1) / kThreads;  // halo rows per thread
+            uint32_t jv[kHaloK];
+            int32_t hv[kHPer];
+#pragma unroll
+            for (int k = 0; k < kHaloK; ++k) jv[k] = k < K ? src[k * kPlanTileRows] : (uint32_t)kPlanAbsent;
+#pragma unroll
+            for (int u = 0; u < kHPer; ++u) hv[u] = tid + u * kThreads < U ? hrows[tid + u * kThreads] : 0;
+            uint16_t *dst = &s_lmap[0][tid >> 7][tid & 15][(tid >> 4) & 7];
+#pragma unroll
+            for (int k = 0; k < kHaloK; ++k) {
+                if (k >= K) break;
+                const int j = (int)jv[k];
+                m |= (uint32_t)(j != kPlanAbsent) << k;
+                dst[k * kPlanTileRows] =
+                    (uint16_t)(j == kPlanAbsent ? kZeroRow * CB : j * CB + 16 * (((j >> 1) ^ (j >> 2)) & 3));
+            }
+            if (tid < CB / 16) reinterpret_cast<uint4 *>(s_halo + kZeroRow * CB)[tid] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+            for (int u = 0; u < kHPer; ++u)
+                if (tid + u * kThreads < U) s_hoff[tid + u * kThreads] = (uint32_t)hv[u] * row_bytes;
         }
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) m |= __shfl_xor(m, off, 64);
         if (lane == 0) s_wmask[wave] = m;
-        if (tid < CB / 16) reinterpret_cast<uint4 *>(s_halo + kZeroRow * CB)[tid] = make_uint4(0, 0, 0, 0);
-#pragma unroll
-        for (int u = 0; u < kHPer; ++u)
-            if (tid + u * kThreads < U) s_hoff[tid + u * kThreads] = (uint32_t)hv[u] * row_bytes;
         s_order[tid] = ord;
         if (tid < kNT) {
             s_bias[tid] = bv;
@@ -1397,6 +1384,15 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
             __builtin_amdgcn_s_barrier();
         };
         auto read_lm = [&](int k) { return *reinterpret_cast<const uint4 *>(&s_lmap[k][rh][l16][0]); };
+        auto mfma_all = [&](const uint4(&x)[kIM], const uint4(&f)[4]) {
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const uint4 w = f[jj];
+#pragma unroll
+                for (int i = 0; i < kIM; ++i)
+                    acc[i][jj] = mfma_16x16x32<TA>(w, x[i], acc[i][jj]);
+            }
+        };
         auto compute = [&](const uint4 &lm, const uint4(&f)[4]) {
             const uint32_t lw[4] = {lm.x, lm.y, lm.z, lm.w};
             const uint32_t qx = (uint32_t)q4 << 4;
@@ -1406,16 +1402,31 @@ __global__ __launch_bounds__(kThreads, 2) void conv_halo_kernel(ConvArgs args, P
                 const uint32_t off = ((i & 1) ? (lw[i >> 1] >> 16) : (lw[i >> 1] & 0xFFFFu)) ^ qx;
                 x[i] = *reinterpret_cast<const uint4 *>(s_halo + off);
             }
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-                const uint4 w = f[jj];
-#pragma unroll
-                for (int i = 0; i < kIM; ++i)
-                    acc[i][jj] = mfma_16x16x32<TA>(w, x[i], acc[i][jj]);
-            }
+            mfma_all(x, f);
         };
 
-        if (m_even == 0u) {
+        if (direct) {
+            // Operands from global memory, stage by stage (the same stage
+            // order and accumulation as the halo path; no barrier, the
+            // neighbour offsets are only read).
+            if (m_even != 0u) {
+                const uint32_t *dof = reinterpret_cast<const uint32_t *>(s_halo) + 128 * rh + l16;
+                const __amdgpu_buffer_rsrc_t x_rsrc =
+                    make_rsrc(input + in_col0, (uint32_t)(args.n_in * row_bytes - in_col0 * (int64_t)sizeof(uint16_t)));
+                Cursor cur;
+                cur_init(cur);
+                while (cur.c < nkc) {
+                    uint4 f[4];
+                    load_w(cur, f);
+                    const uint32_t cb = (uint32_t)(cur.c * CB + q4 * 16);
+                    uint4 x[kIM];
+#pragma unroll
+                    for (int i = 0; i < kIM; ++i) x[i] = bload16(x_rsrc, dof[cur.k * kPlanTileRows + 16 * i] + cb);
+                    mfma_all(x, f);
+                    cur_next(cur);
+                }
+            }
+        } else if (m_even == 0u) {
             // idle wave (stage split, one offset): its share of every halo
             // load and the same barriers as the others
             for (int c = 0; c < nkc; ++c) {
@@ -2164,16 +2175,16 @@ __global__ __launch_bounds__(256) void conv_scalar_kernel(ConvArgs args)
 // int8 weights always take the 64-byte stages: their register staging of the
 // widened pieces does not fit beside the 128-byte stage's operands (the
 // 128-byte int8 variant spilled), so it is not instantiated.
-template <typename TA, typename TW, typename TO, bool PERM>
+template <typename TA, typename TW, typename TO>
 void launch_v2(const ConvArgs &a, dim3 grid, hipStream_t s)
 {
     if constexpr (sizeof(TW) == 2) {
         if (a.cin_g % 64 == 0) {
-            conv_v2_kernel<TA, TW, TO, 128, 1, PERM><<<grid, kThreads, 0, s>>>(a);
+            conv_v2_kernel<TA, TW, TO, 128, 1><<<grid, kThreads, 0, s>>>(a);
             return;
         }
     }
-    conv_v2_kernel<TA, TW, TO, 64, 2, PERM><<<grid, kThreads, 0, s>>>(a);
+    conv_v2_kernel<TA, TW, TO, 64, 2><<<grid, kThreads, 0, s>>>(a);
 }
 
 template <typename TA, typename TW, typename TO>
@@ -2188,9 +2199,8 @@ int launch_conv(const ConvArgs &a, int groups, bool mfma, const void *plan, hipS
         dim3 grid((unsigned)tiles, (unsigned)ntile, (unsigned)groups);
         if constexpr (sizeof(TA) == 2) {
             if (plan && a.wpack) {
-                // Halo-staged tiles, then the tiles whose halo overflowed
-                // (listed by the plan) through the direct kernel in plan
-                // order, each plan tile as kPlanTileRows / kTileRows tiles.
+                // Halo-staged tiles (a tile whose halo overflowed gathers
+                // its operands from global memory in the same launch).
                 // Packed weights are bf16 for either weight type; int8
                 // weights keep their per-channel scales for the epilogue.
                 // A child plan (C2S conv1 over the active children): its own
@@ -2225,14 +2235,6 @@ int launch_conv(const ConvArgs &a, int groups, bool mfma, const void *plan, hipS
                     conv_halo_kernel<TA, TO, false, 128><<<hgrid, kThreads, 0, s>>>(h, pv);
                 }
                 SC_LAUNCH_CHECK("conv_halo_kernel launch");
-                ConvArgs b = a;
-                b.plan_hdr = pv.hdr;
-                b.perm = pv.order;
-                b.tile_list = pv.overflow;
-                b.tile_count = &pv.hdr->n_overflow;
-                b.tile_child = pv.tile_child;
-                dim3 fgrid((unsigned)(n_tiles * kSubTiles), (unsigned)((cols + kBN - 1) / kBN), (unsigned)groups);
-                launch_v2<TA, TW, TO, true>(b, fgrid, s);
             } else if (sizeof(TW) == 2 && !a.map && a.K == 1 && groups == 1 && a.cin % 32 == 0 && !a.skip_idx) {
                 // the dense linear: contiguous rows, reference-layout weights;
                 // row tile x column tile flattened, column tile fastest;
@@ -2295,7 +2297,7 @@ int launch_conv(const ConvArgs &a, int groups, bool mfma, const void *plan, hipS
                 }
                 SC_LAUNCH_CHECK("dense_gemm_kernel launch");
             } else {
-                launch_v2<TA, TW, TO, false>(a, grid, s);
+                launch_v2<TA, TW, TO>(a, grid, s);
             }
         } else {
             if (wide)

@@ -321,9 +321,10 @@ int sc_conv_weight_pack(const sc_conv_config *cfg, int w_dtype, const void *d_we
 /*
  * sc_subm_conv_forward_fused reading a plan of the same map and the packed
  * copy of the weights (both may be NULL).  With both, bf16 activations and at
- * most 27 offsets take the halo-staged kernel; d_weight (reference layout)
- * is still required for tiles whose halo exceeds the kernel's LDS budget and
- * for shapes the halo kernel does not take.  Same result as
+ * most 27 offsets take the halo-staged kernel (a tile whose halo exceeds its
+ * LDS budget reads its operands from global memory, in the same order);
+ * d_weight (reference layout) is still required for shapes the halo kernel
+ * does not take.  Same result as
  * sc_subm_conv_forward_fused up to f32 summation order: the halo kernel sums
  * each row's (32-channel chunk, offset) products chunk-major instead of
  * offset-major, in a fixed order, so results are bit-identical run to run.
@@ -401,8 +402,8 @@ int sc_linear_forward_child_planned(int act_dtype, const void *d_input, int64_t 
  * table and count the child plan was built from), only the active children
  * computed.  Same results as sc_subm_conv_forward_planned with the parent
  * plan and the same epilogue (each stored value is the same sum in the same
- * order), except for children whose tile overflows the halo budget in either
- * plan: the direct kernel sums those in another fixed order.  Needs 16-bit
+ * order), except for children of 64 channels: their tiles split the stages
+ * between two waves by the tile's offsets, another fixed order.  Needs 16-bit
  * activations, packed weights, one group, at most 27
  * offsets, and children of 64 channels or a multiple of 128 (Cout 512 or a
  * multiple of 1024); other shapes fail with SC_ERR_UNSUPPORTED.

@@ -378,8 +378,8 @@ def test_planned_conv_on_own_order(oracle):
 
 
 def test_planned_overflow_tiles_and_query_subset(oracle):
-    """Cluster centres as query rows: every tile's halo overflows, so the whole
-    conv runs through the direct kernel in plan order."""
+    """Cluster centres as query rows: every tile's halo overflows, so every
+    tile gathers its operands from global memory."""
     coords = cluster_coords(700)
     rng = np.random.default_rng(8)
     n, c = len(coords), 64
@@ -394,25 +394,39 @@ def test_planned_overflow_tiles_and_query_subset(oracle):
     assert_close(out.cpu().numpy(), exp, 2e-5, "overflow tiles")
 
 
-def test_planned_mixed_overflow(oracle):
-    """Some tiles overflow, others take the halo kernel, in one call."""
+@pytest.mark.parametrize("cin,cout,form", [(32, 32, "plain"), (64, 128, "ln"), (128, 64, "residual"),
+                                           (96, 200, "plain")])
+def test_planned_mixed_overflow(oracle, cin, cout, form):
+    """Some tiles overflow (their operands gathered from global memory),
+    others take the LDS halo, in one launch: both tile widths, the stage split
+    of 64-channel tiles, LayerNorm -> SiLU in the tile and the residual."""
     a = synth.config1_coords()[:3000]
     cl = cluster_coords(300)
     cl[:, 1:] += 200
     # query rows: the shell, then the cluster centres; the cluster neighbours last
     coords = np.concatenate([a, cl[:300], cl[300:]])
     q = 3300
-    rng = np.random.default_rng(9)
-    n, c = len(coords), 32
-    x = rbf(synth.normal_f32(rng, (n, c)))
-    w = rbf(synth.conv_weight(rng, c, 27, c, 0.05))
-    b = synth.normal_f32(rng, c, 0.1)
-    cfg = F.SparseSubmConvConfig(c, c)
-    out, nbr, plan = planned(cfg, coords, x, w, b, q=q, out_dtype=torch.float32)
+    rng = np.random.default_rng(9 + cin + cout)
+    n = len(coords)
+    x = rbf(synth.normal_f32(rng, (n, cin)))
+    w = rbf(synth.conv_weight(rng, cout, 27, cin, 0.05))
+    b = synth.normal_f32(rng, cout, 0.1)
+    res = synth.normal_f32(rng, (q, cout))
+    cfg = F.SparseSubmConvConfig(cin, cout)
+    kw = {"out_dtype": torch.float32}
+    if form == "ln":
+        kw.update(layer_norm=True, silu=True, ln_eps=1e-6)
+    if form == "residual":
+        kw.update(residual=dev(res))
+    out, nbr, plan = planned(cfg, coords, x, w, b, q=q, **kw)
     h = plan.to_host()
     assert 0 < h["n_overflow"] < h["n_tiles"]
     exp = oracle.conv_ref_f64(ocfg(oracle, cfg), w, b, x, nbr)
-    assert_close(out.cpu().numpy(), exp, 2e-5, "mixed overflow")
+    if form == "ln":
+        exp = oracle.silu(oracle.layer_norm(exp.astype(np.float32), None, None, 1e-6))
+    if form == "residual":
+        exp = exp + res
+    assert_close(out.cpu().numpy(), exp, 2e-5 if form != "ln" else 1e-4, f"mixed overflow {form}")
 
 
 def test_planned_config3_sampled_and_deterministic(oracle):
