@@ -819,13 +819,15 @@ constexpr int kBitmapBits = kBitmapWords * 32;
 // Paged bitmap: neighbour rows wider apart than kBitmapBits (rows in octree
 // or coarse-brick order put the x-adjacent neighbours ~100,000 rows away)
 // but inside at most kPages pages of kPageRows rows get those pages of the
-// bitmap side by side in page order instead of one contiguous window; an
-// LDS hash of the page ids finds them, and a page's rank is the number of
-// smaller ids among them.
+// bitmap side by side in page order instead of one contiguous window.  The
+// tile's pages are found as bits of a page bitmap over its neighbour range
+// (at most kPageBits pages, 4 M rows), and a page's rank is the number of
+// set bits below its own.
 constexpr int kPageShift = 12;
 constexpr int kPageRows = 1 << kPageShift;               // 128 bitmap words
 constexpr int kPages = kBitmapBits / kPageRows;          // 32
-constexpr int kPageSlots = 2 * kPages;                   // page-id hash table
+constexpr int kPageWords = 32;                           // page bitmap words
+constexpr int kPageBits = kPageWords * 32;               // 1024 pages
 
 __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
 {
@@ -836,15 +838,19 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
     __shared__ int32_t s_halo[kPlanHaloMax];        // the halo rows (bitmap path)
     __shared__ int s_wave[kTileThreads / 64];
     __shared__ int s_mm[2][kTileThreads / 64];
-    __shared__ int32_t s_pkey[kPageSlots];  // paged: page ids (relative to lo), -1 empty
-    __shared__ int32_t s_prank[kPageSlots]; // rank of the slot's page among the tile's pages
-    __shared__ int32_t s_pid[kPages];       // page id of rank r
-    __shared__ int s_npages, s_pfull;
+    __shared__ uint32_t s_pbits[kPageWords]; // paged: the tile's pages (ids relative to lo)
+    __shared__ int32_t s_ppre[kPageWords];   // set bits in the words before each word
+    __shared__ int32_t s_pid[kPages];        // page id of rank r
+    __shared__ int s_npages;
     int32_t *s_key = reinterpret_cast<int32_t *>(s_bits);
     uint64_t *s_list = reinterpret_cast<uint64_t *>(s_pre);  // up to 1024 sorted entries
     static_assert(kHashSlots <= kBitmapWords, "hash table fits the bitmap array");
     static_assert(kPlanHaloMax <= 1024 && 1024 * 8 <= kBitmapWords * 2, "sort list fits the prefix array");
     // XCD-contiguous tiles: neighbouring tiles read neighbouring map rows.
+    // Rows in their own (octree) order take the tiles round-robin instead:
+    // there the tiles whose neighbours span several pages (the slower paged
+    // path) come in long runs, and contiguous ranges left half the XCDs idle
+    // for the last third of the launch (config 5's last level).
     int64_t t;
     if (a.tile_list) {
         if ((int)blockIdx.x >= *a.tile_list_n) return;
@@ -855,6 +861,8 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
         const int n_used = a.hdr->n_unique;
         if ((int)blockIdx.x >= n_used) return;
         t = tile_for_block((int)blockIdx.x, n_used);
+    } else if (a.hdr->grid_mode == 2) {
+        t = blockIdx.x;
     } else {
         t = tile_for_block((int)blockIdx.x, (int)gridDim.x);
     }
@@ -932,17 +940,13 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
     const bool window = hi < lo || (int64_t)hi - lo < (int64_t)kBitmapBits;
     bool paged = false;
     int np = 0;
-    if (!window) {
-        // The tile's distinct pages: an LDS hash of page ids (bounded probes;
-        // a page that finds no slot sends the tile to the hash path).
-        if (p < kPageSlots) s_pkey[p] = -1;
-        if (p == 0) {
-            s_npages = 0;
-            s_pfull = 0;
-        }
+    if (!window && (int64_t)hi - lo < (int64_t)kPageBits * kPageRows) {
+        // The tile's distinct pages as bits (a wider range takes the hash
+        // path).
+        if (p < kPageWords) s_pbits[p] = 0u;
         __syncthreads();
         // A row's neighbours come in offset order, z fastest, so runs of
-        // them share a page: each run inserts (and later probes) once.
+        // them share a page: each run sets its bit once.
         int32_t last_pg = -1;
 #pragma unroll
         for (int k = 0; k < 32; ++k) {
@@ -950,37 +954,34 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
             const int32_t pg = (int32_t)((uint32_t)(v[k] - lo) >> kPageShift);
             if (pg == last_pg) continue;
             last_pg = pg;
-            uint32_t h = ((uint32_t)pg * 0x9E3779B1u) >> 26;  // 6 bits: kPageSlots slots
-            bool placed = false;
-            for (int probe = 0; probe < kPageSlots && !placed; ++probe) {
-                int32_t cur = s_pkey[h];
-                if (cur == -1) {
-                    cur = atomicCAS(&s_pkey[h], -1, pg);
-                    if (cur == -1) atomicAdd(&s_npages, 1);
-                }
-                if (cur == -1 || cur == pg) placed = true;
-                h = (h + 1) & (kPageSlots - 1);
+            atomicOr(&s_pbits[pg >> 5], 1u << (pg & 31));
+        }
+        __syncthreads();
+        if (p < kPageWords) {
+            // lanes 0..31 of wave 0: the words' exclusive prefix of set bits,
+            // and the page ids in rank order (while they fit kPages)
+            const uint32_t w = s_pbits[p];
+            const int c = __builtin_popcount(w);
+            int pre = c;
+#pragma unroll
+            for (int off = 1; off < kPageWords; off <<= 1) {
+                const int y = __shfl_up(pre, off, kPageWords);
+                if (p >= off) pre += y;
             }
-            if (!placed) s_pfull = 1;
+            pre -= c;
+            s_ppre[p] = pre;
+            uint32_t rest = w;
+            for (int r = pre; rest != 0u; ++r) {
+                const int b = __builtin_ctz(rest);
+                rest &= rest - 1u;
+                if (r < kPages) s_pid[r] = p * 32 + b;
+            }
+            if (p == kPageWords - 1) s_npages = pre + c;
         }
         __syncthreads();
         np = s_npages;
-        paged = !s_pfull && np <= kPages;
+        paged = np <= kPages;
         if (paged) {
-            // pages in increasing id order: rank = occupied slots with a smaller id
-            if (p < kPageSlots) {
-                const int32_t key = s_pkey[p];
-                if (key >= 0) {
-                    int r = 0;
-                    for (int q = 0; q < kPageSlots; ++q) {
-                        const int32_t o = s_pkey[q];
-                        r += (o >= 0 && o < key);
-                    }
-                    s_prank[p] = r;
-                    s_pid[r] = key;
-                }
-            }
-            __syncthreads();
             // position: page rank * kPageRows + the row's offset in its page
             int32_t run_pg = -1, run_rank = 0;
 #pragma unroll
@@ -989,10 +990,8 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
                 const uint32_t d = (uint32_t)(v[k] - lo);
                 const int32_t pg = (int32_t)(d >> kPageShift);
                 if (pg != run_pg) {
-                    uint32_t h = ((uint32_t)pg * 0x9E3779B1u) >> 26;
-                    for (int probe = 0; probe < kPageSlots && s_pkey[h] != pg; ++probe) h = (h + 1) & (kPageSlots - 1);
                     run_pg = pg;
-                    run_rank = s_prank[h];
+                    run_rank = s_ppre[pg >> 5] + __builtin_popcount(s_pbits[pg >> 5] & ((1u << (pg & 31)) - 1u));
                 }
                 v[k] = (run_rank << kPageShift) | (int32_t)(d & (kPageRows - 1));
             }
