@@ -52,6 +52,27 @@ def parse():
     return ap.parse_args()
 
 
+def queued_ms(fn, iters, warmup=2):
+    """GPU time per call of `fn` with the host's per-call cost taken out:
+    the calls are enqueued behind a ~2 ms spin kernel (torch.cuda._sleep), so
+    by the time the start event is reached every call is already queued and
+    the GPU runs them back to back.  For calls whose kernels take less time
+    than the host needs to issue them (small inputs, Python in the loop)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    torch.cuda._sleep(5_000_000)
+    s.record()
+    for _ in range(iters):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / iters
+
+
 def events_ms(fn, iters, warmup=0):
     import torch
     for _ in range(warmup):
@@ -324,13 +345,20 @@ def config_components(dev, st=None, steps: int = 5):
     pc_t, mask_t = pc[:256].contiguous(), mask_u8[:256].contiguous()
     sbuf_t = F.SubdivisionBuffers(256, dev)
     ms_sub_floor = events_ms(lambda: F.subdivision_launch(pc_t, mask=mask_t, buffers=sbuf_t), steps, 2)
+    # the same two launches with the calls queued ahead of the GPU
+    ms_sub_gpu = queued_ms(lambda: F.subdivision_launch(pc, mask=mask_u8, buffers=sbuf), steps)
+    ms_sub_floor_gpu = queued_ms(lambda: F.subdivision_launch(pc_t, mask=mask_t, buffers=sbuf_t), steps)
     out["c2s_compaction"] = {"parents": P, "children": A, "ms": ms_sub,
                              "gbps": sub_bytes / (ms_sub * 1e-3) / 1e9,
                              "frac_hbm": sub_bytes / (ms_sub * 1e-3) / 8e12,
                              "ms_256_parents": ms_sub_floor,
+                             "gpu_ms": ms_sub_gpu, "gpu_ms_256_parents": ms_sub_floor_gpu,
+                             "gpu_gbps": sub_bytes / (ms_sub_gpu * 1e-3) / 1e9,
+                             "gpu_frac_hbm": sub_bytes / (ms_sub_gpu * 1e-3) / 8e12,
                              "call_ms": ms_call,
                              "note": "ms: the two launches back to back, buffers preallocated (events); ms_256_parents: the "
-                                     "same call on 256 parents; "
+                                     "same call on 256 parents; gpu_ms: the calls queued behind a spin kernel, so the "
+                                     "host's per-call cost is taken out; "
                                      "call_ms: the Python call, which allocates and reads the child count back"}
 
     # ConvNeXt block (conv -> LN(affine) -> mlp_0 -> SiLU -> mlp_2 + x) at
@@ -602,10 +630,15 @@ def main():
     plan_tb = lambda: F.conv_plan_build_into(st.cfg, cd_t, nbr_t, plan_t)
     ms_map_floor = events_ms(map_t, args.steps, wu)
     ms_plan_floor = events_ms(plan_tb, args.steps, wu)
+    # the same with the calls queued ahead of the GPU: the kernels' own floor
+    ms_map_floor_gpu = queued_ms(map_t, args.steps)
+    ms_plan_floor_gpu = queued_ms(plan_tb, args.steps)
+    ms_map_gpu = queued_ms(map_build, args.steps)
     floor_modes = (F.neighbor_map_table_mode(ws_t), F.neighbor_map_table_mode(ws))
     print(f"[bench] step {ms_step:.3f} ms  map+plan {ms_map_plan:.3f}  conv1 {ms_conv1:.3f}  "
           f"conv2 {ms_conv2:.3f}  (alone: map {ms_map:.3f}  plan {ms_plan:.3f}  unfused ln {ms_ln:.3f}; "
-          f"on {n_t} rows: map {ms_map_floor:.3f}  plan {ms_plan_floor:.3f}, table {floor_modes[0]} / {floor_modes[1]})",
+          f"on {n_t} rows: map {ms_map_floor:.3f}  plan {ms_plan_floor:.3f}, queued {ms_map_floor_gpu:.3f} / "
+          f"{ms_plan_floor_gpu:.3f}, map queued {ms_map_gpu:.3f}; table {floor_modes[0]} / {floor_modes[1]})",
           file=sys.stderr, flush=True)
 
     flops = 2.0 * P * C * C
@@ -659,6 +692,8 @@ def main():
             "unfused_ln_silu_ms": ms_ln,
             "map_build_gbps": map_gbps, "map_build_frac_hbm": map_gbps / PEAK_HBM_GBPS,
             "map_build_256_rows_ms": ms_map_floor, "plan_build_256_rows_ms": ms_plan_floor,
+            "map_build_queued_ms": ms_map_gpu, "map_build_256_rows_queued_ms": ms_map_floor_gpu,
+            "plan_build_256_rows_queued_ms": ms_plan_floor_gpu,
             "conv_useful_tflops": conv_tflops,
             "conv_issued_tflops_dense27": 2.0 * n * 27 * C * C / (ms_conv * 1e-3) / 1e12,
         },
