@@ -49,8 +49,8 @@ struct ConvArgs {
     // Weights packed by sc_conv_weight_pack (the halo-staged kernel's layout),
     // starting with their PackHeader.
     const void *wpack;
-    // Header of the plan whose order / tile list the direct kernel follows
-    // (checked against the call's shape before anything else is read).
+    // Header of the plan a planned launch reads (the dense kernel's linear
+    // child plan checks it against the call's shape before anything else).
     const PlanHeader *plan_hdr;
     // LayerNorm over consecutive groups of ln_group channels: the row's
     // Cout, or one child's scatter_ch (64 or 128) in the C2S scatter.

@@ -43,7 +43,8 @@
 //                an LDS bitmap over the tile's neighbour row range (the usual
 //                case) or, for a wide range, an LDS hash table and a bitonic
 //                sort.  Tiles whose halo exceeds kPlanHaloMax are listed in
-//                `overflow` for the direct kernel.
+//                `overflow` (the conv gathers their operands from global
+//                memory; the list is a diagnostic).
 #include <climits>
 
 #include "sc_common.hpp"
@@ -55,7 +56,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kTileThreads = kPlanTileRows;  // plan_tiles_kernel: one thread per tile row
 // Tile hash table: a tile with more than kPlanHaloMax distinct neighbours
-// overflows to the direct kernel, so insertion stops past that many keys and
+// gets no halo (the conv gathers its operands), so insertion stops past that many keys and
 // 2048 slots (load factor < 1/2 for a tile that fits) suffice.
 constexpr int kHashBits = 11;
 constexpr int kHashSlots = 1 << kHashBits;
@@ -1035,7 +1036,7 @@ __global__ __launch_bounds__(kTileThreads) void plan_tiles_kernel(PlanArgs a)
             a.tile_u[t] = U;
             if (U > kPlanHaloMax && !a.tile_list) a.overflow[atomicAdd(&a.hdr->n_overflow, 1)] = (int32_t)t;
         }
-        if (U > kPlanHaloMax) return;  // handled by the direct-gather kernel
+        if (U > kPlanHaloMax) return;  // no halo: the conv gathers this tile's operands
         __syncthreads();
         // Each neighbour's rank is its local index; its row goes to that
         // halo slot (neighbours shared by several rows write the same row).
