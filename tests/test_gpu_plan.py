@@ -352,6 +352,61 @@ def test_planned_ln_silu_and_residual(oracle, affine, cin, cout):
     assert_close(out2.cpu().numpy(), exp2, 2e-5, "planned residual")
 
 
+def spread_neighbour_coords(spacing, far=0):
+    """One tile of 256 query centres (batch 0, x = 3i), each with two
+    neighbours ((3i+1, 0, 0) and (3i, 1, 0)) stored `spacing` rows apart after
+    the centres, the second half of them `far` rows further on; every other
+    row is a filler of batch 1 (unique coords, no neighbour of a centre).  The
+    tile's 768 distinct neighbour rows then span as many rows, and as many
+    4,096-row pages, as the spacing makes them."""
+    n_c = 256
+    nb = np.zeros((2 * n_c, 4), np.int32)
+    nb[0::2, 1] = 3 * np.arange(n_c) + 1
+    nb[1::2, 1] = 3 * np.arange(n_c)
+    nb[1::2, 2] = 1
+    rows = n_c + np.arange(2 * n_c, dtype=np.int64) * spacing
+    rows[n_c:] += far
+    total = int(rows[-1]) + 1
+    i = np.arange(total, dtype=np.int64)
+    coords = np.stack([np.ones(total, np.int64), i & 1023, (i >> 10) & 1023, i >> 20], 1).astype(np.int32)
+    coords[:n_c] = 0
+    coords[:n_c, 1] = 3 * np.arange(n_c)
+    coords[rows] = nb
+    return coords
+
+
+@pytest.mark.parametrize("spacing,far,conv", [(200, 0, True), (1, 200_000, True), (2000, 0, True),
+                                              (1, 4_500_000, False)])
+def test_plan_tile_neighbour_spans(oracle, spacing, far, conv):
+    """The tile kernel's three ways of numbering a tile's distinct neighbour
+    rows, forced by where those rows lie: within the LDS bitmap's 131,072-row
+    window (spacing 200), beyond it in two clusters a few pages wide (the
+    paged bitmap), spread over ~250 pages (more than the paged bitmap's 32:
+    the hash table and sort), and in two clusters more than 4 M rows apart
+    (past the page bitmap's range: the hash table).  The plan against the map
+    it was built from, and the planned conv against the fp64 definition."""
+    coords = spread_neighbour_coords(spacing, far)
+    cfg = F.SparseSubmConvConfig(32, 32)
+    cd = dev(coords)
+    nbr = F.neighbor_rows_tensor_from_coords_tensor(cfg, cd, query_rows=256)
+    plan = F.build_conv_plan(cfg, cd, nbr)
+    nb = nbr.cpu().numpy()
+    assert (nb >= 0).sum() == 3 * 256  # each centre: itself and two neighbours
+    h = check_plan(plan, nb, len(coords))
+    assert h["n_tiles"] == 1 and h["tile_u"][0] == 768
+    if not conv:
+        return
+    rng = np.random.default_rng(spacing + far)
+    x = rbf(synth.normal_f32(rng, (len(coords), 32)))
+    w = rbf(synth.conv_weight(rng, 32, 27, 32, 0.05))
+    b = synth.normal_f32(rng, 32, 0.1)
+    xd, wd = bf16_dev(x), bf16_dev(w)
+    out = F.sparse_subm_conv_forward(cfg, xd, nbr, wd, dev(b), plan=plan, packed_weight=F.pack_conv_weight(cfg, wd),
+                                     out_dtype=torch.float32)
+    exp = oracle.conv_ref_f64(ocfg(oracle, cfg), w, b, x, nb)
+    assert_close(out.cpu().numpy(), exp, 2e-5, f"neighbour span {spacing}/{far}")
+
+
 def test_planned_conv_on_own_order(oracle):
     """The planned conv on rows that keep their own order (3 levels of C2S
     children, 170 k rows) equals the oracle on 2,000 sampled rows and the
