@@ -92,6 +92,41 @@ def test_f16_planned_few_offsets_and_rows(oracle, kernel, n, cout):
     assert_close(host(got), exp, TOL_BF16, f"f16 planned conv, kernel {kernel}, {n} rows")
 
 
+@pytest.mark.parametrize("cout", [64, 128])
+def test_f16_planned_overflow_tiles(oracle, cout):
+    """The f16 tile with some tiles over the halo budget (cluster centres
+    whose 26 neighbours are all distinct): those tiles gather their operands
+    from global memory in the same launch; every row against the fp64
+    definition, both tile widths."""
+    side = 7
+    g = np.stack(np.meshgrid(*[np.arange(side)] * 3, indexing="ij"), -1).reshape(-1, 3)[:300]
+    centres = 200 + 3 * g
+    offs = np.stack(np.meshgrid(*[np.arange(-1, 2)] * 3, indexing="ij"), -1).reshape(-1, 3)
+    offs = offs[np.any(offs != 0, axis=1)]
+    nb = (centres[:, None, :] + offs[None]).reshape(-1, 3)
+    shell = synth.config1_coords()[:3000]
+    xyz = np.concatenate([centres, nb])
+    cl = np.concatenate([np.zeros((len(xyz), 1), np.int32), xyz.astype(np.int32)], 1)
+    coords = np.ascontiguousarray(np.concatenate([shell, cl[:300], cl[300:]]))
+    q = 3300
+    rng = np.random.default_rng(cout + 5)
+    cin = 64
+    x = _fence(oracle, synth.normal_f32(rng, (len(coords), cin)))
+    w = _fence(oracle, synth.conv_weight(rng, cout, 27, cin, 1 / np.sqrt(27 * cin)))
+    b = synth.normal_f32(rng, cout, 0.1)
+    cfg = F.SparseSubmConvConfig(cin, cout)
+    cd = dev(coords)
+    nbr = F.neighbor_rows_tensor_from_coords_tensor(cfg, cd, query_rows=q)
+    plan = F.build_conv_plan(cfg, cd, nbr)
+    h = plan.to_host()
+    assert 0 < h["n_overflow"] < h["n_tiles"]
+    wd = f16_dev(w)
+    got = F.sparse_subm_conv_forward(cfg, f16_dev(x), nbr, wd, dev(b), out_dtype=torch.float32,
+                                     plan=plan, packed_weight=F.pack_conv_weight(cfg, wd))
+    exp = oracle.conv_gemm_f64(oracle.OracleConfig(cin, cout), w, b, x, nbr.cpu().numpy())
+    assert_close(host(got), exp, 2e-5, f"f16 planned conv with overflow tiles, Cout {cout}")
+
+
 def test_config2_conv_f16_planned(oracle):
     """Config 2's shape (113,857 voxels, C = 256) in f16 through the planned
     conv, 2,000 sampled rows (first / last / overflow tiles included)."""
